@@ -1,0 +1,148 @@
+/*
+ * pe_attn.h -- C ABI of the MI355X (gfx950) positional-encoding attention library (libpe_attn.so).
+ *
+ * Fused causal attention, forward and backward, for PoPE / FoPE / RoPE(NTK, YaRN) / no-PE.  The
+ * positional transform (softplus magnitude + polar phase, or the interleaved rotation) is applied
+ * by the library; callers hand over the raw projections.  Plain C types only: device pointers,
+ * sizes, strides, a hipStream_t passed as void*.  The library never allocates, frees or
+ * synchronises: the caller owns every output and the workspace, and every call is asynchronous
+ * on the given stream.  All functions return 0 or a negative PE_ERR_* code.
+ *
+ * Which reference interface each entry point replaces (shyampathak22/pe_ablations):
+ *   pe_attn_fwd  -- PoPEEmbedding.forward_query/forward_key (src/model/pope.py:124-183) or
+ *                   FoPEPoPEEmbedding.forward_query/forward_key (src/model/fpope.py:266-338), the
+ *                   content|position concat, GQA repeat_interleave and the causal
+ *                   F.scaled_dot_product_attention call of FPoPEGroupedQueryAttention.forward
+ *                   (src/model/fpope_attention.py:145-177); for RoPE the apply_rotary_emb +
+ *                   QKNorm + SDPA span of GroupedQueryAttention.forward (src/model/attention.py:69-96,
+ *                   src/model/rope.py:35-57,209-217); and the removed fused kernel entry
+ *                   triton_fpope_attention(q,k,v,freqs,bias,start_pos,return_lse=True)
+ *                   (scripts/diagnose_kernel.py:180-188) / fpope_attention_forward
+ *                   (tests/test_fpope.py:222-226).
+ *   pe_attn_bwd  -- the autograd backward of that span (torch SDPA backward + the eager transform's
+ *                   backward), i.e. the removed _fpope_attention_bwd_kernel_{dk,dq,dv} launches and
+ *                   their host-side partial reduction (scripts/debug_backward.py:118-197,226-227).
+ */
+#ifndef PE_ATTN_H
+#define PE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PE_ATTN_ABI_VERSION 1
+
+/* positional-encoding mode */
+enum {
+  PE_MODE_POPE = 0, /* PoPE / FoPE: x -> [mu cos(pos*freq (+delta)), mu sin(...)], mu = softplus  */
+  PE_MODE_ROPE = 1, /* RoPE / NTK / YaRN: interleaved pairs rotated by pos*inv_freq, times mscale */
+  PE_MODE_NONE = 2  /* no positional transform (reference pe_mode "nope", or fpope=None modules) */
+};
+
+/* element types of tensors crossing the boundary */
+enum { PE_DTYPE_BF16 = 0, PE_DTYPE_FP32 = 1 };
+
+/* causal masking: key s visible to query t iff s <= t + off */
+enum {
+  PE_CAUSAL_NONE = 0,
+  PE_CAUSAL_TOP_LEFT = 1,    /* off = 0: SDPA is_causal (src/model/fpope_attention.py:171-177) */
+  PE_CAUSAL_BOTTOM_RIGHT = 2 /* off = Sk - Sq: KV-cache mask (src/model/fpope_attention.py:313-317) */
+};
+
+/* error codes */
+enum {
+  PE_OK = 0,
+  PE_ERR_NULL = -1,          /* required pointer is NULL */
+  PE_ERR_SHAPE = -2,         /* non-positive size, Hq % Hkv != 0, Sq != Sk for top-left causal, ... */
+  PE_ERR_HEAD_DIM = -3,      /* transformed q/k width or value width outside what the kernels tile */
+  PE_ERR_MODE = -4,          /* unknown mode / dtype / causal value, odd RoPE width */
+  PE_ERR_STRIDE = -5,        /* last-dim stride != 1 or misaligned base pointer */
+  PE_ERR_WORKSPACE = -6,     /* workspace NULL or smaller than pe_attn_*_workspace_bytes */
+  PE_ERR_LAUNCH = -7,        /* a kernel launch failed (hipGetLastError) */
+  PE_ERR_NO_DEVICE = -8      /* no gfx950 device is current */
+};
+
+/* A (B, H, S, D) tensor view: device pointer, element type, element strides in (B, H, S, D)
+ * order.  stride[3] must be 1. */
+typedef struct {
+  const void* data;
+  int32_t dtype;
+  int32_t reserved;
+  int64_t stride[4];
+} pe_tensor_t;
+
+typedef struct {
+  int32_t B, Hq, Hkv, Sq, Sk;
+  int32_t Dc;     /* content (pass-through) dims ahead of the positional part; 0 in the fused form   */
+  int32_t Dr;     /* positional dims before the transform (PoPE adds 2*Dr to the QK width, RoPE Dr) */
+  int32_t Dv;     /* value / output head width                                                       */
+  int32_t mode;   /* PE_MODE_*                                                                       */
+  int32_t dtype;  /* compute dtype of the transformed operands, the output and dV: PE_DTYPE_*       */
+  int32_t causal; /* PE_CAUSAL_*                                                                     */
+  int32_t start_pos_q, start_pos_k; /* absolute position of row 0 (phases only)                      */
+  int32_t qk_l2norm;                /* QKNorm x / (||x|| + 1e-6) after the transform (RoPE / NONE)   */
+  float scale;                      /* softmax scale applied to q~ . k~                              */
+  float rope_mscale;                /* YaRN mscale multiplying rotated q and k (1 otherwise)         */
+  int64_t delta_head_stride;        /* PoPE key phase bias: 0 = (Dr,) shared, else per kv head     */
+} pe_attn_params;
+
+/* Host-only validation of a parameter block (no device work). */
+int pe_attn_check(const pe_attn_params* p);
+
+/* Bytes of caller-provided device workspace each pass needs (0 on invalid params).  The forward
+ * workspace holds the transformed operands; pass the SAME, unmodified forward workspace to
+ * pe_attn_bwd. */
+size_t pe_attn_fwd_workspace_bytes(const pe_attn_params* p);
+size_t pe_attn_bwd_workspace_bytes(const pe_attn_params* p);
+
+/* Forward.  qc/kc: content parts (data may be NULL when Dc == 0); qr/kr: positional parts
+ * (B,Hq|Hkv,S,Dr); v (B,Hkv,Sk,Dv).  freqs: PoPE/FoPE per-dim frequency (Dr,) or RoPE inverse
+ * frequency (Dr/2,), fp32; delta: PoPE key phase bias as used (already clamped by the caller),
+ * NULL for none.  out (B,Hq,Sq,Dv) in p->dtype, written through its strides; lse (B,Hq,Sq) fp32
+ * natural-log logsumexp of the scaled scores (-inf for a row with no visible key). */
+int pe_attn_fwd(const pe_attn_params* p,
+                const pe_tensor_t* qc, const pe_tensor_t* qr,
+                const pe_tensor_t* kc, const pe_tensor_t* kr,
+                const pe_tensor_t* v,
+                const float* freqs, const float* delta,
+                const pe_tensor_t* out, float* lse,
+                void* fwd_workspace, size_t fwd_ws_bytes, void* stream);
+
+/* Backward.  Inputs as for pe_attn_fwd plus out/lse from it and dout (B,Hq,Sq,Dv).  Gradients are
+ * written through the tensor views dqc/dqr/dkc/dkr (same shapes and dtypes as the inputs;
+ * dqc/dkc data may be NULL when Dc == 0) and dv (dtype p->dtype).  dfreqs (Dr,) and ddelta
+ * (Dr,) or (Hkv, Dr) are fp32 and overwritten; either may be NULL to skip it. */
+int pe_attn_bwd(const pe_attn_params* p,
+                const pe_tensor_t* qc, const pe_tensor_t* qr,
+                const pe_tensor_t* kc, const pe_tensor_t* kr,
+                const pe_tensor_t* v,
+                const float* freqs, const float* delta,
+                const pe_tensor_t* out, const float* lse, const pe_tensor_t* dout,
+                const pe_tensor_t* dqc, const pe_tensor_t* dqr,
+                const pe_tensor_t* dkc, const pe_tensor_t* dkr,
+                const pe_tensor_t* dv,
+                float* dfreqs, float* ddelta,
+                const void* fwd_workspace, size_t fwd_ws_bytes,
+                void* bwd_workspace, size_t bwd_ws_bytes, void* stream);
+
+/* Elementwise positional prologue on its own (the HBM-bound half of the forward): writes the
+ * transformed rows [content | transform | zero pad] of x into dst (B,H,S,width) contiguous in
+ * p->dtype, width = pe_attn_operand_width(p).  is_key selects the key phase bias.  Replaces
+ * forward_query / forward_key (src/model/pope.py:124-183) as a standalone op. */
+int pe_attn_transform(const pe_attn_params* p, int is_key,
+                      const pe_tensor_t* xc, const pe_tensor_t* xr,
+                      const float* freqs, const float* delta,
+                      void* dst, void* stream);
+int pe_attn_operand_width(const pe_attn_params* p);
+
+const char* pe_attn_strerror(int code);
+int pe_attn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PE_ATTN_H */

@@ -1,0 +1,308 @@
+// C-ABI entry points of libpe_attn.so (declared in include/pe_attn.h).  Host code only: validates
+// the parameter block, carves the caller's workspace and enqueues the kernels on the caller's
+// stream.  No allocation, no synchronisation, no global mutable state beyond a per-device
+// "is this a gfx950" flag computed once.
+#include <hip/hip_runtime.h>
+#include <string.h>
+#include <mutex>
+
+#include "../../include/pe_attn.h"
+#include "pe_internal.h"
+
+namespace {
+
+constexpr size_t ALIGN = 256;
+inline size_t align_up(size_t x) { return (x + ALIGN - 1) / ALIGN * ALIGN; }
+constexpr int INV_ROWS = 256;  // rows per inverse-transform block
+
+int qk_width(const pe_attn_params* p) {
+  return p->Dc + (p->mode == PE_MODE_POPE ? 2 * p->Dr : p->Dr);
+}
+int pad_qk(int w) { return w <= 64 ? 64 : w <= 128 ? 128 : w <= 256 ? 256 : -1; }
+int pad_v(int d) { return d <= 64 ? 64 : d <= 128 ? 128 : -1; }
+size_t esz(const pe_attn_params* p) { return p->dtype == PE_DTYPE_BF16 ? 2 : 4; }
+
+struct Layout {
+  int dqk, dv;
+  size_t q_off, k_off, v_off, fwd_total;
+  size_t do_off, di_off, dq_off, dk_off, pq_off, pk_off, pkd_off, bwd_total;
+  int nq_blocks, nk_blocks;
+};
+
+Layout layout(const pe_attn_params* p) {
+  Layout L{};
+  L.dqk = pad_qk(qk_width(p));
+  L.dv = pad_v(p->Dv);
+  const size_t e = esz(p);
+  const size_t nq = (size_t)p->B * p->Hq * p->Sq, nk = (size_t)p->B * p->Hkv * p->Sk;
+  L.q_off = 0;
+  L.k_off = L.q_off + align_up(nq * L.dqk * e);
+  L.v_off = L.k_off + align_up(nk * L.dqk * e);
+  L.fwd_total = L.v_off + align_up(nk * L.dv * e);
+  L.nq_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hq, p->Sq, INV_ROWS) : 0;
+  L.nk_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hkv, p->Sk, INV_ROWS) : 0;
+  L.do_off = 0;
+  L.di_off = L.do_off + align_up(nq * L.dv * e);
+  L.dq_off = L.di_off + align_up(nq * 4);
+  L.dk_off = L.dq_off + align_up(nq * L.dqk * 4);
+  L.pq_off = L.dk_off + align_up(nk * L.dqk * 4);
+  L.pk_off = L.pq_off + align_up((size_t)L.nq_blocks * p->Dr * 4);
+  L.pkd_off = L.pk_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
+  L.bwd_total = L.pkd_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
+  return L;
+}
+
+int check_tensor(const pe_tensor_t* t, bool required) {
+  if (!t) return required ? PE_ERR_NULL : PE_OK;
+  if (!t->data) return required ? PE_ERR_NULL : PE_OK;
+  if (t->dtype != PE_DTYPE_BF16 && t->dtype != PE_DTYPE_FP32) return PE_ERR_MODE;
+  if (t->stride[3] != 1) return PE_ERR_STRIDE;
+  return PE_OK;
+}
+
+int device_ok() {
+  static int flags[64];  // 0 unknown, 1 gfx950, 2 other
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return PE_ERR_NO_DEVICE;
+  if (dev >= 64) return PE_OK;
+  std::lock_guard<std::mutex> lk(mu);
+  if (flags[dev] == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return PE_ERR_NO_DEVICE;
+    flags[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+  }
+  return flags[dev] == 1 ? PE_OK : PE_ERR_NO_DEVICE;
+}
+
+bool v_direct(const pe_attn_params* p, const pe_tensor_t* v, int dvp) {
+  const int64_t e = (int64_t)esz(p);
+  return v->dtype == p->dtype && p->Dv == dvp && ((uintptr_t)v->data % 16) == 0 &&
+         (v->stride[0] * e) % 16 == 0 && (v->stride[1] * e) % 16 == 0 && (v->stride[2] * e) % 16 == 0;
+}
+
+void fill_prep(pe::PrepArgs& a, const pe_attn_params* p, int is_key, const pe_tensor_t* xc,
+               const pe_tensor_t* xr, const float* freqs, const float* delta, void* dst, int width) {
+  memset(&a, 0, sizeof(a));
+  if (xc && xc->data) {
+    a.xc = xc->data; a.xc_dtype = xc->dtype;
+    for (int i = 0; i < 4; ++i) a.xc_s[i] = xc->stride[i];
+  }
+  a.xr = xr->data; a.xr_dtype = xr->dtype;
+  for (int i = 0; i < 4; ++i) a.xr_s[i] = xr->stride[i];
+  a.dst = dst; a.dst_dtype = p->dtype; a.width = width;
+  a.B = p->B; a.H = is_key ? p->Hkv : p->Hq; a.S = is_key ? p->Sk : p->Sq;
+  a.Dc = p->Dc; a.Dr = p->Dr; a.mode = p->mode;
+  a.start_pos = is_key ? p->start_pos_k : p->start_pos_q;
+  a.l2norm = p->qk_l2norm; a.is_key = is_key;
+  a.freqs = freqs; a.delta = delta; a.delta_hs = p->delta_head_stride;
+  a.mscale = p->rope_mscale;
+}
+
+pe::CoreArgs core_args(const pe_attn_params* p, const Layout& L, const char* ws,
+                       const pe_tensor_t* v) {
+  pe::CoreArgs c;
+  memset(&c, 0, sizeof(c));
+  c.q = ws + L.q_off;
+  c.k = ws + L.k_off;
+  if (v_direct(p, v, L.dv)) {
+    c.v = v->data; c.v_sb = v->stride[0]; c.v_sh = v->stride[1]; c.v_ss = v->stride[2];
+  } else {
+    c.v = ws + L.v_off; c.v_ss = L.dv; c.v_sh = (int64_t)p->Sk * L.dv; c.v_sb = (int64_t)p->Hkv * p->Sk * L.dv;
+  }
+  c.B = p->B; c.Hq = p->Hq; c.Hkv = p->Hkv; c.Sq = p->Sq; c.Sk = p->Sk;
+  c.dv_real = p->Dv;
+  c.causal = p->causal != PE_CAUSAL_NONE;
+  c.causal_off = p->causal == PE_CAUSAL_BOTTOM_RIGHT ? p->Sk - p->Sq : 0;
+  c.scale = p->scale;
+  return c;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pe_attn_version(void) { return PE_ATTN_ABI_VERSION; }
+
+const char* pe_attn_strerror(int code) {
+  switch (code) {
+    case PE_OK: return "success";
+    case PE_ERR_NULL: return "pe_attn: a required pointer is NULL";
+    case PE_ERR_SHAPE: return "pe_attn: invalid shape (sizes must be positive, Hq divisible by Hkv, Sq <= Sk for bottom-right causal)";
+    case PE_ERR_HEAD_DIM: return "pe_attn: unsupported head width (transformed q/k width must be <= 256, value width <= 128, PoPE dims <= 256)";
+    case PE_ERR_MODE: return "pe_attn: invalid mode, dtype or causal flag (RoPE needs an even width)";
+    case PE_ERR_STRIDE: return "pe_attn: last-dimension stride must be 1";
+    case PE_ERR_WORKSPACE: return "pe_attn: workspace missing or too small";
+    case PE_ERR_LAUNCH: return "pe_attn: kernel launch failed";
+    case PE_ERR_NO_DEVICE: return "pe_attn: current device is not an MI355X (gfx950)";
+    default: return "pe_attn: unknown error";
+  }
+}
+
+int pe_attn_check(const pe_attn_params* p) {
+  if (!p) return PE_ERR_NULL;
+  if (p->B <= 0 || p->Hq <= 0 || p->Hkv <= 0 || p->Sq <= 0 || p->Sk <= 0 || p->Dv <= 0 || p->Dr < 0 || p->Dc < 0)
+    return PE_ERR_SHAPE;
+  if (p->Hq % p->Hkv != 0) return PE_ERR_SHAPE;
+  if (p->mode < 0 || p->mode > 2 || (p->dtype != PE_DTYPE_BF16 && p->dtype != PE_DTYPE_FP32) || p->causal < 0 || p->causal > 2)
+    return PE_ERR_MODE;
+  if (p->mode != PE_MODE_POPE && (p->Dr % 2) != 0) return PE_ERR_MODE;
+  if (p->causal == PE_CAUSAL_BOTTOM_RIGHT && p->Sq > p->Sk) return PE_ERR_SHAPE;
+  if (p->causal == PE_CAUSAL_TOP_LEFT && p->Sq != p->Sk) return PE_ERR_SHAPE;
+  if (qk_width(p) <= 0 || pad_qk(qk_width(p)) < 0 || pad_v(p->Dv) < 0) return PE_ERR_HEAD_DIM;
+  if (p->Dr > 256 || (p->mode != PE_MODE_POPE && p->Dr > 2 * 64 * 4)) return PE_ERR_HEAD_DIM;
+  if (!pe::core_supported(pad_qk(qk_width(p)), pad_v(p->Dv))) return PE_ERR_HEAD_DIM;
+  return PE_OK;
+}
+
+int pe_attn_operand_width(const pe_attn_params* p) {
+  if (pe_attn_check(p) != PE_OK) return -1;
+  return pad_qk(qk_width(p));
+}
+
+size_t pe_attn_fwd_workspace_bytes(const pe_attn_params* p) {
+  if (pe_attn_check(p) != PE_OK) return 0;
+  return layout(p).fwd_total;
+}
+
+size_t pe_attn_bwd_workspace_bytes(const pe_attn_params* p) {
+  if (pe_attn_check(p) != PE_OK) return 0;
+  return layout(p).bwd_total;
+}
+
+int pe_attn_transform(const pe_attn_params* p, int is_key, const pe_tensor_t* xc, const pe_tensor_t* xr,
+                      const float* freqs, const float* delta, void* dst, void* stream) {
+  int rc = pe_attn_check(p);
+  if (rc) return rc;
+  if ((rc = check_tensor(xr, p->Dr > 0))) return rc;
+  if ((rc = check_tensor(xc, p->Dc > 0))) return rc;
+  if (!dst || (p->mode != PE_MODE_NONE && p->Dr > 0 && !freqs)) return PE_ERR_NULL;
+  if ((rc = device_ok())) return rc;
+  pe::PrepArgs a;
+  fill_prep(a, p, is_key, xc, xr, freqs, delta, dst, pad_qk(qk_width(p)));
+  return pe::launch_prep(a, (hipStream_t)stream);
+}
+
+int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,
+                void* fwd_workspace, size_t fwd_ws_bytes, void* stream) {
+  int rc = pe_attn_check(p);
+  if (rc) return rc;
+  if ((rc = check_tensor(qr, p->Dr > 0)) || (rc = check_tensor(kr, p->Dr > 0)) ||
+      (rc = check_tensor(qc, p->Dc > 0)) || (rc = check_tensor(kc, p->Dc > 0)) ||
+      (rc = check_tensor(v, true)) || (rc = check_tensor(out, true)))
+    return rc;
+  if (!lse || (p->mode != PE_MODE_NONE && p->Dr > 0 && !freqs)) return PE_ERR_NULL;
+  if (out->dtype != p->dtype) return PE_ERR_MODE;
+  const Layout L = layout(p);
+  if (!fwd_workspace || fwd_ws_bytes < L.fwd_total) return PE_ERR_WORKSPACE;
+  if ((rc = device_ok())) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)fwd_workspace;
+
+  pe::PrepArgs a;
+  fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
+  if ((rc = pe::launch_prep(a, s))) return rc;
+  fill_prep(a, p, 1, kc, kr, freqs, delta, ws + L.k_off, L.dqk);
+  if ((rc = pe::launch_prep(a, s))) return rc;
+  if (!v_direct(p, v, L.dv)) {
+    pe_attn_params pv = *p;
+    pv.mode = PE_MODE_NONE; pv.Dc = 0; pv.Dr = p->Dv; pv.qk_l2norm = 0;
+    fill_prep(a, &pv, 1, nullptr, v, nullptr, nullptr, ws + L.v_off, L.dv);
+    if ((rc = pe::launch_prep(a, s))) return rc;
+  }
+  pe::CoreArgs c = core_args(p, L, ws, v);
+  c.o = (void*)out->data; c.o_sb = out->stride[0]; c.o_sh = out->stride[1]; c.o_ss = out->stride[2];
+  c.o_dtype = out->dtype;
+  c.lse = lse;
+  return pe::launch_fwd(p->dtype == PE_DTYPE_BF16 ? 0 : 1, L.dqk, L.dv, c, s);
+}
+
+int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                const float* freqs, const float* delta, const pe_tensor_t* out, const float* lse,
+                const pe_tensor_t* dout, const pe_tensor_t* dqc, const pe_tensor_t* dqr,
+                const pe_tensor_t* dkc, const pe_tensor_t* dkr, const pe_tensor_t* dv,
+                float* dfreqs, float* ddelta, const void* fwd_workspace, size_t fwd_ws_bytes,
+                void* bwd_workspace, size_t bwd_ws_bytes, void* stream) {
+  int rc = pe_attn_check(p);
+  if (rc) return rc;
+  if ((rc = check_tensor(qr, p->Dr > 0)) || (rc = check_tensor(kr, p->Dr > 0)) ||
+      (rc = check_tensor(qc, p->Dc > 0)) || (rc = check_tensor(kc, p->Dc > 0)) ||
+      (rc = check_tensor(v, true)) || (rc = check_tensor(out, true)) || (rc = check_tensor(dout, true)) ||
+      (rc = check_tensor(dqr, p->Dr > 0)) || (rc = check_tensor(dkr, p->Dr > 0)) ||
+      (rc = check_tensor(dqc, p->Dc > 0)) || (rc = check_tensor(dkc, p->Dc > 0)) ||
+      (rc = check_tensor(dv, true)))
+    return rc;
+  if (!lse || (p->mode != PE_MODE_NONE && p->Dr > 0 && !freqs)) return PE_ERR_NULL;
+  const Layout L = layout(p);
+  if (!fwd_workspace || fwd_ws_bytes < L.fwd_total || !bwd_workspace || bwd_ws_bytes < L.bwd_total)
+    return PE_ERR_WORKSPACE;
+  if ((rc = device_ok())) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const char* fws = (const char*)fwd_workspace;
+  char* bws = (char*)bwd_workspace;
+  const int dt = p->dtype == PE_DTYPE_BF16 ? 0 : 1;
+
+  pe::PreBwdArgs pb;
+  memset(&pb, 0, sizeof(pb));
+  pb.dout = dout->data; pb.dout_dtype = dout->dtype;
+  pb.out = out->data; pb.out_dtype = out->dtype;
+  for (int i = 0; i < 4; ++i) { pb.do_s[i] = dout->stride[i]; pb.o_s[i] = out->stride[i]; }
+  pb.dO_op = bws + L.do_off; pb.op_dtype = p->dtype; pb.width = L.dv;
+  pb.Di = (float*)(bws + L.di_off);
+  pb.B = p->B; pb.H = p->Hq; pb.S = p->Sq; pb.Dv = p->Dv;
+  if ((rc = pe::launch_prebwd(pb, s))) return rc;
+
+  pe::CoreArgs c = core_args(p, L, fws, v);
+  c.dO = bws + L.do_off;
+  c.Di = (const float*)(bws + L.di_off);
+  c.lse_in = lse;
+  c.dq_t = (float*)(bws + L.dq_off);
+  c.dk_t = (float*)(bws + L.dk_off);
+  c.dv = (void*)dv->data; c.dv_sb = dv->stride[0]; c.dv_sh = dv->stride[1]; c.dv_ss = dv->stride[2];
+  c.dv_dtype = dv->dtype;
+  if ((rc = pe::launch_bwd(dt, L.dqk, L.dv, c, s))) return rc;
+
+  for (int side = 0; side < 2; ++side) {
+    const bool key = side == 1;
+    const pe_tensor_t* xr = key ? kr : qr;
+    const pe_tensor_t* dxc = key ? dkc : dqc;
+    const pe_tensor_t* dxr = key ? dkr : dqr;
+    pe::InvArgs ia;
+    memset(&ia, 0, sizeof(ia));
+    ia.g = (const float*)(bws + (key ? L.dk_off : L.dq_off));
+    ia.width = L.dqk;
+    if (xr && xr->data) { ia.xr = xr->data; ia.xr_dtype = xr->dtype; for (int i = 0; i < 4; ++i) ia.xr_s[i] = xr->stride[i]; }
+    if (dxc && dxc->data) { ia.dxc = (void*)dxc->data; ia.dxc_dtype = dxc->dtype; for (int i = 0; i < 4; ++i) ia.dxc_s[i] = dxc->stride[i]; }
+    if (dxr && dxr->data) { ia.dxr = (void*)dxr->data; ia.dxr_dtype = dxr->dtype; for (int i = 0; i < 4; ++i) ia.dxr_s[i] = dxr->stride[i]; }
+    ia.B = p->B; ia.H = key ? p->Hkv : p->Hq; ia.S = key ? p->Sk : p->Sq;
+    ia.Dc = p->Dc; ia.Dr = p->Dr; ia.mode = p->mode;
+    ia.start_pos = key ? p->start_pos_k : p->start_pos_q;
+    ia.l2norm = p->qk_l2norm; ia.is_key = key;
+    ia.freqs = freqs; ia.delta = key ? delta : nullptr; ia.delta_hs = p->delta_head_stride;
+    ia.mscale = p->rope_mscale;
+    ia.part_delta = key ? (float*)(bws + L.pkd_off) : nullptr;
+    ia.part_freq = (float*)(bws + (key ? L.pk_off : L.pq_off));
+    ia.rows_per_block = INV_ROWS;
+    if (ia.Dr == 0 && ia.Dc > 0) ia.mode = PE_MODE_NONE;
+    int nb = 0;
+    if ((rc = pe::launch_inv(ia, &nb, s))) return rc;
+  }
+  if (p->mode == PE_MODE_POPE && p->Dr > 0 && (dfreqs || ddelta)) {
+    pe::ReduceArgs ra;
+    memset(&ra, 0, sizeof(ra));
+    ra.part_q_freq = (const float*)(bws + L.pq_off); ra.nq = L.nq_blocks;
+    ra.part_k_freq = (const float*)(bws + L.pk_off); ra.part_k_delta = (const float*)(bws + L.pkd_off);
+    ra.nk = L.nk_blocks;
+    ra.k_blocks_per_head = (p->Sk + INV_ROWS - 1) / INV_ROWS;
+    ra.Hkv = p->Hkv; ra.B = p->B; ra.Dr = p->Dr;
+    ra.delta_per_head = p->delta_head_stride != 0;
+    ra.dfreqs = dfreqs; ra.ddelta = ddelta;
+    if ((rc = pe::launch_reduce(ra, s))) return rc;
+  }
+  return PE_OK;
+}
+
+}  // extern "C"

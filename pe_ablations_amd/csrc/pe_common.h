@@ -1,0 +1,225 @@
+// Device-side building blocks shared by the gfx950 PE-attention kernels.
+//
+// Matrix core layout (v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x2_f32, wave64), lane l, l32 = l%32,
+// g = l/32:
+//   A operand : row l32, contraction elements g*EPL .. g*EPL+EPL-1 of the current KC-wide step
+//   B operand : col l32, same contraction elements
+//   C / D     : 16 floats; value j sits at row (j/4)*8 + g*4 + j%4, col l32
+// Each lane feeds one 16-byte fragment per operand per step: 8 bf16 (KC = 16, one MFMA) or
+// 4 fp32 (KC = 8, four 32x32x2 MFMAs whose contraction pairs are {e, 4+e}).
+//
+// A C tile is turned into the contraction operand of the next product (P -> PV, dS -> dS K) in
+// registers.  For that, value j of lane group g must be contraction element s*EPL + e of step s.
+// fp32 satisfies this directly; for bf16 the A-operand rows of the producing product are loaded
+// with bits 2 and 3 of the row index swapped (perm_row), after which value j of lane group g is
+// logical row c_logical(j, g) = (j/8)*16 + g*8 + j%8.
+//
+// LDS tiles are row-major with 16-byte chunks XOR-swizzled per row.  Operands whose contraction
+// runs along tile rows (V in PV, dO / Q~ / K~ in the gradient products) are read with the gfx950
+// transpose load ds_read_b64_tr_b16: inside each 16-lane group, output lane j, element m is
+// element j%4 of the 8 bytes read by source lane j/4 + 4m.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pe {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+
+// ------------------------------------------------------------------ element conversions
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);  // round-to-nearest-even (v_cvt_pk_bf16_f32)
+}
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+
+// storage element per compute dtype: DT 0 = bf16 (raw uint16), DT 1 = fp32
+template <int DT> struct Elem;
+template <> struct Elem<0> { using T = uint16_t; };
+template <> struct Elem<1> { using T = float; };
+
+__device__ __forceinline__ float load_as_float(const void* p, int64_t i, int dtype) {
+  return dtype == 0 ? bf2f(((const uint16_t*)p)[i]) : ((const float*)p)[i];
+}
+__device__ __forceinline__ void store_from_float(void* p, int64_t i, int dtype, float x) {
+  if (dtype == 0) ((uint16_t*)p)[i] = f2bf(x);
+  else ((float*)p)[i] = x;
+}
+
+// ------------------------------------------------------------------ matrix-core traits
+template <int DT> struct MT;
+template <> struct MT<0> {
+  static constexpr int KC = 16, EPL = 8, ESZ = 2;
+  __device__ __forceinline__ static f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  // pack 8 consecutive C values (base j0) of a tile into one operand fragment
+  __device__ __forceinline__ static u32x4 pack(const f32x16& c, int j0) {
+    u32x4 r;
+    r[0] = pack_bf2(c[j0 + 0], c[j0 + 1]);
+    r[1] = pack_bf2(c[j0 + 2], c[j0 + 3]);
+    r[2] = pack_bf2(c[j0 + 4], c[j0 + 5]);
+    r[3] = pack_bf2(c[j0 + 6], c[j0 + 7]);
+    return r;
+  }
+};
+template <> struct MT<1> {
+  static constexpr int KC = 8, EPL = 4, ESZ = 4;
+  __device__ __forceinline__ static f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    // element-wise extraction into scalars first: bit-casting an ext-vector element lvalue
+    // directly has been observed to read element 0 for every e
+    const uint32_t a0 = a.x, a1 = a.y, a2 = a.z, a3 = a.w;
+    const uint32_t b0 = b.x, b1 = b.y, b2 = b.z, b3 = b.w;
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a0), __uint_as_float(b0), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a1), __uint_as_float(b1), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a2), __uint_as_float(b2), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a3), __uint_as_float(b3), c, 0, 0, 0);
+    return c;
+  }
+  __device__ __forceinline__ static u32x4 pack(const f32x16& c, int j0) {
+    u32x4 r;
+    r.x = __float_as_uint(c[j0 + 0]);
+    r.y = __float_as_uint(c[j0 + 1]);
+    r.z = __float_as_uint(c[j0 + 2]);
+    r.w = __float_as_uint(c[j0 + 3]);
+    return r;
+  }
+};
+
+// physical C row of value j in lane group g
+__device__ __forceinline__ int c_row(int j, int g) { return ((j >> 2) << 3) + (g << 2) + (j & 3); }
+
+template <int DT> __device__ __forceinline__ int perm_row(int r) {
+  if constexpr (DT == 0) return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+  else return r;
+}
+// logical row (contraction index) of C value j in lane group g after perm_row loading
+template <int DT> __device__ __forceinline__ int c_logical(int j, int g) {
+  if constexpr (DT == 0) return ((j >> 3) << 4) + (g << 3) + (j & 7);
+  else return ((j >> 2) << 3) + (g << 2) + (j & 3);
+}
+
+// ------------------------------------------------------------------ swizzled LDS tiles
+// NCH = 16-byte chunks per row (a power of two).
+template <int NCH> __device__ __forceinline__ int swz(int r) {
+  return ((((r & 3) | (((r >> 3) & 1) << 2)) << 1)) & (NCH - 1);
+}
+template <int NCH> __device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
+  return (uint32_t)(row * (NCH * 16) + ((chunk ^ swz<NCH>(row)) << 4));
+}
+
+// One lane's 16-byte row fragment: chunk `chunk` of row `row`.
+template <int NCH> __device__ __forceinline__ u32x4 lds_row_frag(const char* tile, int row, int chunk) {
+  return *(const u32x4*)(tile + tile_off<NCH>(row, chunk));
+}
+
+// Operand fragment whose contraction runs down the tile rows: rows k0 + g*EPL .. +EPL-1,
+// column n0 + l32 (element units).
+template <int DT, int NCH> __device__ __forceinline__ u32x4 lds_col_frag(const char* tile, int k0, int n0, int lane) {
+  if constexpr (DT == 0) {
+    const int i = lane & 15, G4 = (lane >> 4) & 3;
+    const int col = n0 + ((G4 & 1) << 4) + ((i & 3) << 2);
+    const int row = k0 + ((lane >> 5) << 3) + (i >> 2);
+    const uint32_t o0 = tile_off<NCH>(row, col >> 3) + ((col & 7) << 1);
+    const uint32_t o1 = tile_off<NCH>(row + 4, col >> 3) + ((col & 7) << 1);
+    s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + o0));
+    s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + o1));
+    u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+    u32x4 r;
+    r[0] = ua[0]; r[1] = ua[1]; r[2] = ub[0]; r[3] = ub[1];
+    return r;
+  } else {
+    const int col = n0 + (lane & 31);
+    const int row = k0 + ((lane >> 5) << 2);
+    u32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      r[e] = *(const uint32_t*)(tile + tile_off<NCH>(row + e, col >> 2) + ((col & 3) << 2));
+    return r;
+  }
+}
+
+// Cooperative copy of ROWS x (NCH*16 bytes) from global (row stride in bytes) into a swizzled
+// tile; rows >= nvalid are zero-filled.  All NT threads of the block participate.
+template <int ROWS, int NCH, int NT>
+__device__ __forceinline__ void copy_tile(char* tile, const char* src, int64_t row_stride_bytes,
+                                          int nvalid, int tid) {
+  constexpr int TOTAL = ROWS * NCH;
+#pragma unroll
+  for (int it = 0; it < (TOTAL + NT - 1) / NT; ++it) {
+    const int q = it * NT + tid;
+    if ((TOTAL % NT) == 0 || q < TOTAL) {
+      const int row = q / NCH, c = q % NCH;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (row < nvalid) v = *(const u32x4*)(src + row * row_stride_bytes + c * 16);
+      *(u32x4*)(tile + tile_off<NCH>(row, c)) = v;
+    }
+  }
+}
+
+// Two-phase variant: issue the global loads into registers first, store to LDS later.
+template <int ROWS, int NCH, int NT> struct TileStage {
+  static constexpr int N = (ROWS * NCH + NT - 1) / NT;
+  u32x4 r[N];
+  __device__ __forceinline__ void load(const char* src, int64_t row_stride_bytes, int nvalid, int tid) {
+#pragma unroll
+    for (int it = 0; it < N; ++it) {
+      const int q = it * NT + tid;
+      const int row = q / NCH, c = q % NCH;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (((ROWS * NCH) % NT == 0 || q < ROWS * NCH) && row < nvalid)
+        v = *(const u32x4*)(src + row * row_stride_bytes + c * 16);
+      r[it] = v;
+    }
+  }
+  __device__ __forceinline__ void store(char* tile, int tid) const {
+#pragma unroll
+    for (int it = 0; it < N; ++it) {
+      const int q = it * NT + tid;
+      if ((ROWS * NCH) % NT == 0 || q < ROWS * NCH) {
+        const int row = q / NCH, c = q % NCH;
+        *(u32x4*)(tile + tile_off<NCH>(row, c)) = r[it];
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
+
+// ------------------------------------------------------------------ scalar math (reference semantics)
+// torch softplus, beta 1, threshold 20
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+
+// Launch-order remap.  Blocks are issued heaviest first (LPT for the causal triangle) and, when the
+// number of (batch, head) pairs divides by the 8 XCDs, every block of one head lands on the same
+// XCD (hardware dispatch is round-robin over XCDs) so its K/V stays in that XCD's L2.
+__device__ __forceinline__ void map_block(int bid, int nblk, int nbh, bool heavy_last_index,
+                                          int& blk, int& bh) {
+  int j, hsel;
+  if ((nbh & 7) == 0) {
+    const int x = bid & 7, hp = nbh >> 3;
+    j = (bid >> 3) / hp;
+    hsel = x * hp + (bid >> 3) % hp;
+  } else {
+    j = bid / nbh;
+    hsel = bid % nbh;
+  }
+  blk = heavy_last_index ? (nblk - 1 - j) : j;
+  bh = hsel;
+}
+
+}  // namespace pe

@@ -1,0 +1,200 @@
+// Causal attention forward over transformed operands (q~, k~ of width DQK; v of width DV) for
+// gfx950.  One workgroup = NW waves = NW*32 query rows; each wave keeps its 32 q~ rows in
+// registers as the MFMA B operand and streams BN-key blocks of k~ and v through LDS.
+//
+// Per key block, per wave:  S^T = k~ q~^T  (A = k~ rows from LDS, C: rows = keys, cols = queries),
+// online softmax with the key axis inside each lane (row max needs one lane^32 exchange),
+// O^T += v^T P^T  (A = v read with the transpose load, B = P^T straight from the C registers).
+// The scores are the reference's SDPA scores on [content | mu cos | mu sin] operands
+// (src/model/fpope_attention.py:166-177, src/model/fpope.py:409-417).
+#include "pe_common.h"
+#include "pe_internal.h"
+
+namespace pe {
+
+template <int DT, int DQK, int DV, int BN, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) {
+  using E = typename Elem<DT>::T;
+  using M = MT<DT>;
+  constexpr int KC = M::KC, EPL = M::EPL, ESZ = M::ESZ;
+  constexpr int BM = NW * 32, NT = NW * 64;
+  constexpr int NCK = DQK * ESZ / 16, NCV = DV * ESZ / 16;
+  constexpr int NQF = DQK / KC, NKT = BN / 32, NPF = BN / KC, NOT = DV / 32, SPT = 32 / KC;
+  constexpr int SK_BYTES = BN * NCK * 16, SV_BYTES = BN * NCV * 16;
+  constexpr int SO_STRIDE = DV * ESZ + 16;
+  constexpr int SO_BYTES = BM * SO_STRIDE;
+  constexpr int SMEM = (SK_BYTES + SV_BYTES) > SO_BYTES ? (SK_BYTES + SV_BYTES) : SO_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[SMEM];
+  char* sK = smem;
+  char* sV = smem + SK_BYTES;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int nqb = (a.Sq + BM - 1) / BM;
+  int qb, bh;
+  map_block(blockIdx.x, nqb, a.B * a.Hq, a.causal != 0, qb, bh);
+  const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
+  const int q0 = qb * BM, qw = q0 + w * 32, myq = qw + l32;
+  const int off = a.causal_off;
+
+  u32x4 qf[NQF];
+  {
+    const E* qrow = (const E*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + (myq < a.Sq ? myq : 0)) * DQK;
+#pragma unroll
+    for (int kk = 0; kk < NQF; ++kk) {
+      u32x4 z = {0u, 0u, 0u, 0u};
+      qf[kk] = myq < a.Sq ? *(const u32x4*)(qrow + kk * KC + g * EPL) : z;
+    }
+  }
+
+  int kend = a.Sk;
+  if (a.causal) kend = min(a.Sk, q0 + BM + off);
+  const int nkb = kend > 0 ? (kend + BN - 1) / BN : 0;
+  const char* kbase = (const char*)((const E*)a.k + (int64_t)(b * a.Hkv + hk) * a.Sk * DQK);
+  const char* vbase = (const char*)((const E*)a.v + b * a.v_sb + hk * a.v_sh);
+  const int64_t krs = (int64_t)DQK * ESZ, vrs = a.v_ss * ESZ;
+
+  f32x16 o[NOT];
+#pragma unroll
+  for (int t = 0; t < NOT; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[t][j] = 0.f;
+  float m = -1e30f, l = 0.f;
+  const float sl2 = a.scale * LOG2E;
+
+  TileStage<BN, NCK, NT> stK;
+  TileStage<BN, NCV, NT> stV;
+  if (nkb > 0) {
+    stK.load(kbase, krs, a.Sk, tid);
+    stV.load(vbase, vrs, a.Sk, tid);
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * BN;
+    __syncthreads();
+    stK.store(sK, tid);
+    stV.store(sV, tid);
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      stK.load(kbase + (int64_t)(k0 + BN) * krs, krs, a.Sk - k0 - BN, tid);
+      stV.load(vbase + (int64_t)(k0 + BN) * vrs, vrs, a.Sk - k0 - BN, tid);
+    }
+    if (a.causal && k0 > qw + 31 + off) continue;  // whole block above this wave's diagonal
+
+    f32x16 s[NKT];
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s[nt][j] = 0.f;
+      const int row = nt * 32 + perm_row<DT>(l32);
+#pragma unroll
+      for (int kk = 0; kk < NQF; ++kk)
+        s[nt] = M::mma(lds_row_frag<NCK>(sK, row, 2 * kk + g), qf[kk], s[nt]);
+    }
+    const bool edge = (a.causal && k0 + BN - 1 > qw + off) || (k0 + BN > a.Sk);
+    float mx = m;
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x = s[nt][j] * sl2;
+        if (edge) {
+          const int key = k0 + nt * 32 + c_logical<DT>(j, g);
+          if (key >= a.Sk || (a.causal && key > myq + off)) x = -INFINITY;
+        }
+        s[nt][j] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, xor32(mx));
+    const float alpha = exp2f(m - mx);
+    m = mx;
+    float rs = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float p = exp2f(s[nt][j] - m);
+        s[nt][j] = p;
+        rs += p;
+      }
+    l = l * alpha + rs;
+#pragma unroll
+    for (int t = 0; t < NOT; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) o[t][j] *= alpha;
+    u32x4 pf[NPF];
+#pragma unroll
+    for (int ks = 0; ks < NPF; ++ks) pf[ks] = M::pack(s[ks / SPT], (ks % SPT) * EPL);
+#pragma unroll
+    for (int t = 0; t < NOT; ++t)
+#pragma unroll
+      for (int ks = 0; ks < NPF; ++ks)
+        o[t] = M::mma(lds_col_frag<DT, NCV>(sV, ks * KC, t * 32, lane), pf[ks], o[t]);
+  }
+
+  const float lt = l + xor32(l);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < NOT; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int dv = t * 32 + c_row(j, g);
+      char* dst = smem + (w * 32 + l32) * SO_STRIDE + dv * ESZ;
+      if constexpr (DT == 0) *(uint16_t*)dst = f2bf(o[t][j] * inv);
+      else *(float*)dst = o[t][j] * inv;
+    }
+  if (g == 0 && myq < a.Sq)
+    a.lse[(int64_t)(b * a.Hq + h) * a.Sq + myq] = lt > 0.f ? (m + log2f(lt)) * LN2 : -INFINITY;
+  __syncthreads();
+  char* obase = (char*)a.o + (b * a.o_sb + h * a.o_sh) * ESZ;
+  if (o_vec) {
+    constexpr int CPR = DV * ESZ / 16;
+    for (int q = tid; q < BM * CPR; q += NT) {
+      const int row = q / CPR, c = q % CPR;
+      if (q0 + row < a.Sq)
+        *(u32x4*)(obase + (int64_t)(q0 + row) * a.o_ss * ESZ + c * 16) = *(const u32x4*)(smem + row * SO_STRIDE + c * 16);
+    }
+  } else {
+    const int dvr = a.dv_real;
+    for (int q = tid; q < BM * dvr; q += NT) {
+      const int row = q / dvr, c = q % dvr;
+      if (q0 + row < a.Sq)
+        ((E*)(obase + (int64_t)(q0 + row) * a.o_ss * ESZ))[c] = *(const E*)(smem + row * SO_STRIDE + c * ESZ);
+    }
+  }
+}
+
+template <int DT, int DQK, int DV>
+static int run_fwd(const CoreArgs& a, hipStream_t s) {
+  constexpr int NW = 4;
+  constexpr int BN = DT == 0 ? 64 : 32;
+  const int BM = NW * 32;
+  const int nqb = (a.Sq + BM - 1) / BM;
+  const int grid = nqb * a.B * a.Hq;
+  const int o_vec = (a.dv_real == DV) && ((uintptr_t)a.o % 16 == 0) &&
+                    ((a.o_ss * MT<DT>::ESZ) % 16 == 0) && ((a.o_sh * MT<DT>::ESZ) % 16 == 0) &&
+                    ((a.o_sb * MT<DT>::ESZ) % 16 == 0);
+  hipLaunchKernelGGL((fwd_kernel<DT, DQK, DV, BN, NW>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
+bool core_supported(int dqk, int dv) {
+  return (dqk == 64 && dv == 64) || (dqk == 128 && dv == 64) || (dqk == 128 && dv == 128) ||
+         (dqk == 256 && dv == 128) || (dqk == 256 && dv == 64) || (dqk == 64 && dv == 128);
+}
+
+template <int DT>
+static int fwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
+  if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64>(a, s);
+  if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128>(a, s);
+  if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64>(a, s);
+  if (dqk == 128 && dv == 128) return run_fwd<DT, 128, 128>(a, s);
+  if (dqk == 256 && dv == 64) return run_fwd<DT, 256, 64>(a, s);
+  if (dqk == 256 && dv == 128) return run_fwd<DT, 256, 128>(a, s);
+  return -3;
+}
+
+int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s) {
+  return dt == 0 ? fwd_dt<0>(dqk, dv, a, s) : fwd_dt<1>(dqk, dv, a, s);
+}
+
+}  // namespace pe

@@ -1,0 +1,85 @@
+// Internal launch interface between the C-ABI host code (pe_api.cpp) and the kernel translation
+// units.  Operand buffers are the library's own layout: (B, H, S, W) contiguous, W a tile width.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pe {
+
+// Attention core over transformed operands.
+struct CoreArgs {
+  const void* q;    // (B, Hq, Sq, DQK) contiguous, compute dtype
+  const void* k;    // (B, Hkv, Sk, DQK)
+  const void* v;    // (B, Hkv, Sk, DV) rows of v_row elements (>= DV), compute dtype
+  int64_t v_sb, v_sh, v_ss;  // element strides of v
+  int B, Hq, Hkv, Sq, Sk;
+  int dv_real;      // value columns actually produced (<= DV)
+  int causal;       // 0 none, else masked when s > t + causal_off
+  int causal_off;
+  float scale;      // softmax scale
+  // forward outputs
+  void* o; int64_t o_sb, o_sh, o_ss; int o_dtype;
+  float* lse;       // (B, Hq, Sq)
+  // backward inputs / outputs
+  const void* dO;   // (B, Hq, Sq, DV) contiguous compute dtype (padded)
+  const float* Di;  // (B, Hq, Sq)  rowsum(dO * O)
+  const float* lse_in;
+  float* dq_t;      // (B, Hq, Sq, DQK) fp32, already multiplied by scale
+  float* dk_t;      // (B, Hkv, Sk, DQK) fp32, already multiplied by scale (summed over the GQA group)
+  void* dv; int64_t dv_sb, dv_sh, dv_ss; int dv_dtype;
+};
+
+int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
+int launch_bwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
+bool core_supported(int dqk, int dv);
+
+// Elementwise transform: one wave per (b, h, s) row.
+struct PrepArgs {
+  const void* xc; int xc_dtype; int64_t xc_s[4];
+  const void* xr; int xr_dtype; int64_t xr_s[4];
+  void* dst; int dst_dtype; int width;           // (B, H, S, width) contiguous
+  int B, H, S, Dc, Dr, mode, start_pos, l2norm, is_key;
+  const float* freqs; const float* delta; int64_t delta_hs;
+  float mscale;
+};
+int launch_prep(const PrepArgs& a, hipStream_t s);
+
+// dO repack (to compute dtype, width DV, contiguous) and Di = rowsum(dO * O).
+struct PreBwdArgs {
+  const void* dout; int dout_dtype; int64_t do_s[4];
+  const void* out; int out_dtype; int64_t o_s[4];
+  void* dO_op; int op_dtype; int width;
+  float* Di;
+  int B, H, S, Dv;
+};
+int launch_prebwd(const PreBwdArgs& a, hipStream_t s);
+
+// Inverse transform: dx~ (fp32, (B,H,S,width)) -> dxc, dxr, plus per-block partial sums of the
+// phase gradient for the key phase bias and for the frequencies.
+struct InvArgs {
+  const float* g; int width;
+  const void* xr; int xr_dtype; int64_t xr_s[4];
+  void* dxc; int dxc_dtype; int64_t dxc_s[4];
+  void* dxr; int dxr_dtype; int64_t dxr_s[4];
+  int B, H, S, Dc, Dr, mode, start_pos, l2norm, is_key;
+  const float* freqs; const float* delta; int64_t delta_hs;
+  float mscale;
+  float* part_delta;   // (nblocks, Dr) or NULL
+  float* part_freq;    // (nblocks, Dr) or NULL
+  int rows_per_block;
+};
+int launch_inv(const InvArgs& a, int* nblocks_out, hipStream_t s);
+int inv_blocks(int B, int H, int S, int rows_per_block);
+
+// Deterministic reduction of the partials.
+struct ReduceArgs {
+  const float* part_q_freq; int nq;       // q-side blocks (freq partials)
+  const float* part_k_freq; const float* part_k_delta; int nk;
+  int k_blocks_per_head;                  // consecutive blocks belong to one (b, h): order (b, h, chunk)
+  int Hkv, B, Dr;
+  int delta_per_head;
+  float* dfreqs; float* ddelta;
+};
+int launch_reduce(const ReduceArgs& a, hipStream_t s);
+
+}  // namespace pe

@@ -1,0 +1,291 @@
+// Elementwise kernels around the attention core (all HBM-bound, one wave or one thread per element
+// row):
+//   prep_kernel   forward positional transform, row -> [content | transform | zero pad]
+//                 PoPE/FoPE (src/model/pope.py:124-183, src/model/fpope.py:266-338):
+//                   mu = softplus(x); phi = fl(pos*freq) (+ delta on keys, added after the product,
+//                   no fused multiply-add); [mu cos phi, mu sin phi]
+//                 RoPE/NTK/YaRN (src/model/rope.py:35-57,209-217): interleaved pairs rotated by
+//                   fl(pos*inv_freq), times mscale; optional QKNorm x/(||x||+1e-6)
+//                   (src/model/normalization.py:54-55)
+//   prebwd_kernel dO -> compute-dtype operand, Di = rowsum(dO o O)
+//   inv_pope_kernel  gradient of the PoPE transform with per-block partial sums of dphi (key
+//                 phase bias) and pos*dphi (frequencies)
+//   inv_row_kernel   gradient of the RoPE / no-PE transform incl. the QKNorm backward
+//   reduce_kernel fixed-order sum of the partials (bitwise reproducible)
+#include "pe_common.h"
+#include "pe_internal.h"
+
+namespace pe {
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+constexpr int MAX_PAIRS_PER_LANE = 4;  // RoPE rows up to 512 dims
+
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nrows = (int64_t)a.B * a.H * a.S;
+  if (row >= nrows) return;
+  const int s = (int)(row % a.S);
+  const int bh = (int)(row / a.S);
+  const int h = bh % a.H, b = bh / a.H;
+  const float pos = (float)(a.start_pos + s);
+  const int64_t dbase = row * a.width;
+
+  for (int c = lane; c < a.Dc; c += 64) {
+    const float x = load_as_float(a.xc, b * a.xc_s[0] + h * a.xc_s[1] + (int64_t)s * a.xc_s[2] + c * a.xc_s[3], a.xc_dtype);
+    store_from_float(a.dst, dbase + c, a.dst_dtype, x);
+  }
+  const int64_t xr0 = b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2];
+  int used = a.Dc;
+  if (a.mode == 0) {  // PoPE / FoPE
+    for (int c = lane; c < a.Dr; c += 64) {
+      const float x = load_as_float(a.xr, xr0 + c * a.xr_s[3], a.xr_dtype);
+      const float mu = softplus_f(x);
+      float ph = __fmul_rn(pos, a.freqs[c]);
+      if (a.is_key && a.delta) ph = __fadd_rn(ph, a.delta[h * a.delta_hs + c]);
+      float sn, cs;
+      sincosf(ph, &sn, &cs);
+      store_from_float(a.dst, dbase + a.Dc + c, a.dst_dtype, __fmul_rn(mu, cs));
+      store_from_float(a.dst, dbase + a.Dc + a.Dr + c, a.dst_dtype, __fmul_rn(mu, sn));
+    }
+    used += 2 * a.Dr;
+  } else {  // RoPE (mode 1) or plain (mode 2): values kept in registers for the optional L2 norm
+    // lane owns pair i = lane + 64k (RoPE) or elements 2i, 2i+1 (plain, odd widths allowed)
+    float y0[MAX_PAIRS_PER_LANE], y1[MAX_PAIRS_PER_LANE];
+    float ss = 0.f;
+    const int npairs = (a.Dr + 1) / 2;
+#pragma unroll
+    for (int k = 0; k < MAX_PAIRS_PER_LANE; ++k) {
+      const int i = lane + 64 * k;
+      y0[k] = 0.f; y1[k] = 0.f;
+      if (i < npairs) {
+        const bool has1 = 2 * i + 1 < a.Dr;
+        const float x0 = load_as_float(a.xr, xr0 + (2 * i) * a.xr_s[3], a.xr_dtype);
+        const float x1 = has1 ? load_as_float(a.xr, xr0 + (2 * i + 1) * a.xr_s[3], a.xr_dtype) : 0.f;
+        if (a.mode == 1) {
+          const float ang = __fmul_rn(pos, a.freqs[i]);
+          float sn, cs;
+          sincosf(ang, &sn, &cs);
+          y0[k] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn)) * a.mscale;
+          y1[k] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs)) * a.mscale;
+        } else {
+          y0[k] = x0; y1[k] = x1;
+        }
+        ss += y0[k] * y0[k] + y1[k] * y1[k];
+      }
+    }
+    float den = 1.f;
+    if (a.l2norm) den = sqrtf(wave_sum(ss)) + 1e-6f;
+#pragma unroll
+    for (int k = 0; k < MAX_PAIRS_PER_LANE; ++k) {
+      const int i = lane + 64 * k;
+      if (i < npairs) {
+        store_from_float(a.dst, dbase + a.Dc + 2 * i, a.dst_dtype, a.l2norm ? y0[k] / den : y0[k]);
+        if (2 * i + 1 < a.Dr)
+          store_from_float(a.dst, dbase + a.Dc + 2 * i + 1, a.dst_dtype, a.l2norm ? y1[k] / den : y1[k]);
+      }
+    }
+    used += a.Dr;
+  }
+  for (int c = used + lane; c < a.width; c += 64) store_from_float(a.dst, dbase + c, a.dst_dtype, 0.f);
+}
+
+__global__ __launch_bounds__(256) void prebwd_kernel(PreBwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nrows = (int64_t)a.B * a.H * a.S;
+  if (row >= nrows) return;
+  const int s = (int)(row % a.S);
+  const int bh = (int)(row / a.S);
+  const int h = bh % a.H, b = bh / a.H;
+  const int64_t d0 = b * a.do_s[0] + h * a.do_s[1] + (int64_t)s * a.do_s[2];
+  const int64_t o0 = b * a.o_s[0] + h * a.o_s[1] + (int64_t)s * a.o_s[2];
+  float acc = 0.f;
+  for (int c = lane; c < a.width; c += 64) {
+    float d = 0.f;
+    if (c < a.Dv) {
+      d = load_as_float(a.dout, d0 + c * a.do_s[3], a.dout_dtype);
+      acc += d * load_as_float(a.out, o0 + c * a.o_s[3], a.out_dtype);
+    }
+    store_from_float(a.dO_op, row * a.width + c, a.op_dtype, d);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) a.Di[row] = acc;
+}
+
+// One block = rows [chunk*R, chunk*R + R) of one (b, h); TPR threads per row, 256/TPR rows at once.
+template <int TPR>
+__global__ __launch_bounds__(256) void inv_pope_kernel(InvArgs a) {
+  constexpr int RS = 256 / TPR;
+  __shared__ float red_d[RS][TPR];
+  __shared__ float red_f[RS][TPR];
+  const int tid = threadIdx.x, c = tid % TPR, rs = tid / TPR;
+  const int chunks = (a.S + a.rows_per_block - 1) / a.rows_per_block;
+  const int blk = blockIdx.x;
+  const int bh = blk / chunks, chunk = blk % chunks;
+  const int h = bh % a.H, b = bh / a.H;
+  const int s0 = chunk * a.rows_per_block;
+  const int s1 = min(a.S, s0 + a.rows_per_block);
+  float acc_d = 0.f, acc_f = 0.f;
+  const float fr = c < a.Dr ? a.freqs[c] : 0.f;
+  const float dl = (c < a.Dr && a.is_key && a.delta) ? a.delta[h * a.delta_hs + c] : 0.f;
+  for (int s = s0 + rs; s < s1; s += RS) {
+    const int64_t grow = ((int64_t)bh * a.S + s) * a.width;
+    for (int cc = c; cc < a.Dc; cc += TPR)
+      store_from_float(a.dxc, b * a.dxc_s[0] + h * a.dxc_s[1] + (int64_t)s * a.dxc_s[2] + cc * a.dxc_s[3], a.dxc_dtype, a.g[grow + cc]);
+    if (c < a.Dr) {
+      const float pos = (float)(a.start_pos + s);
+      const float x = load_as_float(a.xr, b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + c * a.xr_s[3], a.xr_dtype);
+      const float mu = softplus_f(x), sg = sigmoid_f(x);
+      float ph = __fmul_rn(pos, fr);
+      if (a.is_key && a.delta) ph = __fadd_rn(ph, dl);
+      float sn, cs;
+      sincosf(ph, &sn, &cs);
+      const float gc = a.g[grow + a.Dc + c], gs = a.g[grow + a.Dc + a.Dr + c];
+      const float dmu = gc * cs + gs * sn;
+      const float dph = mu * (gs * cs - gc * sn);
+      store_from_float(a.dxr, b * a.dxr_s[0] + h * a.dxr_s[1] + (int64_t)s * a.dxr_s[2] + c * a.dxr_s[3], a.dxr_dtype, dmu * sg);
+      acc_d += dph;
+      acc_f += pos * dph;
+    }
+  }
+  red_d[rs][c] = acc_d;
+  red_f[rs][c] = acc_f;
+  __syncthreads();
+  if (rs == 0 && c < a.Dr) {
+    float sd = 0.f, sf = 0.f;
+    for (int r = 0; r < RS; ++r) { sd += red_d[r][c]; sf += red_f[r][c]; }
+    if (a.part_delta) a.part_delta[(int64_t)blk * a.Dr + c] = sd;
+    if (a.part_freq) a.part_freq[(int64_t)blk * a.Dr + c] = sf;
+  }
+}
+
+// RoPE / no-PE gradient, one wave per row: y = z/(||z||+eps) (optional), z = mscale * rot(x).
+//   dz = dy/(n+eps) - z (z.dy) / (n (n+eps)^2);  dx = mscale * rot^T(dz)
+__global__ __launch_bounds__(256) void inv_row_kernel(InvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nrows = (int64_t)a.B * a.H * a.S;
+  if (row >= nrows) return;
+  const int s = (int)(row % a.S);
+  const int bh = (int)(row / a.S);
+  const int h = bh % a.H, b = bh / a.H;
+  const float pos = (float)(a.start_pos + s);
+  const int64_t grow = row * a.width;
+  for (int c = lane; c < a.Dc; c += 64)
+    store_from_float(a.dxc, b * a.dxc_s[0] + h * a.dxc_s[1] + (int64_t)s * a.dxc_s[2] + c * a.dxc_s[3], a.dxc_dtype, a.g[grow + c]);
+  const int64_t xr0 = b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2];
+  const int64_t dx0 = b * a.dxr_s[0] + h * a.dxr_s[1] + (int64_t)s * a.dxr_s[2];
+  const int npairs = a.Dr / 2;
+  float z0[MAX_PAIRS_PER_LANE], z1[MAX_PAIRS_PER_LANE], g0[MAX_PAIRS_PER_LANE], g1[MAX_PAIRS_PER_LANE];
+  float cs_[MAX_PAIRS_PER_LANE], sn_[MAX_PAIRS_PER_LANE];
+  float ss = 0.f, zd = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAX_PAIRS_PER_LANE; ++k) {
+    const int i = lane + 64 * k;
+    z0[k] = z1[k] = g0[k] = g1[k] = 0.f;
+    cs_[k] = 1.f; sn_[k] = 0.f;
+    if (i < npairs) {
+      const float x0 = load_as_float(a.xr, xr0 + (2 * i) * a.xr_s[3], a.xr_dtype);
+      const float x1 = load_as_float(a.xr, xr0 + (2 * i + 1) * a.xr_s[3], a.xr_dtype);
+      if (a.mode == 1) {
+        const float ang = __fmul_rn(pos, a.freqs[i]);
+        sincosf(ang, &sn_[k], &cs_[k]);
+        z0[k] = __fsub_rn(__fmul_rn(x0, cs_[k]), __fmul_rn(x1, sn_[k])) * a.mscale;
+        z1[k] = __fadd_rn(__fmul_rn(x0, sn_[k]), __fmul_rn(x1, cs_[k])) * a.mscale;
+      } else {
+        z0[k] = x0; z1[k] = x1;
+      }
+      g0[k] = a.g[grow + a.Dc + 2 * i];
+      g1[k] = a.g[grow + a.Dc + 2 * i + 1];
+      ss += z0[k] * z0[k] + z1[k] * z1[k];
+      zd += z0[k] * g0[k] + z1[k] * g1[k];
+    }
+  }
+  float c1 = 1.f, c2 = 0.f;
+  if (a.l2norm) {
+    const float n = sqrtf(wave_sum(ss));
+    zd = wave_sum(zd);
+    const float ne = n + 1e-6f;
+    c1 = 1.f / ne;
+    c2 = n > 0.f ? zd / (n * ne * ne) : 0.f;
+  }
+  const float ms = a.mode == 1 ? a.mscale : 1.f;
+#pragma unroll
+  for (int k = 0; k < MAX_PAIRS_PER_LANE; ++k) {
+    const int i = lane + 64 * k;
+    if (i < npairs) {
+      const float d0 = g0[k] * c1 - z0[k] * c2;
+      const float d1 = g1[k] * c1 - z1[k] * c2;
+      const float dx0v = (d0 * cs_[k] + d1 * sn_[k]) * ms;
+      const float dx1v = (d1 * cs_[k] - d0 * sn_[k]) * ms;
+      store_from_float(a.dxr, dx0 + (2 * i) * a.dxr_s[3], a.dxr_dtype, dx0v);
+      store_from_float(a.dxr, dx0 + (2 * i + 1) * a.dxr_s[3], a.dxr_dtype, dx1v);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int nd = a.delta_per_head ? a.Hkv * a.Dr : a.Dr;
+  if (t < a.Dr && a.dfreqs) {
+    float s = 0.f;
+    for (int i = 0; i < a.nq; ++i) s += a.part_q_freq[(int64_t)i * a.Dr + t];
+    for (int i = 0; i < a.nk; ++i) s += a.part_k_freq[(int64_t)i * a.Dr + t];
+    a.dfreqs[t] = s;
+  }
+  if (t < nd && a.ddelta) {
+    const int c = t % a.Dr, hsel = t / a.Dr;
+    float s = 0.f;
+    for (int i = 0; i < a.nk; ++i) {
+      const int h = (i / a.k_blocks_per_head) % a.Hkv;
+      if (!a.delta_per_head || h == hsel) s += a.part_k_delta[(int64_t)i * a.Dr + c];
+    }
+    a.ddelta[t] = s;
+  }
+}
+
+int launch_prep(const PrepArgs& a, hipStream_t s) {
+  const int64_t nrows = (int64_t)a.B * a.H * a.S;
+  hipLaunchKernelGGL(prep_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
+int launch_prebwd(const PreBwdArgs& a, hipStream_t s) {
+  const int64_t nrows = (int64_t)a.B * a.H * a.S;
+  hipLaunchKernelGGL(prebwd_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
+int inv_blocks(int B, int H, int S, int rows_per_block) {
+  return B * H * ((S + rows_per_block - 1) / rows_per_block);
+}
+
+int launch_inv(const InvArgs& a, int* nblocks_out, hipStream_t s) {
+  if (a.mode == 0) {
+    const int nb = inv_blocks(a.B, a.H, a.S, a.rows_per_block);
+    if (nblocks_out) *nblocks_out = nb;
+    if (a.Dr <= 64) hipLaunchKernelGGL(inv_pope_kernel<64>, dim3(nb), dim3(256), 0, s, a);
+    else if (a.Dr <= 128) hipLaunchKernelGGL(inv_pope_kernel<128>, dim3(nb), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(inv_pope_kernel<256>, dim3(nb), dim3(256), 0, s, a);
+  } else {
+    if (nblocks_out) *nblocks_out = 0;
+    const int64_t nrows = (int64_t)a.B * a.H * a.S;
+    hipLaunchKernelGGL(inv_row_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
+int launch_reduce(const ReduceArgs& a, hipStream_t s) {
+  const int nd = a.delta_per_head ? a.Hkv * a.Dr : a.Dr;
+  const int n = nd > a.Dr ? nd : a.Dr;
+  hipLaunchKernelGGL(reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
+}  // namespace pe

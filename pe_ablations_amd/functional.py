@@ -1,0 +1,224 @@
+"""Fused positional-encoding attention as a torch.autograd.Function over libpe_attn.so.
+
+``pe_attention`` replaces, in one forward and one backward launch sequence, the span
+PE transform -> content|position concat -> GQA repeat_interleave -> causal SDPA of the reference
+modules (src/model/fpope_attention.py:145-177, src/model/attention.py:69-96).  Tensors are
+(B, H, S, D) views with any strides whose last dimension is contiguous (e.g. the projections'
+``view(B, S, H, D).transpose(1, 2)``); nothing is copied on the way in.  The output is a
+(B, H, S, Dv) view of a (B, S, H, Dv) buffer, so the caller's ``transpose(1, 2).reshape`` is free.
+
+Compute dtype: bf16 when autocast is on or any input is bf16/fp16, else fp32 (the reference's
+autocast training path and its fp32 eval path).  Only GPU tensors are accepted.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_MODES = {"pope": _lib.PE_MODE_POPE, "fope": _lib.PE_MODE_POPE, "rope": _lib.PE_MODE_ROPE,
+          "none": _lib.PE_MODE_NONE, "nope": _lib.PE_MODE_NONE}
+_CAUSAL = {False: _lib.PE_CAUSAL_NONE, True: _lib.PE_CAUSAL_TOP_LEFT,
+           "none": _lib.PE_CAUSAL_NONE, "top_left": _lib.PE_CAUSAL_TOP_LEFT,
+           "bottom_right": _lib.PE_CAUSAL_BOTTOM_RIGHT}
+
+
+def _dtype_code(t: torch.dtype) -> int:
+    if t == torch.bfloat16:
+        return _lib.PE_DTYPE_BF16
+    if t == torch.float32:
+        return _lib.PE_DTYPE_FP32
+    raise TypeError(f"pe_attention: unsupported tensor dtype {t}")
+
+
+def _tensor(t: Optional[torch.Tensor]) -> _lib.PeTensor:
+    d = _lib.PeTensor()
+    if t is None:
+        return d
+    if t.dim() != 4:
+        raise ValueError(f"pe_attention expects (B, H, S, D) tensors, got shape {tuple(t.shape)}")
+    d.data = t.data_ptr()
+    d.dtype = _dtype_code(t.dtype)
+    for i, s in enumerate(t.stride()):
+        d.stride[i] = s
+    if t.shape[3] == 1:
+        d.stride[3] = 1
+    return d
+
+
+def _prep_in(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    if t.dtype not in (torch.bfloat16, torch.float32):
+        t = t.to(torch.bfloat16 if t.dtype == torch.float16 else torch.float32)
+    if t.stride(-1) != 1 and t.shape[-1] != 1:
+        t = t.contiguous()
+    return t
+
+
+def _params(cfg, qr, kr, v, qc, delta) -> _lib.PeParams:
+    p = _lib.PeParams()
+    B, Hq, Sq = qr.shape[0], qr.shape[1], qr.shape[2]
+    Hkv, Sk = kr.shape[1], kr.shape[2]
+    p.B, p.Hq, p.Hkv, p.Sq, p.Sk = B, Hq, Hkv, Sq, Sk
+    p.Dc = 0 if qc is None else qc.shape[3]
+    p.Dr = qr.shape[3]
+    p.Dv = v.shape[3]
+    p.mode = cfg["mode"]
+    p.dtype = cfg["dtype"]
+    p.causal = cfg["causal"]
+    p.start_pos_q, p.start_pos_k = cfg["start_pos_q"], cfg["start_pos_k"]
+    p.qk_l2norm = int(cfg["qk_norm"])
+    p.scale = cfg["scale"]
+    p.rope_mscale = cfg["mscale"]
+    p.delta_head_stride = 0 if (delta is None or delta.dim() == 1) else delta.shape[-1]
+    return p
+
+
+def _stream(dev: torch.device):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+class PEAttentionFn(torch.autograd.Function):
+    """forward(qr, kr, v, qc, kc, freqs, delta, cfg) -> out (B, Hq, Sq, Dv).
+
+    Saves the raw inputs, out, lse and the forward workspace (transformed operands); the backward
+    recomputes P from lse.  Gradients: qr, kr, v, qc, kc, freqs (PoPE/FoPE), delta."""
+
+    @staticmethod
+    def forward(ctx, qr, kr, v, qc, kc, freqs, delta, cfg):
+        L = _lib.lib()
+        dev = qr.device
+        p = _params(cfg, qr, kr, v, qc, delta)
+        _lib.check(L.pe_attn_check(ctypes_ref(p)))
+        cdt = torch.bfloat16 if cfg["dtype"] == _lib.PE_DTYPE_BF16 else torch.float32
+        B, Hq, Sq, Dv = qr.shape[0], qr.shape[1], qr.shape[2], v.shape[3]
+        ws_bytes = L.pe_attn_fwd_workspace_bytes(ctypes_ref(p))
+        fws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        out = torch.empty((B, Sq, Hq, Dv), dtype=cdt, device=dev).transpose(1, 2)
+        lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            rc = L.pe_attn_fwd(ctypes_ref(p), ref(_tensor(qc)), ref(_tensor(qr)), ref(_tensor(kc)),
+                               ref(_tensor(kr)), ref(_tensor(v)), _ptr(freqs), _ptr(delta),
+                               ref(_tensor(out)), lse.data_ptr(), fws.data_ptr(), ws_bytes, _stream(dev))
+        _lib.check(rc)
+        ctx.cfg = cfg
+        ctx.ws_bytes = ws_bytes
+        ctx.save_for_backward(qr, kr, v, qc, kc, freqs, delta, out, lse, fws)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        L = _lib.lib()
+        qr, kr, v, qc, kc, freqs, delta, out, lse, fws = ctx.saved_tensors
+        cfg = ctx.cfg
+        dev = qr.device
+        p = _params(cfg, qr, kr, v, qc, delta)
+        dout = dout if dout.stride(-1) == 1 else dout.contiguous()
+        if dout.dtype not in (torch.bfloat16, torch.float32):
+            dout = dout.float()
+        dqr, dkr = torch.empty_like(qr), torch.empty_like(kr)
+        dqc = None if qc is None else torch.empty_like(qc)
+        dkc = None if kc is None else torch.empty_like(kc)
+        cdt = torch.bfloat16 if cfg["dtype"] == _lib.PE_DTYPE_BF16 else torch.float32
+        dv = torch.empty_like(v, dtype=cdt) if v.dtype != cdt else torch.empty_like(v)
+        need_f = freqs is not None and ctx.needs_input_grad[5]
+        need_d = delta is not None and ctx.needs_input_grad[6]
+        dfreqs = torch.empty(freqs.shape, dtype=torch.float32, device=dev) if need_f else None
+        ddelta = torch.empty(delta.shape, dtype=torch.float32, device=dev) if need_d else None
+        bws_bytes = L.pe_attn_bwd_workspace_bytes(ctypes_ref(p))
+        bws = torch.empty(bws_bytes, dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            rc = L.pe_attn_bwd(ctypes_ref(p), ref(_tensor(qc)), ref(_tensor(qr)), ref(_tensor(kc)),
+                               ref(_tensor(kr)), ref(_tensor(v)), _ptr(freqs), _ptr(delta),
+                               ref(_tensor(out)), lse.data_ptr(), ref(_tensor(dout)),
+                               ref(_tensor(dqc)), ref(_tensor(dqr)), ref(_tensor(dkc)), ref(_tensor(dkr)),
+                               ref(_tensor(dv)), _ptr(dfreqs), _ptr(ddelta), fws.data_ptr(), ctx.ws_bytes,
+                               bws.data_ptr(), bws_bytes, _stream(dev))
+        _lib.check(rc)
+        if dv.dtype != v.dtype:
+            dv = dv.to(v.dtype)
+        return dqr, dkr, dv, dqc, dkc, dfreqs, ddelta, None
+
+
+def ref(x):
+    import ctypes
+    return ctypes.byref(x)
+
+
+ctypes_ref = ref
+
+
+def _compute_dtype(tensors) -> int:
+    if torch.is_autocast_enabled():
+        return _lib.PE_DTYPE_BF16
+    for t in tensors:
+        if t is not None and t.dtype in (torch.bfloat16, torch.float16):
+            return _lib.PE_DTYPE_BF16
+    return _lib.PE_DTYPE_FP32
+
+
+def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str = "pope",
+                 q_c: Optional[torch.Tensor] = None, k_c: Optional[torch.Tensor] = None,
+                 freqs: Optional[torch.Tensor] = None, delta: Optional[torch.Tensor] = None,
+                 scale: Optional[float] = None, causal=True, start_pos_q: int = 0,
+                 start_pos_k: int = 0, rope_mscale: float = 1.0, qk_norm: bool = False,
+                 return_lse: bool = False, compute_dtype: Optional[torch.dtype] = None):
+    """Fused PE attention on one GPU.
+
+    q (B,Hq,Sq,Dr), k (B,Hkv,Sk,Dr): positional parts, transformed inside the kernel library;
+    q_c/k_c optional content parts (Dc) placed ahead of them; v (B,Hkv,Sk,Dv).
+    mode "pope"/"fope": freqs (Dr,) per-dim frequency, delta key phase bias ((Dr,) shared or
+    (Hkv, Dr) per head) used as given (clamping is the caller's autograd op).
+    mode "rope": freqs (Dr/2,) inverse frequencies, rope_mscale (YaRN), qk_norm (QKNorm).
+    scale defaults to (Dc + Dqk)^-1/2 with Dqk = 2 Dr (PoPE) or Dr.
+    causal: True / "top_left" (SDPA is_causal), "bottom_right" (KV-cache mask) or False.
+    Returns out (B,Hq,Sq,Dv) [and lse (B,Hq,Sq) fp32]."""
+    if mode not in _MODES:
+        raise ValueError(f"unknown PE mode {mode!r}")
+    for t in (q, k, v, q_c, k_c):
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("pe_attention runs on the GPU only (got a CPU tensor); "
+                               "the HIP kernels have no CPU path")
+    m = _MODES[mode]
+    half_in = q.dtype == torch.float16
+    q, k, v, q_c, k_c = (_prep_in(t) for t in (q, k, v, q_c, k_c))
+    if m != _lib.PE_MODE_NONE:
+        if freqs is None:
+            raise ValueError(f"mode {mode!r} needs freqs")
+        freqs = freqs.float().contiguous()
+    else:
+        freqs = None
+    if delta is not None:
+        if m != _lib.PE_MODE_POPE:
+            raise ValueError("delta (phase bias) only applies to PoPE/FoPE")
+        delta = delta.float().contiguous()
+    Dc = 0 if q_c is None else q_c.shape[-1]
+    dqk = Dc + (2 * q.shape[-1] if m == _lib.PE_MODE_POPE else q.shape[-1])
+    if scale is None:
+        scale = dqk ** -0.5
+    if compute_dtype is None:
+        dt = _compute_dtype((q, k, v, q_c, k_c))
+    else:
+        dt = _dtype_code(compute_dtype)
+    cfg = dict(mode=m, dtype=dt, causal=_CAUSAL[causal], start_pos_q=int(start_pos_q),
+               start_pos_k=int(start_pos_k), qk_norm=bool(qk_norm), scale=float(scale),
+               mscale=float(rope_mscale))
+    out, lse = PEAttentionFn.apply(q, k, v, q_c, k_c, freqs, delta, cfg)
+    if half_in:
+        out = out.to(torch.float16)
+    return (out, lse) if return_lse else out
+
+
+def default_pope_scale(d: int) -> float:
+    """1/sqrt(D), D the pre-transform head dim (legacy fused API, tests/test_fpope.py:1537)."""
+    return 1.0 / math.sqrt(d)
