@@ -141,6 +141,26 @@ int pe_attn_operand_width(const pe_attn_params* p);
 const char* pe_attn_strerror(int code);
 int pe_attn_version(void);
 
+/* Kernel stages of pe_attn_fwd / pe_attn_bwd that can be bracketed by caller-owned HIP events. */
+enum {
+  PE_STAGE_FWD_PREP = 0, /* q/k (and v repack) positional transform kernels     */
+  PE_STAGE_FWD_CORE = 1, /* attention forward kernel                             */
+  PE_STAGE_BWD_PRE = 2,  /* dO repack + Di = rowsum(dO o O)                      */
+  PE_STAGE_BWD_DKDV = 3, /* dK~/dV kernel (owns key blocks)                      */
+  PE_STAGE_BWD_DQ = 4,   /* dQ~ kernel (owns query blocks)                       */
+  PE_STAGE_BWD_INV = 5,  /* inverse transform + phase-bias / frequency reduction */
+  PE_STAGE_COUNT = 6
+};
+
+/* Profiling hook (no counterpart in the reference, whose harnesses time whole calls with
+ * torch.cuda.synchronize + perf_counter, scripts/benchmark_fpope_vs_rope.py:67-78).  Sets, for the
+ * whole process (autograd runs backward passes on its own thread), an array of 2*PE_STAGE_COUNT
+ * hipEvent_t handles: events[2*i] is recorded on the call's stream right before stage i's first
+ * kernel and events[2*i+1] right after its last.  NULL entries are skipped; pass NULL to switch
+ * the hook off.  The array must stay valid until the hook is switched off or replaced.  Meant for
+ * a single-threaded benchmark: concurrent calls would record into the same events. */
+int pe_attn_set_stage_events(void* const* events);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,7 +26,11 @@ ERRORS = {
 EXPORTED = [
     "pe_attn_check", "pe_attn_fwd_workspace_bytes", "pe_attn_bwd_workspace_bytes", "pe_attn_fwd",
     "pe_attn_bwd", "pe_attn_transform", "pe_attn_operand_width", "pe_attn_strerror", "pe_attn_version",
+    "pe_attn_set_stage_events",
 ]
+
+# kernel stages bracketed by pe_attn_set_stage_events
+STAGES = ["fwd_prep", "fwd_core", "bwd_pre", "bwd_dkdv", "bwd_dq", "bwd_inv"]
 
 
 class PeTensor(ctypes.Structure):
@@ -92,6 +96,8 @@ def lib():
             L.pe_attn_strerror.restype = ctypes.c_char_p
             L.pe_attn_version.argtypes = []
             L.pe_attn_version.restype = ctypes.c_int
+            L.pe_attn_set_stage_events.argtypes = [vp]
+            L.pe_attn_set_stage_events.restype = ctypes.c_int
             _lib = L
     return _lib
 

@@ -4,6 +4,7 @@
 // "is this a gfx950" flag computed once.
 #include <hip/hip_runtime.h>
 #include <string.h>
+#include <atomic>
 #include <mutex>
 
 #include "../../include/pe_attn.h"
@@ -50,6 +51,18 @@ Layout layout(const pe_attn_params* p) {
   L.pkd_off = L.pk_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
   L.bwd_total = L.pkd_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
   return L;
+}
+
+// Profiling hook: process-wide array of 2*PE_STAGE_COUNT caller-owned hipEvent_t (may be NULL).
+// Process-wide rather than per thread because torch's autograd engine runs backward passes on
+// its own device thread.
+std::atomic<void* const*> g_stage_events{nullptr};
+
+inline void stage_mark(int stage, int end, hipStream_t s) {
+  void* const* evs = g_stage_events.load(std::memory_order_acquire);
+  if (!evs) return;
+  void* ev = evs[2 * stage + end];
+  if (ev) (void)hipEventRecord((hipEvent_t)ev, s);
 }
 
 int check_tensor(const pe_tensor_t* t, bool required) {
@@ -123,6 +136,11 @@ pe::CoreArgs core_args(const pe_attn_params* p, const Layout& L, const char* ws,
 extern "C" {
 
 int pe_attn_version(void) { return PE_ATTN_ABI_VERSION; }
+
+int pe_attn_set_stage_events(void* const* events) {
+  g_stage_events.store(events, std::memory_order_release);
+  return PE_OK;
+}
 
 const char* pe_attn_strerror(int code) {
   switch (code) {
@@ -202,6 +220,7 @@ int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   char* ws = (char*)fwd_workspace;
 
   pe::PrepArgs a;
+  stage_mark(PE_STAGE_FWD_PREP, 0, s);
   fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
   if ((rc = pe::launch_prep(a, s))) return rc;
   fill_prep(a, p, 1, kc, kr, freqs, delta, ws + L.k_off, L.dqk);
@@ -212,11 +231,15 @@ int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     fill_prep(a, &pv, 1, nullptr, v, nullptr, nullptr, ws + L.v_off, L.dv);
     if ((rc = pe::launch_prep(a, s))) return rc;
   }
+  stage_mark(PE_STAGE_FWD_PREP, 1, s);
   pe::CoreArgs c = core_args(p, L, ws, v);
   c.o = (void*)out->data; c.o_sb = out->stride[0]; c.o_sh = out->stride[1]; c.o_ss = out->stride[2];
   c.o_dtype = out->dtype;
   c.lse = lse;
-  return pe::launch_fwd(p->dtype == PE_DTYPE_BF16 ? 0 : 1, L.dqk, L.dv, c, s);
+  stage_mark(PE_STAGE_FWD_CORE, 0, s);
+  rc = pe::launch_fwd(p->dtype == PE_DTYPE_BF16 ? 0 : 1, L.dqk, L.dv, c, s);
+  stage_mark(PE_STAGE_FWD_CORE, 1, s);
+  return rc;
 }
 
 int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
@@ -253,7 +276,9 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   pb.dO_op = bws + L.do_off; pb.op_dtype = p->dtype; pb.width = L.dv;
   pb.Di = (float*)(bws + L.di_off);
   pb.B = p->B; pb.H = p->Hq; pb.S = p->Sq; pb.Dv = p->Dv;
+  stage_mark(PE_STAGE_BWD_PRE, 0, s);
   if ((rc = pe::launch_prebwd(pb, s))) return rc;
+  stage_mark(PE_STAGE_BWD_PRE, 1, s);
 
   pe::CoreArgs c = core_args(p, L, fws, v);
   c.dO = bws + L.do_off;
@@ -263,7 +288,13 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   c.dk_t = (float*)(bws + L.dk_off);
   c.dv = (void*)dv->data; c.dv_sb = dv->stride[0]; c.dv_sh = dv->stride[1]; c.dv_ss = dv->stride[2];
   c.dv_dtype = dv->dtype;
-  if ((rc = pe::launch_bwd(dt, L.dqk, L.dv, c, s))) return rc;
+  stage_mark(PE_STAGE_BWD_DKDV, 0, s);
+  if ((rc = pe::launch_bwd_dkdv(dt, L.dqk, L.dv, c, s))) return rc;
+  stage_mark(PE_STAGE_BWD_DKDV, 1, s);
+  stage_mark(PE_STAGE_BWD_DQ, 0, s);
+  if ((rc = pe::launch_bwd_dq(dt, L.dqk, L.dv, c, s))) return rc;
+  stage_mark(PE_STAGE_BWD_DQ, 1, s);
+  stage_mark(PE_STAGE_BWD_INV, 0, s);
 
   for (int side = 0; side < 2; ++side) {
     const bool key = side == 1;
@@ -302,6 +333,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     ra.dfreqs = dfreqs; ra.ddelta = ddelta;
     if ((rc = pe::launch_reduce(ra, s))) return rc;
   }
+  stage_mark(PE_STAGE_BWD_INV, 1, s);
   return PE_OK;
 }
 

@@ -275,31 +275,37 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
 }
 
 template <int DT, int DQK, int DV>
-static int run_bwd(const CoreArgs& a, hipStream_t s) {
+static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 4;
   constexpr int BMQ = (DT == 0 && DQK <= 128) ? 64 : 32;
   constexpr int BN = DT == 0 ? 64 : 32;
-  const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
-  hipLaunchKernelGGL((dkdv_kernel<DT, DQK, DV, BMQ, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
-  if (hipGetLastError() != hipSuccess) return -7;
-  const int nqb = (a.Sq + NW * 32 - 1) / (NW * 32);
-  hipLaunchKernelGGL((dq_kernel<DT, DQK, DV, BN, NW>), dim3(nqb * a.B * a.Hq), dim3(NW * 64), 0, s, a);
+  if (which == 0) {
+    const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
+    hipLaunchKernelGGL((dkdv_kernel<DT, DQK, DV, BMQ, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
+  } else {
+    const int nqb = (a.Sq + NW * 32 - 1) / (NW * 32);
+    hipLaunchKernelGGL((dq_kernel<DT, DQK, DV, BN, NW>), dim3(nqb * a.B * a.Hq), dim3(NW * 64), 0, s, a);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
 template <int DT>
-static int bwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
-  if (dqk == 64 && dv == 64) return run_bwd<DT, 64, 64>(a, s);
-  if (dqk == 64 && dv == 128) return run_bwd<DT, 64, 128>(a, s);
-  if (dqk == 128 && dv == 64) return run_bwd<DT, 128, 64>(a, s);
-  if (dqk == 128 && dv == 128) return run_bwd<DT, 128, 128>(a, s);
-  if (dqk == 256 && dv == 64) return run_bwd<DT, 256, 64>(a, s);
-  if (dqk == 256 && dv == 128) return run_bwd<DT, 256, 128>(a, s);
+static int bwd_dt(int which, int dqk, int dv, const CoreArgs& a, hipStream_t s) {
+  if (dqk == 64 && dv == 64) return run_bwd<DT, 64, 64>(which, a, s);
+  if (dqk == 64 && dv == 128) return run_bwd<DT, 64, 128>(which, a, s);
+  if (dqk == 128 && dv == 64) return run_bwd<DT, 128, 64>(which, a, s);
+  if (dqk == 128 && dv == 128) return run_bwd<DT, 128, 128>(which, a, s);
+  if (dqk == 256 && dv == 64) return run_bwd<DT, 256, 64>(which, a, s);
+  if (dqk == 256 && dv == 128) return run_bwd<DT, 256, 128>(which, a, s);
   return -3;
 }
 
-int launch_bwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s) {
-  return dt == 0 ? bwd_dt<0>(dqk, dv, a, s) : bwd_dt<1>(dqk, dv, a, s);
+int launch_bwd_dkdv(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s) {
+  return dt == 0 ? bwd_dt<0>(0, dqk, dv, a, s) : bwd_dt<1>(0, dqk, dv, a, s);
+}
+
+int launch_bwd_dq(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s) {
+  return dt == 0 ? bwd_dt<0>(1, dqk, dv, a, s) : bwd_dt<1>(1, dqk, dv, a, s);
 }
 
 }  // namespace pe

@@ -30,7 +30,8 @@ struct CoreArgs {
 };
 
 int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
-int launch_bwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
+int launch_bwd_dkdv(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
+int launch_bwd_dq(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
 bool core_supported(int dqk, int dv);
 
 // Elementwise transform: one wave per (b, h, s) row.

@@ -1,0 +1,142 @@
+"""C-ABI checks that need no GPU: libpe_attn.so loads, exports every function include/pe_attn.h
+declares, and its host-side validation returns the documented error codes (the failure paths a
+caller can hit before any kernel launch: bad shapes, unsupported widths, bad mode / dtype /
+causal flags)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from pe_ablations_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pe_attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pe_attn_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.available():
+        pytest.fail("libpe_attn.so is not built (python -m pe_ablations_amd.build)")
+    return _lib.lib()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert names, "no declarations parsed from the header"
+    assert sorted(_lib.EXPORTED) == names
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_enums_match_header():
+    text = open(HEADER).read()
+    def val(name):
+        m = re.search(rf"\b{name}\s*=\s*(-?\d+)", text)
+        assert m, name
+        return int(m.group(1))
+    for name, code in _lib.ERRORS.items():
+        assert val(name) == code, name
+    assert val("PE_MODE_POPE") == _lib.PE_MODE_POPE
+    assert val("PE_MODE_ROPE") == _lib.PE_MODE_ROPE
+    assert val("PE_MODE_NONE") == _lib.PE_MODE_NONE
+    assert val("PE_DTYPE_BF16") == _lib.PE_DTYPE_BF16
+    assert val("PE_DTYPE_FP32") == _lib.PE_DTYPE_FP32
+    assert val("PE_CAUSAL_BOTTOM_RIGHT") == _lib.PE_CAUSAL_BOTTOM_RIGHT
+    assert val("PE_STAGE_COUNT") == len(_lib.STAGES)
+
+
+def test_params_struct_layout():
+    # int32 x 14, float x 2, int64: 72 bytes, int64 at offset 64
+    assert ctypes.sizeof(_lib.PeParams) == 72
+    assert _lib.PeParams.delta_head_stride.offset == 64
+    assert ctypes.sizeof(_lib.PeTensor) == 48
+
+
+def params(**kw):
+    p = _lib.PeParams()
+    base = dict(B=1, Hq=4, Hkv=4, Sq=512, Sk=512, Dc=0, Dr=64, Dv=64, mode=_lib.PE_MODE_POPE,
+                dtype=_lib.PE_DTYPE_BF16, causal=_lib.PE_CAUSAL_TOP_LEFT, start_pos_q=0,
+                start_pos_k=0, qk_l2norm=0, scale=0.125, rope_mscale=1.0, delta_head_stride=0)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(p, k, v)
+    return p
+
+
+def check(lib, **kw):
+    return lib.pe_attn_check(ctypes.byref(params(**kw)))
+
+
+def test_valid_configs(lib):
+    assert check(lib) == 0
+    assert check(lib, Dr=128, Dv=128) == 0                       # fused PoPE D=128 (2D = 256)
+    assert check(lib, Dc=64, Dr=32, Dv=64) == 0                  # reference split module
+    assert check(lib, mode=_lib.PE_MODE_ROPE, Dr=64) == 0
+    assert check(lib, mode=_lib.PE_MODE_NONE, Dr=64, qk_l2norm=1) == 0
+    assert check(lib, Hq=8, Hkv=2) == 0                          # GQA
+    assert check(lib, Sq=1, Sk=700, causal=_lib.PE_CAUSAL_BOTTOM_RIGHT) == 0
+    assert check(lib, Sq=3, Sk=5, causal=_lib.PE_CAUSAL_NONE) == 0
+    assert check(lib, dtype=_lib.PE_DTYPE_FP32) == 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=0), "PE_ERR_SHAPE"),
+    (dict(Sq=-1), "PE_ERR_SHAPE"),
+    (dict(Hq=6, Hkv=4), "PE_ERR_SHAPE"),
+    (dict(Sq=4, Sk=8), "PE_ERR_SHAPE"),                          # top-left causal needs Sq == Sk
+    (dict(Sq=9, Sk=8, causal=_lib.PE_CAUSAL_BOTTOM_RIGHT), "PE_ERR_SHAPE"),
+    (dict(Dr=160), "PE_ERR_HEAD_DIM"),                           # 2*160 > 256
+    (dict(Dv=200), "PE_ERR_HEAD_DIM"),
+    (dict(mode=7), "PE_ERR_MODE"),
+    (dict(dtype=3), "PE_ERR_MODE"),
+    (dict(causal=5), "PE_ERR_MODE"),
+    (dict(mode=_lib.PE_MODE_ROPE, Dr=63), "PE_ERR_MODE"),        # RoPE pairs need an even width
+])
+def test_invalid_configs(lib, kw, code):
+    assert check(lib, **kw) == _lib.ERRORS[code]
+
+
+def test_null_params(lib):
+    assert lib.pe_attn_check(None) == _lib.ERRORS["PE_ERR_NULL"]
+    assert lib.pe_attn_fwd_workspace_bytes(None) == 0
+
+
+def test_workspace_sizes(lib):
+    p = params(B=2, Hq=3, Hkv=3, Sq=100, Sk=100, Dr=64, Dv=64)
+    fws = lib.pe_attn_fwd_workspace_bytes(ctypes.byref(p))
+    # q~ and k~ of width 128 in bf16 (v is read in place when it is aligned and unpadded, but the
+    # layout always reserves its repack slot)
+    rows = 2 * 3 * 100
+    assert fws >= 2 * rows * 128 * 2 + rows * 64 * 2
+    bws = lib.pe_attn_bwd_workspace_bytes(ctypes.byref(p))
+    assert bws >= rows * 64 * 2 + rows * 4 + 2 * rows * 128 * 4
+    assert lib.pe_attn_fwd_workspace_bytes(ctypes.byref(params(B=0))) == 0
+    assert lib.pe_attn_operand_width(ctypes.byref(p)) == 128
+    assert lib.pe_attn_operand_width(ctypes.byref(params(Dc=64, Dr=32))) == 128
+    assert lib.pe_attn_operand_width(ctypes.byref(params(Dr=100, Dv=128))) == 256
+
+
+def test_strerror_and_version(lib):
+    for name, code in _lib.ERRORS.items():
+        msg = lib.pe_attn_strerror(code).decode()
+        assert msg
+        if code:
+            assert msg.startswith("pe_attn:")
+    assert lib.pe_attn_version() == 1
+    with pytest.raises(_lib.PEAttnError) as ei:
+        _lib.check(_lib.ERRORS["PE_ERR_WORKSPACE"])
+    assert ei.value.code == _lib.ERRORS["PE_ERR_WORKSPACE"]
+
+
+def test_stage_hook_toggles(lib):
+    arr = (ctypes.c_void_p * (2 * len(_lib.STAGES)))()
+    assert lib.pe_attn_set_stage_events(ctypes.cast(arr, ctypes.c_void_p)) == 0
+    assert lib.pe_attn_set_stage_events(None) == 0
