@@ -26,7 +26,8 @@ size_t esz(const pe_attn_params* p) { return p->dtype == PE_DTYPE_BF16 ? 2 : 4; 
 struct Layout {
   int dqk, dv;
   size_t q_off, k_off, v_off, fwd_total;
-  size_t do_off, di_off, dq_off, dk_off, pq_off, pk_off, pkd_off, bwd_total;
+  size_t do_off, di_off, l2_off, dq_off, dk_off, pq_off, pk_off, pkd_off, bwd_total;
+  int sq_pad;
   int nq_blocks, nk_blocks;
 };
 
@@ -43,8 +44,11 @@ Layout layout(const pe_attn_params* p) {
   L.nq_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hq, p->Sq, INV_ROWS) : 0;
   L.nk_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hkv, p->Sk, INV_ROWS) : 0;
   L.do_off = 0;
+  L.sq_pad = (p->Sq + 127) / 128 * 128;
+  const size_t nq_pad = (size_t)p->B * p->Hq * L.sq_pad;
   L.di_off = L.do_off + align_up(nq * L.dv * e);
-  L.dq_off = L.di_off + align_up(nq * 4);
+  L.l2_off = L.di_off + align_up(nq_pad * 4);
+  L.dq_off = L.l2_off + align_up(nq_pad * 4);
   L.dk_off = L.dq_off + align_up(nq * L.dqk * 4);
   L.pq_off = L.dk_off + align_up(nk * L.dqk * 4);
   L.pk_off = L.pq_off + align_up((size_t)L.nq_blocks * p->Dr * 4);
@@ -275,6 +279,9 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   for (int i = 0; i < 4; ++i) { pb.do_s[i] = dout->stride[i]; pb.o_s[i] = out->stride[i]; }
   pb.dO_op = bws + L.do_off; pb.op_dtype = p->dtype; pb.width = L.dv;
   pb.Di = (float*)(bws + L.di_off);
+  pb.L2 = (float*)(bws + L.l2_off);
+  pb.lse = lse;
+  pb.s_pad = L.sq_pad;
   pb.B = p->B; pb.H = p->Hq; pb.S = p->Sq; pb.Dv = p->Dv;
   stage_mark(PE_STAGE_BWD_PRE, 0, s);
   if ((rc = pe::launch_prebwd(pb, s))) return rc;
@@ -283,6 +290,8 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   pe::CoreArgs c = core_args(p, L, fws, v);
   c.dO = bws + L.do_off;
   c.Di = (const float*)(bws + L.di_off);
+  c.L2 = (const float*)(bws + L.l2_off);
+  c.sq_pad = L.sq_pad;
   c.lse_in = lse;
   c.dq_t = (float*)(bws + L.dq_off);
   c.dk_t = (float*)(bws + L.dk_off);

@@ -26,6 +26,7 @@ namespace pe {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 typedef __attribute__((ext_vector_type(4))) short s16x4;
@@ -197,7 +198,40 @@ template <int ROWS, int NCH, int NT> struct TileStage {
   }
 };
 
+// Direct global -> LDS copy (global_load_lds_dwordx4) of a ROWS x NCH-chunk tile into the
+// swizzled layout above.  One wave instruction fills 64 consecutive 16-byte LDS slots; each lane
+// fetches the logical chunk that the swizzle places in its slot.  Rows at or beyond `nvalid`
+// (>= 1) re-read row nvalid-1, so every address stays inside the source; the kernels mask those
+// rows.  Completion is tracked by vmcnt: call dma_wait() before the barrier that publishes the
+// tile.  All NW waves participate; ROWS*NCH must be a multiple of 64*NW.
+template <int ROWS, int NCH, int NW>
+__device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t row_stride_bytes,
+                                         int nvalid, int w, int lane) {
+  constexpr int TOTAL = ROWS * NCH;
+  static_assert(TOTAL % (64 * NW) == 0, "tile must split into whole wave instructions");
+#pragma unroll
+  for (int i = 0; i < TOTAL / (64 * NW); ++i) {
+    const int base = (i * NW + w) * 64;
+    const int slot = base + lane;
+    const int row = slot / NCH, pc = slot % NCH;
+    const int lc = pc ^ swz<NCH>(row);
+    const int r = row < nvalid ? row : nvalid - 1;
+    __builtin_amdgcn_global_load_lds((const void*)(src + r * row_stride_bytes + lc * 16),
+                                     (__attribute__((address_space(3))) void*)(tile + base * 16), 16, 0, 0);
+  }
+}
+
+// Plain (unswizzled) DMA of `nchunks` <= 64 consecutive 16-byte chunks by one wave.
+__device__ __forceinline__ void dma_row(char* dst, const char* src, int nchunks, int lane) {
+  if (lane < nchunks)
+    __builtin_amdgcn_global_load_lds((const void*)(src + lane * 16),
+                                     (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ------------------------------------------------------------------ scalar math (reference semantics)
 // torch softplus, beta 1, threshold 20

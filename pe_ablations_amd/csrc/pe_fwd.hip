@@ -163,6 +163,169 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) 
   }
 }
 
+// bf16 forward tuned for gfx950: NW waves of 32 queries each (BM = 32*NW) share BN-key tiles of
+// k~ and v that are double-buffered in LDS by direct global->LDS loads, so no prefetch registers
+// are held and each wave keeps only its q~ fragments and the O^T accumulator.  With NW = 8 two
+// waves share each SIMD (<= 256 registers per wave), so one wave's softmax overlaps the other's
+// MFMAs.  The running max is raised lazily: O and l are rescaled only when some query's block
+// max exceeds the current one by more than TAU (in log2 units), which bounds p by 2^TAU.
+template <int DQK, int DV, int BN, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_vec) {
+  using M = MT<0>;
+  constexpr int BM = NW * 32;
+  constexpr int NCK = DQK / 8, NCV = DV / 8;
+  constexpr int NQF = DQK / 16, NKT = BN / 32, NPF = BN / 16, NOT = DV / 32;
+  constexpr int SK_BYTES = BN * NCK * 16, SV_BYTES = BN * NCV * 16, STAGE = SK_BYTES + SV_BYTES;
+  constexpr int SO_STRIDE = DV * 2 + 16;
+  constexpr int SMEM = (2 * STAGE) > (BM * SO_STRIDE) ? (2 * STAGE) : (BM * SO_STRIDE);
+  constexpr float TAU = 8.f;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int nqb = (a.Sq + BM - 1) / BM;
+  int qb, bh;
+  map_block(blockIdx.x, nqb, a.B * a.Hq, a.causal != 0, qb, bh);
+  const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
+  const int q0 = qb * BM, qw = q0 + w * 32, myq = qw + l32;
+  const int off = a.causal_off;
+
+  u32x4 qf[NQF];
+  {
+    const uint16_t* qrow = (const uint16_t*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + (myq < a.Sq ? myq : a.Sq - 1)) * DQK;
+#pragma unroll
+    for (int kk = 0; kk < NQF; ++kk) qf[kk] = *(const u32x4*)(qrow + kk * 16 + g * 8);
+  }
+
+  int kend = a.Sk;
+  if (a.causal) kend = min(a.Sk, q0 + BM + off);
+  const int nkb = kend > 0 ? (kend + BN - 1) / BN : 0;
+  const char* kbase = (const char*)((const uint16_t*)a.k + (int64_t)(b * a.Hkv + hk) * a.Sk * DQK);
+  const char* vbase = (const char*)((const uint16_t*)a.v + b * a.v_sb + hk * a.v_sh);
+  const int64_t krs = (int64_t)DQK * 2, vrs = a.v_ss * 2;
+
+  f32x16 o[NOT];
+#pragma unroll
+  for (int t = 0; t < NOT; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[t][j] = 0.f;
+  float m = -1e30f, l = 0.f;
+  const float sl2 = a.scale * LOG2E;
+
+  if (nkb > 0) {
+    dma_tile<BN, NCK, NW>(smem, kbase, krs, a.Sk, w, lane);
+    dma_tile<BN, NCV, NW>(smem + SK_BYTES, vbase, vrs, a.Sk, w, lane);
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * BN;
+    char* sK = smem + (kb & 1) * STAGE;
+    char* sV = sK + SK_BYTES;
+    dma_wait();
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      char* nK = smem + ((kb + 1) & 1) * STAGE;
+      dma_tile<BN, NCK, NW>(nK, kbase + (int64_t)(k0 + BN) * krs, krs, a.Sk - k0 - BN, w, lane);
+      dma_tile<BN, NCV, NW>(nK + SK_BYTES, vbase + (int64_t)(k0 + BN) * vrs, vrs, a.Sk - k0 - BN, w, lane);
+    }
+    if (a.causal && k0 > qw + 31 + off) continue;  // whole tile above this wave's diagonal
+
+    f32x16 s[NKT];
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s[nt][j] = 0.f;
+      const int row = nt * 32 + perm_row<0>(l32);
+#pragma unroll
+      for (int kk = 0; kk < NQF; ++kk)
+        s[nt] = M::mma(lds_row_frag<NCK>(sK, row, 2 * kk + g), qf[kk], s[nt]);
+    }
+    const bool edge = (a.causal && k0 + BN - 1 > qw + off) || (k0 + BN > a.Sk);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x = s[nt][j] * sl2;
+        if (edge) {
+          const int key = k0 + nt * 32 + c_logical<0>(j, g);
+          if (key >= a.Sk || (a.causal && key > myq + off)) x = -INFINITY;
+        }
+        s[nt][j] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, xor32(mx));
+    if (__any(mx > m + TAU)) {
+      const float mn = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int t = 0; t < NOT; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[t][j] *= alpha;
+    }
+    float rs = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float p = fast_exp2(s[nt][j] - m);
+        s[nt][j] = p;
+        rs += p;
+      }
+    l += rs;
+    u32x4 pf[NPF];
+#pragma unroll
+    for (int ks = 0; ks < NPF; ++ks) pf[ks] = M::pack(s[ks / 2], (ks % 2) * 8);
+#pragma unroll
+    for (int t = 0; t < NOT; ++t)
+#pragma unroll
+      for (int ks = 0; ks < NPF; ++ks)
+        o[t] = M::mma(lds_col_frag<0, NCV>(sV, ks * 16, t * 32, lane), pf[ks], o[t]);
+  }
+
+  const float lt = l + xor32(l);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < NOT; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int dv = t * 32 + c_row(j, g);
+      *(uint16_t*)(smem + (w * 32 + l32) * SO_STRIDE + dv * 2) = f2bf(o[t][j] * inv);
+    }
+  if (g == 0 && myq < a.Sq)
+    a.lse[(int64_t)(b * a.Hq + h) * a.Sq + myq] = lt > 0.f ? (m + __log2f(lt)) * LN2 : -INFINITY;
+  __syncthreads();
+  char* obase = (char*)a.o + (b * a.o_sb + h * a.o_sh) * 2;
+  if (o_vec) {
+    constexpr int CPR = DV * 2 / 16;
+    for (int q = tid; q < BM * CPR; q += NW * 64) {
+      const int row = q / CPR, c = q % CPR;
+      if (q0 + row < a.Sq)
+        *(u32x4*)(obase + (int64_t)(q0 + row) * a.o_ss * 2 + c * 16) = *(const u32x4*)(smem + row * SO_STRIDE + c * 16);
+    }
+  } else {
+    const int dvr = a.dv_real;
+    for (int q = tid; q < BM * dvr; q += NW * 64) {
+      const int row = q / dvr, c = q % dvr;
+      if (q0 + row < a.Sq)
+        ((uint16_t*)(obase + (int64_t)(q0 + row) * a.o_ss * 2))[c] = *(const uint16_t*)(smem + row * SO_STRIDE + c * 2);
+    }
+  }
+}
+
+template <int DQK, int DV>
+static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
+  constexpr int NW = 8, BN = 64;
+  const int BM = NW * 32;
+  const int nqb = (a.Sq + BM - 1) / BM;
+  const int grid = nqb * a.B * a.Hq;
+  const int o_vec = (a.dv_real == DV) && ((uintptr_t)a.o % 16 == 0) && ((a.o_ss * 2) % 16 == 0) &&
+                    ((a.o_sh * 2) % 16 == 0) && ((a.o_sb * 2) % 16 == 0);
+  hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, BN, NW>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
 template <int DT, int DQK, int DV>
 static int run_fwd(const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 4;
@@ -184,6 +347,15 @@ bool core_supported(int dqk, int dv) {
 
 template <int DT>
 static int fwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
+  if constexpr (DT == 0) {
+    if (dqk == 64 && dv == 64) return run_fwd_bf16<64, 64>(a, s);
+    if (dqk == 64 && dv == 128) return run_fwd_bf16<64, 128>(a, s);
+    if (dqk == 128 && dv == 64) return run_fwd_bf16<128, 64>(a, s);
+    if (dqk == 128 && dv == 128) return run_fwd_bf16<128, 128>(a, s);
+    if (dqk == 256 && dv == 64) return run_fwd_bf16<256, 64>(a, s);
+    if (dqk == 256 && dv == 128) return run_fwd_bf16<256, 128>(a, s);
+    return -3;
+  }
   if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64>(a, s);
   if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128>(a, s);
   if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64>(a, s);

@@ -22,7 +22,9 @@ struct CoreArgs {
   float* lse;       // (B, Hq, Sq)
   // backward inputs / outputs
   const void* dO;   // (B, Hq, Sq, DV) contiguous compute dtype (padded)
-  const float* Di;  // (B, Hq, Sq)  rowsum(dO * O)
+  const float* Di;  // (B, Hq, sq_pad)  rowsum(dO * O), 0 on padding rows
+  const float* L2;  // (B, Hq, sq_pad)  lse * log2(e), +inf on padding rows and rows without keys
+  int sq_pad;       // Sq rounded up to a multiple of 64
   const float* lse_in;
   float* dq_t;      // (B, Hq, Sq, DQK) fp32, already multiplied by scale
   float* dk_t;      // (B, Hkv, Sk, DQK) fp32, already multiplied by scale (summed over the GQA group)
@@ -45,12 +47,13 @@ struct PrepArgs {
 };
 int launch_prep(const PrepArgs& a, hipStream_t s);
 
-// dO repack (to compute dtype, width DV, contiguous) and Di = rowsum(dO * O).
+// dO repack (to compute dtype, width DV, contiguous), Di = rowsum(dO * O) and the log2-scaled
+// lse, both into (B, H, S_pad) arrays whose padding rows hold Di = 0, L2 = +inf.
 struct PreBwdArgs {
   const void* dout; int dout_dtype; int64_t do_s[4];
   const void* out; int out_dtype; int64_t o_s[4];
   void* dO_op; int op_dtype; int width;
-  float* Di;
+  const float* lse; float* Di; float* L2; int s_pad;
   int B, H, S, Dv;
 };
 int launch_prebwd(const PreBwdArgs& a, hipStream_t s);

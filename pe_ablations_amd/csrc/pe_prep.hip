@@ -95,14 +95,22 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
   for (int c = used + lane; c < a.width; c += 64) store_from_float(a.dst, dbase + c, a.dst_dtype, 0.f);
 }
 
+// One wave per padded row (b, h, s < S_pad).  Rows s < S: dO repack, Di, L2 = lse*log2(e) (a row
+// without visible keys, lse = -inf, gets +inf so that its probabilities are 0).  Padding rows:
+// Di = 0, L2 = +inf.
 __global__ __launch_bounds__(256) void prebwd_kernel(PreBwdArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t nrows = (int64_t)a.B * a.H * a.S;
-  if (row >= nrows) return;
-  const int s = (int)(row % a.S);
-  const int bh = (int)(row / a.S);
+  const int64_t prow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nprows = (int64_t)a.B * a.H * a.s_pad;
+  if (prow >= nprows) return;
+  const int s = (int)(prow % a.s_pad);
+  const int bh = (int)(prow / a.s_pad);
+  if (s >= a.S) {
+    if (lane == 0) { a.Di[prow] = 0.f; a.L2[prow] = INFINITY; }
+    return;
+  }
   const int h = bh % a.H, b = bh / a.H;
+  const int64_t row = (int64_t)bh * a.S + s;
   const int64_t d0 = b * a.do_s[0] + h * a.do_s[1] + (int64_t)s * a.do_s[2];
   const int64_t o0 = b * a.o_s[0] + h * a.o_s[1] + (int64_t)s * a.o_s[2];
   float acc = 0.f;
@@ -115,7 +123,11 @@ __global__ __launch_bounds__(256) void prebwd_kernel(PreBwdArgs a) {
     store_from_float(a.dO_op, row * a.width + c, a.op_dtype, d);
   }
   acc = wave_sum(acc);
-  if (lane == 0) a.Di[row] = acc;
+  if (lane == 0) {
+    a.Di[prow] = acc;
+    const float lv = a.lse[row];
+    a.L2[prow] = lv == -INFINITY ? INFINITY : lv * LOG2E;
+  }
 }
 
 // One block = rows [chunk*R, chunk*R + R) of one (b, h); TPR threads per row, 256/TPR rows at once.
@@ -257,7 +269,7 @@ int launch_prep(const PrepArgs& a, hipStream_t s) {
 }
 
 int launch_prebwd(const PreBwdArgs& a, hipStream_t s) {
-  const int64_t nrows = (int64_t)a.B * a.H * a.S;
+  const int64_t nrows = (int64_t)a.B * a.H * a.s_pad;
   hipLaunchKernelGGL(prebwd_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
