@@ -138,6 +138,19 @@ int pe_attn_transform(const pe_attn_params* p, int is_key,
                       void* dst, void* stream);
 int pe_attn_operand_width(const pe_attn_params* p);
 
+/* Backward of pe_attn_transform (the autograd of forward_query / forward_key,
+ * src/model/pope.py:124-183, src/model/fpope.py:266-338).  g: gradient of the transformed rows,
+ * fp32 (B,H,S,width) contiguous (width = pe_attn_operand_width).  Writes dxc (data may be NULL
+ * when Dc == 0) and dxr through their views; for PoPE also dfreqs (Dr,) and, for keys, ddelta
+ * ((Dr,) shared or (H,Dr) per head), fp32, overwritten, either may be NULL.  The workspace holds
+ * the per-block partial sums behind the deterministic reduction. */
+size_t pe_attn_transform_bwd_workspace_bytes(const pe_attn_params* p, int is_key);
+int pe_attn_transform_bwd(const pe_attn_params* p, int is_key, const float* g,
+                          const pe_tensor_t* xr, const float* freqs, const float* delta,
+                          const pe_tensor_t* dxc, const pe_tensor_t* dxr,
+                          float* dfreqs, float* ddelta,
+                          void* workspace, size_t ws_bytes, void* stream);
+
 const char* pe_attn_strerror(int code);
 int pe_attn_version(void);
 

@@ -124,28 +124,29 @@ def positions(n: int, start: int = 0) -> torch.Tensor:
 
 
 def pope_phases(n: int, freqs: torch.Tensor, start: int = 0,
-                delta: Optional[torch.Tensor] = None) -> torch.Tensor:
+                delta: Optional[torch.Tensor] = None, dtype=torch.float32) -> torch.Tensor:
     """phi = fl(pos * theta) (+ delta): torch.outer then add, float32 (src/model/pope.py:88-90,172-176).
 
-    delta: None, (D,) shared, or (H, D) per head.  Returns (S, D) or (H, S, D)."""
-    ph = torch.outer(positions(n, start), freqs.float())
+    delta: None, (D,) shared, or (H, D) per head.  Returns (S, D) or (H, S, D).  ``dtype`` float64
+    evaluates the same expression in double precision (used by gradient checks)."""
+    ph = torch.outer(positions(n, start).to(dtype), freqs.to(dtype))
     if delta is None:
         return ph
-    delta = delta.float()
+    delta = delta.to(dtype)
     if delta.dim() == 1:
         return ph + delta
     return ph.unsqueeze(0) + delta.unsqueeze(1)
 
 
 def pope_transform(x: torch.Tensor, freqs: torch.Tensor, start: int = 0,
-                   delta: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """x (B, H, S, D) -> [mu cos phi, mu sin phi] (B, H, S, 2D), float32 math.
+                   delta: Optional[torch.Tensor] = None, dtype=torch.float32) -> torch.Tensor:
+    """x (B, H, S, D) -> [mu cos phi, mu sin phi] (B, H, S, 2D), float32 math (or ``dtype``).
 
     Query: delta None (src/model/pope.py:124-149).  Key: delta already clamped by the caller
     (src/model/pope.py:151-183).  mu = softplus (beta 1, threshold 20)."""
     B, H, S, D = x.shape
-    mu = F.softplus(x.float())
-    ph = pope_phases(S, freqs, start, delta)
+    mu = F.softplus(x.to(dtype))
+    ph = pope_phases(S, freqs, start, delta, dtype)
     if ph.dim() == 2:
         ph = ph.view(1, 1, S, D)
     else:
@@ -233,7 +234,7 @@ def round_ste(x: torch.Tensor, dtype) -> torch.Tensor:
 
 def pope_attention(q, k, v, freqs, delta, scale: Optional[float] = None, causal: bool = True,
                    start_q: int = 0, start_k: int = 0, clamp: bool = True,
-                   operand_dtype=None, core_dtype=torch.float64):
+                   operand_dtype=None, core_dtype=torch.float64, transform_dtype=torch.float32):
     """Fused-form PoPE causal attention, factorised (what the reference module computes,
     src/model/pope.py:124-183 + src/model/fpope_attention.py:166-177 with d_content = 0).
 
@@ -244,11 +245,11 @@ def pope_attention(q, k, v, freqs, delta, scale: Optional[float] = None, causal:
     D = q.shape[-1]
     scale = (1.0 / math.sqrt(D)) if scale is None else scale
     d = clamp_delta(delta) if clamp else delta
-    qt = pope_transform(q, freqs, start_q)
-    kt = pope_transform(k, freqs, start_k, d)
+    qt = pope_transform(q, freqs, start_q, dtype=transform_dtype)
+    kt = pope_transform(k, freqs, start_k, d, dtype=transform_dtype)
     qt = round_ste(qt, operand_dtype)
     kt = round_ste(kt, operand_dtype)
-    vv = round_ste(v.float(), operand_dtype)
+    vv = round_ste(v.to(transform_dtype), operand_dtype)
     return attention(qt, kt, vv, scale, causal, core_dtype)
 
 
@@ -391,3 +392,77 @@ def brute_force_pope(q, k, v, freqs, delta, scale, causal=True):
         z = sum(w)
         out.append([sum(w[s] * v[s][j] for s in range(len(w))) / z for j in range(len(v[0]))])
     return out
+
+
+# --------------------------------------------------------------------------------------------
+# row-chunked closed form for long sequences (one head at S = 16384 fits in memory)
+# --------------------------------------------------------------------------------------------
+
+def pope_attention_chunked(q, k, v, freqs, delta, dout=None, scale=None, causal=True,
+                           start_q: int = 0, start_k: int = 0, chunk: int = 1024,
+                           core_dtype=torch.float32, operand_dtype=None):
+    """Fused-form PoPE attention forward (and, with ``dout``, the closed-form backward of
+    pope_attention_backward_closed_form) evaluated in query-row chunks so the (S, S) score
+    matrix never exists whole.  Single (b, h): q (Sq, D), k/v (Sk, D), delta (D,) as used.
+    Transforms in fp32 in the reference order; ``operand_dtype`` rounds q~, k~, v as autocast
+    would; the GEMMs run in ``core_dtype``.  Causal alignment: top-left when Sq == Sk, else
+    bottom-right.  Returns dict(out, lse[, dq, dk, dv, dfreqs, ddelta])."""
+    Sq, D = q.shape
+    Sk = k.shape[0]
+    scale = (1.0 / math.sqrt(D)) if scale is None else scale
+    ct = core_dtype
+    qt = pope_transform(q.view(1, 1, Sq, D), freqs, start_q)[0, 0]
+    kt = pope_transform(k.view(1, 1, Sk, D), freqs, start_k, delta)[0, 0]
+    vv = v.float()
+    if operand_dtype is not None:
+        qt, kt, vv = (t.to(operand_dtype).float() for t in (qt, kt, vv))
+    qt, kt, vv = qt.to(ct), kt.to(ct), vv.to(ct)
+    off = Sk - Sq
+    out = torch.empty(Sq, v.shape[1], dtype=ct)
+    lse = torch.empty(Sq, dtype=ct)
+    kpos = torch.arange(Sk)
+    for r0 in range(0, Sq, chunk):
+        r1 = min(Sq, r0 + chunk)
+        s = (qt[r0:r1] @ kt.T) * scale
+        if causal:
+            s = s.masked_fill(kpos.view(1, -1) > (torch.arange(r0, r1) + off).view(-1, 1), float("-inf"))
+        l = torch.logsumexp(s, -1)
+        out[r0:r1] = torch.exp(s - l.unsqueeze(-1)) @ vv
+        lse[r0:r1] = l
+    res = dict(out=out, lse=lse)
+    if dout is None:
+        return res
+    do = dout.to(ct)
+    Di = (do * out).sum(-1)
+    dqt = torch.zeros_like(qt)
+    dkt = torch.zeros_like(kt)
+    dv = torch.zeros(Sk, v.shape[1], dtype=ct)
+    for r0 in range(0, Sq, chunk):
+        r1 = min(Sq, r0 + chunk)
+        s = (qt[r0:r1] @ kt.T) * scale
+        if causal:
+            s = s.masked_fill(kpos.view(1, -1) > (torch.arange(r0, r1) + off).view(-1, 1), float("-inf"))
+        P = torch.exp(s - lse[r0:r1].unsqueeze(-1))
+        dP = do[r0:r1] @ vv.T
+        dS = P * (dP - Di[r0:r1].unsqueeze(-1)) * scale
+        dqt[r0:r1] = dS @ kt
+        dkt += dS.T @ qt[r0:r1]
+        dv += P.T @ do[r0:r1]
+    f64 = torch.float64
+    tq = torch.arange(start_q, start_q + Sq, dtype=f64)
+    tk = torch.arange(start_k, start_k + Sk, dtype=f64)
+    phq = pope_phases(Sq, freqs, start_q).to(f64)
+    phk = pope_phases(Sk, freqs, start_k, delta).to(f64)
+    mq, mk = F.softplus(q.double()), F.softplus(k.double())
+
+    def inv(g, mu, ph):
+        g = g.double()
+        gc, gs = g[:, :D], g[:, D:]
+        c, sn = ph.cos(), ph.sin()
+        return gc * c + gs * sn, mu * (gs * c - gc * sn)
+
+    dmq, dphq = inv(dqt, mq, phq)
+    dmk, dphk = inv(dkt, mk, phk)
+    res.update(dq=dmq * torch.sigmoid(q.double()), dk=dmk * torch.sigmoid(k.double()), dv=dv,
+               ddelta=dphk.sum(0), dfreqs=(dphq * tq.view(-1, 1)).sum(0) + (dphk * tk.view(-1, 1)).sum(0))
+    return res

@@ -26,7 +26,7 @@ ERRORS = {
 EXPORTED = [
     "pe_attn_check", "pe_attn_fwd_workspace_bytes", "pe_attn_bwd_workspace_bytes", "pe_attn_fwd",
     "pe_attn_bwd", "pe_attn_transform", "pe_attn_operand_width", "pe_attn_strerror", "pe_attn_version",
-    "pe_attn_set_stage_events",
+    "pe_attn_set_stage_events", "pe_attn_transform_bwd_workspace_bytes", "pe_attn_transform_bwd",
 ]
 
 # kernel stages bracketed by pe_attn_set_stage_events
@@ -96,6 +96,10 @@ def lib():
             L.pe_attn_strerror.restype = ctypes.c_char_p
             L.pe_attn_version.argtypes = []
             L.pe_attn_version.restype = ctypes.c_int
+            L.pe_attn_transform_bwd_workspace_bytes.argtypes = [P, ctypes.c_int]
+            L.pe_attn_transform_bwd_workspace_bytes.restype = sz
+            L.pe_attn_transform_bwd.argtypes = [P, ctypes.c_int, vp, T, vp, vp, T, T, vp, vp, vp, sz, vp]
+            L.pe_attn_transform_bwd.restype = ctypes.c_int
             L.pe_attn_set_stage_events.argtypes = [vp]
             L.pe_attn_set_stage_events.restype = ctypes.c_int
             _lib = L

@@ -1,0 +1,56 @@
+"""Drop-in for src/model/attention.py:GroupedQueryAttention (pe_mode "rope" and "nope").
+
+Same constructor, submodules (wq, wk, wv, wo, qk_norm, rope) and forward.  The span
+RoPE rotation -> QKNorm -> GQA repeat_interleave -> causal SDPA (src/model/attention.py:77-96) is
+one fused HIP forward / backward: the kernel rotates the interleaved pairs by fl(t * w_i) (times
+YaRN's mscale), applies QKNorm x / (||x|| + 1e-6) when the module has one, and uses the
+reference's scale 1/sqrt(head_dim).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from .functional import pe_attention
+from .normalization import QKNorm
+
+
+class GroupedQueryAttention(nn.Module):
+    def __init__(self, hidden_dim: int, num_heads: int, num_kv_heads: int, head_dim: Optional[int] = None,
+                 use_qk_norm: bool = True, rope: Optional[nn.Module] = None):
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim or (hidden_dim // num_heads)
+        self.num_groups = num_heads // num_kv_heads
+        assert num_heads % num_kv_heads == 0, "num_heads must be divisible by num_kv_heads"
+        self.wq = nn.Linear(hidden_dim, num_heads * self.head_dim, bias=False)
+        self.wk = nn.Linear(hidden_dim, num_kv_heads * self.head_dim, bias=False)
+        self.wv = nn.Linear(hidden_dim, num_kv_heads * self.head_dim, bias=False)
+        self.wo = nn.Linear(num_heads * self.head_dim, hidden_dim, bias=False)
+        self.qk_norm = QKNorm(self.head_dim) if use_qk_norm else None
+        self.rope = rope
+
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0) -> torch.Tensor:
+        """``mask`` must be None (the reference's TransformerBlock passes None; an explicit dense
+        mask would need a masked kernel variant that this build does not provide)."""
+        if mask is not None:
+            raise NotImplementedError("GroupedQueryAttention: only the causal (mask=None) path is fused")
+        B, S, _ = x.shape
+        q = self.wq(x).view(B, S, self.num_heads, self.head_dim).transpose(1, 2)
+        k = self.wk(x).view(B, S, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        v = self.wv(x).view(B, S, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        norm = self.qk_norm is not None
+        if self.rope is not None:
+            out = pe_attention(q, k, v, mode="rope", freqs=self.rope.kernel_inv_freq(),
+                               rope_mscale=self.rope.kernel_mscale(), qk_norm=norm,
+                               scale=1.0 / (self.head_dim ** 0.5), causal=True,
+                               start_pos_q=start_pos, start_pos_k=start_pos)
+        else:
+            out = pe_attention(q, k, v, mode="none", qk_norm=norm, scale=1.0 / (self.head_dim ** 0.5),
+                               causal=True, start_pos_q=start_pos, start_pos_k=start_pos)
+        return self.wo(out.transpose(1, 2).reshape(B, S, -1))

@@ -205,6 +205,66 @@ int pe_attn_transform(const pe_attn_params* p, int is_key, const pe_tensor_t* xc
   return pe::launch_prep(a, (hipStream_t)stream);
 }
 
+size_t pe_attn_transform_bwd_workspace_bytes(const pe_attn_params* p, int is_key) {
+  if (pe_attn_check(p) != PE_OK) return 0;
+  if (p->mode != PE_MODE_POPE) return ALIGN;
+  const int nb = pe::inv_blocks(p->B, is_key ? p->Hkv : p->Hq, is_key ? p->Sk : p->Sq, INV_ROWS);
+  return 2 * align_up((size_t)nb * (p->Dr > 0 ? p->Dr : 1) * 4);
+}
+
+int pe_attn_transform_bwd(const pe_attn_params* p, int is_key, const float* g, const pe_tensor_t* xr,
+                          const float* freqs, const float* delta, const pe_tensor_t* dxc,
+                          const pe_tensor_t* dxr, float* dfreqs, float* ddelta, void* workspace,
+                          size_t ws_bytes, void* stream) {
+  int rc = pe_attn_check(p);
+  if (rc) return rc;
+  if ((rc = check_tensor(xr, p->Dr > 0)) || (rc = check_tensor(dxr, p->Dr > 0)) ||
+      (rc = check_tensor(dxc, p->Dc > 0)))
+    return rc;
+  if (!g || (p->mode != PE_MODE_NONE && p->Dr > 0 && !freqs)) return PE_ERR_NULL;
+  const size_t need = pe_attn_transform_bwd_workspace_bytes(p, is_key);
+  if (!workspace || ws_bytes < need) return PE_ERR_WORKSPACE;
+  if ((rc = device_ok())) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const int H = is_key ? p->Hkv : p->Hq, S = is_key ? p->Sk : p->Sq;
+  const int nb = pe::inv_blocks(p->B, H, S, INV_ROWS);
+  float* part_f = (float*)workspace;
+  float* part_d = (float*)((char*)workspace + need / 2);
+  pe::InvArgs ia;
+  memset(&ia, 0, sizeof(ia));
+  ia.g = g;
+  ia.width = pad_qk(qk_width(p));
+  if (xr && xr->data) { ia.xr = xr->data; ia.xr_dtype = xr->dtype; for (int i = 0; i < 4; ++i) ia.xr_s[i] = xr->stride[i]; }
+  if (dxc && dxc->data) { ia.dxc = (void*)dxc->data; ia.dxc_dtype = dxc->dtype; for (int i = 0; i < 4; ++i) ia.dxc_s[i] = dxc->stride[i]; }
+  if (dxr && dxr->data) { ia.dxr = (void*)dxr->data; ia.dxr_dtype = dxr->dtype; for (int i = 0; i < 4; ++i) ia.dxr_s[i] = dxr->stride[i]; }
+  ia.B = p->B; ia.H = H; ia.S = S;
+  ia.Dc = p->Dc; ia.Dr = p->Dr; ia.mode = p->mode;
+  ia.start_pos = is_key ? p->start_pos_k : p->start_pos_q;
+  ia.l2norm = p->qk_l2norm; ia.is_key = is_key;
+  ia.freqs = freqs; ia.delta = is_key ? delta : nullptr; ia.delta_hs = p->delta_head_stride;
+  ia.mscale = p->rope_mscale;
+  ia.part_delta = (is_key && p->mode == PE_MODE_POPE) ? part_d : nullptr;
+  ia.part_freq = p->mode == PE_MODE_POPE ? part_f : nullptr;
+  ia.rows_per_block = INV_ROWS;
+  if (ia.Dr == 0 && ia.Dc > 0) ia.mode = PE_MODE_NONE;
+  if ((rc = pe::launch_inv(ia, nullptr, s))) return rc;
+  if (p->mode == PE_MODE_POPE && p->Dr > 0 && (dfreqs || (is_key && ddelta))) {
+    pe::ReduceArgs ra;
+    memset(&ra, 0, sizeof(ra));
+    if (is_key) {
+      ra.part_k_freq = part_f; ra.part_k_delta = part_d; ra.nk = nb;
+    } else {
+      ra.part_q_freq = part_f; ra.nq = nb;
+    }
+    ra.k_blocks_per_head = (S + INV_ROWS - 1) / INV_ROWS;
+    ra.Hkv = H; ra.B = p->B; ra.Dr = p->Dr;
+    ra.delta_per_head = p->delta_head_stride != 0;
+    ra.dfreqs = dfreqs; ra.ddelta = is_key ? ddelta : nullptr;
+    if ((rc = pe::launch_reduce(ra, s))) return rc;
+  }
+  return PE_OK;
+}
+
 int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
                 const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
                 const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,

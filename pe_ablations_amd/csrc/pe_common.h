@@ -114,9 +114,19 @@ template <int DT> __device__ __forceinline__ int c_logical(int j, int g) {
 }
 
 // ------------------------------------------------------------------ swizzled LDS tiles
-// NCH = 16-byte chunks per row (a power of two).
+// NCH = 16-byte chunks per row (a power of two, >= 8).  Chunk c of row r is stored in slot
+// c ^ swz(r).  gfx950's LDS has 64 4-byte banks (16 slots of 16 bytes); it serves a ds_read_b128
+// by 16-lane groups and a ds_read_b64_tr_b16 by 16-lane groups reading 4 consecutive rows x 32
+// bytes.  Row fragments put 16 consecutive rows on one logical chunk, so swz must be a bijection
+// of r mod 16 (mod 8 per row parity when a row is only 8 slots); transpose reads touch chunk
+// pairs {2a, 2a+1} of 4 consecutive rows, so swz(r) >> 1 must differ across those rows.  A bit
+// permutation of r meets both (checked on the hardware: no bank-conflict cycles for either).
 template <int NCH> __device__ __forceinline__ int swz(int r) {
-  return ((((r & 3) | (((r >> 3) & 1) << 2)) << 1)) & (NCH - 1);
+  static_assert(NCH >= 8, "rows must span at least 8 slots");
+  if constexpr (NCH >= 16)
+    return ((r >> 2) & 1) | ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 3);
+  else
+    return ((r >> 2) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
 }
 template <int NCH> __device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
   return (uint32_t)(row * (NCH * 16) + ((chunk ^ swz<NCH>(row)) << 4));

@@ -1,0 +1,117 @@
+"""Standalone positional transform (PoPE/FoPE polar map or RoPE rotation) on the HIP library.
+
+``pe_transform`` is what the drop-in embeddings' ``forward_query`` / ``forward_key`` / RoPE
+``forward`` run (src/model/pope.py:124-183, src/model/fpope.py:266-338, src/model/rope.py:35-57):
+pe_attn_transform forward, pe_attn_transform_bwd backward.  The fused attention never calls it;
+it exists for callers that use the embeddings on their own.  Inputs are in the reference's
+(B, S, H, D) layout; the output is a (B, S, H, W) view (W = 2D for PoPE, D for RoPE) of the
+library's padded (B, H, S, width) buffer.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+def _params(B, H, S, D, mode, dtype, start_pos, delta, mscale) -> _lib.PeParams:
+    p = _lib.PeParams()
+    p.B, p.Hq, p.Hkv, p.Sq, p.Sk = B, H, H, S, S
+    p.Dc, p.Dr, p.Dv = 0, D, 64
+    p.mode, p.dtype, p.causal = mode, dtype, _lib.PE_CAUSAL_NONE
+    p.start_pos_q = p.start_pos_k = int(start_pos)
+    p.qk_l2norm = 0
+    p.scale, p.rope_mscale = 1.0, float(mscale)
+    p.delta_head_stride = 0 if (delta is None or delta.dim() == 1) else D
+    return p
+
+
+def _view(t: Optional[torch.Tensor]) -> _lib.PeTensor:
+    d = _lib.PeTensor()
+    if t is None:
+        return d
+    d.data = t.data_ptr()
+    d.dtype = _lib.PE_DTYPE_BF16 if t.dtype == torch.bfloat16 else _lib.PE_DTYPE_FP32
+    for i, s in enumerate(t.stride()):
+        d.stride[i] = s
+    if t.shape[3] == 1:
+        d.stride[3] = 1
+    return d
+
+
+class PETransformFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, freqs, delta, mode, start_pos, is_key, mscale):
+        L = _lib.lib()
+        if x.dtype not in (torch.float32, torch.bfloat16):
+            x = x.float()
+        xv = x.transpose(1, 2)                       # (B, H, S, D) view
+        if xv.stride(-1) != 1:
+            xv = xv.contiguous()
+        B, H, S, D = xv.shape
+        cdt = _lib.PE_DTYPE_FP32 if x.dtype == torch.float32 else _lib.PE_DTYPE_BF16
+        p = _params(B, H, S, D, mode, cdt, start_pos, delta if is_key else None, mscale)
+        _lib.check(L.pe_attn_check(ctypes.byref(p)))
+        width = L.pe_attn_operand_width(ctypes.byref(p))
+        out_w = 2 * D if mode == _lib.PE_MODE_POPE else D
+        dst = torch.empty((B, H, S, width), dtype=torch.float32 if cdt == _lib.PE_DTYPE_FP32 else torch.bfloat16,
+                          device=x.device)
+        fptr = None if freqs is None else freqs.data_ptr()
+        dptr = None if (delta is None or not is_key) else delta.data_ptr()
+        with torch.cuda.device(x.device):
+            rc = L.pe_attn_transform(ctypes.byref(p), int(is_key), None, ctypes.byref(_view(xv)), fptr, dptr,
+                                     dst.data_ptr(), torch.cuda.current_stream(x.device).cuda_stream)
+        _lib.check(rc)
+        ctx.save_for_backward(xv, freqs, delta)
+        ctx.cfg = (mode, start_pos, is_key, mscale, cdt, width, x.dtype)
+        return dst[..., :out_w].transpose(1, 2)
+
+    @staticmethod
+    def backward(ctx, grad):
+        L = _lib.lib()
+        xv, freqs, delta = ctx.saved_tensors
+        mode, start_pos, is_key, mscale, cdt, width, xdtype = ctx.cfg
+        B, H, S, D = xv.shape
+        out_w = 2 * D if mode == _lib.PE_MODE_POPE else D
+        g = torch.zeros((B, H, S, width), dtype=torch.float32, device=xv.device)
+        g[..., :out_w] = grad.transpose(1, 2)
+        dx = torch.empty((B, S, H, D), dtype=xv.dtype, device=xv.device)
+        dxv = dx.transpose(1, 2)
+        p = _params(B, H, S, D, mode, cdt, start_pos, delta if is_key else None, mscale)
+        need_f = freqs is not None and ctx.needs_input_grad[1] and mode == _lib.PE_MODE_POPE
+        need_d = delta is not None and is_key and ctx.needs_input_grad[2]
+        dfreqs = torch.empty(freqs.shape, dtype=torch.float32, device=xv.device) if need_f else None
+        ddelta = torch.empty(delta.shape, dtype=torch.float32, device=xv.device) if need_d else None
+        ws_bytes = L.pe_attn_transform_bwd_workspace_bytes(ctypes.byref(p), int(is_key))
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=xv.device)
+        with torch.cuda.device(xv.device):
+            rc = L.pe_attn_transform_bwd(ctypes.byref(p), int(is_key), g.data_ptr(), ctypes.byref(_view(xv)),
+                                         None if freqs is None else freqs.data_ptr(),
+                                         None if (delta is None or not is_key) else delta.data_ptr(),
+                                         None, ctypes.byref(_view(dxv)),
+                                         None if dfreqs is None else dfreqs.data_ptr(),
+                                         None if ddelta is None else ddelta.data_ptr(),
+                                         ws.data_ptr(), ws_bytes, torch.cuda.current_stream(xv.device).cuda_stream)
+        _lib.check(rc)
+        return dx.to(xdtype), dfreqs, ddelta, None, None, None, None
+
+
+def pe_transform(x: torch.Tensor, freqs: torch.Tensor, delta: Optional[torch.Tensor], *, start_pos: int = 0,
+                 is_key: bool = False, mode: str = "pope", mscale: float = 1.0) -> torch.Tensor:
+    """x (B, S, H, D) -> PoPE [mu cos, mu sin] (B, S, H, 2D) or RoPE-rotated (B, S, H, D) on the GPU.
+
+    fp32 inputs are transformed in fp32; bf16 / fp16 inputs produce bf16."""
+    if not x.is_cuda:
+        raise RuntimeError("the positional transform runs on the GPU only (got a CPU tensor); "
+                           "the HIP library has no CPU path")
+    m = {"pope": _lib.PE_MODE_POPE, "rope": _lib.PE_MODE_ROPE}[mode]
+    freqs = freqs.float().contiguous()
+    if delta is not None:
+        delta = delta.float().contiguous()
+    if x.dtype == torch.float16:
+        x = x.to(torch.bfloat16)
+    return PETransformFn.apply(x, freqs, delta, m, int(start_pos), bool(is_key), float(mscale))

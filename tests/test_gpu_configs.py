@@ -1,0 +1,117 @@
+"""BASELINE.json configurations at their full sizes, checked slice by slice.
+
+The kernel runs the whole configuration; the oracle (the row-chunked closed form,
+oracle.pe_attention_chunked: fp32 transforms in the reference order, bf16 operand rounding in
+bf16 mode, fp32 or fp64 GEMMs) recomputes complete (batch, head) slices, which the attention of
+one head depends on alone.  A per-head phase-bias gradient sums its head over the batch, so the
+slices cover every batch entry of the heads they check.  Tolerances: 2e-2 max-abs in bf16 mode,
+1e-5 in fp32 mode (north star); phase-bias gradients relative to their largest entry.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import pe_oracle as O
+from pe_ablations_amd.functional import pe_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def md(a, b):
+    return (a.detach().double().cpu() - b.detach().double().cpu()).abs().max().item()
+
+
+def make(B, H, S, D, seed, dtype=torch.bfloat16, dev="cpu"):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v, do = (torch.randn(B, H, S, D, generator=g).to(dtype) for _ in range(4))
+    delta = torch.rand(H, D, generator=g) * (-2 * math.pi)
+    return q, k, v, do, delta
+
+
+def run_kernel(cuda, q, k, v, do, freqs, delta, scale, backward=True):
+    qg, kg, vg = (t.to(cuda).requires_grad_(backward) for t in (q, k, v))
+    dg = delta.to(cuda).requires_grad_(backward)
+    out, lse = pe_attention(qg, kg, vg, mode="pope", freqs=freqs.to(cuda), delta=dg, scale=scale, return_lse=True)
+    if backward:
+        out.backward(do.to(cuda))
+    torch.cuda.synchronize()
+    res = {"out": out.detach().cpu(), "lse": lse.cpu()}
+    if backward:
+        res.update(dq=qg.grad.cpu(), dk=kg.grad.cpu(), dv=vg.grad.cpu(), ddelta=dg.grad.cpu())
+    return res
+
+
+def check_slices(res, q, k, v, do, freqs, delta, scale, heads, batches, tol, backward=True,
+                 core=torch.float32, bf16=True):
+    od = torch.bfloat16 if bf16 else None
+    for h in heads:
+        dd = torch.zeros(q.shape[-1], dtype=torch.float64)
+        for b in batches:
+            ref = O.pope_attention_chunked(q[b, h].float(), k[b, h].float(), v[b, h].float(), freqs, delta[h],
+                                           dout=do[b, h].float() if backward else None, scale=scale,
+                                           core_dtype=core, operand_dtype=od, chunk=2048)
+            errs = {"out": md(res["out"][b, h], ref["out"]), "lse": md(res["lse"][b, h], ref["lse"])}
+            if backward:
+                errs.update(dq=md(res["dq"][b, h], ref["dq"]), dk=md(res["dk"][b, h], ref["dk"]),
+                            dv=md(res["dv"][b, h], ref["dv"]))
+                dd += ref["ddelta"]
+            for name, e in errs.items():
+                assert e < tol, (h, b, name, errs)
+        if backward and len(batches) == q.shape[0]:
+            rel = md(res["ddelta"][h], dd) / max(1.0, dd.abs().max().item())
+            assert rel < tol, (h, "ddelta", rel)
+
+
+def test_config2_gpt125m_fwd_bwd_bf16(cuda):
+    """C2: B=8, H=12, S=2048, D=64, bf16 fwd+bwd, grads q, k, v, delta."""
+    B, H, S, D = 8, 12, 2048, 64
+    q, k, v, do, delta = make(B, H, S, D, seed=2)
+    freqs = O.pope_freqs(D)
+    res = run_kernel(cuda, q, k, v, do, freqs, delta, 1 / math.sqrt(D))
+    check_slices(res, q, k, v, do, freqs, delta, 1 / math.sqrt(D), heads=[0, 11], batches=range(B), tol=2e-2)
+
+
+def test_config3_fope_fwd_bwd_bf16(cuda):
+    """C3: FoPE, B=4, H=16, S=4096, D=128, 4 frequencies per dim (base + 3 ~ U(0, theta_0)),
+    coefficients ~ N(0, 0.1^2), floor 2pi/2048, bf16 fwd+bwd."""
+    B, H, S, D, M = 4, 16, 4096, 128, 4
+    q, k, v, do, delta = make(B, H, S, D, seed=3)
+    base = O.pope_freqs(D)
+    g = torch.Generator().manual_seed(33)
+    table = torch.cat([base.unsqueeze(1), torch.rand(D, M - 1, generator=g) * float(base[0])], 1)
+    coeffs = torch.randn(D, M, generator=g) * 0.1
+    omega = O.fope_effective_freqs(base, coeffs, freq_table=table, training_length=2048)
+    res = run_kernel(cuda, q, k, v, do, omega, delta, 1 / math.sqrt(D))
+    check_slices(res, q, k, v, do, omega, delta, 1 / math.sqrt(D), heads=[5], batches=range(B), tol=2e-2)
+
+
+def test_config4_long_context_forward_bf16(cuda):
+    """C4: B=1, H=16, S=16384, D=128, bf16 forward (the 16k perplexity sweep's shape)."""
+    B, H, S, D = 1, 16, 16384, 128
+    q, k, v, do, delta = make(B, H, S, D, seed=4)
+    freqs = O.pope_freqs(D)
+    res = run_kernel(cuda, q, k, v, do, freqs, delta, 1 / math.sqrt(D), backward=False)
+    check_slices(res, q, k, v, do, freqs, delta, 1 / math.sqrt(D), heads=[0, 15], batches=[0], tol=2e-2,
+                 backward=False)
+
+
+def test_config4_long_context_forward_fp32(cuda):
+    """The reference's long-context evaluation runs in fp32 (scripts/evaluate_long_context.py:
+    109-112): S=16384, D=128 fp32 forward against an fp64 oracle at 1e-5."""
+    B, H, S, D = 1, 2, 16384, 128
+    q, k, v, do, delta = make(B, H, S, D, seed=5, dtype=torch.float32)
+    freqs = O.pope_freqs(D)
+    res = run_kernel(cuda, q, k, v, do, freqs, delta, 1 / math.sqrt(D), backward=False)
+    check_slices(res, q, k, v, do, freqs, delta, 1 / math.sqrt(D), heads=[1], batches=[0], tol=1e-5,
+                 backward=False, core=torch.float64, bf16=False)
+
+
+def test_headline_fwd_bwd_bf16_full_head(cuda):
+    """Headline: PoPE fwd+bwd, B=1, H=16, S=16384, D=128 bf16; head 3 checked end to end."""
+    B, H, S, D = 1, 16, 16384, 128
+    q, k, v, do, delta = make(B, H, S, D, seed=6)
+    freqs = O.pope_freqs(D)
+    res = run_kernel(cuda, q, k, v, do, freqs, delta, 1 / math.sqrt(D))
+    check_slices(res, q, k, v, do, freqs, delta, 1 / math.sqrt(D), heads=[3], batches=[0], tol=2e-2)

@@ -1,0 +1,178 @@
+"""GPU parity of every mode of the fused kernel (through the C ABI) against the CPU oracle.
+
+Covers FoPE (gradient into the effective frequencies), RoPE / NTK / YaRN with and without the
+fused QKNorm, no-PE, the reference module's split form (content 64 | PoPE 2x32, value 64), GQA,
+bottom-right (KV-cache) and non-causal masks, start positions, fp32 and bf16.  Tolerances: 1e-5
+max-abs in fp32 mode and 2e-2 in bf16 mode for out / dq / dk / dv; the
+frequency and phase-bias gradients are sums over B*H*S rows and are compared relative to their
+largest entry.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import pe_oracle as O
+from pe_ablations_amd.functional import pe_attention
+
+pytestmark = pytest.mark.gpu
+f64 = torch.float64
+
+
+def rnd(*shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * scale
+
+
+def md(a, b):
+    return (a.detach().double().cpu() - b.detach().double().cpu()).abs().max().item()
+
+
+def oracle_operands(mode, qc, kc, qr, kr, freqs, delta, start_q, start_k, mscale, qk_norm):
+    """[content | transform] operands in fp32 the way the reference builds them."""
+    if mode == "pope":
+        tq = O.pope_transform(qr, freqs, start_q)
+        tk = O.pope_transform(kr, freqs, start_k, delta)
+    elif mode == "rope":
+        tq = O.rope_rotate(qr, freqs, start_q) * mscale
+        tk = O.rope_rotate(kr, freqs, start_k) * mscale
+    else:
+        tq, tk = qr.float(), kr.float()
+    if qk_norm:
+        tq, tk = O.qk_l2norm(tq), O.qk_l2norm(tk)
+    if qc is not None:
+        tq = torch.cat([qc.float(), tq], -1)
+        tk = torch.cat([kc.float(), tk], -1)
+    return tq, tk
+
+
+def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=64, Dc=0,
+             dtype=torch.bfloat16, causal=True, freqs=None, delta=None, scale=None, mscale=1.0,
+             qk_norm=False, start_q=0, start_k=0, seed=0, grad_freqs=False, grad_delta=True):
+    Sk = Sq if Sk is None else Sk
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    qr, kr = rnd(B, Hq, Sq, Dr, seed=seed), rnd(B, Hkv, Sk, Dr, seed=seed + 1)
+    v = rnd(B, Hkv, Sk, Dv, seed=seed + 2)
+    dout = rnd(B, Hq, Sq, Dv, seed=seed + 3)
+    qc = rnd(B, Hq, Sq, Dc, seed=seed + 4) if Dc else None
+    kc = rnd(B, Hkv, Sk, Dc, seed=seed + 5) if Dc else None
+    ins = [t if t is None else t.to(dtype) for t in (qr, kr, v, qc, kc)]
+    dout = dout.to(dtype)
+    if scale is None:
+        scale = (Dc + (2 * Dr if mode == "pope" else Dr)) ** -0.5
+    causal_flag = ("bottom_right" if Sq != Sk else True) if causal else False
+
+    # oracle: fp32 transforms, fp64 core, bf16 operand rounding in bf16 mode
+    o_in = [None if t is None else t.float().clone().requires_grad_(True) for t in ins]
+    of = None if freqs is None else freqs.clone().requires_grad_(grad_freqs)
+    od = None if delta is None else delta.clone().requires_grad_(grad_delta)
+    tq, tk = oracle_operands(mode, o_in[3], o_in[4], o_in[0], o_in[1], of, od, start_q, start_k, mscale, qk_norm)
+    rd = torch.bfloat16 if dtype == torch.bfloat16 else None
+    tq, tk, vv = O.round_ste(tq, rd), O.round_ste(tk, rd), O.round_ste(o_in[2].float(), rd)
+    ref, ref_lse = O.attention(tq, tk, vv, scale, causal=bool(causal))
+    ref.backward(dout.double())
+
+    g_in = [None if t is None else t.to(cuda).requires_grad_(True) for t in ins]
+    gf = None if freqs is None else freqs.to(cuda).requires_grad_(grad_freqs)
+    gd = None if delta is None else delta.to(cuda).requires_grad_(grad_delta)
+    out, lse = pe_attention(g_in[0], g_in[1], g_in[2], mode=mode, q_c=g_in[3], k_c=g_in[4], freqs=gf, delta=gd,
+                            scale=scale, causal=causal_flag, start_pos_q=start_q, start_pos_k=start_k,
+                            rope_mscale=mscale, qk_norm=qk_norm, return_lse=True)
+    out.backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    errs = {"out": md(out, ref), "lse": md(lse, ref_lse)}
+    for name, a, b in zip(("dq", "dk", "dv", "dqc", "dkc"), g_in, o_in):
+        if a is not None:
+            errs[name] = md(a.grad, b.grad)
+    for name, e in errs.items():
+        assert e < tol, (name, errs)
+    for name, a, b in (("dfreqs", gf, of), ("ddelta", gd, od)):
+        if a is not None and a.requires_grad:
+            rel = md(a.grad, b.grad) / max(1.0, b.grad.abs().max().item())
+            assert rel < (2e-2 if dtype == torch.bfloat16 else 1e-4), (name, rel, errs)
+    return errs
+
+
+# ------------------------------------------------------------------------------------- PoPE / FoPE
+
+def test_fope_bf16_frequency_gradient(cuda):
+    """FoPE = PoPE kernel with freqs = omega (src/model/fpope.py:107-146); d omega flows back.
+    omega from 4 Fourier terms over random extra frequencies, floor 2pi/2048 (BASELINE config 3
+    in miniature: D=128)."""
+    D, M = 128, 4
+    base = O.pope_freqs(D)
+    table = torch.cat([base.unsqueeze(1), torch.rand(D, M - 1, generator=torch.Generator().manual_seed(9)) * float(base[0])], 1)
+    coeffs = rnd(D, M, seed=10, scale=0.1)
+    omega = O.fope_effective_freqs(base, coeffs, freq_table=table, training_length=2048).detach()
+    delta = -torch.rand(2, D, generator=torch.Generator().manual_seed(11)) * 2 * math.pi
+    run_case(cuda, Dr=D, Dv=D, Sq=320, freqs=omega, delta=delta, grad_freqs=True, seed=20)
+
+
+def test_fope_fp32_frequency_gradient(cuda):
+    D = 32
+    omega = O.fope_effective_freqs(O.pope_freqs(D), rnd(D, 4, seed=12, scale=0.4)).detach()
+    run_case(cuda, Dr=D, Dv=64, Sq=200, B=2, dtype=torch.float32, freqs=omega,
+             delta=-torch.rand(D) * 6, grad_freqs=True, seed=30)
+
+
+def test_pope_shared_delta_start_pos_fp32(cuda):
+    """Reference layout: delta (D,) shared by heads, start_pos > 0 (cached-angle offset)."""
+    run_case(cuda, Dr=64, Dv=64, Sq=150, Hq=3, Hkv=3, dtype=torch.float32, freqs=O.pope_freqs(64),
+             delta=-torch.rand(64) * 6, start_q=77, start_k=77, seed=40)
+
+
+def test_split_form_reference_module_shape(cuda):
+    """The reference module's contraction: [q_c (64) | PoPE(q_r) (2x32)], V 64, GQA 8 -> 4,
+    scale (64 + 64)^-1/2 (src/model/fpope_attention.py:107,166-177)."""
+    run_case(cuda, Dc=64, Dr=32, Dv=64, Hq=8, Hkv=4, Sq=256, B=2, freqs=O.pope_freqs(32),
+             delta=-torch.rand(32) * 6, seed=50)
+
+
+def test_split_form_fp32(cuda):
+    run_case(cuda, Dc=64, Dr=32, Dv=64, Hq=4, Hkv=2, Sq=130, dtype=torch.float32, freqs=O.pope_freqs(32),
+             delta=-torch.rand(32) * 6, seed=60)
+
+
+def test_pope_bottom_right_decode(cuda):
+    """KV-cache shapes: Sq < Sk with the bottom-right mask (src/model/fpope_attention.py:313-317)."""
+    run_case(cuda, Dr=64, Dv=64, Sq=3, Sk=300, Hq=4, Hkv=2, freqs=O.pope_freqs(64),
+             delta=-torch.rand(2, 64) * 6, start_q=297, start_k=0, seed=70)
+    run_case(cuda, Dr=64, Dv=64, Sq=64, Sk=200, dtype=torch.float32, freqs=O.pope_freqs(64),
+             delta=-torch.rand(2, 64) * 6, start_q=136, start_k=0, seed=71)
+
+
+def test_pope_non_causal(cuda):
+    run_case(cuda, Dr=64, Dv=128, Sq=100, Sk=150, causal=False, freqs=O.pope_freqs(64),
+             delta=-torch.rand(2, 64) * 6, seed=80)
+
+
+def test_pope_odd_width_padding(cuda):
+    """D = 48 (transformed width 96, padded to 128 inside the library), V = 40."""
+    run_case(cuda, Dr=48, Dv=40, Sq=90, freqs=O.pope_freqs(48), delta=-torch.rand(2, 48) * 6, seed=85)
+
+
+# ------------------------------------------------------------------------------------- RoPE / none
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rope_qknorm(cuda, dtype):
+    """RoPE (interleaved pairs) + QKNorm, scale 1/sqrt(D), GQA (src/model/attention.py:77-96)."""
+    run_case(cuda, mode="rope", Dr=64, Dv=64, Hq=4, Hkv=2, Sq=200, B=2, dtype=dtype,
+             freqs=O.rope_inv_freq(64), qk_norm=True, scale=1 / 8, seed=90)
+
+
+def test_rope_ntk_no_norm(cuda):
+    run_case(cuda, mode="rope", Dr=128, Dv=128, Sq=160, freqs=O.rope_inv_freq(128, O.ntk_theta(128, 10000.0, 4.0)),
+             qk_norm=False, scale=128 ** -0.5, start_q=11, start_k=11, seed=100)
+
+
+def test_yarn_mscale(cuda):
+    """YaRN inverse frequencies and mscale on both q and k (src/model/rope.py:206-217), no QKNorm
+    (with QKNorm the mscale cancels)."""
+    inv, ms, _, _ = O.yarn_inv_freq(64, 10000.0, 8.0)
+    run_case(cuda, mode="rope", Dr=64, Dv=64, Sq=140, dtype=torch.float32, freqs=inv, mscale=ms,
+             qk_norm=False, scale=1 / 8, seed=110)
+
+
+def test_nope_qknorm(cuda):
+    run_case(cuda, mode="none", Dr=64, Dv=64, Hq=4, Hkv=4, Sq=96, qk_norm=True, scale=1 / 8, seed=120)
