@@ -7,7 +7,7 @@
 #include <atomic>
 #include <mutex>
 
-#include "../../include/pe_attn.h"
+#include "pe_attn.h"
 #include "pe_internal.h"
 
 namespace {
@@ -26,8 +26,9 @@ size_t esz(const pe_attn_params* p) { return p->dtype == PE_DTYPE_BF16 ? 2 : 4; 
 struct Layout {
   int dqk, dv;
   size_t q_off, k_off, v_off, fwd_total;
-  size_t do_off, di_off, l2_off, dq_off, dk_off, pq_off, pk_off, pkd_off, bwd_total;
+  size_t do_off, di_off, l2_off, dq_off, dk_off, pq_off, pk_off, pkd_off, ds_off, bwd_total;
   int sq_pad;
+  int ds_nqt, ds_rows;
   int nq_blocks, nk_blocks;
 };
 
@@ -53,7 +54,14 @@ Layout layout(const pe_attn_params* p) {
   L.pq_off = L.dk_off + align_up(nk * L.dqk * 4);
   L.pk_off = L.pq_off + align_up((size_t)L.nq_blocks * p->Dr * 4);
   L.pkd_off = L.pk_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
-  L.bwd_total = L.pkd_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
+  L.ds_off = L.pkd_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
+  // bf16 path: dS in fragment order (B, Hq, Sk_pad/32, ds_nqt blocks of 4 KiB) stored by the
+  // dK/dV kernel for the dQ GEMM
+  L.ds_nqt = (p->Sq + 255) / 256 * 4;
+  L.ds_rows = (p->Sk + 127) / 128 * 128;
+  const size_t ds_bytes =
+      p->dtype == PE_DTYPE_BF16 ? (size_t)p->B * p->Hq * (L.ds_rows / 32) * L.ds_nqt * 4096 : 0;
+  L.bwd_total = L.ds_off + align_up(ds_bytes);
   return L;
 }
 
@@ -352,6 +360,9 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   c.Di = (const float*)(bws + L.di_off);
   c.L2 = (const float*)(bws + L.l2_off);
   c.sq_pad = L.sq_pad;
+  c.dS = (uint16_t*)(bws + L.ds_off);
+  c.ds_nqt = L.ds_nqt;
+  c.ds_rows = L.ds_rows;
   c.lse_in = lse;
   c.dq_t = (float*)(bws + L.dq_off);
   c.dk_t = (float*)(bws + L.dk_off);

@@ -271,15 +271,23 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // bf16 kernels tuned for gfx950.  Both keep one wave per SIMD (the 32-row fp32 accumulators for a
-// 256-wide dk~/dq~ take 128 registers) and stream 64-row tiles through LDS with direct
-// global->LDS loads into a double buffer (one barrier per tile, no prefetch registers).  A tile
-// is consumed as two 32-row halves so that only one 32x32 score tile and its packed bf16 copy are
-// live at a time.
+// 256-wide dk~/dq~ take 128 registers) and stream 64-row tiles through an LDS ring filled by
+// direct global->LDS loads (one barrier per tile, no prefetch registers).  A tile is consumed as
+// two 32-row halves, software-pipelined inside each wave: the VALU work that turns the scores of
+// half h into packed bf16 P / dS overlaps the MFMAs that consume half h-1, so the matrix core is
+// not idle while the exponentials run (a single wave per SIMD has no other wave to hide them).
 // ---------------------------------------------------------------------------------------------
 
+// Causal mask for value j of a 32x32 score tile whose lanes are keys (key = lane) and whose
+// values are rows of c_logical(j, g): the key is visible to the row iff key - off <= row.
+// `kd` = key - off - (first row of the tile) - 8*g; returns true where the key is masked.
+__device__ __forceinline__ bool masked_row(int kd, int j) { return kd > ((j >> 3) << 4) + (j & 7); }
+
 // dK~/dV: a workgroup owns 32*NW keys of one kv head; wave w keeps k~ and v of its 32 keys as MFMA
-// B operands in registers and walks every visible 64-query block of every query head of its GQA
-// group.  Per tile the LDS stage holds q~ (64 x DQK), dO (64 x DV) and the rows' lse / Di.
+// B operands in registers and walks every visible 64-query tile of every query head of its GQA
+// group.  LDS ring of 3 stages (q~ 64 x DQK, dO 64 x DV, the rows' log2 lse and Di): the tile being
+// loaded, the tile being consumed and the previous tile, whose last half's dV / dK products run
+// during the first half of the current one.
 template <int DQK, int DV, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   using M = MT<0>;
@@ -288,7 +296,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   constexpr int NKF = DQK / 16, NVF = DV / 16, NDK = DQK / 32, NDV = DV / 32;
   constexpr int SQ_BYTES = BMQ * NCQ * 16, SO_BYTES = BMQ * NCO * 16;
   constexpr int STAGE = SQ_BYTES + SO_BYTES + 2 * BMQ * 4;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+  constexpr int NSTAGE = 3;
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int nkb = (a.Sk + BNK - 1) / BNK;
@@ -327,8 +336,6 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   const float sl2 = a.scale * LOG2E;
   const int64_t qrs = (int64_t)DQK * 2, ors = (int64_t)DV * 2;
 
-  // stage one (head, query block) tile: q~ and dO rows (swizzled), then the rows' log2-scaled
-  // lse and Di from the padded per-row arrays (lanes 0-15 and 16-31 of wave 0, one chunk each)
   auto issue = [&](int it, char* st) {
     const int h = hk * grp + it / nper;
     const int q0 = (qb0 + it % nper) * BMQ;
@@ -344,66 +351,127 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     }
   };
 
-  if (niter > 0) issue(0, smem);
-  for (int it = 0; it < niter; ++it) {
-    char* st = smem + (it & 1) * STAGE;
-    const int q0 = (qb0 + it % nper) * BMQ;
+  // One loop step per 32-query half h (two halves per tile t = h / 2, stage t % 3):
+  //   A. P / dS of half h from its scores (VALU), interleaved with the MFMAs of half h-1's
+  //      products dV += P^T dO and dK~ += dS^T q~ (B operands by the transpose load);
+  //   B. at a tile boundary: wait for the tile's loads, barrier, start loading tile t + 2's
+  //      stage predecessor (the ring holds the previous, current and next tile);
+  //   C. scores S = q~ k~^T and dP = dO v^T of half h + 1.
+  const int nhalf = 2 * niter;
+  u32x4 ppf[2], pdsf[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    ppf[i] = u32x4{0u, 0u, 0u, 0u};
+    pdsf[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+  int pbase = 0;  // byte offset of the pending half's stage within smem; its first row = prow
+  int prow = 0;
+  f32x16 s, dp;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) { s[j] = 0.f; dp[j] = 0.f; }
+
+  auto scores = [&](int hh) {  // S / dP of half hh into s / dp
+    const int t = hh >> 1, mt = hh & 1;
+    const char* st = smem + (t % NSTAGE) * STAGE;
+    const int row = mt * 32 + perm_row<0>(l32);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) { s[j] = 0.f; dp[j] = 0.f; }
+#pragma unroll
+    for (int kk = 0; kk < NKF; ++kk) s = M::mma(lds_row_frag<NCQ>(st, row, 2 * kk + g), kf[kk], s);
+#pragma unroll
+    for (int kk = 0; kk < NVF; ++kk) dp = M::mma(lds_row_frag<NCO>(st + SQ_BYTES, row, 2 * kk + g), vf[kk], dp);
+  };
+
+  if (niter > 0) {
+    issue(0, smem);
     dma_wait();
     __syncthreads();
-    if (it + 1 < niter) issue(it + 1, smem + ((it + 1) & 1) * STAGE);
-    if (a.causal && kw0 > q0 + BMQ - 1 + off) continue;  // every key of this wave is after every query
-    const char* sQ = st;
-    const char* sO = st + SQ_BYTES;
-    const float* sL = (const float*)(st + SQ_BYTES + SO_BYTES);
+    if (niter > 1) issue(1, smem + STAGE);
+    scores(0);
+  }
+  for (int hh = 0; hh < nhalf; ++hh) {
+    const int t = hh >> 1, mt = hh & 1;
+    const int sb = (t % NSTAGE) * STAGE;
+    const int q0 = (qb0 + t % nper) * BMQ;
+    const float* sL = (const float*)(smem + sb + SQ_BYTES + SO_BYTES);
     const float* sD = sL + BMQ;
+    __builtin_amdgcn_sched_barrier(0);
+    // A. P = exp2(S*scale*log2e - L2) (rows past Sq carry L2 = +inf -> 0), dS = P (dP - Di)
+    const int kd = myk - off - (q0 + mt * 32) - g * 8;
+    u32x4 cpf[2], cdsf[2];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int qm = q0 + mt * 32;
-      if (a.causal && kw0 > qm + 31 + off) continue;
-      if (qm >= a.Sq) continue;
-      f32x16 s, dp;
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int qi0 = mt * 32 + h2 * 16 + g * 8;
+      const f32x4 l0 = *(const f32x4*)(sL + qi0), l1 = *(const f32x4*)(sL + qi0 + 4);
+      const f32x4 d0 = *(const f32x4*)(sD + qi0), d1 = *(const f32x4*)(sD + qi0 + 4);
+      float pv[8], dsv[8];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) { s[j] = 0.f; dp[j] = 0.f; }
-      const int row = mt * 32 + perm_row<0>(l32);
-#pragma unroll
-      for (int kk = 0; kk < NKF; ++kk) s = M::mma(lds_row_frag<NCQ>(sQ, row, 2 * kk + g), kf[kk], s);
-#pragma unroll
-      for (int kk = 0; kk < NVF; ++kk) dp = M::mma(lds_row_frag<NCO>(sO, row, 2 * kk + g), vf[kk], dp);
-      // query rows of value j: mt*32 + c_logical(j, g) = mt*32 + (j/8)*16 + g*8 + j%8
-      const bool edge = a.causal && kw0 + 31 > qm + off;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int qi0 = mt * 32 + hh * 16 + g * 8;
-        const f32x4 l0 = *(const f32x4*)(sL + qi0), l1 = *(const f32x4*)(sL + qi0 + 4);
-        const f32x4 d0 = *(const f32x4*)(sD + qi0), d1 = *(const f32x4*)(sD + qi0 + 4);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int j = hh * 8 + e;
-          const float lv = e < 4 ? l0[e] : l1[e - 4];
-          const float dd = e < 4 ? d0[e] : d1[e - 4];
-          // rows past Sq carry lse = +inf, so p = 0 there without a test
-          float p = fast_exp2(s[j] * sl2 - lv);
-          if (edge && myk > q0 + qi0 + e + off) p = 0.f;
-          s[j] = p;
-          dp[j] = p * (dp[j] - dd);
-        }
+      for (int e = 0; e < 8; ++e) {
+        const int j = h2 * 8 + e;
+        const float lv = e < 4 ? l0[e] : l1[e - 4];
+        const float dd = e < 4 ? d0[e] : d1[e - 4];
+        float p = fast_exp2(s[j] * sl2 - lv);
+        if (a.causal) p = masked_row(kd, j) ? 0.f : p;
+        pv[e] = p;
+        dsv[e] = p * (dp[j] - dd);
       }
-      u32x4 pf[2], dsf[2];
+      cpf[h2] = u32x4{pack_bf2(pv[0], pv[1]), pack_bf2(pv[2], pv[3]), pack_bf2(pv[4], pv[5]), pack_bf2(pv[6], pv[7])};
+      cdsf[h2] = u32x4{pack_bf2(dsv[0], dsv[1]), pack_bf2(dsv[2], dsv[3]), pack_bf2(dsv[4], dsv[5]), pack_bf2(dsv[6], dsv[7])};
+    }
+    // dS of this half in fragment order for the dQ GEMM: the wave's two 1 KiB chunks rows are
+    // contiguous (block (key/32, q0/64), chunks (mt*2 + h2)*64 + lane); rows past Sk are padding
+    {
+      const int h = hk * grp + t / nper;
+      char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * (a.ds_rows / 32) + (kw0 >> 5)) * a.ds_nqt * 4096 +
+                  (int64_t)(q0 >> 6) * 4096;
+      *(u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16) = cdsf[0];
+      *(u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16) = cdsf[1];
+    }
+    {
+      const char* pQ = smem + pbase;
+      const char* pO = pQ + SQ_BYTES;
 #pragma unroll
-      for (int si = 0; si < 2; ++si) {
-        pf[si] = M::pack(s, si * 8);
-        dsf[si] = M::pack(dp, si * 8);
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int t2 = 0; t2 < NDV; ++t2)
+          dv[t2] = M::mma(ppf[ks], lds_col_frag<0, NCO>(pO, prow + ks * 16, t2 * 32, lane), dv[t2]);
+#pragma unroll
+        for (int t2 = 0; t2 < NDK; ++t2)
+          dk[t2] = M::mma(pdsf[ks], lds_col_frag<0, NCQ>(pQ, prow + ks * 16, t2 * 32, lane), dk[t2]);
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int t = 0; t < NDV; ++t)
+    for (int i = 0; i < 2; ++i) {
+      ppf[i] = cpf[i];
+      pdsf[i] = cdsf[i];
+    }
+    pbase = sb;
+    prow = mt * 32;
+    // B. tile boundary
+    if (hh + 1 < nhalf) {
+      if (mt == 1) {
+        // the next tile's loads were issued before this tile's four dS stores; vector memory
+        // counts retire in issue order, so allowing four outstanding waits for the loads only
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        __syncthreads();
+        if (t + 2 < niter) issue(t + 2, smem + ((t + 2) % NSTAGE) * STAGE);
+      }
+      // C. scores of the next half
+      scores(hh + 1);
+    }
+  }
+  if (niter > 0) {
+    const char* pQ = smem + pbase;
+    const char* pO = pQ + SQ_BYTES;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          dv[t] = M::mma(pf[ks], lds_col_frag<0, NCO>(sO, mt * 32 + ks * 16, t * 32, lane), dv[t]);
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-      for (int t = 0; t < NDK; ++t)
+      for (int t2 = 0; t2 < NDV; ++t2)
+        dv[t2] = M::mma(ppf[ks], lds_col_frag<0, NCO>(pO, prow + ks * 16, t2 * 32, lane), dv[t2]);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          dk[t] = M::mma(dsf[ks], lds_col_frag<0, NCQ>(sQ, mt * 32 + ks * 16, t * 32, lane), dk[t]);
+      for (int t2 = 0; t2 < NDK; ++t2)
+        dk[t2] = M::mma(pdsf[ks], lds_col_frag<0, NCQ>(pQ, prow + ks * 16, t2 * 32, lane), dk[t2]);
     }
   }
 
@@ -424,110 +492,123 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
         store_from_float(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + col, a.dv_dtype, dv[t][j]);
     }
 }
-// dQ~: a workgroup owns 32*NW queries of one head; wave w keeps q~ and dO of its 32 queries as MFMA
-// B operands and walks the visible 64-key tiles of k~ and v.  S^T and dP^T come out with queries
-// across lanes, so each lane's lse / Di are scalars; dS is the A operand of dq~ = dS k~ with k~
-// read by the transpose load.
-template <int DQK, int DV, int NW>
-__global__ __launch_bounds__(NW * 64, 1) void dq_bf16_kernel(CoreArgs a) {
+
+// dQ~ = dS k~ as a GEMM over the dS^T rows the dK/dV kernel stored (no score recompute).  A
+// workgroup owns 256 queries of one head; its 8 waves split them into 4 pairs of 32-query tiles x
+// 2 halves of the dq~ columns, so every fragment read from LDS feeds two MFMAs (A: dS for 32
+// queries x 16 keys, shared by the wave's column tiles; B: k~ for 16 keys x 32 columns, shared by
+// its two query tiles) and the 128 accumulators per wave leave room for two waves per SIMD.  Each
+// 64-key step stages dS^T (64 keys x 256 queries) and k~ (64 x DQK) in a double-buffered LDS pair;
+// both operands are read with the transpose load.  Keys past a query's causal limit or past Sk
+// hold no valid dS (never written), so on those tiles the A fragments are masked to zero.
+__device__ __forceinline__ uint32_t keep_bf2(uint32_t v, bool lo, bool hi) {
+  return (lo ? (v & 0xffffu) : 0u) | (hi ? (v & 0xffff0000u) : 0u);
+}
+
+template <int DQK, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   using M = MT<0>;
-  constexpr int BN = 64, BM = NW * 32;
-  constexpr int NCK = DQK / 8, NCV = DV / 8;
-  constexpr int NQF = DQK / 16, NVF = DV / 16, NDQ = DQK / 32;
-  constexpr int SK_BYTES = BN * NCK * 16, SV_BYTES = BN * NCV * 16, STAGE = SK_BYTES + SV_BYTES;
+  static_assert(NW == 8, "4 query pairs x 2 column halves");
+  constexpr int BQ = 256, BK = 64;
+  constexpr int NCK = DQK / 8, NCS = BQ / 8;
+  constexpr int NTH = DQK / 64;  // 32-column tiles per column half
+  constexpr int SK_BYTES = BK * NCK * 16, SS_BYTES = BK * NCS * 16, STAGE = SK_BYTES + SS_BYTES;
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int nqb = (a.Sq + BM - 1) / BM;
+  const int nqb = (a.Sq + BQ - 1) / BQ;
   int qb, bh;
   map_block(blockIdx.x, nqb, a.B * a.Hq, a.causal != 0, qb, bh);
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
-  const int q0 = qb * BM, qw = q0 + w * 32, myq = qw + l32;
+  const int q0 = qb * BQ;
+  const int qp = w & 3, dh = w >> 2;
+  const int qw = q0 + qp * 64;  // this wave's 64 queries: tiles qw .. qw+31 and qw+32 .. qw+63
   const int off = a.causal_off;
 
-  u32x4 qf[NQF], of[NVF];
-  {
-    const int64_t rowq = (int64_t)(b * a.Hq + h) * a.Sq + (myq < a.Sq ? myq : a.Sq - 1);
-    const uint16_t* qrow = (const uint16_t*)a.q + rowq * DQK;
-    const uint16_t* orow = (const uint16_t*)a.dO + rowq * DV;
+  f32x16 acc[2][NTH];
 #pragma unroll
-    for (int kk = 0; kk < NQF; ++kk) qf[kk] = *(const u32x4*)(qrow + kk * 16 + g * 8);
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int kk = 0; kk < NVF; ++kk) of[kk] = *(const u32x4*)(orow + kk * 16 + g * 8);
-  }
-  const int64_t prow = (int64_t)(b * a.Hq + h) * a.sq_pad + myq;
-  const float lse2 = a.L2[prow], Dq = a.Di[prow];
-  f32x16 dq[NDQ];
+    for (int t = 0; t < NTH; ++t)
 #pragma unroll
-  for (int t = 0; t < NDQ; ++t)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) dq[t][j] = 0.f;
+      for (int j = 0; j < 16; ++j) acc[i][t][j] = 0.f;
 
   int kend = a.Sk;
-  if (a.causal) kend = min(a.Sk, q0 + BM + off);
-  const int nkb = kend > 0 ? (kend + BN - 1) / BN : 0;
+  if (a.causal) kend = min(a.Sk, q0 + BQ + off);
+  const int nkb = kend > 0 ? (kend + BK - 1) / BK : 0;
   const char* kbase = (const char*)((const uint16_t*)a.k + (int64_t)(b * a.Hkv + hk) * a.Sk * DQK);
-  const char* vbase = (const char*)((const uint16_t*)a.v + b * a.v_sb + hk * a.v_sh);
-  const int64_t krs = (int64_t)DQK * 2, vrs = a.v_ss * 2;
-  const float sl2 = a.scale * LOG2E;
+  const char* sbase = (const char*)a.dS + (int64_t)(b * a.Hq + h) * (a.ds_rows / 32) * a.ds_nqt * 4096;
+  const int64_t krs = (int64_t)DQK * 2;
+  // dS window for keys k0 .. k0+63 and this block's 256 queries: LDS slot (row kl, physical chunk
+  // pc) holds query chunk lc = pc ^ swz(kl) of key k0 + kl; its source is that key's 32-key block
+  // at 64-query block (q0/8 + lc)/8, chunk ((r>>1)*64 + (r&1)*32 + kl%32), r = (q0/8 + lc) % 8.
+  auto dma_ds = [&](char* tile, int k0) {
+#pragma unroll
+    for (int i = 0; i < BK * NCS / (64 * NW); ++i) {
+      const int base = (i * NW + w) * 64;
+      const int slot = base + lane;
+      const int kl = slot / NCS, pc = slot % NCS;
+      const int lc = pc ^ swz<NCS>(kl);
+      const int qc = (q0 >> 3) + lc;
+      const int k = k0 + kl, r = qc & 7;
+      const uint32_t src = ((uint32_t)(k >> 5) * a.ds_nqt + (qc >> 3)) * 4096u +
+                           (uint32_t)(((r >> 1) * 64 + (r & 1) * 32 + (k & 31)) * 16);
+      __builtin_amdgcn_global_load_lds((const void*)(sbase + src),
+                                       (__attribute__((address_space(3))) void*)(tile + base * 16), 16, 0, 0);
+    }
+  };
 
   if (nkb > 0) {
-    dma_tile<BN, NCK, NW>(smem, kbase, krs, a.Sk, w, lane);
-    dma_tile<BN, NCV, NW>(smem + SK_BYTES, vbase, vrs, a.Sk, w, lane);
+    dma_tile<BK, NCK, NW>(smem, kbase, krs, a.Sk, w, lane);
+    dma_ds(smem + SK_BYTES, 0);
   }
   for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * BN;
+    const int k0 = kb * BK;
     const char* sK = smem + (kb & 1) * STAGE;
-    const char* sV = sK + SK_BYTES;
+    const char* sS = sK + SK_BYTES;
     dma_wait();
     __syncthreads();
     if (kb + 1 < nkb) {
       char* nK = smem + ((kb + 1) & 1) * STAGE;
-      dma_tile<BN, NCK, NW>(nK, kbase + (int64_t)(k0 + BN) * krs, krs, a.Sk - k0 - BN, w, lane);
-      dma_tile<BN, NCV, NW>(nK + SK_BYTES, vbase + (int64_t)(k0 + BN) * vrs, vrs, a.Sk - k0 - BN, w, lane);
+      dma_tile<BK, NCK, NW>(nK, kbase + (int64_t)(k0 + BK) * krs, krs, a.Sk - k0 - BK, w, lane);
+      dma_ds(nK + SK_BYTES, k0 + BK);
     }
+    if (a.causal && k0 > qw + 63 + off) continue;  // every key after both of this wave's tiles
+    // masking needed when some key of the step is past the causal limit of a query or past Sk
+    const bool edge = (a.causal && k0 + BK - 1 > qw + off) || (k0 + BK > a.Sk);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int kn = k0 + nt * 32;
-      if (a.causal && kn > qw + 31 + off) continue;
-      if (kn >= a.Sk) continue;
-      f32x16 s, dp;
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      u32x4 af[2];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) { s[j] = 0.f; dp[j] = 0.f; }
-      const int row = nt * 32 + perm_row<0>(l32);
-#pragma unroll
-      for (int kk = 0; kk < NQF; ++kk) s = M::mma(lds_row_frag<NCK>(sK, row, 2 * kk + g), qf[kk], s);
-#pragma unroll
-      for (int kk = 0; kk < NVF; ++kk) dp = M::mma(lds_row_frag<NCV>(sV, row, 2 * kk + g), of[kk], dp);
-      const bool edge = (a.causal && kn + 31 > qw + off) || (kn + 32 > a.Sk);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float p = fast_exp2(s[j] * sl2 - lse2);
+      for (int i = 0; i < 2; ++i) {
+        af[i] = lds_col_frag<0, NCS>(sS, ks * 16, qp * 64 + i * 32, lane);
         if (edge) {
-          const int key = kn + c_logical<0>(j, g);
-          if (key >= a.Sk || (a.causal && key > myq + off)) p = 0.f;
+          // element e of lane (l32, g) is key k0 + ks*16 + g*8 + e of query qw + i*32 + l32
+          const int kmax = a.causal ? min(qw + i * 32 + l32 + off, a.Sk - 1) : a.Sk - 1;
+          const int lim = kmax - (k0 + ks * 16 + g * 8);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) af[i][c] = keep_bf2(af[i][c], 2 * c <= lim, 2 * c + 1 <= lim);
         }
-        dp[j] = p * (dp[j] - Dq);
       }
-      u32x4 dsf[2];
 #pragma unroll
-      for (int si = 0; si < 2; ++si) dsf[si] = M::pack(dp, si * 8);
+      for (int t = 0; t < NTH; ++t) {
+        const u32x4 bfr = lds_col_frag<0, NCK>(sK, ks * 16, (dh * NTH + t) * 32, lane);
 #pragma unroll
-      for (int t = 0; t < NDQ; ++t)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          dq[t] = M::mma(dsf[ks], lds_col_frag<0, NCK>(sK, nt * 32 + ks * 16, t * 32, lane), dq[t]);
+        for (int i = 0; i < 2; ++i) acc[i][t] = M::mma(af[i], bfr, acc[i][t]);
+      }
     }
   }
 
   float* dqb = a.dq_t + (int64_t)(b * a.Hq + h) * a.Sq * DQK;
 #pragma unroll
-  for (int t = 0; t < NDQ; ++t)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int q = qw + c_row(j, g);
-      if (q < a.Sq) dqb[(int64_t)q * DQK + t * 32 + l32] = dq[t][j] * a.scale;
-    }
+    for (int t = 0; t < NTH; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int q = qw + i * 32 + c_row(j, g);
+        if (q < a.Sq) dqb[(int64_t)q * DQK + (dh * NTH + t) * 32 + l32] = acc[i][t][j] * a.scale;
+      }
 }
 
 template <int DT, int DQK, int DV>
@@ -538,21 +619,21 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
       hipLaunchKernelGGL((dkdv_bf16_kernel<DQK, DV, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
     } else {
+      const int nqb = (a.Sq + 255) / 256;
+      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8>), dim3(nqb * a.B * a.Hq), dim3(512), 0, s, a);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -7;
+  } else {
+    constexpr int BMQ = 32, BN = 32;
+    if (which == 0) {
+      const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
+      hipLaunchKernelGGL((dkdv_kernel<DT, DQK, DV, BMQ, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
+    } else {
       const int nqb = (a.Sq + NW * 32 - 1) / (NW * 32);
-      hipLaunchKernelGGL((dq_bf16_kernel<DQK, DV, NW>), dim3(nqb * a.B * a.Hq), dim3(NW * 64), 0, s, a);
+      hipLaunchKernelGGL((dq_kernel<DT, DQK, DV, BN, NW>), dim3(nqb * a.B * a.Hq), dim3(NW * 64), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   }
-  constexpr int BMQ = (DT == 0 && DQK <= 128) ? 64 : 32;
-  constexpr int BN = DT == 0 ? 64 : 32;
-  if (which == 0) {
-    const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
-    hipLaunchKernelGGL((dkdv_kernel<DT, DQK, DV, BMQ, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
-  } else {
-    const int nqb = (a.Sq + NW * 32 - 1) / (NW * 32);
-    hipLaunchKernelGGL((dq_kernel<DT, DQK, DV, BN, NW>), dim3(nqb * a.B * a.Hq), dim3(NW * 64), 0, s, a);
-  }
-  return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
 template <int DT>

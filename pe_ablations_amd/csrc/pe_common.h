@@ -214,20 +214,43 @@ template <int ROWS, int NCH, int NT> struct TileStage {
 // (>= 1) re-read row nvalid-1, so every address stays inside the source; the kernels mask those
 // rows.  Completion is tracked by vmcnt: call dma_wait() before the barrier that publishes the
 // tile.  All NW waves participate; ROWS*NCH must be a multiple of 64*NW.
+// Addressing: instruction i of wave w fills the 64/NCH rows r0 | x (x = lane / NCH < 64/NCH, r0 a
+// multiple of 64/NCH).  swz is a bit permutation of the row bits, so swz(r0 | x) = swz(r0) ^
+// swz(x) and the lane's source offset is r0*stride + x*stride + ((lane % NCH) ^ swz(x) ^ swz(r0))*16:
+// two per-lane constants and one XOR + add per instruction with wave-uniform r0 terms.  A tile
+// with rows past the end takes the general path that clamps each row.
 template <int ROWS, int NCH, int NW>
 __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t row_stride_bytes,
                                          int nvalid, int w, int lane) {
   constexpr int TOTAL = ROWS * NCH;
+  constexpr int RPI = 64 / NCH;  // rows per wave instruction
   static_assert(TOTAL % (64 * NW) == 0, "tile must split into whole wave instructions");
+  static_assert(NCH <= 64, "a row must fit one wave instruction");
+  const uint32_t rs = (uint32_t)row_stride_bytes;
+  if (nvalid >= ROWS) {
+    const int x = lane / NCH;
+    const uint32_t U = (uint32_t)(((lane % NCH) ^ swz<NCH>(x)) << 4);
+    const uint32_t X = (uint32_t)x * rs;
 #pragma unroll
-  for (int i = 0; i < TOTAL / (64 * NW); ++i) {
-    const int base = (i * NW + w) * 64;
-    const int slot = base + lane;
-    const int row = slot / NCH, pc = slot % NCH;
-    const int lc = pc ^ swz<NCH>(row);
-    const int r = row < nvalid ? row : nvalid - 1;
-    __builtin_amdgcn_global_load_lds((const void*)(src + r * row_stride_bytes + lc * 16),
-                                     (__attribute__((address_space(3))) void*)(tile + base * 16), 16, 0, 0);
+    for (int i = 0; i < TOTAL / (64 * NW); ++i) {
+      const int base = (i * NW + w) * 64;
+      const int r0 = base / NCH;
+      const uint32_t S = (uint32_t)(swz<NCH>(r0) << 4);
+      __builtin_amdgcn_global_load_lds((const void*)(src + (uint32_t)r0 * rs + (X + (U ^ S))),
+                                       (__attribute__((address_space(3))) void*)(tile + base * 16), 16, 0, 0);
+    }
+    (void)RPI;
+  } else {
+#pragma unroll
+    for (int i = 0; i < TOTAL / (64 * NW); ++i) {
+      const int base = (i * NW + w) * 64;
+      const int slot = base + lane;
+      const int row = slot / NCH, pc = slot % NCH;
+      const int lc = pc ^ swz<NCH>(row);
+      const int r = row < nvalid ? row : nvalid - 1;
+      __builtin_amdgcn_global_load_lds((const void*)(src + (r * rs + (uint32_t)(lc * 16))),
+                                       (__attribute__((address_space(3))) void*)(tile + base * 16), 16, 0, 0);
+    }
   }
 }
 

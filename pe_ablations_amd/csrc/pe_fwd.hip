@@ -355,14 +355,15 @@ static int fwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
     if (dqk == 256 && dv == 64) return run_fwd_bf16<256, 64>(a, s);
     if (dqk == 256 && dv == 128) return run_fwd_bf16<256, 128>(a, s);
     return -3;
+  } else {
+    if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64>(a, s);
+    if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128>(a, s);
+    if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64>(a, s);
+    if (dqk == 128 && dv == 128) return run_fwd<DT, 128, 128>(a, s);
+    if (dqk == 256 && dv == 64) return run_fwd<DT, 256, 64>(a, s);
+    if (dqk == 256 && dv == 128) return run_fwd<DT, 256, 128>(a, s);
+    return -3;
   }
-  if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64>(a, s);
-  if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128>(a, s);
-  if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64>(a, s);
-  if (dqk == 128 && dv == 128) return run_fwd<DT, 128, 128>(a, s);
-  if (dqk == 256 && dv == 64) return run_fwd<DT, 256, 64>(a, s);
-  if (dqk == 256 && dv == 128) return run_fwd<DT, 256, 128>(a, s);
-  return -3;
 }
 
 int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s) {

@@ -26,6 +26,11 @@ struct CoreArgs {
   const float* L2;  // (B, Hq, sq_pad)  lse * log2(e), +inf on padding rows and rows without keys
   int sq_pad;       // Sq rounded up to a multiple of 64
   const float* lse_in;
+  uint16_t* dS;     // bf16 dS per (b, h) in MFMA fragment order: 4 KiB blocks of 32 keys x 64
+                    // queries, block (k/32, q/64) at ((k/32) * ds_nqt + q/64) * 4096 bytes; inside a
+                    // block, key kl and query chunk r = (q%64)/8 at chunk ((r>>1)*64 + (r&1)*32 + kl)
+  int ds_nqt;       // 64-query blocks per 32-key row (ceil(Sq / 256) * 4)
+  int ds_rows;      // key rows per head (Sk rounded up to 128)
   float* dq_t;      // (B, Hq, Sq, DQK) fp32, already multiplied by scale
   float* dk_t;      // (B, Hkv, Sk, DQK) fp32, already multiplied by scale (summed over the GQA group)
   void* dv; int64_t dv_sb, dv_sh, dv_ss; int dv_dtype;
