@@ -42,8 +42,11 @@ Layout layout(const pe_attn_params* p) {
   L.k_off = L.q_off + align_up(nq * L.dqk * e);
   L.v_off = L.k_off + align_up(nk * L.dqk * e);
   L.fwd_total = L.v_off + align_up(nk * L.dv * e);
+  // per-block partial sums of the phase gradient: blocks of the inverse-transform kernel (256
+  // rows), or of the gradient kernels when the transform is fused into their epilogues (dQ GEMM:
+  // 256 queries, dK/dV: 128 keys); the buffers are sized for the larger count
   L.nq_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hq, p->Sq, INV_ROWS) : 0;
-  L.nk_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hkv, p->Sk, INV_ROWS) : 0;
+  L.nk_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hkv, p->Sk, 128) : 0;
   L.do_off = 0;
   L.sq_pad = (p->Sq + 127) / 128 * 128;
   const size_t nq_pad = (size_t)p->B * p->Hq * L.sq_pad;
@@ -369,6 +372,30 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   c.dv = (void*)dv->data; c.dv_sb = dv->stride[0]; c.dv_sh = dv->stride[1]; c.dv_ss = dv->stride[2];
   c.dv_dtype = dv->dtype;
   stage_mark(PE_STAGE_BWD_DKDV, 0, s);
+  // fused form in bf16 with both halves of a column in one wave: the gradient kernels apply the
+  // inverse PoPE transform in their epilogues
+  const bool fuse = dt == 0 && p->mode == PE_MODE_POPE && p->Dc == 0 && L.dqk == 2 * p->Dr &&
+                    (p->Dr == 64 || p->Dr == 128) && qr && qr->data && kr && kr->data &&
+                    dqr && dqr->data && dkr && dkr->data;
+  const int nqg = (p->Sq + 255) / 256, nkg = (p->Sk + 127) / 128;
+  if (fuse) {
+    c.fuse_inv = 1;
+    c.Dr = p->Dr;
+    c.freqs = freqs;
+    c.delta = delta;
+    c.delta_hs = p->delta_head_stride;
+    auto view = [](pe::EpiPoPE& e, const pe_tensor_t* x, const pe_tensor_t* dx, int start) {
+      e.x = x->data; e.x_dtype = x->dtype;
+      e.dx = (void*)dx->data; e.dx_dtype = dx->dtype;
+      for (int i = 0; i < 4; ++i) { e.x_s[i] = x->stride[i]; e.dx_s[i] = dx->stride[i]; }
+      e.start_pos = start;
+    };
+    view(c.eq, qr, dqr, p->start_pos_q);
+    view(c.ek, kr, dkr, p->start_pos_k);
+    c.eq.part_freq = dfreqs ? (float*)(bws + L.pq_off) : nullptr;
+    c.ek.part_freq = dfreqs ? (float*)(bws + L.pk_off) : nullptr;
+    c.ek.part_delta = ddelta ? (float*)(bws + L.pkd_off) : nullptr;
+  }
   if ((rc = pe::launch_bwd_dkdv(dt, L.dqk, L.dv, c, s))) return rc;
   stage_mark(PE_STAGE_BWD_DKDV, 1, s);
   stage_mark(PE_STAGE_BWD_DQ, 0, s);
@@ -376,7 +403,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   stage_mark(PE_STAGE_BWD_DQ, 1, s);
   stage_mark(PE_STAGE_BWD_INV, 0, s);
 
-  for (int side = 0; side < 2; ++side) {
+  for (int side = 0; side < 2 && !fuse; ++side) {
     const bool key = side == 1;
     const pe_tensor_t* xr = key ? kr : qr;
     const pe_tensor_t* dxc = key ? dkc : dqc;
@@ -408,6 +435,13 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     ra.part_k_freq = (const float*)(bws + L.pk_off); ra.part_k_delta = (const float*)(bws + L.pkd_off);
     ra.nk = L.nk_blocks;
     ra.k_blocks_per_head = (p->Sk + INV_ROWS - 1) / INV_ROWS;
+    if (fuse) {
+      ra.nq = p->B * p->Hq * nqg;
+      ra.nk = p->B * p->Hkv * nkg;
+      ra.k_blocks_per_head = nkg;
+    } else {
+      ra.nk = pe::inv_blocks(p->B, p->Hkv, p->Sk, INV_ROWS);
+    }
     ra.Hkv = p->Hkv; ra.B = p->B; ra.Dr = p->Dr;
     ra.delta_per_head = p->delta_head_stride != 0;
     ra.dfreqs = dfreqs; ra.ddelta = ddelta;

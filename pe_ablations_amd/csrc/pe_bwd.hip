@@ -475,14 +475,85 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     }
   }
 
-  float* dkb = a.dk_t + (int64_t)(b * a.Hkv + hk) * a.Sk * DQK;
+  if (a.fuse_inv) {
+    // inverse PoPE transform: the scaled dk~ rows go through LDS (the ring is free now) so that
+    // one plain loop applies the transform, a fixed dim c per thread; dk is written through the
+    // caller's view and dphi / pos*dphi are summed per block in a fixed order
+    const EpiPoPE& e = a.ek;
+    const int Dr = DQK / 2;
+    float* st = (float*)smem;  // [BNK keys][DQK]
+    const int c = tid % Dr;
+    // EU rows per trip, software-pipelined: the x loads of trip i+1 are in flight while trip i
+    // computes (one wave per SIMD has nothing else to hide their latency behind)
+    constexpr int EU = 8;
+    const int rstep = NW * 64 / Dr;
+    const int64_t xb = b * e.x_s[0] + hk * e.x_s[1] + c * e.x_s[3];
+    auto load_trip = [&](int r0, float (&xv)[EU]) {
 #pragma unroll
-  for (int t = 0; t < NDK; ++t)
+      for (int u = 0; u < EU; ++u) {
+        const int r = r0 + u * rstep, key = k0 + r;
+        xv[u] = (r < BNK && key < a.Sk) ? load_as_float(e.x, xb + (int64_t)key * e.x_s[2], e.x_dtype) : 0.f;
+      }
+    };
+    float xv[EU], xn[EU];
+    load_trip(tid / Dr, xv);
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int key = kw0 + c_row(j, g);
-      if (key < a.Sk) dkb[(int64_t)key * DQK + t * 32 + l32] = dk[t][j] * a.scale;
+    for (int t = 0; t < NDK; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) st[(w * 32 + c_row(j, g)) * DQK + t * 32 + l32] = dk[t][j] * a.scale;
+    __syncthreads();
+    const float fr = a.freqs[c];
+    const float dl = a.delta ? a.delta[hk * a.delta_hs + c] : 0.f;
+    float sd = 0.f, sf = 0.f;
+#pragma unroll 1
+    for (int r0 = tid / Dr; r0 < BNK; r0 += EU * rstep) {
+      load_trip(r0 + EU * rstep, xn);
+#pragma unroll
+      for (int u = 0; u < EU; ++u) {
+        const int r = r0 + u * rstep, key = k0 + r;
+        if (r < BNK && key < a.Sk) {
+          const float pos = (float)(e.start_pos + key);
+          float dx;
+          const float dph = inv_pope_elem(xv[u], pos, fr, dl, a.delta != nullptr, st[r * DQK + c],
+                                          st[r * DQK + Dr + c], dx);
+          store_from_float(e.dx, b * e.dx_s[0] + hk * e.dx_s[1] + (int64_t)key * e.dx_s[2] + c * e.dx_s[3],
+                           e.dx_dtype, dx);
+          sd += dph;
+          sf += pos * dph;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < EU; ++u) xv[u] = xn[u];
     }
+    if (e.part_delta || e.part_freq) {
+      __syncthreads();
+      float* red = st;  // [2][NW*64/Dr][Dr]
+      const int nt = NW * 64 / Dr;  // threads per dim
+      red[(0 * nt + tid / Dr) * Dr + c] = sd;
+      red[(1 * nt + tid / Dr) * Dr + c] = sf;
+      __syncthreads();
+      const int64_t blk = (int64_t)bh * nkb + kb;
+      if (tid < Dr) {
+        float d0 = 0.f, f0 = 0.f;
+        for (int i = 0; i < nt; ++i) {
+          d0 += red[(0 * nt + i) * Dr + tid];
+          f0 += red[(1 * nt + i) * Dr + tid];
+        }
+        if (e.part_delta) e.part_delta[blk * Dr + tid] = d0;
+        if (e.part_freq) e.part_freq[blk * Dr + tid] = f0;
+      }
+    }
+  } else {
+    float* dkb = a.dk_t + (int64_t)(b * a.Hkv + hk) * a.Sk * DQK;
+#pragma unroll
+    for (int t = 0; t < NDK; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = kw0 + c_row(j, g);
+        if (key < a.Sk) dkb[(int64_t)key * DQK + t * 32 + l32] = dk[t][j] * a.scale;
+      }
+  }
 #pragma unroll
   for (int t = 0; t < NDV; ++t)
 #pragma unroll
@@ -511,7 +582,18 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   static_assert(NW == 8, "4 query pairs x 2 column halves");
   constexpr int BQ = 256, BK = 64;
   constexpr int NCK = DQK / 8, NCS = BQ / 8;
-  constexpr int NTH = DQK / 64;  // 32-column tiles per column half
+  constexpr int NTH = DQK / 64;  // 32-column tiles per wave
+  // column tile of a wave's t-th accumulator: with an even count, wave dh takes cos tiles
+  // dh*NTH/2 .. +NTH/2-1 and the matching sin tiles (+ DQK/64), so the inverse transform of a
+  // column needs no exchange between waves
+  auto ctile = [&](int t, int dhv) -> int {
+    if constexpr (NTH % 2 == 0) {
+      constexpr int H2 = NTH / 2;
+      return t < H2 ? dhv * H2 + t : NTH + dhv * H2 + (t - H2);
+    } else {
+      return dhv * NTH + t;
+    }
+  };
   constexpr int SK_BYTES = BK * NCK * 16, SS_BYTES = BK * NCS * 16, STAGE = SK_BYTES + SS_BYTES;
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
@@ -592,13 +674,89 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
       }
 #pragma unroll
       for (int t = 0; t < NTH; ++t) {
-        const u32x4 bfr = lds_col_frag<0, NCK>(sK, ks * 16, (dh * NTH + t) * 32, lane);
+        const u32x4 bfr = lds_col_frag<0, NCK>(sK, ks * 16, ctile(t, dh) * 32, lane);
 #pragma unroll
         for (int i = 0; i < 2; ++i) acc[i][t] = M::mma(af[i], bfr, acc[i][t]);
       }
     }
   }
 
+  if constexpr (NTH % 2 == 0) {
+    if (a.fuse_inv) {
+      // inverse PoPE transform (no phase bias on queries): the scaled dq~ rows of two query pairs
+      // at a time go through LDS, then one plain loop with a fixed dim c per thread
+      const EpiPoPE& e = a.eq;
+      const int Dr = DQK / 2;
+      float* st = (float*)smem;  // [128 queries][DQK], one half of the block's rows at a time
+      const int c = tid % Dr;
+      // EU rows per trip, pipelined as in the dK epilogue but with shorter trips and no loads across
+      // a staging barrier: the waves whose half is staged second still hold their accumulators
+      constexpr int EU = 4;
+      const int rstep = NW * 64 / Dr, ntrip = 256 / (EU * rstep);
+      const int64_t xb = b * e.x_s[0] + h * e.x_s[1] + c * e.x_s[3];
+      auto load_trip = [&](int R0, float (&xv)[EU]) {
+#pragma unroll
+        for (int u = 0; u < EU; ++u) {
+          const int q = q0 + R0 + u * rstep;
+          xv[u] = q < a.Sq ? load_as_float(e.x, xb + (int64_t)q * e.x_s[2], e.x_dtype) : 0.f;
+        }
+      };
+      auto stage = [&](int half) {
+        __syncthreads();
+        if ((qp >> 1) == half) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int t = 0; t < NTH; ++t)
+#pragma unroll
+              for (int j = 0; j < 16; ++j)
+                st[((qp & 1) * 64 + i * 32 + c_row(j, g)) * DQK + ctile(t, dh) * 32 + l32] = acc[i][t][j] * a.scale;
+        }
+        __syncthreads();
+      };
+      float xv[EU], xn[EU];
+      const float fr = a.freqs[c];
+      float sf = 0.f;
+#pragma unroll 1
+      for (int it = 0; it < ntrip; ++it) {
+        const int R0 = tid / Dr + it * EU * rstep;
+        if (it % (ntrip / 2) == 0) {
+          stage(it / (ntrip / 2));
+          load_trip(R0, xv);
+        }
+        if ((it + 1) % (ntrip / 2) != 0) load_trip(R0 + EU * rstep, xn);
+#pragma unroll
+        for (int u = 0; u < EU; ++u) {
+          const int R = R0 + u * rstep, q = q0 + R;
+          if (q < a.Sq) {
+            const int r = R & 127;
+            const float pos = (float)(e.start_pos + q);
+            float dx;
+            const float dph = inv_pope_elem(xv[u], pos, fr, 0.f, false, st[r * DQK + c], st[r * DQK + Dr + c], dx);
+            store_from_float(e.dx, b * e.dx_s[0] + h * e.dx_s[1] + (int64_t)q * e.dx_s[2] + c * e.dx_s[3],
+                             e.dx_dtype, dx);
+            sf += pos * dph;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < EU; ++u) xv[u] = xn[u];
+      }
+      if (e.part_freq) {
+        __syncthreads();
+        float* red = st;
+        const int nt = NW * 64 / Dr;
+        red[(tid / Dr) * Dr + c] = sf;
+        __syncthreads();
+        const int64_t blk = (int64_t)bh * nqb + qb;
+        if (tid < Dr) {
+          float f0 = 0.f;
+          for (int i = 0; i < nt; ++i) f0 += red[i * Dr + tid];
+          e.part_freq[blk * Dr + tid] = f0;
+        }
+      }
+      return;
+    }
+  }
   float* dqb = a.dq_t + (int64_t)(b * a.Hq + h) * a.Sq * DQK;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -607,7 +765,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int q = qw + i * 32 + c_row(j, g);
-        if (q < a.Sq) dqb[(int64_t)q * DQK + (dh * NTH + t) * 32 + l32] = acc[i][t][j] * a.scale;
+        if (q < a.Sq) dqb[(int64_t)q * DQK + ctile(t, dh) * 32 + l32] = acc[i][t][j] * a.scale;
       }
 }
 

@@ -267,9 +267,90 @@ __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ------------------------------------------------------------------ scalar math (reference semantics)
-// torch softplus, beta 1, threshold 20
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+// torch softplus (beta 1, threshold 20) and its derivative, the logistic sigmoid, from one
+// exponential: e = exp(-|x|), softplus = max(x, 0) + log1p(e), sigmoid = (x >= 0 ? 1 : e) / (1 + e).
+// log1p(e) = log(u) * e / (u - 1) with u = fl(1 + e) (Goldberg's accurate log1p, "What every computer
+// scientist should know about floating-point arithmetic", Thm. 4) keeps small softplus values to a
+// few ulp.  Hardware exp2 / log2 / rcp: softplus within ~3 ulp, sigmoid within 1.2e-7 of torch.
+__device__ __forceinline__ void softplus_sigmoid(float x, float& sp, float& sg) {
+  const float e = __builtin_amdgcn_exp2f(-__builtin_fabsf(x) * LOG2E);
+  const float u = 1.f + e;
+  const float ru = __builtin_amdgcn_rcpf(u);
+  const float l1p = u == 1.f ? e : __builtin_amdgcn_logf(u) * LN2 * (e * __builtin_amdgcn_rcpf(u - 1.f));
+  sp = x > 20.f ? x : __builtin_fmaxf(x, 0.f) + l1p;
+  sg = (x >= 0.f ? 1.f : e) * ru;
+}
+__device__ __forceinline__ float softplus_f(float x) {
+  float sp, sg;
+  softplus_sigmoid(x, sp, sg);
+  return sp;
+}
+
+// Products and sums rounded one by one, as the reference's torch ops round them (t * w, then
+// + delta).  hipcc contracts a multiply that feeds an add into one fma by default, __fmul_rn /
+// __fadd_rn included once both sit in one basic block; instructions built under this pragma carry
+// no contraction flag, so they stay separate after inlining.
+__device__ __forceinline__ float mul_nc(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_nc(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_nc(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+
+// sin and cos of an fp32 phase.  Cody-Waite reduction by pi/2 with a three-part constant
+// (P1 + P2 + P3 = pi/2 to ~2^-73): for |x| < 2^17 the first fma is exact (x and k*P1 are multiples
+// of 2^-23 whose difference is below 2), so r carries ~1 ulp; then the Taylor series of sin (to r^11)
+// and cos (to r^12) on |r| <= pi/4, whose truncation error is below 1e-11.  Max abs error 9.2e-8
+// over |x| < 2^17, measured against float64; larger phases take the library routine.
+__device__ __forceinline__ void pe_sincos(float x, float& sn, float& cs) {
+  if (__builtin_fabsf(x) >= 131072.f) {
+    sincosf(x, &sn, &cs);
+    return;
+  }
+  constexpr float P1 = 0x1.921fb6p+0f, P2 = -0x1.777a5cp-25f, P3 = -0x1p-49f;
+  const float k = __builtin_rintf(x * 0.636619772f);
+  float r = __builtin_fmaf(-k, P1, x);
+  r = __builtin_fmaf(-k, P2, r);
+  r = __builtin_fmaf(-k, P3, r);
+  const float r2 = r * r;
+  float ps = -2.50521084e-8f;                  // -1/11!
+  ps = __builtin_fmaf(ps, r2, 2.75573192e-6f);  // 1/9!
+  ps = __builtin_fmaf(ps, r2, -1.98412698e-4f); // -1/7!
+  ps = __builtin_fmaf(ps, r2, 8.33333333e-3f);  // 1/5!
+  ps = __builtin_fmaf(ps, r2, -1.66666667e-1f); // -1/3!
+  const float s = __builtin_fmaf(r2 * r, ps, r);
+  float pc = 2.08767570e-9f;                    // 1/12!
+  pc = __builtin_fmaf(pc, r2, -2.75573192e-7f); // -1/10!
+  pc = __builtin_fmaf(pc, r2, 2.48015873e-5f);  // 1/8!
+  pc = __builtin_fmaf(pc, r2, -1.38888889e-3f); // -1/6!
+  pc = __builtin_fmaf(pc, r2, 4.16666667e-2f);  // 1/4!
+  const float c = __builtin_fmaf(r2 * r2, pc, __builtin_fmaf(-0.5f, r2, 1.f));
+  const int q = (int)k & 3;
+  const float s1 = (q & 1) ? c : s, c1 = (q & 1) ? s : c;
+  sn = (q & 2) ? -s1 : s1;
+  cs = ((q + 1) & 2) ? -c1 : c1;
+}
+
+// Gradient of one PoPE element y = [mu cos phi, mu sin phi] (mu = softplus(x), phi = fl(pos*freq)
+// (+ delta, added after the product)): from the pair (gc, gs) writes dx = (gc cos + gs sin)
+// sigmoid(x) and returns dphi = mu (gs cos - gc sin).
+__device__ __forceinline__ float inv_pope_elem(float x, float pos, float freq, float dl, bool key,
+                                               float gc, float gs, float& dx) {
+  float mu, sg;
+  softplus_sigmoid(x, mu, sg);
+  float ph = mul_nc(pos, freq);
+  if (key) ph = add_nc(ph, dl);
+  float sn, cs;
+  pe_sincos(ph, sn, cs);
+  dx = (gc * cs + gs * sn) * sg;
+  return mu * (gs * cs - gc * sn);
+}
 
 // Launch-order remap.  Blocks are issued heaviest first (LPT for the causal triangle) and, when the
 // number of (batch, head) pairs divides by the 8 XCDs, every block of one head lands on the same

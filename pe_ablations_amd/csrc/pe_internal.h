@@ -6,6 +6,17 @@
 
 namespace pe {
 
+// Inverse PoPE transform fused into a gradient kernel's epilogue: the raw positional input x and
+// the view its gradient is written through, plus per-block partial sums of dphi and pos*dphi
+// (block = (b, h, tile) in that order; either pointer may be NULL).
+struct EpiPoPE {
+  const void* x; int x_dtype; int64_t x_s[4];
+  void* dx; int dx_dtype; int64_t dx_s[4];
+  int start_pos;
+  float* part_delta;
+  float* part_freq;
+};
+
 // Attention core over transformed operands.
 struct CoreArgs {
   const void* q;    // (B, Hq, Sq, DQK) contiguous, compute dtype
@@ -34,6 +45,11 @@ struct CoreArgs {
   float* dq_t;      // (B, Hq, Sq, DQK) fp32, already multiplied by scale
   float* dk_t;      // (B, Hkv, Sk, DQK) fp32, already multiplied by scale (summed over the GQA group)
   void* dv; int64_t dv_sb, dv_sh, dv_ss; int dv_dtype;
+  // fused inverse transform (bf16 fused PoPE form: Dc = 0, DQK = 2*Dr): when set the gradient
+  // kernels write dq / dk through eq / ek instead of dq_t / dk_t
+  int fuse_inv; int Dr;
+  const float* freqs; const float* delta; int64_t delta_hs;
+  EpiPoPE eq, ek;
 };
 
 int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);

@@ -46,12 +46,12 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     for (int c = lane; c < a.Dr; c += 64) {
       const float x = load_as_float(a.xr, xr0 + c * a.xr_s[3], a.xr_dtype);
       const float mu = softplus_f(x);
-      float ph = __fmul_rn(pos, a.freqs[c]);
-      if (a.is_key && a.delta) ph = __fadd_rn(ph, a.delta[h * a.delta_hs + c]);
+      float ph = mul_nc(pos, a.freqs[c]);
+      if (a.is_key && a.delta) ph = add_nc(ph, a.delta[h * a.delta_hs + c]);
       float sn, cs;
-      sincosf(ph, &sn, &cs);
-      store_from_float(a.dst, dbase + a.Dc + c, a.dst_dtype, __fmul_rn(mu, cs));
-      store_from_float(a.dst, dbase + a.Dc + a.Dr + c, a.dst_dtype, __fmul_rn(mu, sn));
+      pe_sincos(ph, sn, cs);
+      store_from_float(a.dst, dbase + a.Dc + c, a.dst_dtype, mul_nc(mu, cs));
+      store_from_float(a.dst, dbase + a.Dc + a.Dr + c, a.dst_dtype, mul_nc(mu, sn));
     }
     used += 2 * a.Dr;
   } else {  // RoPE (mode 1) or plain (mode 2): values kept in registers for the optional L2 norm
@@ -68,11 +68,11 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
         const float x0 = load_as_float(a.xr, xr0 + (2 * i) * a.xr_s[3], a.xr_dtype);
         const float x1 = has1 ? load_as_float(a.xr, xr0 + (2 * i + 1) * a.xr_s[3], a.xr_dtype) : 0.f;
         if (a.mode == 1) {
-          const float ang = __fmul_rn(pos, a.freqs[i]);
+          const float ang = mul_nc(pos, a.freqs[i]);
           float sn, cs;
-          sincosf(ang, &sn, &cs);
-          y0[k] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn)) * a.mscale;
-          y1[k] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs)) * a.mscale;
+          pe_sincos(ang, sn, cs);
+          y0[k] = sub_nc(mul_nc(x0, cs), mul_nc(x1, sn)) * a.mscale;
+          y1[k] = add_nc(mul_nc(x0, sn), mul_nc(x1, cs)) * a.mscale;
         } else {
           y0[k] = x0; y1[k] = x1;
         }
@@ -153,11 +153,12 @@ __global__ __launch_bounds__(256) void inv_pope_kernel(InvArgs a) {
     if (c < a.Dr) {
       const float pos = (float)(a.start_pos + s);
       const float x = load_as_float(a.xr, b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + c * a.xr_s[3], a.xr_dtype);
-      const float mu = softplus_f(x), sg = sigmoid_f(x);
-      float ph = __fmul_rn(pos, fr);
-      if (a.is_key && a.delta) ph = __fadd_rn(ph, dl);
+      float mu, sg;
+      softplus_sigmoid(x, mu, sg);
+      float ph = mul_nc(pos, fr);
+      if (a.is_key && a.delta) ph = add_nc(ph, dl);
       float sn, cs;
-      sincosf(ph, &sn, &cs);
+      pe_sincos(ph, sn, cs);
       const float gc = a.g[grow + a.Dc + c], gs = a.g[grow + a.Dc + a.Dr + c];
       const float dmu = gc * cs + gs * sn;
       const float dph = mu * (gs * cs - gc * sn);
@@ -206,10 +207,10 @@ __global__ __launch_bounds__(256) void inv_row_kernel(InvArgs a) {
       const float x0 = load_as_float(a.xr, xr0 + (2 * i) * a.xr_s[3], a.xr_dtype);
       const float x1 = load_as_float(a.xr, xr0 + (2 * i + 1) * a.xr_s[3], a.xr_dtype);
       if (a.mode == 1) {
-        const float ang = __fmul_rn(pos, a.freqs[i]);
-        sincosf(ang, &sn_[k], &cs_[k]);
-        z0[k] = __fsub_rn(__fmul_rn(x0, cs_[k]), __fmul_rn(x1, sn_[k])) * a.mscale;
-        z1[k] = __fadd_rn(__fmul_rn(x0, sn_[k]), __fmul_rn(x1, cs_[k])) * a.mscale;
+        const float ang = mul_nc(pos, a.freqs[i]);
+        pe_sincos(ang, sn_[k], cs_[k]);
+        z0[k] = sub_nc(mul_nc(x0, cs_[k]), mul_nc(x1, sn_[k])) * a.mscale;
+        z1[k] = add_nc(mul_nc(x0, sn_[k]), mul_nc(x1, cs_[k])) * a.mscale;
       } else {
         z0[k] = x0; z1[k] = x1;
       }
@@ -242,23 +243,54 @@ __global__ __launch_bounds__(256) void inv_row_kernel(InvArgs a) {
   }
 }
 
-__global__ __launch_bounds__(256) void reduce_kernel(ReduceArgs a) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+// One block per 64 output columns (the frequency gradient first, then the phase-bias gradient).
+// Wave w sums rows w, w + RW, w + 2 RW, ... in increasing order and wave 0 adds the RW wave sums in
+// order, so the result depends only on the partial layout, never on timing.
+constexpr int RW = 16;
+
+__global__ __launch_bounds__(RW * 64) void reduce_kernel(ReduceArgs a) {
+  __shared__ float red[RW][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nfc = (a.Dr + 63) / 64;
   const int nd = a.delta_per_head ? a.Hkv * a.Dr : a.Dr;
-  if (t < a.Dr && a.dfreqs) {
-    float s = 0.f;
-    for (int i = 0; i < a.nq; ++i) s += a.part_q_freq[(int64_t)i * a.Dr + t];
-    for (int i = 0; i < a.nk; ++i) s += a.part_k_freq[(int64_t)i * a.Dr + t];
-    a.dfreqs[t] = s;
-  }
-  if (t < nd && a.ddelta) {
-    const int c = t % a.Dr, hsel = t / a.Dr;
-    float s = 0.f;
-    for (int i = 0; i < a.nk; ++i) {
-      const int h = (i / a.k_blocks_per_head) % a.Hkv;
-      if (!a.delta_per_head || h == hsel) s += a.part_k_delta[(int64_t)i * a.Dr + c];
+  float s = 0.f;
+  float* dst = nullptr;
+  if ((int)blockIdx.x < nfc) {
+    if (!a.dfreqs) return;
+    const int c = blockIdx.x * 64 + lane;
+    if (c < a.Dr) {
+      dst = a.dfreqs + c;
+      const int n = a.nq + a.nk;
+#pragma unroll 8
+      for (int i = w; i < n; i += RW)
+        s += i < a.nq ? a.part_q_freq[(int64_t)i * a.Dr + c] : a.part_k_freq[(int64_t)(i - a.nq) * a.Dr + c];
     }
-    a.ddelta[t] = s;
+  } else {
+    if (!a.ddelta) return;
+    const int t = (blockIdx.x - nfc) * 64 + lane;
+    if (t < nd) {
+      dst = a.ddelta + t;
+      const int c = t % a.Dr, hsel = t / a.Dr;
+      if (a.delta_per_head) {  // rows of head hsel: (b * Hkv + hsel) * kbph + chunk
+        const int kb = a.k_blocks_per_head, n = a.B * kb;
+#pragma unroll 8
+        for (int j = w; j < n; j += RW) {
+          const int i = ((j / kb) * a.Hkv + hsel) * kb + j % kb;
+          s += a.part_k_delta[(int64_t)i * a.Dr + c];
+        }
+      } else {
+#pragma unroll 8
+        for (int i = w; i < a.nk; i += RW) s += a.part_k_delta[(int64_t)i * a.Dr + c];
+      }
+    }
+  }
+  red[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && dst) {
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < RW; ++i) tot += red[i][lane];
+    *dst = tot;
   }
 }
 
@@ -295,8 +327,8 @@ int launch_inv(const InvArgs& a, int* nblocks_out, hipStream_t s) {
 
 int launch_reduce(const ReduceArgs& a, hipStream_t s) {
   const int nd = a.delta_per_head ? a.Hkv * a.Dr : a.Dr;
-  const int n = nd > a.Dr ? nd : a.Dr;
-  hipLaunchKernelGGL(reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a);
+  const int nblk = (a.Dr + 63) / 64 + (nd + 63) / 64;
+  hipLaunchKernelGGL(reduce_kernel, dim3(nblk), dim3(RW * 64), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 

@@ -5,7 +5,8 @@ oracle.pe_attention_chunked: fp32 transforms in the reference order, bf16 operan
 bf16 mode, fp32 or fp64 GEMMs) recomputes complete (batch, head) slices, which the attention of
 one head depends on alone.  A per-head phase-bias gradient sums its head over the batch, so the
 slices cover every batch entry of the heads they check.  Tolerances: 2e-2 max-abs in bf16 mode,
-1e-5 in fp32 mode (north star); phase-bias gradients relative to their largest entry.
+1e-5 in fp32 mode (north star), bf16 results net of their own rounding to bf16 (tests/_cmp.py);
+phase-bias gradients relative to their largest entry.
 """
 
 import math
@@ -14,13 +15,14 @@ import pytest
 import torch
 
 from oracle import pe_oracle as O
+from tests._cmp import err
 from pe_ablations_amd.functional import pe_attention
 
 pytestmark = pytest.mark.gpu
 
 
 def md(a, b):
-    return (a.detach().double().cpu() - b.detach().double().cpu()).abs().max().item()
+    return err(a, b)
 
 
 def make(B, H, S, D, seed, dtype=torch.bfloat16, dev="cpu"):

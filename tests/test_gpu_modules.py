@@ -18,6 +18,7 @@ from pe_ablations_amd.fpope_attention import FPoPEGroupedQueryAttention, FPoPEGr
 from pe_ablations_amd.kernels import fpope_attention_forward, hip_fpope_attention
 from pe_ablations_amd.pope import PoPEEmbedding
 from pe_ablations_amd.rope import NTKAwareRotaryEmbedding, RotaryEmbedding, YaRNRotaryEmbedding
+from pe_ablations_amd.transform import pe_transform
 
 pytestmark = pytest.mark.gpu
 
@@ -202,3 +203,29 @@ def test_legacy_fused_api(cuda, dim):
     assert lse.shape == (B * H, S)
     assert md(lse, ref_lse.reshape(B * H, S)) < 1e-3
     assert torch.equal(out2, out.detach())
+
+
+@pytest.mark.parametrize("start_pos", [0, 16000, 131040, 1_000_000])
+def test_transform_phase_range(cuda, start_pos):
+    """Phases fl(t * w) from 0 up to ~1e6 rad: the device sin/cos (Cody-Waite below 2^17 rad, the
+    library routine above; start 131040 straddles the switch) against torch's float32 sin/cos in
+    the oracle transform, forward and backward, PoPE keys with phase bias and RoPE."""
+    torch.manual_seed(6)
+    D = 128
+    x = torch.randn(1, 64, 2, D)
+    freqs = O.pope_freqs(D)
+    delta = O.clamp_delta(torch.rand(2, D) * -7.0)
+    xo = x.clone().requires_grad_(True)
+    ref = O.pope_transform(xo.transpose(1, 2), freqs, start_pos, delta).transpose(1, 2)
+    gout = torch.randn_like(ref)
+    ref.backward(gout)
+    xg = x.to(cuda).requires_grad_(True)
+    out = pe_transform(xg, freqs.to(cuda), delta.to(cuda), start_pos=start_pos, is_key=True)
+    out.backward(gout.to(cuda))
+    torch.cuda.synchronize()
+    assert md(out, ref) < 1e-5
+    assert md(xg.grad, xo.grad) < 1e-5
+    inv = O.rope_inv_freq(D)
+    rr = O.rope_rotate(x.transpose(1, 2), inv, start_pos).transpose(1, 2)
+    rg = pe_transform(x.to(cuda), inv.to(cuda), None, start_pos=start_pos, mode="rope")
+    assert md(rg, rr) < 1e-5
