@@ -348,7 +348,9 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   pb.dout = dout->data; pb.dout_dtype = dout->dtype;
   pb.out = out->data; pb.out_dtype = out->dtype;
   for (int i = 0; i < 4; ++i) { pb.do_s[i] = dout->stride[i]; pb.o_s[i] = out->stride[i]; }
-  pb.dO_op = bws + L.do_off; pb.op_dtype = p->dtype; pb.width = L.dv;
+  // the bf16 dK/dV kernel reads dO in place when its rows are 16-byte aligned and exactly Dv wide
+  const bool do_direct = dt == 0 && v_direct(p, dout, L.dv);
+  pb.dO_op = do_direct ? nullptr : bws + L.do_off; pb.op_dtype = p->dtype; pb.width = L.dv;
   pb.Di = (float*)(bws + L.di_off);
   pb.L2 = (float*)(bws + L.l2_off);
   pb.lse = lse;
@@ -359,7 +361,11 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   stage_mark(PE_STAGE_BWD_PRE, 1, s);
 
   pe::CoreArgs c = core_args(p, L, fws, v);
-  c.dO = bws + L.do_off;
+  if (do_direct) {
+    c.dO = dout->data; c.do_sb = dout->stride[0]; c.do_sh = dout->stride[1]; c.do_ss = dout->stride[2];
+  } else {
+    c.dO = bws + L.do_off; c.do_ss = L.dv; c.do_sh = (int64_t)p->Sq * L.dv; c.do_sb = (int64_t)p->Hq * p->Sq * L.dv;
+  }
   c.Di = (const float*)(bws + L.di_off);
   c.L2 = (const float*)(bws + L.l2_off);
   c.sq_pad = L.sq_pad;

@@ -334,14 +334,16 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   const int nper = nqb - qb0;
   const int niter = nper * grp;
   const float sl2 = a.scale * LOG2E;
-  const int64_t qrs = (int64_t)DQK * 2, ors = (int64_t)DV * 2;
+  const int64_t qrs = (int64_t)DQK * 2;
 
   auto issue = [&](int it, char* st) {
     const int h = hk * grp + it / nper;
     const int q0 = (qb0 + it % nper) * BMQ;
     const int64_t r0 = (int64_t)(b * a.Hq + h) * a.Sq + q0;
     dma_tile<BMQ, NCQ, NW>(st, (const char*)a.q + r0 * qrs, qrs, a.Sq - q0, w, lane);
-    dma_tile<BMQ, NCO, NW>(st + SQ_BYTES, (const char*)a.dO + r0 * ors, ors, a.Sq - q0, w, lane);
+    dma_tile<BMQ, NCO, NW>(st + SQ_BYTES,
+                           (const char*)a.dO + (b * a.do_sb + h * a.do_sh + (int64_t)q0 * a.do_ss) * 2,
+                           a.do_ss * 2, a.Sq - q0, w, lane);
     if (w == 0) {
       const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
       const float* src = (lane < 16 ? a.L2 : a.Di) + p0 + (lane & 15) * 4;
@@ -569,18 +571,25 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
 // 2 halves of the dq~ columns, so every fragment read from LDS feeds two MFMAs (A: dS for 32
 // queries x 16 keys, shared by the wave's column tiles; B: k~ for 16 keys x 32 columns, shared by
 // its two query tiles) and the 128 accumulators per wave leave room for two waves per SIMD.  Each
-// 64-key step stages dS^T (64 keys x 256 queries) and k~ (64 x DQK) in a double-buffered LDS pair;
-// both operands are read with the transpose load.  Keys past a query's causal limit or past Sk
-// hold no valid dS (never written), so on those tiles the A fragments are masked to zero.
+// BK-key step stages dS^T (BK keys x 256 queries) and k~ (BK x DQK) in one slot of an NSTAGE ring,
+// NSTAGE - 1 steps ahead: dS is read once from HBM, so the kernel streams it and needs several
+// tiles in flight to cover the memory latency.  Both operands are read with the transpose load.
+// Keys past a query's causal limit or past Sk hold no valid dS (never written), so on those tiles
+// the A fragments are masked to zero.
 __device__ __forceinline__ uint32_t keep_bf2(uint32_t v, bool lo, bool hi) {
   return (lo ? (v & 0xffffu) : 0u) | (hi ? (v & 0xffff0000u) : 0u);
 }
 
-template <int DQK, int NW>
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int DQK, int NW, int BK, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   using M = MT<0>;
   static_assert(NW == 8, "4 query pairs x 2 column halves");
-  constexpr int BQ = 256, BK = 64;
+  static_assert(NSTAGE >= 2 && NSTAGE <= 4, "ring depth");
+  constexpr int BQ = 256;
   constexpr int NCK = DQK / 8, NCS = BQ / 8;
   constexpr int NTH = DQK / 64;  // 32-column tiles per wave
   // column tile of a wave's t-th accumulator: with an even count, wave dh takes cos tiles
@@ -595,7 +604,12 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
     }
   };
   constexpr int SK_BYTES = BK * NCK * 16, SS_BYTES = BK * NCS * 16, STAGE = SK_BYTES + SS_BYTES;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+  // DMA instructions one wave issues per step (k~ tile + dS tile)
+  constexpr int PER = BK * NCK / (64 * NW) + BK * NCS / (64 * NW);
+  static_assert(BK * NCS % (64 * NW) == 0, "dS tile must split into whole wave instructions");
+  constexpr int EPI_BYTES = NTH % 2 == 0 ? 128 * DQK * 4 : 0;  // fused epilogue staging
+  constexpr int SMEM = NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int nqb = (a.Sq + BQ - 1) / BQ;
@@ -640,21 +654,25 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
     }
   };
 
-  if (nkb > 0) {
-    dma_tile<BK, NCK, NW>(smem, kbase, krs, a.Sk, w, lane);
-    dma_ds(smem + SK_BYTES, 0);
-  }
+  auto issue = [&](int kb) {
+    char* st = smem + (kb % NSTAGE) * STAGE;
+    dma_tile<BK, NCK, NW>(st, kbase + (int64_t)kb * BK * krs, krs, a.Sk - kb * BK, w, lane);
+    dma_ds(st + SK_BYTES, kb * BK);
+  };
+#pragma unroll
+  for (int i = 0; i < NSTAGE - 1; ++i)
+    if (i < nkb) issue(i);
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * BK;
-    const char* sK = smem + (kb & 1) * STAGE;
+    const char* sK = smem + (kb % NSTAGE) * STAGE;
     const char* sS = sK + SK_BYTES;
-    dma_wait();
-    __syncthreads();
-    if (kb + 1 < nkb) {
-      char* nK = smem + ((kb + 1) & 1) * STAGE;
-      dma_tile<BK, NCK, NW>(nK, kbase + (int64_t)(k0 + BK) * krs, krs, a.Sk - k0 - BK, w, lane);
-      dma_ds(nK + SK_BYTES, k0 + BK);
-    }
+    // tile kb has landed once at most (steps issued after it) * PER loads are outstanding
+    const int after = min(NSTAGE - 2, nkb - 1 - kb);
+    if (after >= 2) wait_vmcnt<2 * PER>();
+    else if (after == 1) wait_vmcnt<PER>();
+    else wait_vmcnt<0>();
+    __syncthreads();  // tile kb visible; every wave is done with slot (kb - 1) % NSTAGE
+    if (kb + NSTAGE - 1 < nkb) issue(kb + NSTAGE - 1);
     if (a.causal && k0 > qw + 63 + off) continue;  // every key after both of this wave's tiles
     // masking needed when some key of the step is past the causal limit of a query or past Sk
     const bool edge = (a.causal && k0 + BK - 1 > qw + off) || (k0 + BK > a.Sk);
@@ -778,7 +796,8 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       hipLaunchKernelGGL((dkdv_bf16_kernel<DQK, DV, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
     } else {
       const int nqb = (a.Sq + 255) / 256;
-      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8>), dim3(nqb * a.B * a.Hq), dim3(512), 0, s, a);
+      // 64-key steps, double-buffered: measured faster than 32-key steps at any ring depth
+      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8, 64, 2>), dim3(nqb * a.B * a.Hq), dim3(512), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {

@@ -32,7 +32,8 @@ struct CoreArgs {
   void* o; int64_t o_sb, o_sh, o_ss; int o_dtype;
   float* lse;       // (B, Hq, Sq)
   // backward inputs / outputs
-  const void* dO;   // (B, Hq, Sq, DV) contiguous compute dtype (padded)
+  const void* dO;   // (B, Hq, Sq, DV) compute dtype; the generic kernels need it contiguous (padded)
+  int64_t do_sb, do_sh, do_ss;  // element strides of dO (read by the bf16 dK/dV kernel)
   const float* Di;  // (B, Hq, sq_pad)  rowsum(dO * O), 0 on padding rows
   const float* L2;  // (B, Hq, sq_pad)  lse * log2(e), +inf on padding rows and rows without keys
   int sq_pad;       // Sq rounded up to a multiple of 64

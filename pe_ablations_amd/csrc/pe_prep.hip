@@ -120,7 +120,7 @@ __global__ __launch_bounds__(256) void prebwd_kernel(PreBwdArgs a) {
       d = load_as_float(a.dout, d0 + c * a.do_s[3], a.dout_dtype);
       acc += d * load_as_float(a.out, o0 + c * a.o_s[3], a.out_dtype);
     }
-    store_from_float(a.dO_op, row * a.width + c, a.op_dtype, d);
+    if (a.dO_op) store_from_float(a.dO_op, row * a.width + c, a.op_dtype, d);
   }
   acc = wave_sum(acc);
   if (lane == 0) {
@@ -294,15 +294,132 @@ __global__ __launch_bounds__(RW * 64) void reduce_kernel(ReduceArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Vector forms of prep_kernel (PoPE / FoPE) and prebwd_kernel for bf16 rows with unit inner stride
+// and 16-byte aligned row starts, the layout training hands over.  One thread owns 8 consecutive
+// columns of one row: 16-byte loads and stores, same per-element arithmetic (bitwise identical
+// operands), rows spread over as many threads as there are 8-column chunks.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void unpack8(const u32x4& v, float (&x)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __builtin_bit_cast(float, v[i] << 16);
+    x[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
+  }
+}
+
+// thread t of a row: transform chunk t (cos chunk t, sin chunk t), then content chunks t, t + TPR,
+// ... and zero padding chunks the same way; TPR = Dr / 8
+__global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
+  const int tpr = a.Dr >> 3;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / tpr;
+  const int t = (int)(gid - row * tpr);
+  if (row >= (int64_t)a.B * a.H * a.S) return;
+  const int s = (int)(row % a.S);
+  const int bh = (int)(row / a.S);
+  const int h = bh % a.H, b = bh / a.H;
+  const float pos = (float)(a.start_pos + s);
+  uint16_t* drow = (uint16_t*)a.dst + row * a.width;
+  const u32x4 xv = *(const u32x4*)((const uint16_t*)a.xr + b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + t * 8);
+  const f32x4 f0 = *(const f32x4*)(a.freqs + t * 8), f1 = *(const f32x4*)(a.freqs + t * 8 + 4);
+  f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
+  const bool add = a.is_key && a.delta;
+  if (add) {
+    d0 = *(const f32x4*)(a.delta + h * a.delta_hs + t * 8);
+    d1 = *(const f32x4*)(a.delta + h * a.delta_hs + t * 8 + 4);
+  }
+  float x[8];
+  unpack8(xv, x);
+  float cv[8], sv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float mu = softplus_f(x[e]);
+    float ph = mul_nc(pos, e < 4 ? f0[e] : f1[e - 4]);
+    if (add) ph = add_nc(ph, e < 4 ? d0[e] : d1[e - 4]);
+    float sn, cs;
+    pe_sincos(ph, sn, cs);
+    cv[e] = mul_nc(mu, cs);
+    sv[e] = mul_nc(mu, sn);
+  }
+  *(u32x4*)(drow + a.Dc + t * 8) =
+      u32x4{pack_bf2(cv[0], cv[1]), pack_bf2(cv[2], cv[3]), pack_bf2(cv[4], cv[5]), pack_bf2(cv[6], cv[7])};
+  *(u32x4*)(drow + a.Dc + a.Dr + t * 8) =
+      u32x4{pack_bf2(sv[0], sv[1]), pack_bf2(sv[2], sv[3]), pack_bf2(sv[4], sv[5]), pack_bf2(sv[6], sv[7])};
+  if (a.Dc > 0) {
+    const uint16_t* xc = (const uint16_t*)a.xc + b * a.xc_s[0] + h * a.xc_s[1] + (int64_t)s * a.xc_s[2];
+    for (int j = t; j < a.Dc / 8; j += tpr) *(u32x4*)(drow + j * 8) = *(const u32x4*)(xc + j * 8);
+  }
+  for (int j = (a.Dc + 2 * a.Dr) / 8 + t; j < a.width / 8; j += tpr) *(u32x4*)(drow + j * 8) = u32x4{0u, 0u, 0u, 0u};
+}
+
+// one group of TPR = Dv / 8 lanes per padded row (TPR a power of two, groups never straddle a
+// wave); Di is the group's fixed-order butterfly sum
+__global__ __launch_bounds__(256) void prebwd_vec_kernel(PreBwdArgs a, int lg_tpr) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t prow = gid >> lg_tpr;
+  const int t = (int)(gid & ((1 << lg_tpr) - 1));
+  if (prow >= (int64_t)a.B * a.H * a.s_pad) return;
+  const int s = (int)(prow % a.s_pad);
+  const int bh = (int)(prow / a.s_pad);
+  if (s >= a.S) {
+    if (t == 0) { a.Di[prow] = 0.f; a.L2[prow] = INFINITY; }
+    return;
+  }
+  const int h = bh % a.H, b = bh / a.H;
+  const int64_t row = (int64_t)bh * a.S + s;
+  const u32x4 dv = *(const u32x4*)((const uint16_t*)a.dout + b * a.do_s[0] + h * a.do_s[1] + (int64_t)s * a.do_s[2] + t * 8);
+  const u32x4 ov = *(const u32x4*)((const uint16_t*)a.out + b * a.o_s[0] + h * a.o_s[1] + (int64_t)s * a.o_s[2] + t * 8);
+  if (a.dO_op) *(u32x4*)((uint16_t*)a.dO_op + row * a.width + t * 8) = dv;
+  float d[8], o[8];
+  unpack8(dv, d);
+  unpack8(ov, o);
+  float acc = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc += d[e] * o[e];
+  for (int m = (1 << lg_tpr) >> 1; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if (t == 0) {
+    a.Di[prow] = acc;
+    const float lv = a.lse[row];
+    a.L2[prow] = lv == -INFINITY ? INFINITY : lv * LOG2E;
+  }
+}
+
+bool aligned16(const void* p, int64_t s0, int64_t s1, int64_t s2) {
+  return ((uintptr_t)p % 16) == 0 && s0 % 8 == 0 && s1 % 8 == 0 && s2 % 8 == 0;
+}
+
 int launch_prep(const PrepArgs& a, hipStream_t s) {
   const int64_t nrows = (int64_t)a.B * a.H * a.S;
-  hipLaunchKernelGGL(prep_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+  const bool vec = a.mode == 0 && a.dst_dtype == 0 && a.xr_dtype == 0 && a.Dr > 0 && a.Dr % 8 == 0 &&
+                   a.Dc % 8 == 0 && a.width % 8 == 0 && a.xr_s[3] == 1 &&
+                   aligned16(a.xr, a.xr_s[0], a.xr_s[1], a.xr_s[2]) && ((uintptr_t)a.dst % 16) == 0 &&
+                   ((uintptr_t)a.freqs % 16) == 0 &&
+                   (!a.is_key || !a.delta || (((uintptr_t)a.delta % 16) == 0 && a.delta_hs % 4 == 0)) &&
+                   (a.Dc == 0 || (a.xc_dtype == 0 && a.xc_s[3] == 1 && aligned16(a.xc, a.xc_s[0], a.xc_s[1], a.xc_s[2])));
+  if (vec) {
+    const int64_t nthr = nrows * (a.Dr / 8);
+    hipLaunchKernelGGL(prep_pope_vec_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(prep_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
 int launch_prebwd(const PreBwdArgs& a, hipStream_t s) {
+  const int tpr = a.Dv / 8;
+  const bool vec = a.dout_dtype == 0 && a.out_dtype == 0 && a.Dv % 8 == 0 && tpr <= 64 && (tpr & (tpr - 1)) == 0 &&
+                   a.do_s[3] == 1 && a.o_s[3] == 1 && aligned16(a.dout, a.do_s[0], a.do_s[1], a.do_s[2]) &&
+                   aligned16(a.out, a.o_s[0], a.o_s[1], a.o_s[2]) &&
+                   (!a.dO_op || (a.op_dtype == 0 && a.width == a.Dv && ((uintptr_t)a.dO_op % 16) == 0));
   const int64_t nrows = (int64_t)a.B * a.H * a.s_pad;
-  hipLaunchKernelGGL(prebwd_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+  if (vec) {
+    int lg = 0;
+    while ((1 << lg) < tpr) ++lg;
+    hipLaunchKernelGGL(prebwd_vec_kernel, dim3((unsigned)((nrows * tpr + 255) / 256)), dim3(256), 0, s, a, lg);
+  } else {
+    hipLaunchKernelGGL(prebwd_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
