@@ -36,6 +36,27 @@ HBM_PEAK_GBS = 8000.0
 
 WORKLOAD = dict(B=1, H=16, S=16384, D=128)
 
+# HBM bytes per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this workload,
+# scaled by a calibration copy (python -m pe_ablations_amd.profiling traffic ...); the file records
+# the commands.  A stage's kernel missing from it reports traffic null.
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "pope_fwdbwd_S16k_D128_hbm_traffic.json")
+STAGE_KERNEL = {"fwd_core": "fwd_bf16_kernel", "bwd_dkdv": "dkdv_bf16_kernel", "bwd_dq": "dq_gemm_kernel"}
+
+
+def measured_traffic(stage: str):
+    """(bytes per launch, kernel name) of the stage's kernel from the committed PMC summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    for name, v in data.get("kernels", {}).items():
+        if name.startswith(STAGE_KERNEL[stage] + "<") and v.get("fetch_bytes") is not None \
+                and v.get("write_bytes") is not None:
+            return v["fetch_bytes"] + v["write_bytes"], name
+    return None, None
+
 
 def flops(B, H, S, D):
     """Algorithmic FLOPs of fused PoPE causal attention (Dqk = 2D, Dv = D, c = 1/2)."""
@@ -166,6 +187,7 @@ def main() -> int:
     core = ["fwd_core", "bwd_dkdv", "bwd_dq"]
     dom = max(core, key=lambda n: stage_ms[n])
     achieved = F[dom] / (stage_ms[dom] * 1e-3) / 1e12
+    traffic, traffic_kernel = measured_traffic(dom)
     value = F["total"] / (ms * 1e-3) / 1e12
 
     props = torch.cuda.get_device_properties(dev)
@@ -194,7 +216,9 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": None if traffic is None else int(traffic),
+            "traffic_unit": "bytes per launch (HBM read + write)",
+            "traffic_source": None if traffic is None else f"profiles/{os.path.basename(TRAFFIC_FILE)}: {traffic_kernel}",
         },
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }

@@ -115,12 +115,14 @@ template <int DT> __device__ __forceinline__ int c_logical(int j, int g) {
 
 // ------------------------------------------------------------------ swizzled LDS tiles
 // NCH = 16-byte chunks per row (a power of two, >= 8).  Chunk c of row r is stored in slot
-// c ^ swz(r).  gfx950's LDS has 64 4-byte banks (16 slots of 16 bytes); it serves a ds_read_b128
-// by 16-lane groups and a ds_read_b64_tr_b16 by 16-lane groups reading 4 consecutive rows x 32
-// bytes.  Row fragments put 16 consecutive rows on one logical chunk, so swz must be a bijection
-// of r mod 16 (mod 8 per row parity when a row is only 8 slots); transpose reads touch chunk
-// pairs {2a, 2a+1} of 4 consecutive rows, so swz(r) >> 1 must differ across those rows.  A bit
-// permutation of r meets both (checked on the hardware: no bank-conflict cycles for either).
+// c ^ swz(r).  gfx950's LDS has 64 4-byte banks (16 slots of 16 bytes).  Row fragments
+// (ds_read_b128) put 16 consecutive rows on one logical chunk, so swz must be a bijection of r mod
+// 16 (with the row parity when a row is only 8 slots); transpose reads (ds_read_b64_tr_b16) touch
+// chunks 4a .. 4a+3 of 4 consecutive rows.  With this permutation SQ_LDS_BANK_CONFLICT charges 2
+// of the 4 LDS cycles of every transpose read (its 32-lane halves share banks two ways), yet a
+// permutation without those conflicts measured no faster on transpose reads (4.8 clk per wave
+// instruction per CU either way), 6% slower on row fragments (7.05 vs 6.63 clk) and made the
+// one-wave-per-SIMD dK/dV kernel 25% slower, so this one is kept.
 template <int NCH> __device__ __forceinline__ int swz(int r) {
   static_assert(NCH >= 8, "rows must span at least 8 slots");
   if constexpr (NCH >= 16)
