@@ -580,10 +580,6 @@ __device__ __forceinline__ uint32_t keep_bf2(uint32_t v, bool lo, bool hi) {
   return (lo ? (v & 0xffffu) : 0u) | (hi ? (v & 0xffff0000u) : 0u);
 }
 
-template <int N> __device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 template <int DQK, int NW, int BK, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   using M = MT<0>;
@@ -629,6 +625,11 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[i][t][j] = 0.f;
 
+  // per-lane fragment bases: the wave's two dS query tiles and its NTH k~ column tiles
+  const ColBase<NCS> cA[2] = {ColBase<NCS>(lane, qp * 64), ColBase<NCS>(lane, qp * 64 + 32)};
+  ColBase<NCK> cB[NTH];
+#pragma unroll
+  for (int t = 0; t < NTH; ++t) cB[t] = ColBase<NCK>(lane, ctile(t, dh) * 32);
   int kend = a.Sk;
   if (a.causal) kend = min(a.Sk, q0 + BQ + off);
   const int nkb = kend > 0 ? (kend + BK - 1) / BK : 0;
@@ -676,13 +677,26 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
     if (a.causal && k0 > qw + 63 + off) continue;  // every key after both of this wave's tiles
     // masking needed when some key of the step is past the causal limit of a query or past Sk
     const bool edge = (a.causal && k0 + BK - 1 > qw + off) || (k0 + BK > a.Sk);
+    // Fenced double buffer over the 16-key slices: region ks issues every read of slice ks + 1 and
+    // then the products of slice ks, whose fragments were read one region earlier (left to itself
+    // the scheduler waits on each read right before its product).
+    u32x4 fa[2][2], fb[2][NTH];
+    auto read_slice = [&](int ks, u32x4 (&ra)[2], u32x4 (&rb)[NTH]) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) ra[i] = cA[i].read(sS, ks * 16);
+#pragma unroll
+      for (int t = 0; t < NTH; ++t) rb[t] = cB[t].read(sK, ks * 16);
+    };
+    read_slice(0, fa[0], fb[0]);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      u32x4 af[2];
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < BK / 16) read_slice(ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);  // the reads go out before this slice's products
+      u32x4 af[2] = {fa[ks & 1][0], fa[ks & 1][1]};
+      if (edge) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        af[i] = lds_col_frag<0, NCS>(sS, ks * 16, qp * 64 + i * 32, lane);
-        if (edge) {
+        for (int i = 0; i < 2; ++i) {
           // element e of lane (l32, g) is key k0 + ks*16 + g*8 + e of query qw + i*32 + l32
           const int kmax = a.causal ? min(qw + i * 32 + l32 + off, a.Sk - 1) : a.Sk - 1;
           const int lim = kmax - (k0 + ks * 16 + g * 8);
@@ -691,12 +705,11 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
         }
       }
 #pragma unroll
-      for (int t = 0; t < NTH; ++t) {
-        const u32x4 bfr = lds_col_frag<0, NCK>(sK, ks * 16, ctile(t, dh) * 32, lane);
+      for (int t = 0; t < NTH; ++t)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][t] = M::mma(af[i], bfr, acc[i][t]);
-      }
+        for (int i = 0; i < 2; ++i) acc[i][t] = M::mma(af[i], fb[ks & 1][t], acc[i][t]);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   if constexpr (NTH % 2 == 0) {

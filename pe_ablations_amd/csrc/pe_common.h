@@ -165,6 +165,69 @@ template <int DT, int NCH> __device__ __forceinline__ u32x4 lds_col_frag(const c
   }
 }
 
+// Fragment addressing with per-lane bases.  The XOR swizzle only touches chunk bits 0-3 (0-2 for
+// 8-slot rows) and depends only on row bits 0-3, so a fragment at row offset k0 (a multiple of 16
+// rows) and column offset n0 (a multiple of 32 columns) is a per-lane base chosen by (n0 / 32) % 4
+// plus the immediate k0 * row_bytes + (n0 / 128) * 256.  Hoisted, eight base registers stand in for
+// the per-fragment address registers the compiler otherwise keeps for every fragment read.
+template <int NCH> struct ColFrags {  // transpose reads, as lds_col_frag<0, NCH>
+  uint32_t b[4][2];                   // [(n0 / 32) % 4][rows +0 / +4]
+  __device__ __forceinline__ explicit ColFrags(int lane) {
+    const int i = lane & 15, G4 = (lane >> 4) & 3;
+    const int colq = ((G4 & 1) << 4) + ((i & 3) << 2);
+    const int row = ((lane >> 5) << 3) + (i >> 2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int col = (j * 32 + colq) % (NCH * 8);
+        b[j][hh] = tile_off<NCH>(row + 4 * hh, col >> 3) + ((col & 7) << 1);
+      }
+  }
+  // k0 % 16 == 0, n0 % 32 == 0, both compile-time after unrolling
+  __device__ __forceinline__ u32x4 read(const char* tile, int k0, int n0) const {
+    const uint32_t add = (uint32_t)(k0 * NCH * 16 + (n0 / 128) * 256);
+    const int j = (n0 / 32) & 3;
+    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + b[j][0] + add));
+    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + b[j][1] + add));
+    const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
+    return u32x4{ux[0], ux[1], uy[0], uy[1]};
+  }
+};
+// One 32-column group of transpose-read fragments at a runtime column offset n0 (any multiple of
+// 8): the per-lane base of rows 0 / 4 of the group; fragment rows k0 (a multiple of 16) are an
+// immediate.  Two registers per column group.
+template <int NCH> struct ColBase {
+  uint32_t b0, b1;
+  ColBase() = default;
+  __device__ __forceinline__ ColBase(int lane, int n0) {
+    const int i = lane & 15, G4 = (lane >> 4) & 3;
+    const int col = n0 + ((G4 & 1) << 4) + ((i & 3) << 2);
+    const int row = ((lane >> 5) << 3) + (i >> 2);
+    b0 = tile_off<NCH>(row, col >> 3) + ((col & 7) << 1);
+    b1 = tile_off<NCH>(row + 4, col >> 3) + ((col & 7) << 1);
+  }
+  __device__ __forceinline__ u32x4 read(const char* tile, int k0) const {
+    const uint32_t add = (uint32_t)(k0 * NCH * 16);
+    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + b0 + add));
+    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + b1 + add));
+    const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
+    return u32x4{ux[0], ux[1], uy[0], uy[1]};
+  }
+};
+template <int NCH> struct RowFrags {  // row fragments, as lds_row_frag<NCH>(tile, row0 + rl, 2 * kk + g)
+  uint32_t b[8];                      // [kk % 8]
+  // rl < 32: the lane's row within a 32-row tile (perm_row(l32) for the products that need it)
+  __device__ __forceinline__ RowFrags(int rl, int g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = tile_off<NCH>(rl, (2 * j + g) % NCH);
+  }
+  // row0 % 32 == 0, compile-time kk
+  __device__ __forceinline__ u32x4 read(const char* tile, int row0, int kk) const {
+    return *(const u32x4*)(tile + b[kk & 7] + (uint32_t)(row0 * NCH * 16 + (kk >> 3) * 256));
+  }
+};
+
 // Cooperative copy of ROWS x (NCH*16 bytes) from global (row stride in bytes) into a swizzled
 // tile; rows >= nvalid are zero-filled.  All NT threads of the block participate.
 template <int ROWS, int NCH, int NT>
@@ -264,6 +327,11 @@ __device__ __forceinline__ void dma_row(char* dst, const char* src, int nchunks,
 }
 
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// wait until at most N vector memory operations of this wave are outstanding (they retire in issue
+// order, so everything issued before the last N has completed)
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 __device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
