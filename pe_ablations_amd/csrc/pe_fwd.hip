@@ -53,6 +53,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) 
   const char* vbase = (const char*)((const E*)a.v + b * a.v_sb + hk * a.v_sh);
   const int64_t krs = (int64_t)DQK * ESZ, vrs = a.v_ss * ESZ;
 
+  const RowFrags<NCK> rk(perm_row<0>(l32), g);  // k~ row fragments (rows nt*32 + perm_row(l32))
+  const ColFrags<NCV> cv(lane);                  // v transpose fragments
   f32x16 o[NOT];
 #pragma unroll
   for (int t = 0; t < NOT; ++t)
@@ -203,6 +205,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
   const char* vbase = (const char*)((const uint16_t*)a.v + b * a.v_sb + hk * a.v_sh);
   const int64_t krs = (int64_t)DQK * 2, vrs = a.v_ss * 2;
 
+  const RowFrags<NCK> rk(perm_row<0>(l32), g);  // k~ row fragments (rows nt*32 + perm_row(l32))
+  const ColFrags<NCV> cv(lane);                  // v transpose fragments
   f32x16 o[NOT];
 #pragma unroll
   for (int t = 0; t < NOT; ++t)
@@ -230,13 +234,26 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
 
     f32x16 s[NKT];
 #pragma unroll
-    for (int nt = 0; nt < NKT; ++nt) {
+    for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) s[nt][j] = 0.f;
-      const int row = nt * 32 + perm_row<0>(l32);
+    {
+      // S = k~ q~^T: NKT*NQF products, each with its own k~ row fragment, through a fenced ring
+      // of depth FD (reads FD products ahead; left to itself the scheduler waits on every read
+      // right before its product); consecutive products alternate accumulators
+      constexpr int NF = NKT * NQF, FD = 4;
+      u32x4 kq[FD];
 #pragma unroll
-      for (int kk = 0; kk < NQF; ++kk)
-        s[nt] = M::mma(lds_row_frag<NCK>(sK, row, 2 * kk + g), qf[kk], s[nt]);
+      for (int i = 0; i < FD; ++i) kq[i] = rk.read(sK, (i % NKT) * 32, i / NKT);
+#pragma unroll
+      for (int i = 0; i < NF; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 cur = kq[i % FD];
+        if (i + FD < NF) kq[i % FD] = rk.read(sK, ((i + FD) % NKT) * 32, (i + FD) / NKT);
+        __builtin_amdgcn_sched_barrier(0);
+        s[i % NKT] = M::mma(cur, qf[i / NKT], s[i % NKT]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     const bool edge = (a.causal && k0 + BN - 1 > qw + off) || (k0 + BN > a.Sk);
     float mx = -INFINITY;
@@ -276,11 +293,22 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
     u32x4 pf[NPF];
 #pragma unroll
     for (int ks = 0; ks < NPF; ++ks) pf[ks] = M::pack(s[ks / 2], (ks % 2) * 8);
+    {
+      // O^T += v^T P^T: NOT*NPF products with v transpose fragments, same fenced ring
+      constexpr int NF = NOT * NPF, FD = 4;
+      u32x4 vq[FD];
 #pragma unroll
-    for (int t = 0; t < NOT; ++t)
+      for (int i = 0; i < FD; ++i) vq[i] = cv.read(sV, (i / NOT) * 16, (i % NOT) * 32);
 #pragma unroll
-      for (int ks = 0; ks < NPF; ++ks)
-        o[t] = M::mma(lds_col_frag<0, NCV>(sV, ks * 16, t * 32, lane), pf[ks], o[t]);
+      for (int i = 0; i < NF; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 cur = vq[i % FD];
+        if (i + FD < NF) vq[i % FD] = cv.read(sV, ((i + FD) / NOT) * 16, ((i + FD) % NOT) * 32);
+        __builtin_amdgcn_sched_barrier(0);
+        o[i % NOT] = M::mma(cur, pf[i / NOT], o[i % NOT]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   const float lt = l + xor32(l);
