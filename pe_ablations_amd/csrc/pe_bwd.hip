@@ -372,16 +372,51 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
 #pragma unroll
   for (int j = 0; j < 16; ++j) { s[j] = 0.f; dp[j] = 0.f; }
 
+  // Fragment reads run FD products ahead of the matrix core through fenced register rings (left to
+  // itself the scheduler waits on every read right before its product); per-lane XOR bases, shared
+  // by the q~ and dO tiles, make every fragment address a row pointer plus base plus immediate.
+  constexpr int FD = 3;  // 3 and 4 measured equal; 3 leaves fewer registers to spill
+  const RowX<NCQ> rq(perm_row<0>(l32), g);  // q~ / dO rows mt*32 + perm_row(l32)
+  const RowX<NCO> ro(perm_row<0>(l32), g);
+  const ColX<NCQ> cq(lane);                 // q~ / dO transpose fragments
+  const ColX<NCO> co(lane);
+  const uint32_t rrq = (uint32_t)perm_row<0>(l32) * NCQ * 16, rro = (uint32_t)perm_row<0>(l32) * NCO * 16;
+  const uint32_t crq = ColX<NCQ>::row_term(lane), cro = ColX<NCO>::row_term(lane);
+
   auto scores = [&](int hh) {  // S / dP of half hh into s / dp
     const int t = hh >> 1, mt = hh & 1;
-    const char* st = smem + (t % NSTAGE) * STAGE;
-    const int row = mt * 32 + perm_row<0>(l32);
+    const char* sq = smem + (t % NSTAGE) * STAGE + mt * 32 * NCQ * 16 + rrq;
+    const char* so = smem + (t % NSTAGE) * STAGE + SQ_BYTES + mt * 32 * NCO * 16 + rro;
 #pragma unroll
     for (int j = 0; j < 16; ++j) { s[j] = 0.f; dp[j] = 0.f; }
+    constexpr int NS = NKF + NVF;
+    auto rd = [&](int i) -> u32x4 { return i < NKF ? rq.read(sq, 0, i) : ro.read(so, 0, i - NKF); };
+    u32x4 ring[FD];
 #pragma unroll
-    for (int kk = 0; kk < NKF; ++kk) s = M::mma(lds_row_frag<NCQ>(st, row, 2 * kk + g), kf[kk], s);
+    for (int i = 0; i < FD; ++i) ring[i] = rd(i);
 #pragma unroll
-    for (int kk = 0; kk < NVF; ++kk) dp = M::mma(lds_row_frag<NCO>(st + SQ_BYTES, row, 2 * kk + g), vf[kk], dp);
+    for (int i = 0; i < NS; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 cur = ring[i % FD];
+      if (i + FD < NS) ring[i % FD] = rd(i + FD);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < NKF) s = M::mma(cur, kf[i], s);
+      else dp = M::mma(cur, vf[i - NKF], dp);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // products of the pending half (dV += P^T dO, dK~ += dS^T q~): NP products, ks-major so the two
+  // products of one accumulator are NDV + NDK apart
+  constexpr int NP = 2 * (NDV + NDK);
+  auto rdp = [&](const char* pq, const char* po, int i) -> u32x4 {
+    const int ks = i / (NDV + NDK), u = i % (NDV + NDK);
+    return u < NDV ? co.read(po, ks * 16, u * 32) : cq.read(pq, ks * 16, (u - NDV) * 32);
+  };
+  auto prod = [&](int i, const u32x4& fr) {
+    const int ks = i / (NDV + NDK), u = i % (NDV + NDK);
+    if (u < NDV) dv[u] = M::mma(ppf[ks], fr, dv[u]);
+    else dk[u - NDV] = M::mma(pdsf[ks], fr, dk[u - NDV]);
   };
 
   if (niter > 0) {
@@ -398,28 +433,52 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     const float* sL = (const float*)(smem + sb + SQ_BYTES + SO_BYTES);
     const float* sD = sL + BMQ;
     __builtin_amdgcn_sched_barrier(0);
-    // A. P = exp2(S*scale*log2e - L2) (rows past Sq carry L2 = +inf -> 0), dS = P (dP - Di)
+    // A. P = exp2(S*scale*log2e - L2) (rows past Sq carry L2 = +inf -> 0), dS = P (dP - Di), one
+    //    element per product region of the pending half's products, so the VALU work interleaves
+    //    with the matrix core
     const int kd = myk - off - (q0 + mt * 32) - g * 8;
+    // L2 / Di of the lane's 16 rows: element j is row mt*32 + (j/8)*16 + g*8 + j%8; groups of 4
+    // elements are read two product regions ahead into a double buffer
+    f32x4 lg[2], dg[2];
+    auto load_ld = [&](int G) {
+      const int qi0 = mt * 32 + (G >> 1) * 16 + g * 8 + (G & 1) * 4;
+      lg[G & 1] = *(const f32x4*)(sL + qi0);
+      dg[G & 1] = *(const f32x4*)(sD + qi0);
+    };
+    load_ld(0);
+    load_ld(1);
+    const char* pq = smem + pbase + prow * NCQ * 16 + crq;
+    const char* po = smem + pbase + SQ_BYTES + prow * NCO * 16 + cro;
+    u32x4 ring[FD];
+#pragma unroll
+    for (int i = 0; i < FD; ++i) ring[i] = rdp(pq, po, i);
+    float pprev = 0.f, dprev = 0.f;  // even element of the pair being packed
     u32x4 cpf[2], cdsf[2];
+    // max(NP, 16) regions: every one of the 16 softmax elements gets a region even when the
+    // pending half has fewer products (small head widths)
+    constexpr int NR = NP > 16 ? NP : 16;
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const int qi0 = mt * 32 + h2 * 16 + g * 8;
-      const f32x4 l0 = *(const f32x4*)(sL + qi0), l1 = *(const f32x4*)(sL + qi0 + 4);
-      const f32x4 d0 = *(const f32x4*)(sD + qi0), d1 = *(const f32x4*)(sD + qi0 + 4);
-      float pv[8], dsv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int j = h2 * 8 + e;
-        const float lv = e < 4 ? l0[e] : l1[e - 4];
-        const float dd = e < 4 ? d0[e] : d1[e - 4];
-        float p = fast_exp2(s[j] * sl2 - lv);
-        if (a.causal) p = masked_row(kd, j) ? 0.f : p;
-        pv[e] = p;
-        dsv[e] = p * (dp[j] - dd);
+    for (int i = 0; i < NR; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 cur = ring[i % FD];
+      if (i + FD < NP) ring[i % FD] = rdp(pq, po, i + FD);
+      if (i % 4 == 2 && i + 2 < 16) load_ld((i + 2) / 4);
+      if (i < 16) {
+        const float lv = lg[(i / 4) & 1][i % 4], dd = dg[(i / 4) & 1][i % 4];
+        float p = fast_exp2(s[i] * sl2 - lv);
+        if (a.causal) p = masked_row(kd, i) ? 0.f : p;
+        const float ds = p * (dp[i] - dd);
+        if (i & 1) {  // element pairs are packed as soon as they are complete
+          cpf[i / 8][(i % 8) / 2] = pack_bf2(pprev, p);
+          cdsf[i / 8][(i % 8) / 2] = pack_bf2(dprev, ds);
+        } else {
+          pprev = p;
+          dprev = ds;
+        }
       }
-      cpf[h2] = u32x4{pack_bf2(pv[0], pv[1]), pack_bf2(pv[2], pv[3]), pack_bf2(pv[4], pv[5]), pack_bf2(pv[6], pv[7])};
-      cdsf[h2] = u32x4{pack_bf2(dsv[0], dsv[1]), pack_bf2(dsv[2], dsv[3]), pack_bf2(dsv[4], dsv[5]), pack_bf2(dsv[6], dsv[7])};
+      if (i < NP) prod(i, cur);
     }
+    __builtin_amdgcn_sched_barrier(0);
     // dS of this half in fragment order for the dQ GEMM: the wave's two 1 KiB chunks rows are
     // contiguous (block (key/32, q0/64), chunks (mt*2 + h2)*64 + lane); rows past Sk are padding
     {
@@ -429,20 +488,6 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
       *(u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16) = cdsf[0];
       *(u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16) = cdsf[1];
     }
-    {
-      const char* pQ = smem + pbase;
-      const char* pO = pQ + SQ_BYTES;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int t2 = 0; t2 < NDV; ++t2)
-          dv[t2] = M::mma(ppf[ks], lds_col_frag<0, NCO>(pO, prow + ks * 16, t2 * 32, lane), dv[t2]);
-#pragma unroll
-        for (int t2 = 0; t2 < NDK; ++t2)
-          dk[t2] = M::mma(pdsf[ks], lds_col_frag<0, NCQ>(pQ, prow + ks * 16, t2 * 32, lane), dk[t2]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       ppf[i] = cpf[i];
@@ -464,17 +509,20 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     }
   }
   if (niter > 0) {
-    const char* pQ = smem + pbase;
-    const char* pO = pQ + SQ_BYTES;
+    const char* pq = smem + pbase + prow * NCQ * 16 + crq;
+    const char* po = smem + pbase + SQ_BYTES + prow * NCO * 16 + cro;
+    u32x4 ring[FD];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int i = 0; i < FD; ++i) ring[i] = rdp(pq, po, i);
 #pragma unroll
-      for (int t2 = 0; t2 < NDV; ++t2)
-        dv[t2] = M::mma(ppf[ks], lds_col_frag<0, NCO>(pO, prow + ks * 16, t2 * 32, lane), dv[t2]);
-#pragma unroll
-      for (int t2 = 0; t2 < NDK; ++t2)
-        dk[t2] = M::mma(pdsf[ks], lds_col_frag<0, NCQ>(pQ, prow + ks * 16, t2 * 32, lane), dk[t2]);
+    for (int i = 0; i < NP; ++i) {
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 cur = ring[i % FD];
+      if (i + FD < NP) ring[i % FD] = rdp(pq, po, i + FD);
+      __builtin_amdgcn_sched_barrier(0);
+      prod(i, cur);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   if (a.fuse_inv) {

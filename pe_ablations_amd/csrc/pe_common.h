@@ -215,6 +215,44 @@ template <int NCH> struct ColBase {
     return u32x4{ux[0], ux[1], uy[0], uy[1]};
   }
 };
+// The same two address forms with the lane's row term left out: the caller adds it once per tile
+// (row_ptr), and the XOR parts, which are equal for 16- and 32-chunk rows, are shared between
+// tiles of both widths.  ColX: row term ((lane >> 5) * 8 + (lane & 15) / 4) * NCH * 16; RowX: rl *
+// NCH * 16.
+template <int NCH> struct ColX {
+  uint32_t b[4][2];
+  __device__ __forceinline__ explicit ColX(int lane) {
+    const int i = lane & 15, G4 = (lane >> 4) & 3;
+    const int colq = ((G4 & 1) << 4) + ((i & 3) << 2);
+    const int row = ((lane >> 5) << 3) + (i >> 2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        b[j][hh] = (uint32_t)((((((j * 32 + colq) % (NCH * 8)) >> 3) ^ swz<NCH>(row + 4 * hh)) << 4) | ((colq & 7) << 1));
+  }
+  __device__ __forceinline__ static uint32_t row_term(int lane) {
+    return (uint32_t)((((lane >> 5) << 3) + ((lane & 15) >> 2)) * NCH * 16);
+  }
+  __device__ __forceinline__ u32x4 read(const char* row_ptr, int k0, int n0) const {
+    const uint32_t add = (uint32_t)(k0 * NCH * 16 + (n0 / 128) * 256);
+    const int j = (n0 / 32) & 3;
+    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(row_ptr + b[j][0] + add));
+    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(row_ptr + b[j][1] + add + 4 * NCH * 16));
+    const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
+    return u32x4{ux[0], ux[1], uy[0], uy[1]};
+  }
+};
+template <int NCH> struct RowX {
+  uint32_t b[8];
+  __device__ __forceinline__ RowX(int rl, int g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = (uint32_t)((((2 * j + g) % NCH) ^ swz<NCH>(rl)) << 4);
+  }
+  __device__ __forceinline__ u32x4 read(const char* row_ptr, int row0, int kk) const {
+    return *(const u32x4*)(row_ptr + b[kk & 7] + (uint32_t)(row0 * NCH * 16 + (kk >> 3) * 256));
+  }
+};
 template <int NCH> struct RowFrags {  // row fragments, as lds_row_frag<NCH>(tile, row0 + rl, 2 * kk + g)
   uint32_t b[8];                      // [kk % 8]
   // rl < 32: the lane's row within a 32-row tile (perm_row(l32) for the products that need it)
