@@ -333,17 +333,24 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   if (qb0 > nqb) qb0 = nqb;
   const int nper = nqb - qb0;
   const int niter = nper * grp;
+  // Query tiles are walked from the last one down to qb0: every key block of a head then reads the
+  // same q~ / dO tile at the same time (a head's blocks share one XCD and its L2), where the causal
+  // start qb0 would have each block reading its own tile from HBM.
   const float sl2 = a.scale * LOG2E;
   const int64_t qrs = (int64_t)DQK * 2;
 
   auto issue = [&](int it, char* st) {
+    // lane-derived DMA offsets are recomputed per tile from an opaque copy of the lane id: held
+    // across the loop they would be spilled, and a scratch reload waits for every load in flight
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
     const int h = hk * grp + it / nper;
-    const int q0 = (qb0 + it % nper) * BMQ;
+    const int q0 = (nqb - 1 - it % nper) * BMQ;  // last tile first, see below
     const int64_t r0 = (int64_t)(b * a.Hq + h) * a.Sq + q0;
-    dma_tile<BMQ, NCQ, NW>(st, (const char*)a.q + r0 * qrs, qrs, a.Sq - q0, w, lane);
+    dma_tile<BMQ, NCQ, NW>(st, (const char*)a.q + r0 * qrs, qrs, a.Sq - q0, w, ln);
     dma_tile<BMQ, NCO, NW>(st + SQ_BYTES,
                            (const char*)a.dO + (b * a.do_sb + h * a.do_sh + (int64_t)q0 * a.do_ss) * 2,
-                           a.do_ss * 2, a.Sq - q0, w, lane);
+                           a.do_ss * 2, a.Sq - q0, w, ln);
     if (w == 0) {
       const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
       const float* src = (lane < 16 ? a.L2 : a.Di) + p0 + (lane & 15) * 4;
@@ -394,12 +401,15 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     u32x4 ring[FD];
 #pragma unroll
     for (int i = 0; i < FD; ++i) ring[i] = rd(i);
+    // fences for MFMA / LDS reads only (0x417 lets ALU, VALU, SALU, transcendental and global
+    // memory instructions cross), so the next tile's DMA issue, which precedes the scores at a tile
+    // boundary, can be spread between the products
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0x417);
       const u32x4 cur = ring[i % FD];
       if (i + FD < NS) ring[i % FD] = rd(i + FD);
-      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0x417);
       if (i < NKF) s = M::mma(cur, kf[i], s);
       else dp = M::mma(cur, vf[i - NKF], dp);
     }
@@ -429,14 +439,15 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   for (int hh = 0; hh < nhalf; ++hh) {
     const int t = hh >> 1, mt = hh & 1;
     const int sb = (t % NSTAGE) * STAGE;
-    const int q0 = (qb0 + t % nper) * BMQ;
+    const int q0 = (nqb - 1 - t % nper) * BMQ;
     const float* sL = (const float*)(smem + sb + SQ_BYTES + SO_BYTES);
     const float* sD = sL + BMQ;
     __builtin_amdgcn_sched_barrier(0);
     // A. P = exp2(S*scale*log2e - L2) (rows past Sq carry L2 = +inf -> 0), dS = P (dP - Di), one
     //    element per product region of the pending half's products, so the VALU work interleaves
     //    with the matrix core
-    const int kd = myk - off - (q0 + mt * 32) - g * 8;
+    // causal limit folded into kd (non-causal: never masked), so masking is one compare + select
+    const int kd = a.causal ? myk - off - (q0 + mt * 32) - g * 8 : -(1 << 30);
     // L2 / Di of the lane's 16 rows: element j is row mt*32 + (j/8)*16 + g*8 + j%8; groups of 4
     // elements are read two product regions ahead into a double buffer
     f32x4 lg[2], dg[2];
@@ -459,14 +470,16 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     constexpr int NR = NP > 16 ? NP : 16;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      __builtin_amdgcn_sched_barrier(0);
+      // fence for MFMA / LDS reads only (mask 0x407 lets ALU, VALU, SALU and transcendental
+      // instructions cross), so the softmax chains of consecutive elements overlap
+      __builtin_amdgcn_sched_barrier(0x407);
       const u32x4 cur = ring[i % FD];
       if (i + FD < NP) ring[i % FD] = rdp(pq, po, i + FD);
       if (i % 4 == 2 && i + 2 < 16) load_ld((i + 2) / 4);
       if (i < 16) {
         const float lv = lg[(i / 4) & 1][i % 4], dd = dg[(i / 4) & 1][i % 4];
         float p = fast_exp2(s[i] * sl2 - lv);
-        if (a.causal) p = masked_row(kd, i) ? 0.f : p;
+        p = masked_row(kd, i) ? 0.f : p;
         const float ds = p * (dp[i] - dd);
         if (i & 1) {  // element pairs are packed as soon as they are complete
           cpf[i / 8][(i % 8) / 2] = pack_bf2(pprev, p);
