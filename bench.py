@@ -77,8 +77,9 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(heads: int):
-    """Oracle fwd+bwd (fp32, torch eager, all host threads) on `heads` heads of the workload."""
+def cpu_baseline(heads: int, reps: int):
+    """Oracle fwd+bwd (fp32, torch eager, all host threads) on `heads` heads of the workload: one
+    untimed warm-up pass, then the median of `reps` timed passes."""
     import torch
     from oracle import pe_oracle as O
 
@@ -87,14 +88,22 @@ def cpu_baseline(heads: int):
     q = torch.randn(1, heads, S, D, generator=g).requires_grad_(True)
     k = torch.randn(1, heads, S, D, generator=g).requires_grad_(True)
     v = torch.randn(1, heads, S, D, generator=g).requires_grad_(True)
-    dO = torch.randn(1, heads, S, D, generator=g, dtype=torch.float64)
+    dO = torch.randn(1, heads, S, D, generator=g)
     delta = (torch.rand(heads, D, generator=g) * (-2 * math.pi)).requires_grad_(True)
     freqs = O.pope_freqs(D)
-    t0 = time.perf_counter()
-    out, _ = O.pope_attention(q, k, v, freqs, delta, scale=1.0 / math.sqrt(D), clamp=False,
-                              core_dtype=torch.float32)
-    out.backward(dO.to(out.dtype))
-    dt = time.perf_counter() - t0
+
+    def one_pass():
+        for t in (q, k, v, delta):
+            t.grad = None
+        t0 = time.perf_counter()
+        out, _ = O.pope_attention(q, k, v, freqs, delta, scale=1.0 / math.sqrt(D), clamp=False,
+                                  core_dtype=torch.float32)
+        out.backward(dO.to(out.dtype))
+        return time.perf_counter() - t0
+
+    one_pass()
+    times = sorted(one_pass() for _ in range(reps))
+    dt = times[len(times) // 2]
     f = flops(1, heads, S, D)["total"]
     return {
         "value": f / dt / 1e12,
@@ -102,7 +111,8 @@ def cpu_baseline(heads: int):
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"oracle/pe_oracle.py pope_attention fwd+bwd, fp32 torch eager, {heads} of {H} heads "
-                  f"(B=1, S={S}, D={D}), one pass, {dt:.1f} s",
+                  f"(B=1, S={S}, D={D}); 1 warm-up + median of {reps} passes, {dt:.2f} s per pass, "
+                  f"{sum(times):.1f} s timed",
         "seconds": dt,
     }
 
@@ -114,6 +124,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=2)
+    ap.add_argument("--cpu-reps", type=int, default=4)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -224,7 +235,7 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         log(f"bench: CPU baseline ({args.cpu_heads} heads)")
-        cb = cpu_baseline(args.cpu_heads)
+        cb = cpu_baseline(args.cpu_heads, args.cpu_reps)
         res["cpu_baseline"] = {k2: v2 for k2, v2 in cb.items() if k2 != "seconds"}
         res["cpu_baseline"]["value"] = round(cb["value"], 5)
     print(json.dumps(res), flush=True)

@@ -333,9 +333,6 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   if (qb0 > nqb) qb0 = nqb;
   const int nper = nqb - qb0;
   const int niter = nper * grp;
-  // Query tiles are walked from the last one down to qb0: every key block of a head then reads the
-  // same q~ / dO tile at the same time (a head's blocks share one XCD and its L2), where the causal
-  // start qb0 would have each block reading its own tile from HBM.
   const float sl2 = a.scale * LOG2E;
   const int64_t qrs = (int64_t)DQK * 2;
 
@@ -345,7 +342,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int h = hk * grp + it / nper;
-    const int q0 = (nqb - 1 - it % nper) * BMQ;  // last tile first, see below
+    const int q0 = (qb0 + it % nper) * BMQ;
     const int64_t r0 = (int64_t)(b * a.Hq + h) * a.Sq + q0;
     dma_tile<BMQ, NCQ, NW>(st, (const char*)a.q + r0 * qrs, qrs, a.Sq - q0, w, ln);
     dma_tile<BMQ, NCO, NW>(st + SQ_BYTES,
@@ -439,7 +436,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   for (int hh = 0; hh < nhalf; ++hh) {
     const int t = hh >> 1, mt = hh & 1;
     const int sb = (t % NSTAGE) * STAGE;
-    const int q0 = (nqb - 1 - t % nper) * BMQ;
+    const int q0 = (qb0 + t % nper) * BMQ;
     const float* sL = (const float*)(smem + sb + SQ_BYTES + SO_BYTES);
     const float* sD = sL + BMQ;
     __builtin_amdgcn_sched_barrier(0);
