@@ -18,7 +18,19 @@ The CPU baseline times this repository's CPU restatement of the reference's eage
 (oracle/pe_oracle.py, fp32) on a bounded sample of the same workload: ``--cpu-heads`` of the 16
 heads at the full S=16384, forward + backward.
 
+Two more workloads, selected with ``--workload`` (the default is the headline above):
+
+* ``fwd``: the long-context evaluation forward (the same shape, forward only, under
+  ``torch.inference_mode``; 3*B*H*S^2*D FLOPs per step).
+* ``decoder``: the whole ~1B decoder forward of the long-context configuration: 24 layers,
+  d_model 2048, 16 fused-PoPE heads of D=128, SwiGLU 5632, RMSNorm, vocab 32000, bf16 weights
+  ~ N(0, 0.02^2), one sequence of 16384 uniform token ids, with the next-token cross entropy
+  (which must come out near ln 32000 + 0.02^2 * 2048 / 2 = 10.78 at this init: the tied head's
+  logits have variance 0.02^2 * d_model).  Reported as tokens/s; the roofline entry is
+  the attention kernel of the last layer.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--workload fwdbwd|fwd|decoder]
 """
 
 from __future__ import annotations
@@ -77,133 +89,158 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(heads: int, reps: int):
-    """Oracle fwd+bwd (fp32, torch eager, all host threads) on `heads` heads of the workload: one
-    untimed warm-up pass, then the median of `reps` timed passes."""
+def cpu_baseline(heads: int, reps: int, backward: bool = True):
+    """Oracle forward (+ backward) (fp32, torch eager, all host threads) on `heads` heads of the
+    workload: one untimed warm-up pass, then the median of `reps` timed passes."""
     import torch
     from oracle import pe_oracle as O
 
     B, H, S, D = WORKLOAD["B"], WORKLOAD["H"], WORKLOAD["S"], WORKLOAD["D"]
     g = torch.Generator().manual_seed(0)
-    q = torch.randn(1, heads, S, D, generator=g).requires_grad_(True)
-    k = torch.randn(1, heads, S, D, generator=g).requires_grad_(True)
-    v = torch.randn(1, heads, S, D, generator=g).requires_grad_(True)
+    q = torch.randn(1, heads, S, D, generator=g).requires_grad_(backward)
+    k = torch.randn(1, heads, S, D, generator=g).requires_grad_(backward)
+    v = torch.randn(1, heads, S, D, generator=g).requires_grad_(backward)
     dO = torch.randn(1, heads, S, D, generator=g)
-    delta = (torch.rand(heads, D, generator=g) * (-2 * math.pi)).requires_grad_(True)
+    delta = (torch.rand(heads, D, generator=g) * (-2 * math.pi)).requires_grad_(backward)
     freqs = O.pope_freqs(D)
 
     def one_pass():
         for t in (q, k, v, delta):
             t.grad = None
         t0 = time.perf_counter()
-        out, _ = O.pope_attention(q, k, v, freqs, delta, scale=1.0 / math.sqrt(D), clamp=False,
-                                  core_dtype=torch.float32)
-        out.backward(dO.to(out.dtype))
+        with torch.set_grad_enabled(backward):
+            out, _ = O.pope_attention(q, k, v, freqs, delta, scale=1.0 / math.sqrt(D), clamp=False,
+                                      core_dtype=torch.float32)
+            if backward:
+                out.backward(dO.to(out.dtype))
         return time.perf_counter() - t0
 
     one_pass()
     times = sorted(one_pass() for _ in range(reps))
     dt = times[len(times) // 2]
-    f = flops(1, heads, S, D)["total"]
+    f = flops(1, heads, S, D)["total" if backward else "fwd"]
+    what = "fwd+bwd" if backward else "fwd"
     return {
         "value": f / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"oracle/pe_oracle.py pope_attention fwd+bwd, fp32 torch eager, {heads} of {H} heads "
+        "sample": f"oracle/pe_oracle.py pope_attention {what}, fp32 torch eager, {heads} of {H} heads "
                   f"(B=1, S={S}, D={D}); 1 warm-up + median of {reps} passes, {dt:.2f} s per pass, "
                   f"{sum(times):.1f} s timed",
         "seconds": dt,
     }
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=2)
-    ap.add_argument("--cpu-reps", type=int, default=4)
-    args = ap.parse_args()
-
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
-              f"WORLD_SIZE {world}); the PE attention path has no multi-GPU leg", file=sys.stderr)
-        return 2
-
-    import torch
+def stage_events(torch, steps: int, stream):
+    """Per timed step, a ctypes array of 2 events per library stage (start, end), each recorded
+    once up front so the HIP event exists before the library records into it."""
     from pe_ablations_amd import _lib
-    from pe_ablations_amd.functional import pe_attention
-
-    if not torch.cuda.is_available():
-        print("bench.py: no GPU visible", file=sys.stderr)
-        return 1
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    B, H, S, D = WORKLOAD["B"], WORKLOAD["H"], WORKLOAD["S"], WORKLOAD["D"]
-    F = flops(B, H, S, D)
-
-    g = torch.Generator(device=dev).manual_seed(0)
-    bf = torch.bfloat16
-    q = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(True)
-    k = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(True)
-    v = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(True)
-    dO = torch.randn(B, H, S, D, generator=g, device=dev).to(bf)
-    delta = (torch.rand(H, D, generator=g, device=dev) * (-2 * math.pi)).requires_grad_(True)
-    freqs = (10000.0 ** (-(torch.arange(0, D, dtype=torch.float32) / D))).to(dev)
-    scale = 1.0 / math.sqrt(D)
-
-    def step():
-        out = pe_attention(q, k, v, mode="pope", freqs=freqs, delta=delta, scale=scale)
-        return torch.autograd.grad(out, (q, k, v, delta), dO)
-
-    L = _lib.lib()
-    stream = torch.cuda.current_stream(dev)
     nst = len(_lib.STAGES)
-
-    log(f"bench: warmup {args.warmup} steps (B={B} H={H} S={S} D={D} bf16)")
-    for _ in range(args.warmup):
-        grads = step()
-    torch.cuda.synchronize()
-    for gr in grads:
-        if not torch.isfinite(gr.float()).all():
-            raise RuntimeError("non-finite gradient in warmup")
-
-    # events per timed step, created up front (a first record materialises the HIP event)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nst)] for _ in range(args.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nst)] for _ in range(steps)]
     for row in evs:
         for e in row:
             e.record(stream)
     torch.cuda.synchronize()
     arrays = [(ctypes.c_void_p * (2 * nst))(*[e.cuda_event for e in row]) for row in evs]
+    return evs, arrays
 
-    log(f"bench: timing {args.steps} steps")
+
+def stage_times(evs, names):
+    """Average ms of each named stage over the timed steps."""
+    from pe_ablations_amd import _lib
+    out = {}
+    for si, name in enumerate(_lib.STAGES):
+        if name in names:
+            vals = [row[2 * si].elapsed_time(row[2 * si + 1]) for row in evs]
+            out[name] = sum(vals) / len(vals)
+    return out
+
+
+def timed_loop(torch, L, step, arrays, steps):
+    """Run `steps` steps between two device synchronisations, handing the library one event array
+    per step; returns ms per step."""
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(steps):
         L.pe_attn_set_stage_events(ctypes.cast(arrays[i], ctypes.c_void_p))
         step()
     L.pe_attn_set_stage_events(None)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / args.steps
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def roofline(stage: str, flop: float, ms: float) -> dict:
+    traffic, traffic_kernel = measured_traffic(stage)
+    achieved = flop / (ms * 1e-3) / 1e12
+    return {
+        "kernel": stage,
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "traffic": None if traffic is None else int(traffic),
+        "traffic_unit": "bytes per launch (HBM read + write)",
+        "traffic_source": None if traffic is None else f"profiles/{os.path.basename(TRAFFIC_FILE)}: {traffic_kernel}",
+    }
+
+
+def run_attention(args, torch, dev, backward: bool) -> dict:
+    """Headline (fwd+bwd) or evaluation-forward step on the attention workload."""
+    from pe_ablations_amd import _lib
+    from pe_ablations_amd.functional import pe_attention
+
+    B, H, S, D = WORKLOAD["B"], WORKLOAD["H"], WORKLOAD["S"], WORKLOAD["D"]
+    F = flops(B, H, S, D)
+    g = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    q = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(backward)
+    k = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(backward)
+    v = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(backward)
+    dO = torch.randn(B, H, S, D, generator=g, device=dev).to(bf)
+    delta = (torch.rand(H, D, generator=g, device=dev) * (-2 * math.pi)).requires_grad_(backward)
+    freqs = (10000.0 ** (-(torch.arange(0, D, dtype=torch.float32) / D))).to(dev)
+    scale = 1.0 / math.sqrt(D)
+
+    if backward:
+        def step():
+            out = pe_attention(q, k, v, mode="pope", freqs=freqs, delta=delta, scale=scale)
+            return torch.autograd.grad(out, (q, k, v, delta), dO)
+    else:
+        def step():
+            with torch.inference_mode():
+                return (pe_attention(q, k, v, mode="pope", freqs=freqs, delta=delta, scale=scale),)
+
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+    what = "fwd+bwd" if backward else "fwd"
+    log(f"bench: warmup {args.warmup} steps ({what}, B={B} H={H} S={S} D={D} bf16)")
+    for _ in range(args.warmup):
+        res = step()
+    torch.cuda.synchronize()
+    for t in res:
+        if not torch.isfinite(t.float()).all():
+            raise RuntimeError("non-finite result in warmup")
+    evs, arrays = stage_events(torch, args.steps, stream)
+    log(f"bench: timing {args.steps} steps")
+    ms = timed_loop(torch, L, step, arrays, args.steps)
     log(f"bench: {ms:.3f} ms/step")
 
-    stage_ms = {}
-    for si, name in enumerate(_lib.STAGES):
-        vals = [row[2 * si].elapsed_time(row[2 * si + 1]) for row in evs]
-        stage_ms[name] = sum(vals) / len(vals)
-    core = ["fwd_core", "bwd_dkdv", "bwd_dq"]
+    core = ["fwd_core", "bwd_dkdv", "bwd_dq"] if backward else ["fwd_core"]
+    names = _lib.STAGES if backward else ["fwd_prep", "fwd_core"]
+    stage_ms = stage_times(evs, names)
     dom = max(core, key=lambda n: stage_ms[n])
-    achieved = F[dom] / (stage_ms[dom] * 1e-3) / 1e12
-    traffic, traffic_kernel = measured_traffic(dom)
-    value = F["total"] / (ms * 1e-3) / 1e12
-
-    props = torch.cuda.get_device_properties(dev)
-    res = {
-        "metric": "fused PoPE attn fwd+bwd TFLOP/s @S=16k,D=128; % of bf16 MFMA peak",
+    total = F["total"] if backward else F["fwd"]
+    value = total / (ms * 1e-3) / 1e12
+    if backward:
+        metric = "fused PoPE attn fwd+bwd TFLOP/s @S=16k,D=128; % of bf16 MFMA peak"
+        workload = "PoPE causal attention fwd+bwd"
+    else:
+        metric = "fused PoPE attn fwd TFLOP/s @S=16k,D=128 (long-context eval forward); % of bf16 MFMA peak"
+        workload = "PoPE causal attention forward (long-context eval)"
+    return {
+        "metric": metric,
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -215,27 +252,185 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v/dO, delta ~ U(-2pi,0) per head)",
-        "config": {"workload": "PoPE causal attention fwd+bwd", "B": B, "H": H, "S": S, "D": D,
-                   "delta": "per-head (H, D)", "grads": "q,k,v,delta", "parallelism": "single GPU"},
+        "config": {"workload": workload, "B": B, "H": H, "S": S, "D": D, "delta": "per-head (H, D)",
+                   "grads": "q,k,v,delta" if backward else "none", "parallelism": "single GPU"},
         "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
-        "fa_convention_tflops": round(F["fa_convention"] / (ms * 1e-3) / 1e12, 2),
+        "fa_convention_tflops": round((F["fa_convention"] if backward else 2.0 * B * H * S * S * D)
+                                      / (ms * 1e-3) / 1e12, 2),
         "stage_ms": {k2: round(v2, 4) for k2, v2 in stage_ms.items()},
-        "roofline": {
-            "kernel": dom,
-            "bound": "mfma",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None if traffic is None else int(traffic),
-            "traffic_unit": "bytes per launch (HBM read + write)",
-            "traffic_source": None if traffic is None else f"profiles/{os.path.basename(TRAFFIC_FILE)}: {traffic_kernel}",
-        },
-        "device": {"name": props.name, "cus": props.multi_processor_count},
+        "roofline": roofline(dom, F[dom], stage_ms[dom]),
     }
+
+
+DECODER = dict(vocab_size=32000, hidden_dim=2048, num_layers=24, num_heads=16, num_kv_heads=16, head_dim=128,
+               ffn_dim=5632, S=16384)
+
+
+def decoder_flops(c: dict) -> dict:
+    """Algorithmic FLOPs of one decoder forward over S tokens: projections + SwiGLU + LM head
+    GEMMs (2*S*K*N each) and the fused PoPE attention (3*H*S^2*D per layer)."""
+    S, d, L = c["S"], c["hidden_dim"], c["num_layers"]
+    hd = c["num_heads"] * c["head_dim"]
+    gemm = L * 2 * S * (d * hd * 2 + d * c["num_kv_heads"] * c["head_dim"] * 2 + 3 * d * c["ffn_dim"])
+    head = 2 * S * d * c["vocab_size"]
+    attn = L * 3.0 * c["num_heads"] * S * S * c["head_dim"]
+    return {"gemm": gemm, "lm_head": head, "attention": attn, "total": gemm + head + attn}
+
+
+def init_loss(cfg) -> float:
+    """Expected next-token CE at the N(0, 0.02^2) init: the tied LM head sees a unit-RMS input, so
+    the logits are ~ N(0, 0.02^2 d) and E[logsumexp] ~ ln V + 0.02^2 d / 2 (10.78 at V=32000,
+    d=2048)."""
+    return math.log(cfg.vocab_size) + 0.02 ** 2 * cfg.hidden_dim / 2
+
+
+def _decoder_config(torch):
+    from pe_ablations_amd.transformer import TransformerConfig
+    c = {k: v for k, v in DECODER.items() if k != "S"}
+    return TransformerConfig(pe_mode="pope", pope_fused=True, max_seq_len=DECODER["S"], pope_delta_init="uniform",
+                             **c)
+
+
+def _bf16_weights(torch, model):
+    """Every parameter to bf16 except the shared PoPE module's (its fp32 frequency and angle
+    tables are buffers and stay fp32; its phase bias stays fp32 too)."""
+    for name, p in model.named_parameters():
+        if not name.startswith("pope.") and ".fpope." not in name:
+            p.data = p.data.to(torch.bfloat16)
+    return model
+
+
+def decoder_cpu_baseline(torch, model, ids, tokens: int):
+    """Oracle decoder forward (oracle.decoder_forward: fp32 weights, fp64 attention core, all host
+    threads) over the first `tokens` token ids: one warm-up on 128 tokens, one timed pass."""
+    from oracle import pe_oracle as O
+    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    x = ids[:, :tokens].cpu()
+    with torch.no_grad():
+        O.decoder_forward(sd, model.config, x[:, :128], labels=x[:, :128])
+        t0 = time.perf_counter()
+        loss = O.decoder_forward(sd, model.config, x, labels=x)["loss"].item()
+        dt = time.perf_counter() - t0
+    return {
+        "value": tokens / dt,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle/pe_oracle.py decoder_forward (fp32 weights, fp64 attention), all 24 layers, "
+                  f"first {tokens} of the {DECODER['S']} tokens, one pass of {dt:.1f} s (loss {loss:.3f}); "
+                  f"attention per token at {tokens} tokens is {tokens}/{DECODER['S']} of that at the full length",
+        "seconds": dt,
+    }
+
+
+def run_decoder(args, torch, dev) -> dict:
+    from pe_ablations_amd import _lib
+    from pe_ablations_amd.transformer import Transformer
+
+    cfg = _decoder_config(torch)
+    S = DECODER["S"]
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Transformer(cfg)
+    model = _bf16_weights(torch, model).eval()
+    g = torch.Generator(device=dev).manual_seed(0)
+    ids = torch.randint(0, cfg.vocab_size, (1, S), generator=g, device=dev)
+    nparam = sum(p.numel() for p in model.parameters())
+
+    def step():
+        with torch.inference_mode():
+            return model(ids, labels=ids)["loss"]
+
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+    log(f"bench: decoder {nparam / 1e9:.2f}B params, warmup {args.warmup} forwards over {S} tokens")
+    for _ in range(args.warmup):
+        loss = step()
+    torch.cuda.synchronize()
+    loss = float(loss.float().item())
+    expected = init_loss(cfg)
+    if not abs(loss - expected) < 0.25:
+        raise RuntimeError(f"decoder loss {loss:.4f} is not near ln(V) + 0.02^2 d / 2 = {expected:.4f}")
+    evs, arrays = stage_events(torch, args.steps, stream)
+    log(f"bench: timing {args.steps} forwards")
+    ms = timed_loop(torch, L, step, arrays, args.steps)
+    log(f"bench: {ms:.3f} ms/forward")
+    stage_ms = stage_times(evs, ["fwd_prep", "fwd_core"])  # the last layer's attention call of each step
+    Fd = decoder_flops(DECODER)
+    H, D = DECODER["num_heads"], DECODER["head_dim"]
+    attn_ms = stage_ms["fwd_prep"] + stage_ms["fwd_core"]
+    return {
+        "metric": "~1B PoPE decoder forward tokens/s @16k tokens (CE loss at init ~ ln 32000 + 0.02^2*2048/2)",
+        "value": round(S / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (16384 uniform token ids; random-init weights N(0, 0.02^2))",
+        "config": {"workload": "decoder forward with next-token CE loss", "layers": DECODER["num_layers"],
+                   "d_model": DECODER["hidden_dim"], "heads": H, "head_dim": D, "ffn": DECODER["ffn_dim"],
+                   "vocab": DECODER["vocab_size"], "tokens": S, "attention": "fused PoPE (all head dims)",
+                   "params": nparam, "parallelism": "single GPU"},
+        "loss": round(loss, 4),
+        "expected_loss_at_init": round(expected, 4),
+        "model_tflops": round(Fd["total"] / (ms * 1e-3) / 1e12, 2),
+        "flops_per_forward": {k2: float(f"{v2:.4g}") for k2, v2 in Fd.items()},
+        "attention_ms_per_layer": round(attn_ms, 4),
+        "attention_share": round(attn_ms * DECODER["num_layers"] / ms, 4),
+        "stage_ms": {k2: round(v2, 4) for k2, v2 in stage_ms.items()},
+        "roofline": roofline("fwd_core", 3.0 * H * S * S * D, stage_ms["fwd_core"]),
+        "_model": model,
+        "_ids": ids,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 20; decoder 5)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 3; decoder 2)")
+    ap.add_argument("--workload", choices=["fwdbwd", "fwd", "decoder"], default="fwdbwd")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=2)
+    ap.add_argument("--cpu-reps", type=int, default=4)
+    ap.add_argument("--cpu-tokens", type=int, default=2048, help="decoder CPU baseline: tokens of the sample")
+    args = ap.parse_args()
+    dec = args.workload == "decoder"
+    args.steps = args.steps if args.steps is not None else (5 if dec else 20)
+    args.warmup = args.warmup if args.warmup is not None else (2 if dec else 3)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}); the PE attention path has no multi-GPU leg", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if dec:
+        res = run_decoder(args, torch, dev)
+    else:
+        res = run_attention(args, torch, dev, backward=args.workload == "fwdbwd")
+    props = torch.cuda.get_device_properties(dev)
+    res["device"] = {"name": props.name, "cus": props.multi_processor_count}
+    model, ids = res.pop("_model", None), res.pop("_ids", None)
     if not args.no_cpu_baseline:
-        log(f"bench: CPU baseline ({args.cpu_heads} heads)")
-        cb = cpu_baseline(args.cpu_heads, args.cpu_reps)
+        if dec:
+            log(f"bench: CPU baseline (decoder, {args.cpu_tokens} tokens)")
+            cb = decoder_cpu_baseline(torch, model, ids, args.cpu_tokens)
+        else:
+            log(f"bench: CPU baseline ({args.cpu_heads} heads)")
+            cb = cpu_baseline(args.cpu_heads, args.cpu_reps, backward=args.workload == "fwdbwd")
         res["cpu_baseline"] = {k2: v2 for k2, v2 in cb.items() if k2 != "seconds"}
         res["cpu_baseline"]["value"] = round(cb["value"], 5)
     print(json.dumps(res), flush=True)

@@ -466,3 +466,84 @@ def pope_attention_chunked(q, k, v, freqs, delta, dout=None, scale=None, causal=
     res.update(dq=dmq * torch.sigmoid(q.double()), dk=dmk * torch.sigmoid(k.double()), dv=dv,
                ddelta=dphk.sum(0), dfreqs=(dphq * tq.view(-1, 1)).sum(0) + (dphk * tk.view(-1, 1)).sum(0))
     return res
+
+
+# --------------------------------------------------------------------------------------------
+# whole decoder (the long-context evaluation and 1B-forward callers of the attention)
+# --------------------------------------------------------------------------------------------
+
+def decoder_forward(state: dict, cfg, input_ids: torch.Tensor, start: int = 0,
+                    labels: Optional[torch.Tensor] = None) -> dict:
+    """Transformer.forward of the reference (src/model/transformer.py:313-364) restated over a
+    state dict: token embedding -> per layer x + attn(RMSNorm(x)), x + w2(silu(w3 h) * w1 h)
+    (src/model/transformer.py:186-205, src/model/ffn.py:17-27,53-68) -> RMSNorm -> LM head ->
+    shifted cross entropy (ignore_index -100).  Weights in float32, the attention core in float64.
+
+    ``cfg`` has TransformerConfig's attributes.  The attention per pe_mode follows
+    src/model/transformer.py:127-178: "pope" / "pope_floor" / "fpope" use the split module
+    contraction (or, with ``cfg.pope_fused``, the fused form of the legacy API: every head dim
+    PoPE-encoded, scale 1/sqrt(head_dim)); "rope" / "nope" use the RoPE module path."""
+    w = {k: v.float() for k, v in state.items()}
+    B, S = input_ids.shape
+    H, Hkv, D, eps = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.norm_eps
+    mode = cfg.pe_mode
+    fused = bool(getattr(cfg, "pope_fused", False)) and mode in ("pope", "pope_floor")
+
+    if mode in ("pope", "pope_floor"):
+        freqs, delta = w["pope.effective_freqs"], clamp_delta(w["pope.phase_bias"])
+    elif mode == "fpope":
+        freqs = fope_effective_freqs(w["fpope.base_freqs"], w["fpope.fourier_coeffs"], w["fpope.fourier_indices"],
+                                     training_length=cfg.fpope_training_length,
+                                     normalize=cfg.fpope_normalize_coeffs, use_ceiling=cfg.fpope_use_ceiling)
+        delta = clamp_delta(w["fpope.phase_bias"])
+    elif mode == "rope":
+        if cfg.rope_type == "yarn":
+            inv_freq, mscale, _, _ = yarn_inv_freq(D, cfg.rope_theta, cfg.rope_scale, 512)
+        elif cfg.rope_type == "ntk":
+            inv_freq, mscale = rope_inv_freq(D, ntk_theta(D, cfg.rope_theta, cfg.rope_scale)), 1.0
+        else:
+            inv_freq, mscale = rope_inv_freq(D, cfg.rope_theta), 1.0
+
+    def heads(t, n, d):
+        return t.view(B, S, n, d).transpose(1, 2)
+
+    def attn(p, h):
+        v = heads(F.linear(h, w[p + "wv.weight"]), Hkv, D)
+        if mode in ("pope", "pope_floor", "fpope"):
+            qr, kr = F.linear(h, w[p + "wq_r.weight"]), F.linear(h, w[p + "wk_r.weight"])
+            if cfg.use_qk_norm:
+                qr, kr = rms_norm(qr, w[p + "qr_norm.weight"]), rms_norm(kr, w[p + "kr_norm.weight"])
+            dr = qr.shape[-1] // H
+            qr, kr = heads(qr, H, dr), heads(kr, Hkv, dr)
+            if fused:
+                out, _ = pope_attention(qr, kr, v, freqs, delta, scale=D ** -0.5, start_q=start,
+                                        start_k=start, clamp=False)
+            else:
+                qc = heads(F.linear(h, w[p + "wq_c.weight"]), H, D)
+                kc = heads(F.linear(h, w[p + "wk_c.weight"]), Hkv, D)
+                out, _ = split_pope_attention(qc, kc, qr, kr, v, freqs, delta, start=start)
+        else:
+            q = heads(F.linear(h, w[p + "wq.weight"]), H, D)
+            k = heads(F.linear(h, w[p + "wk.weight"]), Hkv, D)
+            if mode == "rope":
+                out, _ = rope_attention(q, k, v, inv_freq, mscale, cfg.use_qk_norm, start=start)
+            else:
+                if cfg.use_qk_norm:
+                    q, k = qk_l2norm(q), qk_l2norm(k)
+                out, _ = attention(q, k, v, D ** -0.5)
+        out = out.float().transpose(1, 2).reshape(B, S, H * v.shape[-1])
+        return F.linear(out, w[p + "wo.weight"])
+
+    x = F.embedding(input_ids, w["token_embedding.embedding.weight"])
+    for i in range(cfg.num_layers):
+        p = f"layers.{i}."
+        x = x + attn(p + "attention.", rms_norm(x, w[p + "attention_norm.weight"], eps))
+        h = rms_norm(x, w[p + "ffn_norm.weight"], eps)
+        f = p + "feed_forward."
+        x = x + F.linear(F.silu(F.linear(h, w[f + "w3.weight"])) * F.linear(h, w[f + "w1.weight"]), w[f + "w2.weight"])
+    logits = F.linear(rms_norm(x, w["norm.weight"], eps), w["output.weight"])
+    res = {"logits": logits}
+    if labels is not None:
+        res["loss"] = F.cross_entropy(logits[..., :-1, :].reshape(-1, logits.shape[-1]),
+                                      labels[..., 1:].reshape(-1), ignore_index=-100)
+    return res
