@@ -128,6 +128,40 @@ int pe_attn_bwd(const pe_attn_params* p,
                 const void* fwd_workspace, size_t fwd_ws_bytes,
                 void* bwd_workspace, size_t bwd_ws_bytes, void* stream);
 
+/* RMSNorm weights of the position projections (qr_norm / kr_norm of FPoPEGroupedQueryAttention,
+ * src/model/fpope_attention.py:88-90,132-137; RMSNorm, src/model/normalization.py:7-27). */
+typedef struct {
+  const void* q_weight;  /* (Hq * Dr,) */
+  const void* k_weight;  /* (Hkv * Dr,) */
+  int32_t weight_dtype;  /* PE_DTYPE_* of both */
+  float eps;             /* RMSNorm eps (the module default is 1e-6) */
+} pe_norm_params;
+
+/* Forward with the RMSNorm of the raw position projections fused into the PoPE prologue: qr / kr
+ * are wq_r(x) / wk_r(x) as (B,H,S,Dr) views of (B,S,H*Dr) rows, and each token's H*Dr features are
+ * normalised together, y = (x * rsqrt(mean(x^2) + eps)).type_as(x) * weight, before the transform
+ * (one kernel per side instead of the module's eager norm plus the prologue).  Replaces the
+ * qr_norm / kr_norm calls of src/model/fpope_attention.py:132-137 together with everything
+ * pe_attn_fwd replaces.  PoPE / FoPE mode only; H*Dr <= 8192, Dr % 8 == 0, 16-byte aligned rows.
+ * Forward only: the workspace holds operands of the normalised projections, so training calls
+ * apply the norm themselves and use pe_attn_fwd / pe_attn_bwd. */
+int pe_attn_fwd_normed(const pe_attn_params* p, const pe_norm_params* n,
+                       const pe_tensor_t* qc, const pe_tensor_t* qr,
+                       const pe_tensor_t* kc, const pe_tensor_t* kr,
+                       const pe_tensor_t* v,
+                       const float* freqs, const float* delta,
+                       const pe_tensor_t* out, float* lse,
+                       void* fwd_workspace, size_t fwd_ws_bytes, void* stream);
+
+/* RMSNorm forward over the last dim of a (rows, n) view with unit element stride
+ * (src/model/normalization.py:7-27, the module on hidden states and on the position
+ * projections): y = (x * rsqrt(mean(x^2) + eps)).type_as(x) * weight, in fp32; y_dtype must be
+ * bf16 when x and weight are both bf16 and fp32 otherwise (torch's type promotion).  n % 8 == 0,
+ * n <= 8192, 16-byte aligned base pointers, row strides multiples of 16 bytes. */
+int pe_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t x_row_stride, int64_t rows, int32_t n,
+                   const void* weight, int32_t weight_dtype, float eps,
+                   void* y, int32_t y_dtype, int64_t y_row_stride, void* stream);
+
 /* Elementwise positional prologue on its own (the HBM-bound half of the forward): writes the
  * transformed rows [content | transform | zero pad] of x into dst (B,H,S,width) contiguous in
  * p->dtype, width = pe_attn_operand_width(p).  is_key selects the key phase bias.  Replaces

@@ -27,6 +27,7 @@ EXPORTED = [
     "pe_attn_check", "pe_attn_fwd_workspace_bytes", "pe_attn_bwd_workspace_bytes", "pe_attn_fwd",
     "pe_attn_bwd", "pe_attn_transform", "pe_attn_operand_width", "pe_attn_strerror", "pe_attn_version",
     "pe_attn_set_stage_events", "pe_attn_transform_bwd_workspace_bytes", "pe_attn_transform_bwd",
+    "pe_attn_fwd_normed", "pe_rmsnorm_fwd",
 ]
 
 # kernel stages bracketed by pe_attn_set_stage_events
@@ -47,6 +48,11 @@ class PeParams(ctypes.Structure):
                 ("qk_l2norm", ctypes.c_int32),
                 ("scale", ctypes.c_float), ("rope_mscale", ctypes.c_float),
                 ("delta_head_stride", ctypes.c_int64)]
+
+
+class PeNormParams(ctypes.Structure):
+    _fields_ = [("q_weight", ctypes.c_void_p), ("k_weight", ctypes.c_void_p),
+                ("weight_dtype", ctypes.c_int32), ("eps", ctypes.c_float)]
 
 
 _lib = None
@@ -100,6 +106,12 @@ def lib():
             L.pe_attn_transform_bwd_workspace_bytes.restype = sz
             L.pe_attn_transform_bwd.argtypes = [P, ctypes.c_int, vp, T, vp, vp, T, T, vp, vp, vp, sz, vp]
             L.pe_attn_transform_bwd.restype = ctypes.c_int
+            L.pe_attn_fwd_normed.argtypes = [P, ctypes.POINTER(PeNormParams), T, T, T, T, T, vp, vp, T, vp,
+                                             vp, sz, vp]
+            L.pe_attn_fwd_normed.restype = ctypes.c_int
+            i32, i64 = ctypes.c_int32, ctypes.c_int64
+            L.pe_rmsnorm_fwd.argtypes = [vp, i32, i64, i64, i32, vp, i32, ctypes.c_float, vp, i32, i64, vp]
+            L.pe_rmsnorm_fwd.restype = ctypes.c_int
             L.pe_attn_set_stage_events.argtypes = [vp]
             L.pe_attn_set_stage_events.restype = ctypes.c_int
             _lib = L

@@ -276,12 +276,17 @@ int pe_attn_transform_bwd(const pe_attn_params* p, int is_key, const float* g, c
   return PE_OK;
 }
 
-int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
-                const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
-                const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,
-                void* fwd_workspace, size_t fwd_ws_bytes, void* stream) {
+static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe_tensor_t* qc,
+                    const pe_tensor_t* qr, const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                    const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,
+                    void* fwd_workspace, size_t fwd_ws_bytes, void* stream) {
   int rc = pe_attn_check(p);
   if (rc) return rc;
+  if (nrm) {
+    if (p->mode != PE_MODE_POPE || p->Dr <= 0) return PE_ERR_MODE;
+    if (!nrm->q_weight || !nrm->k_weight) return PE_ERR_NULL;
+    if (nrm->weight_dtype != PE_DTYPE_BF16 && nrm->weight_dtype != PE_DTYPE_FP32) return PE_ERR_MODE;
+  }
   if ((rc = check_tensor(qr, p->Dr > 0)) || (rc = check_tensor(kr, p->Dr > 0)) ||
       (rc = check_tensor(qc, p->Dc > 0)) || (rc = check_tensor(kc, p->Dc > 0)) ||
       (rc = check_tensor(v, true)) || (rc = check_tensor(out, true)))
@@ -297,9 +302,19 @@ int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   pe::PrepArgs a;
   stage_mark(PE_STAGE_FWD_PREP, 0, s);
   fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
-  if ((rc = pe::launch_prep(a, s))) return rc;
+  if (nrm) {
+    a.norm_w = nrm->q_weight; a.norm_w_dtype = nrm->weight_dtype; a.norm_eps = nrm->eps;
+    if ((rc = pe::launch_prep_norm(a, s))) return rc;
+  } else if ((rc = pe::launch_prep(a, s))) {
+    return rc;
+  }
   fill_prep(a, p, 1, kc, kr, freqs, delta, ws + L.k_off, L.dqk);
-  if ((rc = pe::launch_prep(a, s))) return rc;
+  if (nrm) {
+    a.norm_w = nrm->k_weight; a.norm_w_dtype = nrm->weight_dtype; a.norm_eps = nrm->eps;
+    if ((rc = pe::launch_prep_norm(a, s))) return rc;
+  } else if ((rc = pe::launch_prep(a, s))) {
+    return rc;
+  }
   if (!v_direct(p, v, L.dv)) {
     pe_attn_params pv = *p;
     pv.mode = PE_MODE_NONE; pv.Dc = 0; pv.Dr = p->Dv; pv.qk_l2norm = 0;
@@ -315,6 +330,36 @@ int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   rc = pe::launch_fwd(p->dtype == PE_DTYPE_BF16 ? 0 : 1, L.dqk, L.dv, c, s);
   stage_mark(PE_STAGE_FWD_CORE, 1, s);
   return rc;
+}
+
+int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,
+                void* fwd_workspace, size_t fwd_ws_bytes, void* stream) {
+  return fwd_impl(p, nullptr, qc, qr, kc, kr, v, freqs, delta, out, lse, fwd_workspace, fwd_ws_bytes, stream);
+}
+
+int pe_attn_fwd_normed(const pe_attn_params* p, const pe_norm_params* n, const pe_tensor_t* qc,
+                       const pe_tensor_t* qr, const pe_tensor_t* kc, const pe_tensor_t* kr,
+                       const pe_tensor_t* v, const float* freqs, const float* delta,
+                       const pe_tensor_t* out, float* lse, void* fwd_workspace, size_t fwd_ws_bytes,
+                       void* stream) {
+  if (!n) return PE_ERR_NULL;
+  return fwd_impl(p, n, qc, qr, kc, kr, v, freqs, delta, out, lse, fwd_workspace, fwd_ws_bytes, stream);
+}
+
+int pe_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t x_row_stride, int64_t rows, int32_t n,
+                   const void* weight, int32_t weight_dtype, float eps, void* y, int32_t y_dtype,
+                   int64_t y_row_stride, void* stream) {
+  if (!x || !weight || !y) return PE_ERR_NULL;
+  int rc = device_ok();
+  if (rc) return rc;
+  pe::NormArgs a;
+  a.x = x; a.x_dtype = x_dtype; a.x_rs = x_row_stride;
+  a.w = weight; a.w_dtype = weight_dtype;
+  a.y = y; a.y_dtype = y_dtype; a.y_rs = y_row_stride;
+  a.rows = rows; a.n = n; a.eps = eps;
+  return pe::launch_rmsnorm(a, (hipStream_t)stream);
 }
 
 int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,

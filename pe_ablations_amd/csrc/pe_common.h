@@ -46,6 +46,37 @@ __device__ __forceinline__ float bf2f(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);
 }
 
+__device__ __forceinline__ float round_bf16(float x) { return bf2f(f2bf(x)); }
+
+__device__ __forceinline__ void unpack8(const u32x4& v, float (&x)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __builtin_bit_cast(float, v[i] << 16);
+    x[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
+  }
+}
+
+// 8 consecutive elements starting at element i (16-byte aligned) as floats / from floats;
+// dtype 0 = bf16 (one 16-byte access), 1 = fp32 (two)
+__device__ __forceinline__ void load8(const void* p, int64_t i, int dtype, float (&x)[8]) {
+  if (dtype == 0) {
+    unpack8(*(const u32x4*)((const uint16_t*)p + i), x);
+  } else {
+    const f32x4 a = *(const f32x4*)((const float*)p + i), b = *(const f32x4*)((const float*)p + i + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
+  }
+}
+__device__ __forceinline__ void store8(void* p, int64_t i, int dtype, const float (&x)[8]) {
+  if (dtype == 0) {
+    *(u32x4*)((uint16_t*)p + i) =
+        u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])};
+  } else {
+    *(f32x4*)((float*)p + i) = f32x4{x[0], x[1], x[2], x[3]};
+    *(f32x4*)((float*)p + i + 4) = f32x4{x[4], x[5], x[6], x[7]};
+  }
+}
+
 // storage element per compute dtype: DT 0 = bf16 (raw uint16), DT 1 = fp32
 template <int DT> struct Elem;
 template <> struct Elem<0> { using T = uint16_t; };

@@ -66,8 +66,21 @@ struct PrepArgs {
   int B, H, S, Dc, Dr, mode, start_pos, l2norm, is_key;
   const float* freqs; const float* delta; int64_t delta_hs;
   float mscale;
+  // RMSNorm of xr over all H*Dr features of a token before the transform (launch_prep_norm only)
+  const void* norm_w; int norm_w_dtype; float norm_eps;
 };
 int launch_prep(const PrepArgs& a, hipStream_t s);
+// PoPE prologue with the RMSNorm fused in: one workgroup per token (all heads)
+int launch_prep_norm(const PrepArgs& a, hipStream_t s);
+
+// Stand-alone RMSNorm over the last dim of a (rows, n) view.
+struct NormArgs {
+  const void* x; int x_dtype; int64_t x_rs;
+  const void* w; int w_dtype;
+  void* y; int y_dtype; int64_t y_rs;
+  int64_t rows; int n; float eps;
+};
+int launch_rmsnorm(const NormArgs& a, hipStream_t s);
 
 // dO repack (to compute dtype, width DV, contiguous), Di = rowsum(dO * O) and the log2-scaled
 // lse, both into (B, H, S_pad) arrays whose padding rows hold Di = 0, L2 = +inf.

@@ -1,0 +1,178 @@
+// RMSNorm kernels (HBM-bound, one workgroup per row / token).
+//
+//   rmsnorm_kernel         y = (x * rsqrt(mean(x^2) + eps)).type_as(x) * w over the last dim
+//                          (src/model/normalization.py:7-27): statistics and products in fp32, the
+//                          normalised value rounded to x's dtype, the product with the weight
+//                          rounded to bf16 only when x and w are both bf16 (torch's type promotion)
+//   prep_pope_norm_kernel  the same RMSNorm over all H*Dr features of a token's position
+//                          projection (qr_norm / kr_norm, src/model/fpope_attention.py:88-90,
+//                          132-137) followed by the PoPE transform of each head's Dr slice
+//                          (src/model/pope.py:124-183), written straight into the attention
+//                          kernels' operand rows [content | mu cos | mu sin | 0]
+//
+// Each thread owns up to MAXC 8-element chunks of the row in registers, so the row is read from
+// HBM once; the sum of squares is reduced per wave (butterfly) and across the 4 waves in a fixed
+// order, so results do not depend on scheduling.
+#include "pe_common.h"
+#include "pe_internal.h"
+
+namespace pe {
+
+constexpr int NT = 256;   // threads per workgroup
+constexpr int MAXC = 4;   // chunks per thread: rows up to NT * MAXC * 8 = 8192 elements
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) t += red[i];
+  return t;
+}
+
+// normalise one chunk in place: n = fl(x * r) rounded to x's dtype, y = fl(n * w) (bf16 if both are)
+__device__ __forceinline__ void norm_chunk(float (&x)[8], float r, bool x_bf, const void* w, int w_dtype,
+                                           int64_t wi) {
+  float wv[8];
+  load8(w, wi, w_dtype, wv);
+  const bool y_bf = x_bf && w_dtype == 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float n = x[e] * r;
+    if (x_bf) n = round_bf16(n);
+    const float y = n * wv[e];
+    x[e] = y_bf ? round_bf16(y) : y;
+  }
+}
+
+__global__ __launch_bounds__(NT) void rmsnorm_kernel(NormArgs a) {
+  __shared__ float red[NT / 64];
+  const int64_t row = blockIdx.x;
+  const int nch = a.n >> 3;
+  float x[MAXC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    const int c = threadIdx.x + k * NT;
+    if (c < nch) {
+      load8(a.x, row * a.x_rs + c * 8, a.x_dtype, x[k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[k][e] * x[k][e];
+    }
+  }
+  // torch: mean = sum * (1/n), then rsqrt(mean + eps)
+  const float r = rsqrtf(block_sum(ss, red) * (1.0f / (float)a.n) + a.eps);
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    const int c = threadIdx.x + k * NT;
+    if (c < nch) {
+      norm_chunk(x[k], r, a.x_dtype == 0, a.w, a.w_dtype, c * 8);
+      store8(a.y, row * a.y_rs + c * 8, a.y_dtype, x[k]);
+    }
+  }
+}
+
+template <int DDT>
+__global__ __launch_bounds__(NT) void prep_pope_norm_kernel(PrepArgs a) {
+  __shared__ float red[NT / 64];
+  const int tpr = a.Dr >> 3;
+  const int nch = a.H * tpr;
+  const int tok = blockIdx.x;
+  const int b = tok / a.S, s = tok - b * a.S;
+  const float pos = (float)(a.start_pos + s);
+  float x[MAXC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    const int c = threadIdx.x + k * NT;
+    if (c < nch) {
+      const int h = c / tpr, t = c - h * tpr;
+      load8(a.xr, b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + t * 8, a.xr_dtype, x[k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[k][e] * x[k][e];
+    }
+  }
+  const float r = rsqrtf(block_sum(ss, red) * (1.0f / (float)(a.H * a.Dr)) + a.norm_eps);
+  const bool add = a.is_key && a.delta;
+#pragma unroll
+  for (int k = 0; k < MAXC; ++k) {
+    const int c = threadIdx.x + k * NT;
+    if (c < nch) {
+      const int h = c / tpr, t = c - h * tpr;
+      norm_chunk(x[k], r, a.xr_dtype == 0, a.norm_w, a.norm_w_dtype, c * 8);
+      const f32x4 f0 = *(const f32x4*)(a.freqs + t * 8), f1 = *(const f32x4*)(a.freqs + t * 8 + 4);
+      f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
+      if (add) {
+        d0 = *(const f32x4*)(a.delta + h * a.delta_hs + t * 8);
+        d1 = *(const f32x4*)(a.delta + h * a.delta_hs + t * 8 + 4);
+      }
+      float cv[8], sv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float mu = softplus_f(x[k][e]);
+        float ph = mul_nc(pos, e < 4 ? f0[e] : f1[e - 4]);
+        if (add) ph = add_nc(ph, e < 4 ? d0[e] : d1[e - 4]);
+        float sn, cs;
+        pe_sincos(ph, sn, cs);
+        cv[e] = mul_nc(mu, cs);
+        sv[e] = mul_nc(mu, sn);
+      }
+      const int64_t drow = ((int64_t)(b * a.H + h) * a.S + s) * a.width;
+      store8(a.dst, drow + a.Dc + t * 8, DDT, cv);
+      store8(a.dst, drow + a.Dc + a.Dr + t * 8, DDT, sv);
+    }
+  }
+  if (a.Dc > 0) {  // content part: converted copy
+    const int cpr = a.Dc >> 3;
+    for (int c = threadIdx.x; c < a.H * cpr; c += NT) {
+      const int h = c / cpr, j = c - h * cpr;
+      float v[8];
+      load8(a.xc, b * a.xc_s[0] + h * a.xc_s[1] + (int64_t)s * a.xc_s[2] + j * 8, a.xc_dtype, v);
+      store8(a.dst, ((int64_t)(b * a.H + h) * a.S + s) * a.width + j * 8, DDT, v);
+    }
+  }
+  const int used = a.Dc + 2 * a.Dr;
+  const int ppr = (a.width - used) >> 3;
+  for (int c = threadIdx.x; c < a.H * ppr; c += NT) {
+    const int h = c / ppr, j = c - h * ppr;
+    const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    store8(a.dst, ((int64_t)(b * a.H + h) * a.S + s) * a.width + used + j * 8, DDT, z);
+  }
+}
+
+// 16-byte aligned base and 8-element chunks that stay 16-byte aligned along every stride
+static bool rows_aligned(const void* p, int dtype, int64_t s0, int64_t s1, int64_t s2) {
+  const int64_t q = dtype == 0 ? 8 : 4;
+  return ((uintptr_t)p % 16) == 0 && s0 % q == 0 && s1 % q == 0 && s2 % q == 0;
+}
+
+int launch_rmsnorm(const NormArgs& a, hipStream_t s) {
+  if (a.rows <= 0 || a.rows > 0x7fffffff || a.n <= 0) return -2;
+  if (a.n % 8 != 0 || a.n > NT * MAXC * 8) return -3;
+  if ((a.x_dtype | a.w_dtype | a.y_dtype) & ~1) return -4;
+  if (a.y_dtype != ((a.x_dtype == 0 && a.w_dtype == 0) ? 0 : 1)) return -4;
+  if (!rows_aligned(a.x, a.x_dtype, a.x_rs, 0, 0) || !rows_aligned(a.y, a.y_dtype, a.y_rs, 0, 0) ||
+      ((uintptr_t)a.w % 16) != 0)
+    return -5;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)a.rows), dim3(NT), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
+int launch_prep_norm(const PrepArgs& a, hipStream_t s) {
+  if (a.mode != 0 || !a.norm_w || ((a.norm_w_dtype | a.xr_dtype | a.dst_dtype) & ~1)) return -4;
+  if (a.Dr <= 0 || a.Dr % 8 != 0 || a.Dc % 8 != 0 || a.width % 8 != 0 || a.H * (a.Dr / 8) > NT * MAXC) return -3;
+  if ((int64_t)a.B * a.S > 0x7fffffff) return -2;
+  const bool ok = a.xr_s[3] == 1 && rows_aligned(a.xr, a.xr_dtype, a.xr_s[0], a.xr_s[1], a.xr_s[2]) &&
+                  ((uintptr_t)a.dst % 16) == 0 && ((uintptr_t)a.freqs % 16) == 0 && ((uintptr_t)a.norm_w % 16) == 0 &&
+                  (!a.is_key || !a.delta || (((uintptr_t)a.delta % 16) == 0 && a.delta_hs % 4 == 0)) &&
+                  (a.Dc == 0 || (a.xc_s[3] == 1 && rows_aligned(a.xc, a.xc_dtype, a.xc_s[0], a.xc_s[1], a.xc_s[2])));
+  if (!ok) return -5;
+  const dim3 grid((unsigned)((int64_t)a.B * a.S));
+  if (a.dst_dtype == 0) hipLaunchKernelGGL(prep_pope_norm_kernel<0>, grid, dim3(NT), 0, s, a);
+  else hipLaunchKernelGGL(prep_pope_norm_kernel<1>, grid, dim3(NT), 0, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
+}  // namespace pe

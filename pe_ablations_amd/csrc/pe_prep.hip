@@ -300,14 +300,6 @@ __global__ __launch_bounds__(RW * 64) void reduce_kernel(ReduceArgs a) {
 // columns of one row: 16-byte loads and stores, same per-element arithmetic (bitwise identical
 // operands), rows spread over as many threads as there are 8-column chunks.
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ void unpack8(const u32x4& v, float (&x)[8]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = __builtin_bit_cast(float, v[i] << 16);
-    x[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
-  }
-}
-
 // thread t of a row: transform chunk t (cos chunk t, sin chunk t), then content chunks t, t + TPR,
 // ... and zero padding chunks the same way; TPR = Dr / 8
 __global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {

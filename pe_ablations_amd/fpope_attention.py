@@ -66,7 +66,14 @@ class FPoPEGroupedQueryAttention(nn.Module):
         self.fpope = fpope
         self.scale = (self.d_content + d_rope * 2) ** -0.5 if self.d_content else head_dim ** -0.5
 
-    def _project(self, x: torch.Tensor):
+    def _fuse_norm(self, x: torch.Tensor) -> bool:
+        """Inference with PoPE / FoPE and QK RMSNorm on the GPU: the norm runs inside the
+        transform kernel (pe_attn_fwd_normed) instead of as a separate op."""
+        return (x.is_cuda and self.qr_norm is not None and self.fpope is not None
+                and not torch.is_grad_enabled() and self.qr_norm.eps == self.kr_norm.eps
+                and self.qr_norm.weight.dtype == self.kr_norm.weight.dtype)
+
+    def _project(self, x: torch.Tensor, fuse_norm: bool = False):
         B, S, _ = x.shape
         if self.d_content:
             q_c = self.wq_c(x).view(B, S, self.num_heads, self.d_content).transpose(1, 2)
@@ -75,7 +82,7 @@ class FPoPEGroupedQueryAttention(nn.Module):
             q_c = k_c = None
         q_r = self.wq_r(x)
         k_r = self.wk_r(x)
-        if self.qr_norm is not None:
+        if self.qr_norm is not None and not fuse_norm:
             q_r = self.qr_norm(q_r)
             k_r = self.kr_norm(k_r)
         q_r = q_r.view(B, S, self.num_heads, self.d_rope).transpose(1, 2)
@@ -83,7 +90,8 @@ class FPoPEGroupedQueryAttention(nn.Module):
         v = self.wv(x).view(B, S, self.num_kv_heads, self.head_dim).transpose(1, 2)
         return q_c, k_c, q_r, k_r, v
 
-    def _attend(self, q_c, k_c, q_r, k_r, v, start_q: int, start_k: int, causal) -> torch.Tensor:
+    def _attend(self, q_c, k_c, q_r, k_r, v, start_q: int, start_k: int, causal,
+                fuse_norm: bool = False) -> torch.Tensor:
         if self.fpope is None:
             # reference fallback: q = [q_c | q_r | q_r] without any transform (:148-151)
             dt = v.dtype
@@ -91,15 +99,20 @@ class FPoPEGroupedQueryAttention(nn.Module):
             kc = torch.cat(([k_c] if k_c is not None else []) + [k_r.to(dt), k_r.to(dt)], dim=-1)
             return pe_attention(qc, kc, v, mode="none", scale=self.scale, causal=causal,
                                 start_pos_q=start_q, start_pos_k=start_k)
+        norm = {}
+        if fuse_norm:
+            norm = dict(qr_norm_weight=self.qr_norm.weight, kr_norm_weight=self.kr_norm.weight,
+                        norm_eps=self.qr_norm.eps)
         return pe_attention(q_r, k_r, v, mode="pope", q_c=q_c, k_c=k_c, freqs=self.fpope.kernel_freqs(),
                             delta=self.fpope.kernel_delta(), scale=self.scale, causal=causal,
-                            start_pos_q=start_q, start_pos_k=start_k)
+                            start_pos_q=start_q, start_pos_k=start_k, **norm)
 
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0) -> torch.Tensor:
         """(B, S, hidden) -> (B, S, hidden); ``mask`` is ignored (causal always, as the reference)."""
         B, S, _ = x.shape
-        q_c, k_c, q_r, k_r, v = self._project(x)
-        out = self._attend(q_c, k_c, q_r, k_r, v, start_pos, start_pos, True)
+        fuse = self._fuse_norm(x)
+        q_c, k_c, q_r, k_r, v = self._project(x, fuse)
+        out = self._attend(q_c, k_c, q_r, k_r, v, start_pos, start_pos, True, fuse)
         return self.wo(out.transpose(1, 2).reshape(B, S, -1))
 
 

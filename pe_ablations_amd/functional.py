@@ -172,7 +172,9 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
                  freqs: Optional[torch.Tensor] = None, delta: Optional[torch.Tensor] = None,
                  scale: Optional[float] = None, causal=True, start_pos_q: int = 0,
                  start_pos_k: int = 0, rope_mscale: float = 1.0, qk_norm: bool = False,
-                 return_lse: bool = False, compute_dtype: Optional[torch.dtype] = None):
+                 return_lse: bool = False, compute_dtype: Optional[torch.dtype] = None,
+                 qr_norm_weight: Optional[torch.Tensor] = None, kr_norm_weight: Optional[torch.Tensor] = None,
+                 norm_eps: float = 1e-6):
     """Fused PE attention on one GPU.
 
     q (B,Hq,Sq,Dr), k (B,Hkv,Sk,Dr): positional parts, transformed inside the kernel library;
@@ -182,6 +184,9 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
     mode "rope": freqs (Dr/2,) inverse frequencies, rope_mscale (YaRN), qk_norm (QKNorm).
     scale defaults to (Dc + Dqk)^-1/2 with Dqk = 2 Dr (PoPE) or Dr.
     causal: True / "top_left" (SDPA is_causal), "bottom_right" (KV-cache mask) or False.
+    qr_norm_weight / kr_norm_weight (PoPE only, forward only): q / k are the raw position
+    projections and the library applies the modules' RMSNorm over each token's H*Dr features in
+    the transform kernel (pe_attn_fwd_normed); raises when a gradient would be needed.
     Returns out (B,Hq,Sq,Dv) [and lse (B,Hq,Sq) fp32]."""
     if mode not in _MODES:
         raise ValueError(f"unknown PE mode {mode!r}")
@@ -213,7 +218,10 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
     cfg = dict(mode=m, dtype=dt, causal=_CAUSAL[causal], start_pos_q=int(start_pos_q),
                start_pos_k=int(start_pos_k), qk_norm=bool(qk_norm), scale=float(scale),
                mscale=float(rope_mscale))
-    out, lse = PEAttentionFn.apply(q, k, v, q_c, k_c, freqs, delta, cfg)
+    if qr_norm_weight is not None or kr_norm_weight is not None:
+        out, lse = _fwd_normed(q, k, v, q_c, k_c, freqs, delta, cfg, qr_norm_weight, kr_norm_weight, norm_eps)
+    else:
+        out, lse = PEAttentionFn.apply(q, k, v, q_c, k_c, freqs, delta, cfg)
     if half_in:
         out = out.to(torch.float16)
     return (out, lse) if return_lse else out
@@ -222,3 +230,64 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
 def default_pope_scale(d: int) -> float:
     """1/sqrt(D), D the pre-transform head dim (legacy fused API, tests/test_fpope.py:1537)."""
     return 1.0 / math.sqrt(d)
+
+
+def _fwd_normed(qr, kr, v, qc, kc, freqs, delta, cfg, wq, wk, eps):
+    """Forward through pe_attn_fwd_normed: RMSNorm of the raw position projections fused into the
+    PoPE prologue.  Inference only (no autograd graph is recorded)."""
+    if cfg["mode"] != _lib.PE_MODE_POPE:
+        raise ValueError("the fused position-projection RMSNorm applies to PoPE / FoPE only")
+    if wq is None or wk is None:
+        raise ValueError("pass both qr_norm_weight and kr_norm_weight")
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (qr, kr, v, qc, kc, freqs, delta, wq, wk)):
+        raise RuntimeError("pe_attention with fused RMSNorm is forward-only; apply the norm with the "
+                           "module (RMSNorm) for training")
+    if wq.dtype != wk.dtype or wq.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("qr/kr norm weights must share one dtype, bf16 or fp32")
+    L = _lib.lib()
+    dev = qr.device
+    wq, wk = wq.contiguous(), wk.contiguous()
+    p = _params(cfg, qr, kr, v, qc, delta)
+    _lib.check(L.pe_attn_check(ctypes_ref(p)))
+    n = _lib.PeNormParams()
+    n.q_weight, n.k_weight = wq.data_ptr(), wk.data_ptr()
+    n.weight_dtype, n.eps = _dtype_code(wq.dtype), float(eps)
+    cdt = torch.bfloat16 if cfg["dtype"] == _lib.PE_DTYPE_BF16 else torch.float32
+    B, Hq, Sq, Dv = qr.shape[0], qr.shape[1], qr.shape[2], v.shape[3]
+    ws_bytes = L.pe_attn_fwd_workspace_bytes(ctypes_ref(p))
+    fws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty((B, Sq, Hq, Dv), dtype=cdt, device=dev).transpose(1, 2)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.pe_attn_fwd_normed(ctypes_ref(p), ctypes_ref(n), ref(_tensor(qc)), ref(_tensor(qr)),
+                                  ref(_tensor(kc)), ref(_tensor(kr)), ref(_tensor(v)), _ptr(freqs), _ptr(delta),
+                                  ref(_tensor(out)), lse.data_ptr(), fws.data_ptr(), ws_bytes, _stream(dev))
+    _lib.check(rc)
+    return out, lse
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm forward over the last dim through pe_rmsnorm_fwd (src/model/normalization.py:22-27):
+    (x * rsqrt(mean(x^2) + eps)).type_as(x) * weight, result dtype bf16 when x and weight are both
+    bf16, else fp32.  No autograd: the module uses it when no gradient is needed."""
+    if not x.is_cuda:
+        raise RuntimeError("rms_norm runs on the GPU only (got a CPU tensor)")
+    if x.dtype not in (torch.bfloat16, torch.float32) or weight.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("rms_norm supports bf16 / fp32 tensors")
+    n = x.shape[-1]
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % (8 if x.dtype == torch.bfloat16 else 4):
+        x2 = x2.contiguous()
+    w = weight.contiguous()
+    ydt = torch.bfloat16 if (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16) else torch.float32
+    y = torch.empty((x2.shape[0], n), dtype=ydt, device=x.device)
+    if x2.shape[0] == 0:
+        return y.view(*x.shape[:-1], n)
+    L = _lib.lib()
+    with torch.cuda.device(x.device):
+        rc = L.pe_rmsnorm_fwd(x2.data_ptr(), _dtype_code(x2.dtype), x2.stride(0), x2.shape[0], n,
+                              w.data_ptr(), _dtype_code(w.dtype), float(eps), y.data_ptr(), _dtype_code(ydt),
+                              y.stride(0), _stream(x.device))
+    _lib.check(rc)
+    return y.view(*x.shape[:-1], n)
