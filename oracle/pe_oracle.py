@@ -17,6 +17,7 @@ shyampathak22/pe_ablations (all citations are files under the reference tree):
 * split-form module contraction (content | PE) ...... src/model/fpope_attention.py:109-181
 * RoPE module (rotate, QKNorm, SDPA) ................ src/model/attention.py:50-100
 * closed-form backward .............................. tests/test_fpope.py:1571-1602
+* whole decoder forward (embedding, blocks, head, CE) src/model/transformer.py:186-205,313-364
 
 The transforms are computed in float32 exactly as the reference orders them (``fl(pos*theta)``
 then ``+ delta``, no fused multiply-add) so that the fp32 kernel path can be held to 1e-5; the
@@ -31,6 +32,10 @@ Parity pins (each checked in ``tests/test_oracle.py``):
 * known answers ............. V = 0 -> O = 0, S = 1 -> O = V, diagonal phase = delta,
                                causal upper triangle = -inf, start_pos invariance, floor-clip counts
 * RoPE ...................... complex-multiply formulation, norm preservation, NTK / YaRN closed forms
+* whole decoder ............. S = 1 reduction to wo.wv (tests/test_decoder_host.py), zero layers,
+                               causal prefix, loss at init; the SwiGLU gate order and the pre-norm
+                               placement are restated from the source only (parity unpinned beyond
+                               reading for those two)
 """
 
 from __future__ import annotations
