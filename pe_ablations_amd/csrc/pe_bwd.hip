@@ -352,8 +352,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
       const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
       const float* src = (lane < 16 ? a.L2 : a.Di) + p0 + (lane & 15) * 4;
       if (lane < 32)
-        __builtin_amdgcn_global_load_lds((const void*)src,
-                                         (__attribute__((address_space(3))) void*)(st + SQ_BYTES + SO_BYTES), 16, 0, 0);
+        dma16(src, lds_addr(st + SQ_BYTES + SO_BYTES));
     }
   };
 
@@ -457,6 +456,13 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     load_ld(1);
     const char* pq = smem + pbase + prow * NCQ * 16 + crq;
     const char* po = smem + pbase + SQ_BYTES + prow * NCO * 16 + cro;
+    // the causal mask only where the half straddles the diagonal (wave-uniform branch): masked
+    // scores become -inf, so exp2 gives P = 0; tiles wholly below the diagonal, almost all of
+    // them, skip the compare and select
+    if (__builtin_amdgcn_readfirstlane(a.causal && kw0 + 31 - off - (q0 + mt * 32) > 0)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] = masked_row(kd, i) ? -INFINITY : s[i];
+    }
     u32x4 ring[FD];
 #pragma unroll
     for (int i = 0; i < FD; ++i) ring[i] = rdp(pq, po, i);
@@ -475,8 +481,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
       if (i % 4 == 2 && i + 2 < 16) load_ld((i + 2) / 4);
       if (i < 16) {
         const float lv = lg[(i / 4) & 1][i % 4], dd = dg[(i / 4) & 1][i % 4];
-        float p = fast_exp2(s[i] * sl2 - lv);
-        p = masked_row(kd, i) ? 0.f : p;
+        const float p = fast_exp2(s[i] * sl2 - lv);
         const float ds = p * (dp[i] - dd);
         if (i & 1) {  // element pairs are packed as soon as they are complete
           cpf[i / 8][(i % 8) / 2] = pack_bf2(pprev, p);
@@ -624,6 +629,340 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     }
 }
 
+// dK~/dV with two waves per SIMD.  A workgroup of 8 waves owns 128 keys of one kv head; the 32
+// keys of pair p are shared by wave p (role A: scores S, P = softmax numerator, dV += P^T dO) and
+// wave p + 4 (role B: dP = dO v^T, dS = P (dP - Di), the dS store, dK~ += dS^T q~), which land on
+// the same SIMD, so each SIMD interleaves two instruction streams of 24 products per 32-query tile
+// and neither wave's exponentials, loads or waits leave the matrix core idle.  B keeps the fp32 P
+// it needs from an LDS exchange buffer, so dS is formed from unrounded P exactly as in the
+// one-wave kernel.  Each loop step t runs A's dV of tile t-1 and S / P of tile t, and B's dS /
+// dK~ of tile t-1 and dP of tile t, then one barrier; the 32-query tiles stream through a ring of
+// 4 LDS stages (q~ 32 x DQK, dO 32 x DV, the rows' log2 lse and Di) loaded two steps ahead.
+template <int DQK, int DV>
+__global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
+  using M = MT<0>;
+  constexpr int NW = 8, BMQ = 32, BNK = 128, NSTG = 4;
+  constexpr int NCQ = DQK / 8, NCO = DV / 8;
+  constexpr int NKF = DQK / 16, NVF = DV / 16, NDK = DQK / 32, NDV = DV / 32;
+  constexpr int SQ_BYTES = BMQ * NCQ * 16, SO_BYTES = BMQ * NCO * 16;
+  constexpr int STAGE = SQ_BYTES + SO_BYTES + 2 * BMQ * 4;
+  constexpr int XB_BYTES = 2 * 4 * 4096;  // P exchange: [step parity][pair] 16 floats x 64 lanes
+  constexpr int RING = NSTG * STAGE + XB_BYTES;
+  constexpr int EPI = BNK * DQK * 4;
+  constexpr int SMEM = RING > EPI ? RING : EPI;
+  // DMA instructions per wave per tile: q~, dO and one for the 64 floats of L2 / Di
+  constexpr int PER = BMQ * NCQ / (64 * NW) + BMQ * NCO / (64 * NW) + 1;
+  static_assert(BMQ * NCQ % (64 * NW) == 0 && BMQ * NCO % (64 * NW) == 0, "whole wave instructions");
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+  char* xbuf = smem + NSTG * STAGE;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int pw = w & 3;
+  const bool roleB = __builtin_amdgcn_readfirstlane(w >> 2) != 0;
+  const int nkb = (a.Sk + BNK - 1) / BNK;
+  int kb, bh;
+  map_block(blockIdx.x, nkb, a.B * a.Hkv, false, kb, bh);
+  const int b = bh / a.Hkv, hk = bh % a.Hkv, grp = a.Hq / a.Hkv;
+  const int k0 = kb * BNK, kw0 = k0 + pw * 32, myk = kw0 + l32;
+  const int off = a.causal_off;
+
+  const int nqt = (a.Sq + BMQ - 1) / BMQ;
+  int qb0 = 0;
+  if (a.causal) qb0 = max(0, k0 - off) / BMQ;
+  if (qb0 > nqt) qb0 = nqt;
+  const int nper = nqt - qb0;
+  const int niter = nper * grp;
+  const float sl2 = a.scale * LOG2E;
+  const int64_t qrs = (int64_t)DQK * 2;
+
+  auto issue = [&](int it) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    char* st = smem + (it % NSTG) * STAGE;
+    const int h = hk * grp + it / nper;
+    const int q0 = (qb0 + it % nper) * BMQ;
+    const int64_t r0 = (int64_t)(b * a.Hq + h) * a.Sq + q0;
+    dma_tile<BMQ, NCQ, NW>(st, (const char*)a.q + r0 * qrs, qrs, a.Sq - q0, w, ln);
+    dma_tile<BMQ, NCO, NW>(st + SQ_BYTES,
+                           (const char*)a.dO + (b * a.do_sb + h * a.do_sh + (int64_t)q0 * a.do_ss) * 2,
+                           a.do_ss * 2, a.Sq - q0, w, ln);
+    // every wave issues the same 16-lane load of the tile's L2 (lanes 0-7) and Di (lanes 8-15)
+    const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
+    if (ln < 16)
+      dma16((ln < 8 ? a.L2 : a.Di) + p0 + (ln & 7) * 4, lds_addr(st + SQ_BYTES + SO_BYTES));
+  };
+
+  constexpr int FD = 3;
+  const RowX<NCQ> rq(perm_row<0>(l32), g);
+  const RowX<NCO> ro(perm_row<0>(l32), g);
+  const ColX<NCQ> cq(lane);
+  const ColX<NCO> co(lane);
+  const uint32_t rrq = (uint32_t)perm_row<0>(l32) * NCQ * 16, rro = (uint32_t)perm_row<0>(l32) * NCO * 16;
+  const uint32_t crq = ColX<NCQ>::row_term(lane), cro = ColX<NCO>::row_term(lane);
+
+  // A: S of tile t into s (16 k-steps of the q~ rows against the wave's k~)
+  auto scores_s = [&](const char* sq, const u32x4 (&kf)[NKF], f32x16& s) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s[j] = 0.f;
+    u32x4 ring[FD];
+#pragma unroll
+    for (int i = 0; i < FD; ++i) ring[i] = rq.read(sq, 0, i);
+#pragma unroll
+    for (int i = 0; i < NKF; ++i) {
+      __builtin_amdgcn_sched_barrier(0x417);
+      const u32x4 cur = ring[i % FD];
+      if (i + FD < NKF) ring[i % FD] = rq.read(sq, 0, i + FD);
+      __builtin_amdgcn_sched_barrier(0x417);
+      s = M::mma(cur, kf[i], s);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // B: dP of tile t into dp
+  auto scores_dp = [&](const char* so, const u32x4 (&vf)[NVF], f32x16& dp) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dp[j] = 0.f;
+    u32x4 ring[FD];
+#pragma unroll
+    for (int i = 0; i < FD; ++i) ring[i] = ro.read(so, 0, i);
+#pragma unroll
+    for (int i = 0; i < NVF; ++i) {
+      __builtin_amdgcn_sched_barrier(0x417);
+      const u32x4 cur = ring[i % FD];
+      if (i + FD < NVF) ring[i % FD] = ro.read(so, 0, i + FD);
+      __builtin_amdgcn_sched_barrier(0x417);
+      dp = M::mma(cur, vf[i], dp);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // products of one 32-query tile: NPR = 2 * NT MFMAs over accumulators acc[0..NT), B operands by
+  // the transpose load from the tile at `base` (k-step major, so the two products of one
+  // accumulator are NT apart)
+  auto products = [&](auto& acc, const u32x4 (&af)[2], const char* base, const auto& cx) {
+    constexpr int NT = sizeof(acc) / sizeof(acc[0]);
+    constexpr int NPR = 2 * NT;
+    u32x4 ring[FD];
+#pragma unroll
+    for (int i = 0; i < FD; ++i) ring[i] = cx.read(base, (i / NT) * 16, (i % NT) * 32);
+#pragma unroll
+    for (int i = 0; i < NPR; ++i) {
+      __builtin_amdgcn_sched_barrier(0x407);
+      const u32x4 cur = ring[i % FD];
+      if (i + FD < NPR) ring[i % FD] = cx.read(base, ((i + FD) / NT) * 16, ((i + FD) % NT) * 32);
+      __builtin_amdgcn_sched_barrier(0x407);
+      acc[i % NT] = M::mma(af[i / NT], cur, acc[i % NT]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // vmcnt allowed while the next tile's loads must have landed (see the loop): younger loads of
+  // the tile after it and, for B, its dS stores
+  auto wait_next = [&](int allowed) {
+    static_assert(PER + 4 <= 11, "wait table");
+    switch (allowed) {
+      case 0: wait_vmcnt<0>(); break;
+      case 1: wait_vmcnt<1>(); break;
+      case 2: wait_vmcnt<2>(); break;
+      case 3: wait_vmcnt<3>(); break;
+      case 4: wait_vmcnt<4>(); break;
+      case 5: wait_vmcnt<5>(); break;
+      case 6: wait_vmcnt<6>(); break;
+      case 7: wait_vmcnt<7>(); break;
+      case 8: wait_vmcnt<8>(); break;
+      case 9: wait_vmcnt<9>(); break;
+      case 10: wait_vmcnt<10>(); break;
+      default: wait_vmcnt<11>(); break;
+    }
+  };
+
+  const int kr = myk < a.Sk ? myk : a.Sk - 1;
+  if (niter > 0) issue(0);
+  if (niter > 1) issue(1);
+  if (niter > 1) wait_vmcnt<PER>();
+  else wait_vmcnt<0>();
+  __syncthreads();
+  float* st_epi = (float*)smem;  // [BNK keys][DQK] fp32 dk~ for the fused inverse transform
+  // The two roles run separate loops with the same number of barriers (one per step), so each
+  // role's registers (A: k~ and the dV accumulators, B: v and the dK~ accumulators) are live only
+  // in its own branch.
+  if (!roleB) {
+    u32x4 kf[NKF];
+    {
+      const uint16_t* krow = (const uint16_t*)a.k + ((int64_t)(b * a.Hkv + hk) * a.Sk + kr) * DQK;
+#pragma unroll
+      for (int kk = 0; kk < NKF; ++kk) kf[kk] = *(const u32x4*)(krow + kk * 16 + g * 8);
+    }
+    f32x16 dv[NDV];
+#pragma unroll
+    for (int t = 0; t < NDV; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) dv[t][j] = 0.f;
+    u32x4 pa[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};  // bf16 P of the pending tile
+    f32x16 s;
+    for (int t = 0; t <= niter; ++t) {
+      if (t + 2 < niter) issue(t + 2);  // its stage held tile t - 2, released by the last barrier
+      if (t >= 1) products(dv, pa, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);  // dV of tile t - 1
+      if (t < niter) {  // S and P of tile t: fp32 P to the exchange buffer, bf16 P kept for dV
+        const char* st = smem + (t % NSTG) * STAGE;
+        scores_s(st + rrq, kf, s);
+        const int q0 = (qb0 + t % nper) * BMQ;
+        if (__builtin_amdgcn_readfirstlane(a.causal && kw0 + 31 - off - q0 > 0)) {
+          const int kd = myk - off - q0 - g * 8;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[i] = masked_row(kd, i) ? -INFINITY : s[i];
+        }
+        const float* sL = (const float*)(st + SQ_BYTES + SO_BYTES);
+        float* xb = (float*)(xbuf + ((t & 1) * 4 + pw) * 4096);
+#pragma unroll
+        for (int G = 0; G < 4; ++G) {
+          const f32x4 lv = *(const f32x4*)(sL + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
+          f32x4 p;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[4 * G + e] * sl2 - lv[e]);
+          *(f32x4*)(xb + (G * 64 + lane) * 4) = p;
+          pa[G >> 1][(G & 1) * 2] = pack_bf2(p[0], p[1]);
+          pa[G >> 1][(G & 1) * 2 + 1] = pack_bf2(p[2], p[3]);
+        }
+      }
+      if (t + 1 < niter) wait_next(t + 2 < niter ? PER : 0);  // tile t + 1 has landed
+      __syncthreads();
+    }
+#pragma unroll
+    for (int t = 0; t < NDV; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = kw0 + c_row(j, g), col = t * 32 + l32;
+        if (key < a.Sk && col < a.dv_real)
+          store_from_float(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + col, a.dv_dtype, dv[t][j]);
+      }
+  } else {
+    u32x4 vf[NVF];
+    {
+      const uint16_t* vrow = (const uint16_t*)a.v + b * a.v_sb + hk * a.v_sh + (int64_t)kr * a.v_ss;
+#pragma unroll
+      for (int kk = 0; kk < NVF; ++kk) vf[kk] = *(const u32x4*)(vrow + kk * 16 + g * 8);
+    }
+    f32x16 dk[NDK];
+#pragma unroll
+    for (int t = 0; t < NDK; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) dk[t][j] = 0.f;
+    f32x16 dp;
+    for (int t = 0; t <= niter; ++t) {
+      if (t + 2 < niter) issue(t + 2);
+      if (t >= 1) {  // dS of tile t - 1 from A's fp32 P; store it; dK~ += dS^T q~
+        const char* st = smem + ((t - 1) % NSTG) * STAGE;
+        const float* sD = (const float*)(st + SQ_BYTES + SO_BYTES) + BMQ;
+        const float* xb = (const float*)(xbuf + (((t - 1) & 1) * 4 + pw) * 4096);
+        u32x4 dsf[2];
+#pragma unroll
+        for (int G = 0; G < 4; ++G) {
+          const f32x4 p = *(const f32x4*)(xb + (G * 64 + lane) * 4);
+          const f32x4 dd = *(const f32x4*)(sD + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
+          float ds[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ds[e] = p[e] * (dp[4 * G + e] - dd[e]);
+          dsf[G >> 1][(G & 1) * 2] = pack_bf2(ds[0], ds[1]);
+          dsf[G >> 1][(G & 1) * 2 + 1] = pack_bf2(ds[2], ds[3]);
+        }
+        const int it = t - 1;
+        const int h = hk * grp + it / nper;
+        const int q0 = (qb0 + it % nper) * BMQ;
+        char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * (a.ds_rows / 32) + (kw0 >> 5)) * a.ds_nqt * 4096 +
+                    (int64_t)(q0 >> 6) * 4096;
+        const int mt = (q0 >> 5) & 1;
+        *(u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16) = dsf[0];
+        *(u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16) = dsf[1];
+        products(dk, dsf, st + crq, cq);
+      }
+      if (t < niter) scores_dp(smem + (t % NSTG) * STAGE + SQ_BYTES + rro, vf, dp);
+      if (t + 1 < niter) {
+        // tile t + 1 has landed: allowed outstanding = the loads of tile t + 2 (issued this step)
+        // and the dS stores issued after tile t + 1's loads (last step's and this step's)
+        int allowed = t + 2 < niter ? PER : 0;
+        if (t >= 1) allowed += t >= 2 ? 4 : 2;
+        wait_next(allowed);
+      }
+      __syncthreads();
+    }
+    if (a.fuse_inv) {
+#pragma unroll
+      for (int t = 0; t < NDK; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) st_epi[(pw * 32 + c_row(j, g)) * DQK + t * 32 + l32] = dk[t][j] * a.scale;
+    } else {
+      float* dkb = a.dk_t + (int64_t)(b * a.Hkv + hk) * a.Sk * DQK;
+#pragma unroll
+      for (int t = 0; t < NDK; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = kw0 + c_row(j, g);
+          if (key < a.Sk) dkb[(int64_t)key * DQK + t * 32 + l32] = dk[t][j] * a.scale;
+        }
+    }
+  }
+
+  if (a.fuse_inv) {  // inverse PoPE transform of the staged dk~ rows, all 8 waves
+    const EpiPoPE& e = a.ek;
+    const int Dr = DQK / 2;
+    float* st = st_epi;
+    const int c = tid % Dr;
+    constexpr int EU = 4;
+    const int rstep = NW * 64 / Dr;
+    const int64_t xb = b * e.x_s[0] + hk * e.x_s[1] + c * e.x_s[3];
+    auto load_trip = [&](int r0, float (&xv)[EU]) {
+#pragma unroll
+      for (int u = 0; u < EU; ++u) {
+        const int r = r0 + u * rstep, key = k0 + r;
+        xv[u] = (r < BNK && key < a.Sk) ? load_as_float(e.x, xb + (int64_t)key * e.x_s[2], e.x_dtype) : 0.f;
+      }
+    };
+    float xv[EU], xn[EU];
+    load_trip(tid / Dr, xv);
+    __syncthreads();
+    const float fr = a.freqs[c];
+    const float dl = a.delta ? a.delta[hk * a.delta_hs + c] : 0.f;
+    float sdl = 0.f, sf = 0.f;
+#pragma unroll 1
+    for (int r0 = tid / Dr; r0 < BNK; r0 += EU * rstep) {
+      load_trip(r0 + EU * rstep, xn);
+#pragma unroll
+      for (int u = 0; u < EU; ++u) {
+        const int r = r0 + u * rstep, key = k0 + r;
+        if (r < BNK && key < a.Sk) {
+          const float pos = (float)(e.start_pos + key);
+          float dx;
+          const float dph = inv_pope_elem(xv[u], pos, fr, dl, a.delta != nullptr, st[r * DQK + c],
+                                          st[r * DQK + Dr + c], dx);
+          store_from_float(e.dx, b * e.dx_s[0] + hk * e.dx_s[1] + (int64_t)key * e.dx_s[2] + c * e.dx_s[3],
+                           e.dx_dtype, dx);
+          sdl += dph;
+          sf += pos * dph;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < EU; ++u) xv[u] = xn[u];
+    }
+    if (e.part_delta || e.part_freq) {
+      __syncthreads();
+      float* red = st;  // [2][NW*64/Dr][Dr]
+      const int nt = NW * 64 / Dr;
+      red[(0 * nt + tid / Dr) * Dr + c] = sdl;
+      red[(1 * nt + tid / Dr) * Dr + c] = sf;
+      __syncthreads();
+      const int64_t blk = (int64_t)bh * nkb + kb;
+      if (tid < Dr) {
+        float d0 = 0.f, f0 = 0.f;
+        for (int i = 0; i < nt; ++i) {
+          d0 += red[(0 * nt + i) * Dr + tid];
+          f0 += red[(1 * nt + i) * Dr + tid];
+        }
+        if (e.part_delta) e.part_delta[blk * Dr + tid] = d0;
+        if (e.part_freq) e.part_freq[blk * Dr + tid] = f0;
+      }
+    }
+  }
+}
+
 // dQ~ = dS k~ as a GEMM over the dS^T rows the dK/dV kernel stored (no score recompute).  A
 // workgroup owns 256 queries of one head; its 8 waves split them into 4 pairs of 32-query tiles x
 // 2 halves of the dq~ columns, so every fragment read from LDS feeds two MFMAs (A: dS for 32
@@ -708,8 +1047,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
       const int k = k0 + kl, r = qc & 7;
       const uint32_t src = ((uint32_t)(k >> 5) * a.ds_nqt + (qc >> 3)) * 4096u +
                            (uint32_t)(((r >> 1) * 64 + (r & 1) * 32 + (k & 31)) * 16);
-      __builtin_amdgcn_global_load_lds((const void*)(sbase + src),
-                                       (__attribute__((address_space(3))) void*)(tile + base * 16), 16, 0, 0);
+      dma16(sbase + src, lds_addr(tile) + base * 16);
     }
   };
 
@@ -864,7 +1202,12 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
   if constexpr (DT == 0) {
     if (which == 0) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
-      hipLaunchKernelGGL((dkdv_bf16_kernel<DQK, DV, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
+      if constexpr ((DQK == 128 || DQK == 256) && DV == 128) {
+        // two waves per SIMD (role-split pairs); the one-wave kernel serves the other widths
+        hipLaunchKernelGGL((dkdv_pair_kernel<DQK, DV>), dim3(nkb * a.B * a.Hkv), dim3(512), 0, s, a);
+      } else {
+        hipLaunchKernelGGL((dkdv_bf16_kernel<DQK, DV, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
+      }
     } else {
       const int nqb = (a.Sq + 255) / 256;
       // 64-key steps, double-buffered: measured faster than 32-key steps at any ring depth

@@ -39,8 +39,13 @@ constexpr float LN2 = 0.6931471805599453f;
 __device__ __forceinline__ uint16_t f2bf(float x) {
   return __builtin_bit_cast(uint16_t, (__bf16)x);  // round-to-nearest-even (v_cvt_pk_bf16_f32)
 }
+// two floats -> one dword of bf16 (lo in bits 0-15), round-to-nearest-even; written as a vector
+// conversion so that it is one v_cvt_pk_bf16_f32 with both sources (the scalar form compiles to a
+// conversion per element plus shifts and ORs)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 __device__ __forceinline__ float bf2f(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);
@@ -353,6 +358,20 @@ template <int ROWS, int NCH, int NT> struct TileStage {
 // swz(x) and the lane's source offset is r0*stride + x*stride + ((lane % NCH) ^ swz(x) ^ swz(r0))*16:
 // two per-lane constants and one XOR + add per instruction with wave-uniform r0 terms.  A tile
 // with rows past the end takes the general path that clamps each row.
+// One wave-wide 16-byte-per-lane global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes
+// land at LDS address `lds` + 16*l.  It is issued as inline asm so that the compiler does not
+// track it: for the builtin, the compiler cannot tell the transpose reads (ds_read_b64_tr_b16) from
+// reads of the tile being loaded and makes the first such read after every DMA issue wait for all
+// DMA in flight (vmcnt(0)), which serialises the load of the next tile with the current one.
+// Every caller instead waits for its DMA with an explicit vmcnt and a barrier before the
+// destination is read.  The s_nop covers the one wait state an M0 write needs before an LDS DMA.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+// LDS byte address of a __shared__ object: the low 32 bits of its generic (flat) address
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
+
 template <int ROWS, int NCH, int NW>
 __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t row_stride_bytes,
                                          int nvalid, int w, int lane) {
@@ -370,8 +389,7 @@ __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t ro
       const int base = (i * NW + w) * 64;
       const int r0 = base / NCH;
       const uint32_t S = (uint32_t)(swz<NCH>(r0) << 4);
-      __builtin_amdgcn_global_load_lds((const void*)(src + (uint32_t)r0 * rs + (X + (U ^ S))),
-                                       (__attribute__((address_space(3))) void*)(tile + base * 16), 16, 0, 0);
+      dma16(src + (uint32_t)r0 * rs + (X + (U ^ S)), lds_addr(tile) + base * 16);
     }
     (void)RPI;
   } else {
@@ -382,17 +400,14 @@ __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t ro
       const int row = slot / NCH, pc = slot % NCH;
       const int lc = pc ^ swz<NCH>(row);
       const int r = row < nvalid ? row : nvalid - 1;
-      __builtin_amdgcn_global_load_lds((const void*)(src + (r * rs + (uint32_t)(lc * 16))),
-                                       (__attribute__((address_space(3))) void*)(tile + base * 16), 16, 0, 0);
+      dma16(src + (r * rs + (uint32_t)(lc * 16)), lds_addr(tile) + base * 16);
     }
   }
 }
 
 // Plain (unswizzled) DMA of `nchunks` <= 64 consecutive 16-byte chunks by one wave.
 __device__ __forceinline__ void dma_row(char* dst, const char* src, int nchunks, int lane) {
-  if (lane < nchunks)
-    __builtin_amdgcn_global_load_lds((const void*)(src + lane * 16),
-                                     (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+  if (lane < nchunks) dma16(src + lane * 16, lds_addr(dst));
 }
 
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
