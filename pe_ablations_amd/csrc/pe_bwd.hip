@@ -675,21 +675,31 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const float sl2 = a.scale * LOG2E;
   const int64_t qrs = (int64_t)DQK * 2;
 
+  // tiles are issued in loop order: query tile qt of query head h advances qt, then h
+  const DmaPlan<BMQ, NCQ, NW> plan_q(w, lane, (uint32_t)qrs);
+  const DmaPlan<BMQ, NCO, NW> plan_o(w, lane, (uint32_t)(a.do_ss * 2));
+  const uint32_t smem_l = lds_addr(smem);
+  int iss_h = hk * grp, iss_qt = qb0;
   auto issue = [&](int it) {
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
     char* st = smem + (it % NSTG) * STAGE;
-    const int h = hk * grp + it / nper;
-    const int q0 = (qb0 + it % nper) * BMQ;
-    const int64_t r0 = (int64_t)(b * a.Hq + h) * a.Sq + q0;
-    dma_tile<BMQ, NCQ, NW>(st, (const char*)a.q + r0 * qrs, qrs, a.Sq - q0, w, ln);
-    dma_tile<BMQ, NCO, NW>(st + SQ_BYTES,
-                           (const char*)a.dO + (b * a.do_sb + h * a.do_sh + (int64_t)q0 * a.do_ss) * 2,
-                           a.do_ss * 2, a.Sq - q0, w, ln);
+    const uint32_t stl = smem_l + (uint32_t)((it % NSTG) * STAGE);
+    const int h = iss_h, q0 = iss_qt * BMQ;
+    const char* qsrc = (const char*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + q0) * qrs;
+    const char* osrc = (const char*)a.dO + (b * a.do_sb + h * a.do_sh + (int64_t)q0 * a.do_ss) * 2;
+    if (a.Sq - q0 >= BMQ) {
+      plan_q.full(qsrc, stl, w);
+      plan_o.full(osrc, stl + SQ_BYTES, w);
+    } else {
+      dma_tile<BMQ, NCQ, NW>(st, qsrc, qrs, a.Sq - q0, w, lane);
+      dma_tile<BMQ, NCO, NW>(st + SQ_BYTES, osrc, a.do_ss * 2, a.Sq - q0, w, lane);
+    }
     // every wave issues the same 16-lane load of the tile's L2 (lanes 0-7) and Di (lanes 8-15)
     const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
-    if (ln < 16)
-      dma16((ln < 8 ? a.L2 : a.Di) + p0 + (ln & 7) * 4, lds_addr(st + SQ_BYTES + SO_BYTES));
+    if (lane < 16) dma16((lane < 8 ? a.L2 : a.Di) + p0 + (lane & 7) * 4, stl + SQ_BYTES + SO_BYTES);
+    if (++iss_qt == nqt) {
+      iss_qt = qb0;
+      ++iss_h;
+    }
   };
 
   constexpr int FD = 3;
@@ -798,13 +808,15 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       for (int j = 0; j < 16; ++j) dv[t][j] = 0.f;
     u32x4 pa[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};  // bf16 P of the pending tile
     f32x16 s;
+    int cur_qt = qb0;  // query tile of step t
     for (int t = 0; t <= niter; ++t) {
       if (t + 2 < niter) issue(t + 2);  // its stage held tile t - 2, released by the last barrier
       if (t >= 1) products(dv, pa, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);  // dV of tile t - 1
       if (t < niter) {  // S and P of tile t: fp32 P to the exchange buffer, bf16 P kept for dV
         const char* st = smem + (t % NSTG) * STAGE;
         scores_s(st + rrq, kf, s);
-        const int q0 = (qb0 + t % nper) * BMQ;
+        const int q0 = cur_qt * BMQ;
+        if (++cur_qt == nqt) cur_qt = qb0;
         if (__builtin_amdgcn_readfirstlane(a.causal && kw0 + 31 - off - q0 > 0)) {
           const int kd = myk - off - q0 - g * 8;
 #pragma unroll
@@ -847,6 +859,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) dk[t][j] = 0.f;
     f32x16 dp;
+    int prev_h = hk * grp, prev_qt = qb0;  // head and query tile of step t - 1
     for (int t = 0; t <= niter; ++t) {
       if (t + 2 < niter) issue(t + 2);
       if (t >= 1) {  // dS of tile t - 1 from A's fp32 P; store it; dK~ += dS^T q~
@@ -864,9 +877,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           dsf[G >> 1][(G & 1) * 2] = pack_bf2(ds[0], ds[1]);
           dsf[G >> 1][(G & 1) * 2 + 1] = pack_bf2(ds[2], ds[3]);
         }
-        const int it = t - 1;
-        const int h = hk * grp + it / nper;
-        const int q0 = (qb0 + it % nper) * BMQ;
+        const int h = prev_h, q0 = prev_qt * BMQ;
+        if (++prev_qt == nqt) {
+          prev_qt = qb0;
+          ++prev_h;
+        }
         char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * (a.ds_rows / 32) + (kw0 >> 5)) * a.ds_nqt * 4096 +
                     (int64_t)(q0 >> 6) * 4096;
         const int mt = (q0 >> 5) & 1;

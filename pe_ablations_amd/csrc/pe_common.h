@@ -371,6 +371,20 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
 }
 // LDS byte address of a __shared__ object: the low 32 bits of its generic (flat) address
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
+// a wave-uniform 64-bit address in an SGPR pair (readfirstlane returns int: each half is taken
+// back as uint32_t so that the low half is zero-extended, not sign-extended into the high one)
+__device__ __forceinline__ uint64_t uniform64(const void* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+  return ((uint64_t)hi << 32) | (uint64_t)lo;
+}
+// dma16 with a wave-uniform base in SGPRs and a 32-bit per-lane byte offset (no per-lane 64-bit
+// address arithmetic)
+__device__ __forceinline__ void dma16s(uint32_t voff, const void* base, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(uniform64(base)), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
 
 template <int ROWS, int NCH, int NW>
 __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t row_stride_bytes,
@@ -404,6 +418,30 @@ __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t ro
     }
   }
 }
+
+// dma_tile with the per-lane source offsets of a whole tile computed once: a wave's TPW
+// instructions per tile each take one precomputed 32-bit offset and a wave-uniform row base, so a
+// full tile costs no vector instructions beyond the loads.  Tiles with rows past the end of the
+// source take dma_tile's clamping path instead.
+template <int ROWS, int NCH, int NW> struct DmaPlan {
+  static constexpr int TPW = ROWS * NCH / (64 * NW);
+  static_assert(ROWS * NCH % (64 * NW) == 0 && NCH <= 64, "whole wave instructions");
+  uint32_t off[TPW];
+  __device__ __forceinline__ DmaPlan(int w, int lane, uint32_t rs) {
+    const int x = lane / NCH;
+    const uint32_t U = (uint32_t)(((lane % NCH) ^ swz<NCH>(x)) << 4);
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int r0 = ((i * NW + w) * 64) / NCH;
+      off[i] = (uint32_t)(r0 + x) * rs + (U ^ (uint32_t)(swz<NCH>(r0) << 4));
+    }
+  }
+  // all ROWS rows of the tile starting at `src` (wave-uniform) are inside the source
+  __device__ __forceinline__ void full(const char* src, uint32_t lds_tile, int w) const {
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) dma16s(off[i], src, lds_tile + (uint32_t)((i * NW + w) * 64 * 16));
+  }
+};
 
 // Plain (unswizzled) DMA of `nchunks` <= 64 consecutive 16-byte chunks by one wave.
 __device__ __forceinline__ void dma_row(char* dst, const char* src, int nchunks, int lane) {

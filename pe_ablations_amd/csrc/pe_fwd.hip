@@ -255,21 +255,24 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    // the running max is kept in log2 units; as sl2 > 0 it is the max of the raw scores times
+    // sl2, and each probability is one fma and one exp2 of a raw score
     const bool edge = (a.causal && k0 + BN - 1 > qw + off) || (k0 + BN > a.Sk);
+    if (edge) {
+#pragma unroll
+      for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = k0 + nt * 32 + c_logical<0>(j, g);
+          if (key >= a.Sk || (a.causal && key > myq + off)) s[nt][j] = -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float x = s[nt][j] * sl2;
-        if (edge) {
-          const int key = k0 + nt * 32 + c_logical<0>(j, g);
-          if (key >= a.Sk || (a.causal && key > myq + off)) x = -INFINITY;
-        }
-        s[nt][j] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, xor32(mx));
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[nt][j]);
+    mx = fmaxf(mx, xor32(mx)) * sl2;
     if (__any(mx > m + TAU)) {
       const float mn = fmaxf(m, mx);
       const float alpha = fast_exp2(m - mn);
@@ -285,7 +288,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
     for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float p = fast_exp2(s[nt][j] - m);
+        const float p = fast_exp2(fmaf(s[nt][j], sl2, -m));
         s[nt][j] = p;
         rs += p;
       }
