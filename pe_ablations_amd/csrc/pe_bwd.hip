@@ -1051,25 +1051,30 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   // dS window for keys k0 .. k0+63 and this block's 256 queries: LDS slot (row kl, physical chunk
   // pc) holds query chunk lc = pc ^ swz(kl) of key k0 + kl; its source is that key's 32-key block
   // at 64-query block (q0/8 + lc)/8, chunk ((r>>1)*64 + (r&1)*32 + kl%32), r = (q0/8 + lc) % 8.
-  auto dma_ds = [&](char* tile, int k0) {
+  // k0 is a multiple of 32, so a lane's source offset is (k0/32) * ds_nqt * 4096 (wave-uniform)
+  // plus a per-lane constant, computed once
+  constexpr int NDS = BK * NCS / (64 * NW);
+  uint32_t ds_off[NDS];
 #pragma unroll
-    for (int i = 0; i < BK * NCS / (64 * NW); ++i) {
-      const int base = (i * NW + w) * 64;
-      const int slot = base + lane;
-      const int kl = slot / NCS, pc = slot % NCS;
-      const int lc = pc ^ swz<NCS>(kl);
-      const int qc = (q0 >> 3) + lc;
-      const int k = k0 + kl, r = qc & 7;
-      const uint32_t src = ((uint32_t)(k >> 5) * a.ds_nqt + (qc >> 3)) * 4096u +
-                           (uint32_t)(((r >> 1) * 64 + (r & 1) * 32 + (k & 31)) * 16);
-      dma16(sbase + src, lds_addr(tile) + base * 16);
-    }
-  };
-
+  for (int i = 0; i < NDS; ++i) {
+    const int slot = (i * NW + w) * 64 + lane;
+    const int kl = slot / NCS, pc = slot % NCS;
+    const int lc = pc ^ swz<NCS>(kl);
+    const int qc = (q0 >> 3) + lc, r = qc & 7;
+    ds_off[i] = ((uint32_t)(kl >> 5) * a.ds_nqt + (qc >> 3)) * 4096u +
+                (uint32_t)(((r >> 1) * 64 + (r & 1) * 32 + (kl & 31)) * 16);
+  }
+  const DmaPlan<BK, NCK, NW> plan_k(w, lane, (uint32_t)krs);
+  const uint32_t smem_l = lds_addr(smem);
   auto issue = [&](int kb) {
     char* st = smem + (kb % NSTAGE) * STAGE;
-    dma_tile<BK, NCK, NW>(st, kbase + (int64_t)kb * BK * krs, krs, a.Sk - kb * BK, w, lane);
-    dma_ds(st + SK_BYTES, kb * BK);
+    const uint32_t stl = smem_l + (uint32_t)((kb % NSTAGE) * STAGE);
+    const char* ksrc = kbase + (int64_t)kb * BK * krs;
+    if (a.Sk - kb * BK >= BK) plan_k.full(ksrc, stl, w);
+    else dma_tile<BK, NCK, NW>(st, ksrc, krs, a.Sk - kb * BK, w, lane);
+    const char* dsrc = sbase + (int64_t)((kb * BK) >> 5) * a.ds_nqt * 4096;
+#pragma unroll
+    for (int i = 0; i < NDS; ++i) dma16s(ds_off[i], dsrc, stl + SK_BYTES + (uint32_t)((i * NW + w) * 64 * 16));
   };
 #pragma unroll
   for (int i = 0; i < NSTAGE - 1; ++i)

@@ -215,6 +215,10 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
   float m = -1e30f, l = 0.f;
   const float sl2 = a.scale * LOG2E;
 
+  // per-lane offsets of the k~ / v tile loads, computed once (full tiles need no vector math)
+  const DmaPlan<BN, NCK, NW> plan_k(w, lane, (uint32_t)krs);
+  const DmaPlan<BN, NCV, NW> plan_v(w, lane, (uint32_t)vrs);
+  const uint32_t smem_l = lds_addr(smem);
   if (nkb > 0) {
     dma_tile<BN, NCK, NW>(smem, kbase, krs, a.Sk, w, lane);
     dma_tile<BN, NCV, NW>(smem + SK_BYTES, vbase, vrs, a.Sk, w, lane);
@@ -227,8 +231,16 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
     __syncthreads();
     if (kb + 1 < nkb) {
       char* nK = smem + ((kb + 1) & 1) * STAGE;
-      dma_tile<BN, NCK, NW>(nK, kbase + (int64_t)(k0 + BN) * krs, krs, a.Sk - k0 - BN, w, lane);
-      dma_tile<BN, NCV, NW>(nK + SK_BYTES, vbase + (int64_t)(k0 + BN) * vrs, vrs, a.Sk - k0 - BN, w, lane);
+      const char* ksrc = kbase + (int64_t)(k0 + BN) * krs;
+      const char* vsrc = vbase + (int64_t)(k0 + BN) * vrs;
+      if (a.Sk - k0 - BN >= BN) {
+        const uint32_t nl = smem_l + (uint32_t)(((kb + 1) & 1) * STAGE);
+        plan_k.full(ksrc, nl, w);
+        plan_v.full(vsrc, nl + SK_BYTES, w);
+      } else {
+        dma_tile<BN, NCK, NW>(nK, ksrc, krs, a.Sk - k0 - BN, w, lane);
+        dma_tile<BN, NCV, NW>(nK + SK_BYTES, vsrc, vrs, a.Sk - k0 - BN, w, lane);
+      }
     }
     if (a.causal && k0 > qw + 31 + off) continue;  // whole tile above this wave's diagonal
 
