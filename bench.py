@@ -53,7 +53,8 @@ WORKLOAD = dict(B=1, H=16, S=16384, D=128)
 # the commands.  A stage's kernel missing from it reports traffic null.
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "pope_fwdbwd_S16k_D128_hbm_traffic.json")
-STAGE_KERNEL = {"fwd_core": "fwd_bf16_kernel", "bwd_dkdv": "dkdv_bf16_kernel", "bwd_dq": "dq_gemm_kernel"}
+STAGE_KERNEL = {"fwd_core": ("fwd_bf16_kernel",), "bwd_dkdv": ("dkdv_pair_kernel", "dkdv_bf16_kernel"),
+                "bwd_dq": ("dq_gemm_kernel",)}
 
 
 def measured_traffic(stage: str):
@@ -64,7 +65,7 @@ def measured_traffic(stage: str):
     except (OSError, ValueError):
         return None, None
     for name, v in data.get("kernels", {}).items():
-        if name.startswith(STAGE_KERNEL[stage] + "<") and v.get("fetch_bytes") is not None \
+        if any(name.startswith(k + "<") for k in STAGE_KERNEL[stage]) and v.get("fetch_bytes") is not None \
                 and v.get("write_bytes") is not None:
             return v["fetch_bytes"] + v["write_bytes"], name
     return None, None

@@ -37,5 +37,5 @@ def test_committed_traffic_covers_the_attention_kernels():
         assert traffic is not None and traffic > 0, stage
         assert name.startswith(bench.STAGE_KERNEL[stage])
     # the dK/dV kernel writes the bf16 dS of the causal triangle, B*H*S^2/2 * 2 bytes at S = 16384
-    dk = next(v for k, v in data["kernels"].items() if k.startswith("dkdv_bf16_kernel<"))
+    dk = next(v for k, v in data["kernels"].items() if k.startswith(("dkdv_pair_kernel<", "dkdv_bf16_kernel<")))
     assert dk["write_bytes"] > 16 * 16384 * 16384 // 2 * 2 * 0.95
