@@ -650,9 +650,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   constexpr int RING = NSTG * STAGE + XB_BYTES;
   constexpr int EPI = BNK * DQK * 4;
   constexpr int SMEM = RING > EPI ? RING : EPI;
-  // DMA instructions per wave per tile: q~, dO and one for the 64 floats of L2 / Di
-  constexpr int PER = BMQ * NCQ / (64 * NW) + BMQ * NCO / (64 * NW) + 1;
-  static_assert(BMQ * NCQ % (64 * NW) == 0 && BMQ * NCO % (64 * NW) == 0, "whole wave instructions");
+  // the four role-A waves issue all tile loads (role B is the critical path): DMA instructions
+  // per A wave per tile for q~, dO and one for the 64 floats of L2 / Di
+  constexpr int NA = 4;
+  constexpr int PER = BMQ * NCQ / (64 * NA) + BMQ * NCO / (64 * NA) + 1;
+  static_assert(BMQ * NCQ % (64 * NA) == 0 && BMQ * NCO % (64 * NA) == 0, "whole wave instructions");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
   char* xbuf = smem + NSTG * STAGE;
 
@@ -676,8 +678,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const int64_t qrs = (int64_t)DQK * 2;
 
   // tiles are issued in loop order: query tile qt of query head h advances qt, then h
-  const DmaPlan<BMQ, NCQ, NW> plan_q(w, lane, (uint32_t)qrs);
-  const DmaPlan<BMQ, NCO, NW> plan_o(w, lane, (uint32_t)(a.do_ss * 2));
+  const DmaPlan<BMQ, NCQ, NA> plan_q(pw, lane, (uint32_t)qrs);
+  const DmaPlan<BMQ, NCO, NA> plan_o(pw, lane, (uint32_t)(a.do_ss * 2));
   const uint32_t smem_l = lds_addr(smem);
   int iss_h = hk * grp, iss_qt = qb0;
   auto issue = [&](int it) {
@@ -687,13 +689,13 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     const char* qsrc = (const char*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + q0) * qrs;
     const char* osrc = (const char*)a.dO + (b * a.do_sb + h * a.do_sh + (int64_t)q0 * a.do_ss) * 2;
     if (a.Sq - q0 >= BMQ) {
-      plan_q.full(qsrc, stl, w);
-      plan_o.full(osrc, stl + SQ_BYTES, w);
+      plan_q.full(qsrc, stl, pw);
+      plan_o.full(osrc, stl + SQ_BYTES, pw);
     } else {
-      dma_tile<BMQ, NCQ, NW>(st, qsrc, qrs, a.Sq - q0, w, lane);
-      dma_tile<BMQ, NCO, NW>(st + SQ_BYTES, osrc, a.do_ss * 2, a.Sq - q0, w, lane);
+      dma_tile<BMQ, NCQ, NA>(st, qsrc, qrs, a.Sq - q0, pw, lane);
+      dma_tile<BMQ, NCO, NA>(st + SQ_BYTES, osrc, a.do_ss * 2, a.Sq - q0, pw, lane);
     }
-    // every wave issues the same 16-lane load of the tile's L2 (lanes 0-7) and Di (lanes 8-15)
+    // every A wave issues the same 16-lane load of the tile's L2 (lanes 0-7) and Di (lanes 8-15)
     const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
     if (lane < 16) dma16((lane < 8 ? a.L2 : a.Di) + p0 + (lane & 7) * 4, stl + SQ_BYTES + SO_BYTES);
     if (++iss_qt == nqt) {
@@ -764,31 +766,14 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // vmcnt allowed while the next tile's loads must have landed (see the loop): younger loads of
-  // the tile after it and, for B, its dS stores
-  auto wait_next = [&](int allowed) {
-    static_assert(PER + 4 <= 11, "wait table");
-    switch (allowed) {
-      case 0: wait_vmcnt<0>(); break;
-      case 1: wait_vmcnt<1>(); break;
-      case 2: wait_vmcnt<2>(); break;
-      case 3: wait_vmcnt<3>(); break;
-      case 4: wait_vmcnt<4>(); break;
-      case 5: wait_vmcnt<5>(); break;
-      case 6: wait_vmcnt<6>(); break;
-      case 7: wait_vmcnt<7>(); break;
-      case 8: wait_vmcnt<8>(); break;
-      case 9: wait_vmcnt<9>(); break;
-      case 10: wait_vmcnt<10>(); break;
-      default: wait_vmcnt<11>(); break;
-    }
-  };
 
   const int kr = myk < a.Sk ? myk : a.Sk - 1;
-  if (niter > 0) issue(0);
-  if (niter > 1) issue(1);
-  if (niter > 1) wait_vmcnt<PER>();
-  else wait_vmcnt<0>();
+  if (!roleB) {
+    if (niter > 0) issue(0);
+    if (niter > 1) issue(1);
+    if (niter > 1) wait_vmcnt<PER>();
+    else wait_vmcnt<0>();
+  }
   __syncthreads();
   float* st_epi = (float*)smem;  // [BNK keys][DQK] fp32 dk~ for the fused inverse transform
   // The two roles run separate loops with the same number of barriers (one per step), so each
@@ -835,7 +820,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           pa[G >> 1][(G & 1) * 2 + 1] = pack_bf2(p[2], p[3]);
         }
       }
-      if (t + 1 < niter) wait_next(t + 2 < niter ? PER : 0);  // tile t + 1 has landed
+      if (t + 1 < niter) {  // tile t + 1 has landed: only tile t + 2's loads may be outstanding
+        if (t + 2 < niter) wait_vmcnt<PER>();
+        else wait_vmcnt<0>();
+      }
       __syncthreads();
     }
 #pragma unroll
@@ -860,8 +848,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       for (int j = 0; j < 16; ++j) dk[t][j] = 0.f;
     f32x16 dp;
     int prev_h = hk * grp, prev_qt = qb0;  // head and query tile of step t - 1
+    // role B is the critical path of every step: its instructions go first when both waves of a
+    // SIMD are ready to issue
+    __builtin_amdgcn_s_setprio(2);
     for (int t = 0; t <= niter; ++t) {
-      if (t + 2 < niter) issue(t + 2);
       if (t >= 1) {  // dS of tile t - 1 from A's fp32 P; store it; dK~ += dS^T q~
         const char* st = smem + ((t - 1) % NSTG) * STAGE;
         const float* sD = (const float*)(st + SQ_BYTES + SO_BYTES) + BMQ;
@@ -890,14 +880,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
         products(dk, dsf, st + crq, cq);
       }
       if (t < niter) scores_dp(smem + (t % NSTG) * STAGE + SQ_BYTES + rro, vf, dp);
-      if (t + 1 < niter) {
-        // tile t + 1 has landed: allowed outstanding = the loads of tile t + 2 (issued this step)
-        // and the dS stores issued after tile t + 1's loads (last step's and this step's)
-        int allowed = t + 2 < niter ? PER : 0;
-        if (t >= 1) allowed += t >= 2 ? 4 : 2;
-        wait_next(allowed);
-      }
-      __syncthreads();
+      __syncthreads();  // role A waited for tile t + 1's loads before this barrier
     }
     if (a.fuse_inv) {
 #pragma unroll
