@@ -689,8 +689,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     const char* qsrc = (const char*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + q0) * qrs;
     const char* osrc = (const char*)a.dO + (b * a.do_sb + h * a.do_sh + (int64_t)q0 * a.do_ss) * 2;
     if (a.Sq - q0 >= BMQ) {
-      plan_q.full(qsrc, stl, pw);
-      plan_o.full(osrc, stl + SQ_BYTES, pw);
+      plan_q.full(qsrc, stl, pw, (uint32_t)qrs);
+      plan_o.full(osrc, stl + SQ_BYTES, pw, (uint32_t)(a.do_ss * 2));
     } else {
       dma_tile<BMQ, NCQ, NA>(st, qsrc, qrs, a.Sq - q0, pw, lane);
       dma_tile<BMQ, NCO, NA>(st + SQ_BYTES, osrc, a.do_ss * 2, a.Sq - q0, pw, lane);
@@ -1053,7 +1053,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
     char* st = smem + (kb % NSTAGE) * STAGE;
     const uint32_t stl = smem_l + (uint32_t)((kb % NSTAGE) * STAGE);
     const char* ksrc = kbase + (int64_t)kb * BK * krs;
-    if (a.Sk - kb * BK >= BK) plan_k.full(ksrc, stl, w);
+    if (a.Sk - kb * BK >= BK) plan_k.full(ksrc, stl, w, (uint32_t)krs);
     else dma_tile<BK, NCK, NW>(st, ksrc, krs, a.Sk - kb * BK, w, lane);
     const char* dsrc = sbase + (int64_t)((kb * BK) >> 5) * a.ds_nqt * 4096;
 #pragma unroll

@@ -419,27 +419,38 @@ __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t ro
   }
 }
 
-// dma_tile with the per-lane source offsets of a whole tile computed once: a wave's TPW
-// instructions per tile each take one precomputed 32-bit offset and a wave-uniform row base, so a
-// full tile costs no vector instructions beyond the loads.  Tiles with rows past the end of the
-// source take dma_tile's clamping path instead.
+// dma_tile with the per-lane source offsets of a whole tile computed once: each of a wave's TPW
+// instructions per tile takes a wave-uniform row base (tile source + its first row times the row
+// stride, in SGPRs) and a 32-bit per-lane offset, so a full tile costs no vector instructions
+// beyond the loads.  The per-lane part (row within the instruction, swizzled chunk) depends on the
+// instruction's first row only through the swizzle, i.e. through that row mod 16, so a wave keeps
+// one offset per residue class: P = 16 / gcd(16, NW * rows per instruction) of them, at most TPW.
+// Tiles with rows past the end of the source take dma_tile's clamping path instead.
 template <int ROWS, int NCH, int NW> struct DmaPlan {
   static constexpr int TPW = ROWS * NCH / (64 * NW);
+  static constexpr int RPI = 64 / NCH;
+  static constexpr int STEP = (NW * RPI) % 16;  // first-row advance per instruction, mod 16
+  static constexpr int P0 = STEP == 0 ? 1 : (STEP % 8 == 0 ? 2 : (STEP % 4 == 0 ? 4 : (STEP % 2 == 0 ? 8 : 16)));
+  static constexpr int P = P0 < TPW ? P0 : TPW;
   static_assert(ROWS * NCH % (64 * NW) == 0 && NCH <= 64, "whole wave instructions");
-  uint32_t off[TPW];
+  uint32_t off[P];
   __device__ __forceinline__ DmaPlan(int w, int lane, uint32_t rs) {
     const int x = lane / NCH;
     const uint32_t U = (uint32_t)(((lane % NCH) ^ swz<NCH>(x)) << 4);
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int r0 = ((i * NW + w) * 64) / NCH;
-      off[i] = (uint32_t)(r0 + x) * rs + (U ^ (uint32_t)(swz<NCH>(r0) << 4));
+    for (int c = 0; c < P; ++c) {
+      const int r0 = (c * NW + w) * RPI;
+      off[c] = (uint32_t)x * rs + (U ^ (uint32_t)(swz<NCH>(r0) << 4));
     }
   }
   // all ROWS rows of the tile starting at `src` (wave-uniform) are inside the source
-  __device__ __forceinline__ void full(const char* src, uint32_t lds_tile, int w) const {
+  __device__ __forceinline__ void full(const char* src, uint32_t lds_tile, int w, uint32_t rs) const {
+    const int wu = __builtin_amdgcn_readfirstlane(w);
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) dma16s(off[i], src, lds_tile + (uint32_t)((i * NW + w) * 64 * 16));
+    for (int i = 0; i < TPW; ++i) {
+      const uint32_t r0 = (uint32_t)((i * NW + wu) * RPI);
+      dma16s(off[i % P], src + (uint64_t)r0 * rs, lds_tile + (uint32_t)((i * NW + wu) * 64 * 16));
+    }
   }
 };
 

@@ -171,7 +171,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) 
 // waves share each SIMD (<= 256 registers per wave), so one wave's softmax overlaps the other's
 // MFMAs.  The running max is raised lazily: O and l are rescaled only when some query's block
 // max exceeds the current one by more than TAU (in log2 units), which bounds p by 2^TAU.
-template <int DQK, int DV, int BN, int NW>
+template <int DQK, int DV, int BN, int NW, int NDW, int NSTG>
 __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_vec) {
   using M = MT<0>;
   constexpr int BM = NW * 32;
@@ -179,7 +179,9 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
   constexpr int NQF = DQK / 16, NKT = BN / 32, NPF = BN / 16, NOT = DV / 32;
   constexpr int SK_BYTES = BN * NCK * 16, SV_BYTES = BN * NCV * 16, STAGE = SK_BYTES + SV_BYTES;
   constexpr int SO_STRIDE = DV * 2 + 16;
-  constexpr int SMEM = (2 * STAGE) > (BM * SO_STRIDE) ? (2 * STAGE) : (BM * SO_STRIDE);
+  constexpr int SMEM = (NSTG * STAGE) > (BM * SO_STRIDE) ? (NSTG * STAGE) : (BM * SO_STRIDE);
+  static_assert(NSTG == 2 || NSTG == 3, "ring depth");
+  static_assert(NDW >= 1 && NDW <= NW, "DMA waves");
   constexpr float TAU = 8.f;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
@@ -215,33 +217,42 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
   float m = -1e30f, l = 0.f;
   const float sl2 = a.scale * LOG2E;
 
-  // per-lane offsets of the k~ / v tile loads, computed once (full tiles need no vector math)
-  const DmaPlan<BN, NCK, NW> plan_k(w, lane, (uint32_t)krs);
-  const DmaPlan<BN, NCV, NW> plan_v(w, lane, (uint32_t)vrs);
+  // The last NDW waves issue every tile load (per-lane offsets computed once; full tiles need no
+  // vector math), NSTG - 1 tiles ahead.  Waves that issue none go straight to their products after
+  // the barrier, so the two waves of a SIMD start each tile out of step.
+  const bool dmaw = __builtin_amdgcn_readfirstlane(w) >= NW - NDW;
+  const int dw = dmaw ? w - (NW - NDW) : 0;
+  const DmaPlan<BN, NCK, NDW> plan_k(dw, lane, (uint32_t)krs);
+  const DmaPlan<BN, NCV, NDW> plan_v(dw, lane, (uint32_t)vrs);
+  constexpr int PER = DmaPlan<BN, NCK, NDW>::TPW + DmaPlan<BN, NCV, NDW>::TPW;
   const uint32_t smem_l = lds_addr(smem);
-  if (nkb > 0) {
-    dma_tile<BN, NCK, NW>(smem, kbase, krs, a.Sk, w, lane);
-    dma_tile<BN, NCV, NW>(smem + SK_BYTES, vbase, vrs, a.Sk, w, lane);
-  }
+  auto issue = [&](int kb) {
+    if (!dmaw) return;
+    const int k0 = kb * BN;
+    char* nK = smem + (kb % NSTG) * STAGE;
+    const char* ksrc = kbase + (int64_t)k0 * krs;
+    const char* vsrc = vbase + (int64_t)k0 * vrs;
+    if (a.Sk - k0 >= BN) {
+      const uint32_t nl = smem_l + (uint32_t)((kb % NSTG) * STAGE);
+      plan_k.full(ksrc, nl, dw, (uint32_t)krs);
+      plan_v.full(vsrc, nl + SK_BYTES, dw, (uint32_t)vrs);
+    } else {
+      dma_tile<BN, NCK, NDW>(nK, ksrc, krs, a.Sk - k0, dw, lane);
+      dma_tile<BN, NCV, NDW>(nK + SK_BYTES, vsrc, vrs, a.Sk - k0, dw, lane);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < NSTG - 1; ++i)
+    if (i < nkb) issue(i);
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * BN;
-    char* sK = smem + (kb & 1) * STAGE;
+    char* sK = smem + (kb % NSTG) * STAGE;
     char* sV = sK + SK_BYTES;
-    dma_wait();
+    // tile kb has landed once at most the loads of the tiles issued after it are outstanding
+    if (NSTG == 3 && kb + 1 < nkb) wait_vmcnt<PER>();
+    else dma_wait();
     __syncthreads();
-    if (kb + 1 < nkb) {
-      char* nK = smem + ((kb + 1) & 1) * STAGE;
-      const char* ksrc = kbase + (int64_t)(k0 + BN) * krs;
-      const char* vsrc = vbase + (int64_t)(k0 + BN) * vrs;
-      if (a.Sk - k0 - BN >= BN) {
-        const uint32_t nl = smem_l + (uint32_t)(((kb + 1) & 1) * STAGE);
-        plan_k.full(ksrc, nl, w);
-        plan_v.full(vsrc, nl + SK_BYTES, w);
-      } else {
-        dma_tile<BN, NCK, NW>(nK, ksrc, krs, a.Sk - k0 - BN, w, lane);
-        dma_tile<BN, NCV, NW>(nK + SK_BYTES, vsrc, vrs, a.Sk - k0 - BN, w, lane);
-      }
-    }
+    if (kb + NSTG - 1 < nkb) issue(kb + NSTG - 1);  // its slot held tile kb - 1
     if (a.causal && k0 > qw + 31 + off) continue;  // whole tile above this wave's diagonal
 
     f32x16 s[NKT];
@@ -253,7 +264,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
       // S = k~ q~^T: NKT*NQF products, each with its own k~ row fragment, through a fenced ring
       // of depth FD (reads FD products ahead; left to itself the scheduler waits on every read
       // right before its product); consecutive products alternate accumulators
-      constexpr int NF = NKT * NQF, FD = 4;
+      constexpr int NF = NKT * NQF, FD = 3;
       u32x4 kq[FD];
 #pragma unroll
       for (int i = 0; i < FD; ++i) kq[i] = rk.read(sK, (i % NKT) * 32, i / NKT);
@@ -360,12 +371,19 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
 template <int DQK, int DV>
 static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 8, BN = 64;
+#ifndef FWD_NDW
+#define FWD_NDW 4
+#endif
+#ifndef FWD_NSTG
+#define FWD_NSTG 2
+#endif
+  constexpr int NDW = (DQK == 256 && DV == 128) ? FWD_NDW : 8, NSTG = (DQK == 256 && DV == 128) ? FWD_NSTG : 2;
   const int BM = NW * 32;
   const int nqb = (a.Sq + BM - 1) / BM;
   const int grid = nqb * a.B * a.Hq;
   const int o_vec = (a.dv_real == DV) && ((uintptr_t)a.o % 16 == 0) && ((a.o_ss * 2) % 16 == 0) &&
                     ((a.o_sh * 2) % 16 == 0) && ((a.o_sb * 2) % 16 == 0);
-  hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, BN, NW>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
+  hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, BN, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
