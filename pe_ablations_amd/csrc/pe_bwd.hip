@@ -635,8 +635,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
 // the same SIMD, so each SIMD interleaves two instruction streams of 24 products per 32-query tile
 // and neither wave's exponentials, loads or waits leave the matrix core idle.  B keeps the fp32 P
 // it needs from an LDS exchange buffer, so dS is formed from unrounded P exactly as in the
-// one-wave kernel.  Each loop step t runs A's dV of tile t-1 and S / P of tile t, and B's dS /
-// dK~ of tile t-1 and dP of tile t, then one barrier; the 32-query tiles stream through a ring of
+// one-wave kernel.  Each loop step t runs A's S / P of tile t, the loads of tile t+2 and dV of
+// tile t-1 (so A starts the step on products while B forms dS), and B's dS / dK~ of tile t-1 and
+// dP of tile t, then one barrier; the 32-query tiles stream through a ring of
 // 4 LDS stages (q~ 32 x DQK, dO 32 x DV, the rows' log2 lse and Di) loaded two steps ahead.
 template <int DQK, int DV>
 __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
@@ -791,13 +792,14 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     for (int t = 0; t < NDV; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) dv[t][j] = 0.f;
-    u32x4 pa[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};  // bf16 P of the pending tile
+    u32x4 pa0[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};  // bf16 P, alternating tiles
+    u32x4 pa1[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
     f32x16 s;
     int cur_qt = qb0;  // query tile of step t
-    for (int t = 0; t <= niter; ++t) {
-      if (t + 2 < niter) issue(t + 2);  // its stage held tile t - 2, released by the last barrier
-      if (t >= 1) products(dv, pa, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);  // dV of tile t - 1
-      if (t < niter) {  // S and P of tile t: fp32 P to the exchange buffer, bf16 P kept for dV
+    // step t: S and P of tile t (products right after the barrier), the loads of tile t + 2, then
+    // dV of tile t - 1 from the other P buffer
+    auto astep = [&](int t, u32x4 (&pn)[2], u32x4 (&pp)[2]) {
+      if (t < niter) {
         const char* st = smem + (t % NSTG) * STAGE;
         scores_s(st + rrq, kf, s);
         const int q0 = cur_qt * BMQ;
@@ -816,15 +818,21 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[4 * G + e] * sl2 - lv[e]);
           *(f32x4*)(xb + (G * 64 + lane) * 4) = p;
-          pa[G >> 1][(G & 1) * 2] = pack_bf2(p[0], p[1]);
-          pa[G >> 1][(G & 1) * 2 + 1] = pack_bf2(p[2], p[3]);
+          pn[G >> 1][(G & 1) * 2] = pack_bf2(p[0], p[1]);
+          pn[G >> 1][(G & 1) * 2 + 1] = pack_bf2(p[2], p[3]);
         }
       }
+      if (t + 2 < niter) issue(t + 2);  // its stage held tile t - 2, released by the last barrier
+      if (t >= 1) products(dv, pp, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);
       if (t + 1 < niter) {  // tile t + 1 has landed: only tile t + 2's loads may be outstanding
         if (t + 2 < niter) wait_vmcnt<PER>();
         else wait_vmcnt<0>();
       }
       __syncthreads();
+    };
+    for (int t = 0; t <= niter; t += 2) {
+      astep(t, pa0, pa1);
+      if (t + 1 <= niter) astep(t + 1, pa1, pa0);
     }
 #pragma unroll
     for (int t = 0; t < NDV; ++t)
