@@ -987,6 +987,7 @@ template <int DQK, int NW, int BK, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   using M = MT<0>;
   static_assert(NW == 8, "4 query pairs x 2 column halves");
+  constexpr int NQG = NW / 2, QT = 8 / NQG;  // query groups; 32-query tiles per wave
   static_assert(NSTAGE >= 2 && NSTAGE <= 4, "ring depth");
   constexpr int BQ = 256;
   constexpr int NCK = DQK / 8, NCS = BQ / 8;
@@ -1016,20 +1017,22 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   map_block(blockIdx.x, nqb, a.B * a.Hq, a.causal != 0, qb, bh);
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
   const int q0 = qb * BQ;
-  const int qp = w & 3, dh = w >> 2;
-  const int qw = q0 + qp * 64;  // this wave's 64 queries: tiles qw .. qw+31 and qw+32 .. qw+63
+  const int qp = w % NQG, dh = w / NQG;
+  const int qw = q0 + qp * QT * 32;  // this wave's QT*32 queries: tiles qw + 32 i
   const int off = a.causal_off;
 
-  f32x16 acc[2][NTH];
+  f32x16 acc[QT][NTH];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < QT; ++i)
 #pragma unroll
     for (int t = 0; t < NTH; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[i][t][j] = 0.f;
 
   // per-lane fragment bases: the wave's two dS query tiles and its NTH k~ column tiles
-  const ColBase<NCS> cA[2] = {ColBase<NCS>(lane, qp * 64), ColBase<NCS>(lane, qp * 64 + 32)};
+  ColBase<NCS> cA[QT];
+#pragma unroll
+  for (int i = 0; i < QT; ++i) cA[i] = ColBase<NCS>(lane, qp * QT * 32 + i * 32);
   ColBase<NCK> cB[NTH];
 #pragma unroll
   for (int t = 0; t < NTH; ++t) cB[t] = ColBase<NCK>(lane, ctile(t, dh) * 32);
@@ -1070,7 +1073,12 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
 #pragma unroll
   for (int i = 0; i < NSTAGE - 1; ++i)
     if (i < nkb) issue(i);
-  for (int kb = 0; kb < nkb; ++kb) {
+  // One BK-key step.  Steps in which no key passes a query's causal limit or Sk (every step but the
+  // last few of a causal block) run without masking; the rest (EDGE) mask every A fragment and,
+  // for a wave whose queries all end before the step, multiply zeros.  Both loop bodies are
+  // straight-line code, so the accumulators stay in place across iterations.
+  auto step = [&](int kb, auto edge_tag) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
     const int k0 = kb * BK;
     const char* sK = smem + (kb % NSTAGE) * STAGE;
     const char* sS = sK + SK_BYTES;
@@ -1081,16 +1089,13 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
     else wait_vmcnt<0>();
     __syncthreads();  // tile kb visible; every wave is done with slot (kb - 1) % NSTAGE
     if (kb + NSTAGE - 1 < nkb) issue(kb + NSTAGE - 1);
-    if (a.causal && k0 > qw + 63 + off) continue;  // every key after both of this wave's tiles
-    // masking needed when some key of the step is past the causal limit of a query or past Sk
-    const bool edge = (a.causal && k0 + BK - 1 > qw + off) || (k0 + BK > a.Sk);
     // Fenced double buffer over the 16-key slices: region ks issues every read of slice ks + 1 and
     // then the products of slice ks, whose fragments were read one region earlier (left to itself
     // the scheduler waits on each read right before its product).
-    u32x4 fa[2][2], fb[2][NTH];
-    auto read_slice = [&](int ks, u32x4 (&ra)[2], u32x4 (&rb)[NTH]) {
+    u32x4 fa[2][QT], fb[2][NTH];
+    auto read_slice = [&](int ks, u32x4 (&ra)[QT], u32x4 (&rb)[NTH]) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) ra[i] = cA[i].read(sS, ks * 16);
+      for (int i = 0; i < QT; ++i) ra[i] = cA[i].read(sS, ks * 16);
 #pragma unroll
       for (int t = 0; t < NTH; ++t) rb[t] = cB[t].read(sK, ks * 16);
     };
@@ -1100,10 +1105,12 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       if (ks + 1 < BK / 16) read_slice(ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);  // the reads go out before this slice's products
-      u32x4 af[2] = {fa[ks & 1][0], fa[ks & 1][1]};
-      if (edge) {
+      u32x4 af[QT];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < QT; ++i) af[i] = fa[ks & 1][i];
+      if constexpr (EDGE) {
+#pragma unroll
+        for (int i = 0; i < QT; ++i) {
           // element e of lane (l32, g) is key k0 + ks*16 + g*8 + e of query qw + i*32 + l32
           const int kmax = a.causal ? min(qw + i * 32 + l32 + off, a.Sk - 1) : a.Sk - 1;
           const int lim = kmax - (k0 + ks * 16 + g * 8);
@@ -1114,10 +1121,16 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
 #pragma unroll
       for (int t = 0; t < NTH; ++t)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][t] = M::mma(af[i], fb[ks & 1][t], acc[i][t]);
+        for (int i = 0; i < QT; ++i) acc[i][t] = M::mma(af[i], fb[ks & 1][t], acc[i][t]);
     }
     __builtin_amdgcn_sched_barrier(0);
-  }
+  };
+  // steps whose keys all lie at or below the causal limit of the block's first query and below Sk
+  const int kfull = a.causal ? min(a.Sk, q0 + off + 1) : a.Sk;
+  const int nfull = min(nkb, max(kfull, 0) / BK);
+  int kb = 0;
+  for (; kb < nfull; ++kb) step(kb, std::false_type{});
+  for (; kb < nkb; ++kb) step(kb, std::true_type{});
 
   if constexpr (NTH % 2 == 0) {
     if (a.fuse_inv) {
@@ -1141,14 +1154,14 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
       };
       auto stage = [&](int half) {
         __syncthreads();
-        if ((qp >> 1) == half) {
+        if (((qp * QT * 32) >> 7) == half) {  // waves whose query rows lie in this half
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < QT; ++i)
 #pragma unroll
             for (int t = 0; t < NTH; ++t)
 #pragma unroll
               for (int j = 0; j < 16; ++j)
-                st[((qp & 1) * 64 + i * 32 + c_row(j, g)) * DQK + ctile(t, dh) * 32 + l32] = acc[i][t][j] * a.scale;
+                st[(((qp * QT * 32) & 127) + i * 32 + c_row(j, g)) * DQK + ctile(t, dh) * 32 + l32] = acc[i][t][j] * a.scale;
         }
         __syncthreads();
       };
@@ -1197,7 +1210,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   }
   float* dqb = a.dq_t + (int64_t)(b * a.Hq + h) * a.Sq * DQK;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < QT; ++i)
 #pragma unroll
     for (int t = 0; t < NTH; ++t)
 #pragma unroll
@@ -1221,8 +1234,14 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       }
     } else {
       const int nqb = (a.Sq + 255) / 256;
+#ifndef DQ_BK
+#define DQ_BK 64
+#endif
+#ifndef DQ_NSTG
+#define DQ_NSTG 2
+#endif
       // 64-key steps, double-buffered: measured faster than 32-key steps at any ring depth
-      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8, 64, 2>), dim3(nqb * a.B * a.Hq), dim3(512), 0, s, a);
+      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8, (DQK == 256 ? DQ_BK : 64), (DQK == 256 ? DQ_NSTG : 2)>), dim3(nqb * a.B * a.Hq), dim3(512), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {
