@@ -986,7 +986,7 @@ __device__ __forceinline__ uint32_t keep_bf2(uint32_t v, bool lo, bool hi) {
 template <int DQK, int NW, int BK, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   using M = MT<0>;
-  static_assert(NW == 8, "4 query pairs x 2 column halves");
+  static_assert(NW == 8 || NW == 4, "NW/2 query groups x 2 column halves");
   constexpr int NQG = NW / 2, QT = 8 / NQG;  // query groups; 32-query tiles per wave
   static_assert(NSTAGE >= 2 && NSTAGE <= 4, "ring depth");
   constexpr int BQ = 256;
@@ -1241,7 +1241,11 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
 #define DQ_NSTG 2
 #endif
       // 64-key steps, double-buffered: measured faster than 32-key steps at any ring depth
-      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8, (DQK == 256 ? DQ_BK : 64), (DQK == 256 ? DQ_NSTG : 2)>), dim3(nqb * a.B * a.Hq), dim3(512), 0, s, a);
+#ifndef DQ_NW
+#define DQ_NW 8
+#endif
+      constexpr int DNW = DQK == 256 ? DQ_NW : 8;
+      hipLaunchKernelGGL((dq_gemm_kernel<DQK, DNW, (DQK == 256 ? DQ_BK : 64), (DQK == 256 ? DQ_NSTG : 2)>), dim3(nqb * a.B * a.Hq), dim3(DNW * 64), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {

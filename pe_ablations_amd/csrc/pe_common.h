@@ -380,10 +380,17 @@ __device__ __forceinline__ uint64_t uniform64(const void* p) {
   return ((uint64_t)hi << 32) | (uint64_t)lo;
 }
 // dma16 with a wave-uniform base in SGPRs and a 32-bit per-lane byte offset (no per-lane 64-bit
-// address arithmetic)
+// address arithmetic).  When the compiler holds the base in VGPRs, uniform64 becomes
+// v_readfirstlane, a VALU write of SGPRs; a VMEM instruction that reads such SGPRs needs 5 wait
+// states after the write, and the compiler does not pad across inline asm (with fewer, the load
+// read a stale base half and faulted).  The asm therefore copies the base with one SALU move,
+// which has no such hazard towards the load, and which also provides the wait state an M0 write
+// needs before an LDS DMA.
 __device__ __forceinline__ void dma16s(uint32_t voff, const void* base, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(uniform64(base)), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+  uint64_t sb;
+  asm volatile("s_mov_b64 %0, %2\n\tglobal_load_lds_dwordx4 %1, %0"
+               : "=&s"(sb)
+               : "v"(voff), "s"(uniform64(base)), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 
 template <int ROWS, int NCH, int NW>
