@@ -1235,12 +1235,13 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
     } else {
       const int nqb = (a.Sq + 255) / 256;
 #ifndef DQ_BK
-#define DQ_BK 64
+#define DQ_BK 32
 #endif
 #ifndef DQ_NSTG
-#define DQ_NSTG 2
+#define DQ_NSTG 4
 #endif
-      // 64-key steps, double-buffered: measured faster than 32-key steps at any ring depth
+      // wide operands: 32-key steps in a 4-deep ring (three steps of loads in flight) measured
+      // 4 % faster than 64-key steps double-buffered or a 3-deep ring of 32-key steps
 #ifndef DQ_NW
 #define DQ_NW 8
 #endif
