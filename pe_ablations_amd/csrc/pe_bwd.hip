@@ -679,8 +679,12 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const int64_t qrs = (int64_t)DQK * 2;
 
   // tiles are issued in loop order: query tile qt of query head h advances qt, then h
-  const DmaPlan<BMQ, NCQ, NA> plan_q(pw, lane, (uint32_t)qrs);
-  const DmaPlan<BMQ, NCO, NA> plan_o(pw, lane, (uint32_t)(a.do_ss * 2));
+#ifndef DKDV_SWZ
+#define DKDV_SWZ 1
+#endif
+  constexpr int SZ = DKDV_SWZ;  // swizzle kind of the q~ and dO tiles
+  const DmaPlan<BMQ, NCQ, NA, SZ> plan_q(pw, lane, (uint32_t)qrs);
+  const DmaPlan<BMQ, NCO, NA, SZ> plan_o(pw, lane, (uint32_t)(a.do_ss * 2));
   const uint32_t smem_l = lds_addr(smem);
   int iss_h = hk * grp, iss_qt = qb0;
   auto issue = [&](int it) {
@@ -693,8 +697,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       plan_q.full(qsrc, stl, pw, (uint32_t)qrs);
       plan_o.full(osrc, stl + SQ_BYTES, pw, (uint32_t)(a.do_ss * 2));
     } else {
-      dma_tile<BMQ, NCQ, NA>(st, qsrc, qrs, a.Sq - q0, pw, lane);
-      dma_tile<BMQ, NCO, NA>(st + SQ_BYTES, osrc, a.do_ss * 2, a.Sq - q0, pw, lane);
+      dma_tile<BMQ, NCQ, NA, SZ>(st, qsrc, qrs, a.Sq - q0, pw, lane);
+      dma_tile<BMQ, NCO, NA, SZ>(st + SQ_BYTES, osrc, a.do_ss * 2, a.Sq - q0, pw, lane);
     }
     // every A wave issues the same 16-lane load of the tile's L2 (lanes 0-7) and Di (lanes 8-15)
     const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
@@ -706,10 +710,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   };
 
   constexpr int FD = 3;
-  const RowX<NCQ> rq(perm_row<0>(l32), g);
-  const RowX<NCO> ro(perm_row<0>(l32), g);
-  const ColX<NCQ> cq(lane);
-  const ColX<NCO> co(lane);
+  const RowX<NCQ, SZ> rq(perm_row<0>(l32), g);
+  const RowX<NCO, SZ> ro(perm_row<0>(l32), g);
+  const ColX<NCQ, SZ> cq(lane);
+  const ColX<NCO, SZ> co(lane);
   const uint32_t rrq = (uint32_t)perm_row<0>(l32) * NCQ * 16, rro = (uint32_t)perm_row<0>(l32) * NCO * 16;
   const uint32_t crq = ColX<NCQ>::row_term(lane), cro = ColX<NCO>::row_term(lane);
 
@@ -987,6 +991,10 @@ template <int DQK, int NW, int BK, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   using M = MT<0>;
   static_assert(NW == 8 || NW == 4, "NW/2 query groups x 2 column halves");
+#ifndef DQ_SWZ
+#define DQ_SWZ 1
+#endif
+  constexpr int SZ = DQ_SWZ;  // tile swizzle kind (both tiles are only read with the transpose load)
   constexpr int NQG = NW / 2, QT = 8 / NQG;  // query groups; 32-query tiles per wave
   static_assert(NSTAGE >= 2 && NSTAGE <= 4, "ring depth");
   constexpr int BQ = 256;
@@ -1030,12 +1038,12 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
       for (int j = 0; j < 16; ++j) acc[i][t][j] = 0.f;
 
   // per-lane fragment bases: the wave's two dS query tiles and its NTH k~ column tiles
-  ColBase<NCS> cA[QT];
+  ColBase<NCS, SZ> cA[QT];
 #pragma unroll
-  for (int i = 0; i < QT; ++i) cA[i] = ColBase<NCS>(lane, qp * QT * 32 + i * 32);
-  ColBase<NCK> cB[NTH];
+  for (int i = 0; i < QT; ++i) cA[i] = ColBase<NCS, SZ>(lane, qp * QT * 32 + i * 32);
+  ColBase<NCK, SZ> cB[NTH];
 #pragma unroll
-  for (int t = 0; t < NTH; ++t) cB[t] = ColBase<NCK>(lane, ctile(t, dh) * 32);
+  for (int t = 0; t < NTH; ++t) cB[t] = ColBase<NCK, SZ>(lane, ctile(t, dh) * 32);
   int kend = a.Sk;
   if (a.causal) kend = min(a.Sk, q0 + BQ + off);
   const int nkb = kend > 0 ? (kend + BK - 1) / BK : 0;
@@ -1053,19 +1061,19 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   for (int i = 0; i < NDS; ++i) {
     const int slot = (i * NW + w) * 64 + lane;
     const int kl = slot / NCS, pc = slot % NCS;
-    const int lc = pc ^ swz<NCS>(kl);
+    const int lc = pc ^ swz<NCS, SZ>(kl);
     const int qc = (q0 >> 3) + lc, r = qc & 7;
     ds_off[i] = ((uint32_t)(kl >> 5) * a.ds_nqt + (qc >> 3)) * 4096u +
                 (uint32_t)(((r >> 1) * 64 + (r & 1) * 32 + (kl & 31)) * 16);
   }
-  const DmaPlan<BK, NCK, NW> plan_k(w, lane, (uint32_t)krs);
+  const DmaPlan<BK, NCK, NW, SZ> plan_k(w, lane, (uint32_t)krs);
   const uint32_t smem_l = lds_addr(smem);
   auto issue = [&](int kb) {
     char* st = smem + (kb % NSTAGE) * STAGE;
     const uint32_t stl = smem_l + (uint32_t)((kb % NSTAGE) * STAGE);
     const char* ksrc = kbase + (int64_t)kb * BK * krs;
     if (a.Sk - kb * BK >= BK) plan_k.full(ksrc, stl, w, (uint32_t)krs);
-    else dma_tile<BK, NCK, NW>(st, ksrc, krs, a.Sk - kb * BK, w, lane);
+    else dma_tile<BK, NCK, NW, SZ>(st, ksrc, krs, a.Sk - kb * BK, w, lane);
     const char* dsrc = sbase + (int64_t)((kb * BK) >> 5) * a.ds_nqt * 4096;
 #pragma unroll
     for (int i = 0; i < NDS; ++i) dma16s(ds_off[i], dsrc, stl + SK_BYTES + (uint32_t)((i * NW + w) * 64 * 16));

@@ -154,20 +154,25 @@ template <int DT> __device__ __forceinline__ int c_logical(int j, int g) {
 // c ^ swz(r).  gfx950's LDS has 64 4-byte banks (16 slots of 16 bytes).  Row fragments
 // (ds_read_b128) put 16 consecutive rows on one logical chunk, so swz must be a bijection of r mod
 // 16 (with the row parity when a row is only 8 slots); transpose reads (ds_read_b64_tr_b16) touch
-// chunks 4a .. 4a+3 of 4 consecutive rows.  With this permutation SQ_LDS_BANK_CONFLICT charges 2
-// of the 4 LDS cycles of every transpose read (its 32-lane halves share banks two ways), yet a
-// permutation without those conflicts measured no faster on transpose reads (4.8 clk per wave
-// instruction per CU either way), 6% slower on row fragments (7.05 vs 6.63 clk) and made the
-// one-wave-per-SIMD dK/dV kernel 25% slower, so this one is kept.
-template <int NCH> __device__ __forceinline__ int swz(int r) {
+// chunks 4a .. 4a+3 of 4 consecutive rows.  With the default permutation (SZ = 0) the 32-lane halves
+// of every transpose read share banks two ways (SQ_LDS_BANK_CONFLICT charges 2 of its 4 LDS cycles).
+// SZ = 1 selects r2 | r3<<1 | r0<<2 | r1<<3 for rows of 16 or more slots, under which both access
+// kinds are conflict-free.  An isolated read probe showed no gain from it (4.8 clk per transpose read
+// per CU either way, row fragments 6% slower), but in the kernels it measured faster on every tile
+// that takes transpose reads: the dQ GEMM's dS and k~ tiles (dQ 3.6% faster), the forward's v tile
+// and the dK/dV kernel's q~ and dO tiles (together 0.5-1% of a step).  Tiles read only by rows keep
+// SZ = 0.
+template <int NCH, int SZ = 0> __device__ __forceinline__ int swz(int r) {
   static_assert(NCH >= 8, "rows must span at least 8 slots");
-  if constexpr (NCH >= 16)
+  if constexpr (NCH >= 16 && SZ == 1)
+    return ((r >> 2) & 1) | (((r >> 3) & 1) << 1) | ((r & 1) << 2) | (((r >> 1) & 1) << 3);
+  else if constexpr (NCH >= 16)
     return ((r >> 2) & 1) | ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 3);
   else
     return ((r >> 2) & 1) | (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
 }
-template <int NCH> __device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
-  return (uint32_t)(row * (NCH * 16) + ((chunk ^ swz<NCH>(row)) << 4));
+template <int NCH, int SZ = 0> __device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
+  return (uint32_t)(row * (NCH * 16) + ((chunk ^ swz<NCH, SZ>(row)) << 4));
 }
 
 // One lane's 16-byte row fragment: chunk `chunk` of row `row`.
@@ -206,8 +211,8 @@ template <int DT, int NCH> __device__ __forceinline__ u32x4 lds_col_frag(const c
 // rows) and column offset n0 (a multiple of 32 columns) is a per-lane base chosen by (n0 / 32) % 4
 // plus the immediate k0 * row_bytes + (n0 / 128) * 256.  Hoisted, eight base registers stand in for
 // the per-fragment address registers the compiler otherwise keeps for every fragment read.
-template <int NCH> struct ColFrags {  // transpose reads, as lds_col_frag<0, NCH>
-  uint32_t b[4][2];                   // [(n0 / 32) % 4][rows +0 / +4]
+template <int NCH, int SZ = 0> struct ColFrags {  // transpose reads, as lds_col_frag<0, NCH>
+  uint32_t b[4][2];                               // [(n0 / 32) % 4][rows +0 / +4]
   __device__ __forceinline__ explicit ColFrags(int lane) {
     const int i = lane & 15, G4 = (lane >> 4) & 3;
     const int colq = ((G4 & 1) << 4) + ((i & 3) << 2);
@@ -217,7 +222,7 @@ template <int NCH> struct ColFrags {  // transpose reads, as lds_col_frag<0, NCH
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int col = (j * 32 + colq) % (NCH * 8);
-        b[j][hh] = tile_off<NCH>(row + 4 * hh, col >> 3) + ((col & 7) << 1);
+        b[j][hh] = tile_off<NCH, SZ>(row + 4 * hh, col >> 3) + ((col & 7) << 1);
       }
   }
   // k0 % 16 == 0, n0 % 32 == 0, both compile-time after unrolling
@@ -233,15 +238,15 @@ template <int NCH> struct ColFrags {  // transpose reads, as lds_col_frag<0, NCH
 // One 32-column group of transpose-read fragments at a runtime column offset n0 (any multiple of
 // 8): the per-lane base of rows 0 / 4 of the group; fragment rows k0 (a multiple of 16) are an
 // immediate.  Two registers per column group.
-template <int NCH> struct ColBase {
+template <int NCH, int SZ = 0> struct ColBase {
   uint32_t b0, b1;
   ColBase() = default;
   __device__ __forceinline__ ColBase(int lane, int n0) {
     const int i = lane & 15, G4 = (lane >> 4) & 3;
     const int col = n0 + ((G4 & 1) << 4) + ((i & 3) << 2);
     const int row = ((lane >> 5) << 3) + (i >> 2);
-    b0 = tile_off<NCH>(row, col >> 3) + ((col & 7) << 1);
-    b1 = tile_off<NCH>(row + 4, col >> 3) + ((col & 7) << 1);
+    b0 = tile_off<NCH, SZ>(row, col >> 3) + ((col & 7) << 1);
+    b1 = tile_off<NCH, SZ>(row + 4, col >> 3) + ((col & 7) << 1);
   }
   __device__ __forceinline__ u32x4 read(const char* tile, int k0) const {
     const uint32_t add = (uint32_t)(k0 * NCH * 16);
@@ -255,7 +260,7 @@ template <int NCH> struct ColBase {
 // (row_ptr), and the XOR parts, which are equal for 16- and 32-chunk rows, are shared between
 // tiles of both widths.  ColX: row term ((lane >> 5) * 8 + (lane & 15) / 4) * NCH * 16; RowX: rl *
 // NCH * 16.
-template <int NCH> struct ColX {
+template <int NCH, int SZ = 0> struct ColX {
   uint32_t b[4][2];
   __device__ __forceinline__ explicit ColX(int lane) {
     const int i = lane & 15, G4 = (lane >> 4) & 3;
@@ -265,7 +270,7 @@ template <int NCH> struct ColX {
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
-        b[j][hh] = (uint32_t)((((((j * 32 + colq) % (NCH * 8)) >> 3) ^ swz<NCH>(row + 4 * hh)) << 4) | ((colq & 7) << 1));
+        b[j][hh] = (uint32_t)((((((j * 32 + colq) % (NCH * 8)) >> 3) ^ swz<NCH, SZ>(row + 4 * hh)) << 4) | ((colq & 7) << 1));
   }
   __device__ __forceinline__ static uint32_t row_term(int lane) {
     return (uint32_t)((((lane >> 5) << 3) + ((lane & 15) >> 2)) * NCH * 16);
@@ -279,11 +284,11 @@ template <int NCH> struct ColX {
     return u32x4{ux[0], ux[1], uy[0], uy[1]};
   }
 };
-template <int NCH> struct RowX {
+template <int NCH, int SZ = 0> struct RowX {
   uint32_t b[8];
   __device__ __forceinline__ RowX(int rl, int g) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) b[j] = (uint32_t)((((2 * j + g) % NCH) ^ swz<NCH>(rl)) << 4);
+    for (int j = 0; j < 8; ++j) b[j] = (uint32_t)((((2 * j + g) % NCH) ^ swz<NCH, SZ>(rl)) << 4);
   }
   __device__ __forceinline__ u32x4 read(const char* row_ptr, int row0, int kk) const {
     return *(const u32x4*)(row_ptr + b[kk & 7] + (uint32_t)(row0 * NCH * 16 + (kk >> 3) * 256));
@@ -393,7 +398,7 @@ __device__ __forceinline__ void dma16s(uint32_t voff, const void* base, uint32_t
                : "v"(voff), "s"(uniform64(base)), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 
-template <int ROWS, int NCH, int NW>
+template <int ROWS, int NCH, int NW, int SZ = 0>
 __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t row_stride_bytes,
                                          int nvalid, int w, int lane) {
   constexpr int TOTAL = ROWS * NCH;
@@ -403,13 +408,13 @@ __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t ro
   const uint32_t rs = (uint32_t)row_stride_bytes;
   if (nvalid >= ROWS) {
     const int x = lane / NCH;
-    const uint32_t U = (uint32_t)(((lane % NCH) ^ swz<NCH>(x)) << 4);
+    const uint32_t U = (uint32_t)(((lane % NCH) ^ swz<NCH, SZ>(x)) << 4);
     const uint32_t X = (uint32_t)x * rs;
 #pragma unroll
     for (int i = 0; i < TOTAL / (64 * NW); ++i) {
       const int base = (i * NW + w) * 64;
       const int r0 = base / NCH;
-      const uint32_t S = (uint32_t)(swz<NCH>(r0) << 4);
+      const uint32_t S = (uint32_t)(swz<NCH, SZ>(r0) << 4);
       dma16(src + (uint32_t)r0 * rs + (X + (U ^ S)), lds_addr(tile) + base * 16);
     }
     (void)RPI;
@@ -419,7 +424,7 @@ __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t ro
       const int base = (i * NW + w) * 64;
       const int slot = base + lane;
       const int row = slot / NCH, pc = slot % NCH;
-      const int lc = pc ^ swz<NCH>(row);
+      const int lc = pc ^ swz<NCH, SZ>(row);
       const int r = row < nvalid ? row : nvalid - 1;
       dma16(src + (r * rs + (uint32_t)(lc * 16)), lds_addr(tile) + base * 16);
     }
@@ -433,7 +438,7 @@ __device__ __forceinline__ void dma_tile(char* tile, const char* src, int64_t ro
 // instruction's first row only through the swizzle, i.e. through that row mod 16, so a wave keeps
 // one offset per residue class: P = 16 / gcd(16, NW * rows per instruction) of them, at most TPW.
 // Tiles with rows past the end of the source take dma_tile's clamping path instead.
-template <int ROWS, int NCH, int NW> struct DmaPlan {
+template <int ROWS, int NCH, int NW, int SZ = 0> struct DmaPlan {
   static constexpr int TPW = ROWS * NCH / (64 * NW);
   static constexpr int RPI = 64 / NCH;
   static constexpr int STEP = (NW * RPI) % 16;  // first-row advance per instruction, mod 16
@@ -443,11 +448,11 @@ template <int ROWS, int NCH, int NW> struct DmaPlan {
   uint32_t off[P];
   __device__ __forceinline__ DmaPlan(int w, int lane, uint32_t rs) {
     const int x = lane / NCH;
-    const uint32_t U = (uint32_t)(((lane % NCH) ^ swz<NCH>(x)) << 4);
+    const uint32_t U = (uint32_t)(((lane % NCH) ^ swz<NCH, SZ>(x)) << 4);
 #pragma unroll
     for (int c = 0; c < P; ++c) {
       const int r0 = (c * NW + w) * RPI;
-      off[c] = (uint32_t)x * rs + (U ^ (uint32_t)(swz<NCH>(r0) << 4));
+      off[c] = (uint32_t)x * rs + (U ^ (uint32_t)(swz<NCH, SZ>(r0) << 4));
     }
   }
   // all ROWS rows of the tile starting at `src` (wave-uniform) are inside the source

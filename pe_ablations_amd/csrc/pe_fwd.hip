@@ -208,7 +208,11 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
   const int64_t krs = (int64_t)DQK * 2, vrs = a.v_ss * 2;
 
   const RowFrags<NCK> rk(perm_row<0>(l32), g);  // k~ row fragments (rows nt*32 + perm_row(l32))
-  const ColFrags<NCV> cv(lane);                  // v transpose fragments
+#ifndef FWD_VSWZ
+#define FWD_VSWZ 1
+#endif
+  constexpr int VSZ = FWD_VSWZ;  // v tile swizzle kind (it is only read with the transpose load)
+  const ColFrags<NCV, VSZ> cv(lane);                  // v transpose fragments
   f32x16 o[NOT];
 #pragma unroll
   for (int t = 0; t < NOT; ++t)
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
   const bool dmaw = __builtin_amdgcn_readfirstlane(w) >= NW - NDW;
   const int dw = dmaw ? w - (NW - NDW) : 0;
   const DmaPlan<BN, NCK, NDW> plan_k(dw, lane, (uint32_t)krs);
-  const DmaPlan<BN, NCV, NDW> plan_v(dw, lane, (uint32_t)vrs);
+  const DmaPlan<BN, NCV, NDW, VSZ> plan_v(dw, lane, (uint32_t)vrs);
   constexpr int PER = DmaPlan<BN, NCK, NDW>::TPW + DmaPlan<BN, NCV, NDW>::TPW;
   const uint32_t smem_l = lds_addr(smem);
   auto issue = [&](int kb) {
@@ -238,7 +242,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
       plan_v.full(vsrc, nl + SK_BYTES, dw, (uint32_t)vrs);
     } else {
       dma_tile<BN, NCK, NDW>(nK, ksrc, krs, a.Sk - k0, dw, lane);
-      dma_tile<BN, NCV, NDW>(nK + SK_BYTES, vsrc, vrs, a.Sk - k0, dw, lane);
+      dma_tile<BN, NCV, NDW, VSZ>(nK + SK_BYTES, vsrc, vrs, a.Sk - k0, dw, lane);
     }
   };
 #pragma unroll
