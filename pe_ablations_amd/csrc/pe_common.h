@@ -294,12 +294,12 @@ template <int NCH, int SZ = 0> struct RowX {
     return *(const u32x4*)(row_ptr + b[kk & 7] + (uint32_t)(row0 * NCH * 16 + (kk >> 3) * 256));
   }
 };
-template <int NCH> struct RowFrags {  // row fragments, as lds_row_frag<NCH>(tile, row0 + rl, 2 * kk + g)
-  uint32_t b[8];                      // [kk % 8]
+template <int NCH, int SZ = 0> struct RowFrags {  // row fragments, as lds_row_frag<NCH>(tile, row0 + rl, 2 * kk + g)
+  uint32_t b[8];                                  // [kk % 8]
   // rl < 32: the lane's row within a 32-row tile (perm_row(l32) for the products that need it)
   __device__ __forceinline__ RowFrags(int rl, int g) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) b[j] = tile_off<NCH>(rl, (2 * j + g) % NCH);
+    for (int j = 0; j < 8; ++j) b[j] = tile_off<NCH, SZ>(rl, (2 * j + g) % NCH);
   }
   // row0 % 32 == 0, compile-time kk
   __device__ __forceinline__ u32x4 read(const char* tile, int row0, int kk) const {

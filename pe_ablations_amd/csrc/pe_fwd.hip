@@ -207,7 +207,11 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
   const char* vbase = (const char*)((const uint16_t*)a.v + b * a.v_sb + hk * a.v_sh);
   const int64_t krs = (int64_t)DQK * 2, vrs = a.v_ss * 2;
 
-  const RowFrags<NCK> rk(perm_row<0>(l32), g);  // k~ row fragments (rows nt*32 + perm_row(l32))
+#ifndef FWD_KSWZ
+#define FWD_KSWZ 0
+#endif
+  constexpr int KSZ = FWD_KSWZ;  // k~ tile swizzle kind (row reads only)
+  const RowFrags<NCK, KSZ> rk(perm_row<0>(l32), g);  // k~ row fragments (rows nt*32 + perm_row(l32))
 #ifndef FWD_VSWZ
 #define FWD_VSWZ 1
 #endif
@@ -226,7 +230,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
   // the barrier, so the two waves of a SIMD start each tile out of step.
   const bool dmaw = __builtin_amdgcn_readfirstlane(w) >= NW - NDW;
   const int dw = dmaw ? w - (NW - NDW) : 0;
-  const DmaPlan<BN, NCK, NDW> plan_k(dw, lane, (uint32_t)krs);
+  const DmaPlan<BN, NCK, NDW, KSZ> plan_k(dw, lane, (uint32_t)krs);
   const DmaPlan<BN, NCV, NDW, VSZ> plan_v(dw, lane, (uint32_t)vrs);
   constexpr int PER = DmaPlan<BN, NCK, NDW>::TPW + DmaPlan<BN, NCV, NDW>::TPW;
   const uint32_t smem_l = lds_addr(smem);
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
       plan_k.full(ksrc, nl, dw, (uint32_t)krs);
       plan_v.full(vsrc, nl + SK_BYTES, dw, (uint32_t)vrs);
     } else {
-      dma_tile<BN, NCK, NDW>(nK, ksrc, krs, a.Sk - k0, dw, lane);
+      dma_tile<BN, NCK, NDW, KSZ>(nK, ksrc, krs, a.Sk - k0, dw, lane);
       dma_tile<BN, NCV, NDW, VSZ>(nK + SK_BYTES, vsrc, vrs, a.Sk - k0, dw, lane);
     }
   };
