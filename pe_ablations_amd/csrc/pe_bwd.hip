@@ -709,7 +709,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     }
   };
 
-  constexpr int FD = 3;
+#ifndef DKDV_FD
+#define DKDV_FD 3
+#endif
+  constexpr int FD = DKDV_FD;
   const RowX<NCQ, SZ> rq(perm_row<0>(l32), g);
   const RowX<NCO, SZ> ro(perm_row<0>(l32), g);
   const ColX<NCQ, SZ> cq(lane);
@@ -862,7 +865,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     int prev_h = hk * grp, prev_qt = qb0;  // head and query tile of step t - 1
     // role B is the critical path of every step: its instructions go first when both waves of a
     // SIMD are ready to issue
-    __builtin_amdgcn_s_setprio(2);
+#ifndef DKDV_PRIO
+#define DKDV_PRIO 2
+#endif
+    __builtin_amdgcn_s_setprio(DKDV_PRIO);
     for (int t = 0; t <= niter; ++t) {
       if (t >= 1) {  // dS of tile t - 1 from A's fp32 P; store it; dK~ += dS^T q~
         const char* st = smem + ((t - 1) % NSTG) * STAGE;
