@@ -629,6 +629,58 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     }
 }
 
+// Vectorised form of the fused inverse PoPE epilogue.  It needs x and dx with a unit dim stride
+// and every row 16-byte aligned (true of the projections' (B, S, H, D) views).
+__device__ __forceinline__ bool epi_vec_ok(const EpiPoPE& e) {
+  const int64_t xe = e.x_dtype == 0 ? 2 : 4, de = e.dx_dtype == 0 ? 2 : 4;
+  return e.x_s[3] == 1 && e.dx_s[3] == 1 && (uintptr_t)e.x % 16 == 0 && (uintptr_t)e.dx % 16 == 0 &&
+         (e.x_s[0] * xe) % 16 == 0 && (e.x_s[1] * xe) % 16 == 0 && (e.x_s[2] * xe) % 16 == 0 &&
+         (e.dx_s[0] * de) % 16 == 0 && (e.dx_s[1] * de) % 16 == 0 && (e.dx_s[2] * de) % 16 == 0;
+}
+// Inverse transform of NR staged rows (st: fp32 [NR][DQK], cos half then sin half of each row's
+// gradient).  Thread (cg, rr) of the NT threads takes dims 8cg .. 8cg+7 of rows rr + RPP*i, with
+// RPP = NT / (DQK/16): it loads all its x rows first (16 or 32 bytes each), so their latency is
+// paid once, then reads the two gradient halves as 16-byte LDS vectors and stores 8 dx at a time.
+// Row r is sequence index base + r (valid below nidx).  With key set, dl (8 values) is the key
+// phase bias; sdl / sf accumulate sum(dphi) and sum(pos * dphi) per dim over the thread's rows.
+template <int DQK, int NT, int NR>
+__device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st, int tid, int64_t xb,
+                                              int64_t dxb, int base, int nidx, const float (&fr)[8],
+                                              const float (&dl)[8], bool key, float (&sdl)[8], float (&sf)[8]) {
+  constexpr int Dr = DQK / 2, CG = Dr / 8, RPP = NT / CG, NI = NR / RPP;
+  static_assert(NT % CG == 0 && NR % RPP == 0, "whole rows per thread");
+  const int c0 = (tid % CG) * 8, rr = tid / CG;
+  float xv[NI][8];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int idx = base + rr + RPP * i;
+    if (idx < nidx) {
+      load8(e.x, xb + (int64_t)idx * e.x_s[2] + c0, e.x_dtype, xv[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int r = rr + RPP * i, idx = base + r;
+    if (idx < nidx) {
+      const f32x4 c_lo = *(const f32x4*)(st + r * DQK + c0), c_hi = *(const f32x4*)(st + r * DQK + c0 + 4);
+      const f32x4 s_lo = *(const f32x4*)(st + r * DQK + Dr + c0), s_hi = *(const f32x4*)(st + r * DQK + Dr + c0 + 4);
+      const float pos = (float)(e.start_pos + idx);
+      float dx[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float gc = j < 4 ? c_lo[j] : c_hi[j - 4], gs = j < 4 ? s_lo[j] : s_hi[j - 4];
+        const float dph = inv_pope_elem(xv[i][j], pos, fr[j], dl[j], key, gc, gs, dx[j]);
+        sdl[j] += dph;
+        sf[j] += pos * dph;
+      }
+      store8(e.dx, dxb + (int64_t)idx * e.dx_s[2] + c0, e.dx_dtype, dx);
+    }
+  }
+}
+
 // dK~/dV with two waves per SIMD.  A workgroup of 8 waves owns 128 keys of one kv head; the 32
 // keys of pair p are shared by wave p (role A: scores S, P = softmax numerator, dV += P^T dO) and
 // wave p + 4 (role B: dP = dO v^T, dS = P (dP - Di), the dS store, dK~ += dS^T q~), which land on
@@ -917,7 +969,41 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     }
   }
 
-  if (a.fuse_inv) {  // inverse PoPE transform of the staged dk~ rows, all 8 waves
+  if (a.fuse_inv && epi_vec_ok(a.ek)) {  // inverse PoPE transform of the staged dk~ rows, all 8 waves
+    const EpiPoPE& e = a.ek;
+    constexpr int Dr = DQK / 2, CG = Dr / 8, RPP = NW * 64 / CG;
+    const int c0 = (tid % CG) * 8, rr = tid / CG;
+    float fr[8], dl[8], sdl[8], sf[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      fr[j] = a.freqs[c0 + j];
+      dl[j] = a.delta ? a.delta[hk * a.delta_hs + c0 + j] : 0.f;
+      sdl[j] = sf[j] = 0.f;
+    }
+    __syncthreads();  // every dk~ row staged
+    inv_pope_rows<DQK, NW * 64, BNK>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1], b * e.dx_s[0] + hk * e.dx_s[1],
+                                     k0, a.Sk, fr, dl, a.delta != nullptr, sdl, sf);
+    if (e.part_delta || e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
+      __syncthreads();
+      float* red = st_epi;  // [2][RPP][Dr]
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        red[(0 * RPP + rr) * Dr + c0 + j] = sdl[j];
+        red[(1 * RPP + rr) * Dr + c0 + j] = sf[j];
+      }
+      __syncthreads();
+      const int64_t blk = (int64_t)bh * nkb + kb;
+      if (tid < Dr) {
+        float d0 = 0.f, f0 = 0.f;
+        for (int i = 0; i < RPP; ++i) {
+          d0 += red[(0 * RPP + i) * Dr + tid];
+          f0 += red[(1 * RPP + i) * Dr + tid];
+        }
+        if (e.part_delta) e.part_delta[blk * Dr + tid] = d0;
+        if (e.part_freq) e.part_freq[blk * Dr + tid] = f0;
+      }
+    }
+  } else if (a.fuse_inv) {  // the same, element by element, for strided x / dx
     const EpiPoPE& e = a.ek;
     const int Dr = DQK / 2;
     float* st = st_epi;
@@ -1152,6 +1238,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
       // at a time go through LDS, then one plain loop with a fixed dim c per thread
       const EpiPoPE& e = a.eq;
       const int Dr = DQK / 2;
+      constexpr int Dr_c = DQK / 2;
       float* st = (float*)smem;  // [128 queries][DQK], one half of the block's rows at a time
       const int c = tid % Dr;
       // EU rows per trip, pipelined as in the dK epilogue but with shorter trips and no loads across
@@ -1179,6 +1266,35 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
         }
         __syncthreads();
       };
+      if (epi_vec_ok(e)) {
+        constexpr int CG = Dr_c / 8, RPP = NW * 64 / CG;
+        const int c0 = (tid % CG) * 8, rr = tid / CG;
+        float fr8[8], dl8[8], sdl8[8], sf8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          fr8[j] = a.freqs[c0 + j];
+          dl8[j] = sdl8[j] = sf8[j] = 0.f;
+        }
+        for (int half = 0; half < 2; ++half) {
+          stage(half);
+          inv_pope_rows<DQK, NW * 64, 128>(e, st, tid, b * e.x_s[0] + h * e.x_s[1], b * e.dx_s[0] + h * e.dx_s[1],
+                                           q0 + half * 128, a.Sq, fr8, dl8, false, sdl8, sf8);
+        }
+        if (e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
+          __syncthreads();
+          float* red = st;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) red[rr * Dr_c + c0 + j] = sf8[j];
+          __syncthreads();
+          const int64_t blk = (int64_t)bh * nqb + qb;
+          if (tid < Dr_c) {
+            float f0 = 0.f;
+            for (int i = 0; i < RPP; ++i) f0 += red[i * Dr_c + tid];
+            e.part_freq[blk * Dr_c + tid] = f0;
+          }
+        }
+        return;
+      }
       float xv[EU], xn[EU];
       const float fr = a.freqs[c];
       float sf = 0.f;
