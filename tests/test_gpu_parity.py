@@ -131,3 +131,43 @@ def test_deterministic(cuda):
         res.append([out.detach(), qg.grad, kg.grad, vg.grad, dg.grad])
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_unaligned_views_take_the_elementwise_epilogue(cuda, D):
+    """bf16 fwd+bwd with q and k as views that start one element into a wider buffer.  The fused
+    inverse transform in the gradient kernels cannot use 16-byte vectors on them and takes its
+    element-by-element path; dq / dk must equal those of the vectorised path (same inputs in
+    aligned tensors) bit for bit, since both apply the same per-element arithmetic, and the
+    phase-gradient sums (reduced in another order) must agree with the oracle."""
+    B, H, S = 1, 2, 384
+    q, k, v, freqs, delta = _inputs(B, H, H, S, D, dtype=torch.bfloat16, seed=7)
+    g = torch.Generator().manual_seed(77)
+    dout = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16).to(cuda)
+    scale = 1 / math.sqrt(D)
+
+    def run(qx, kx):
+        vg, fg, dg = (t.to(cuda).requires_grad_(True) for t in (v, freqs, delta))
+        out = pe_attention(qx, kx, vg, mode="pope", freqs=fg, delta=dg, scale=scale)
+        out.backward(dout)
+        torch.cuda.synchronize()
+        return out.detach(), qx.grad, kx.grad, vg.grad, fg.grad, dg.grad
+
+    def unaligned(t):
+        wide = torch.zeros(*t.shape[:-1], t.shape[-1] + 8, dtype=t.dtype, device=cuda)
+        wide[..., 1:1 + t.shape[-1]] = t.to(cuda)
+        view = wide[..., 1:1 + t.shape[-1]].detach().requires_grad_(True)
+        assert view.data_ptr() % 16 != 0
+        return view
+
+    ref = run(q.to(cuda).requires_grad_(True), k.to(cuda).requires_grad_(True))
+    got = run(unaligned(q), unaligned(k))
+    for name, a, b in zip(("out", "dq", "dk", "dv"), ref[:4], got[:4]):
+        assert torch.equal(a, b), name
+    qo, ko, vo = (t.detach().float().clone().requires_grad_(True) for t in (q, k, v))
+    fo, do_ = freqs.clone().requires_grad_(True), delta.clone().requires_grad_(True)
+    ref_out, _ = O.pope_attention(qo, ko, vo, fo, do_, scale=scale, clamp=False, operand_dtype=torch.bfloat16)
+    ref_out.backward(dout.cpu().double())
+    assert _maxdiff(got[1], qo.grad) < 2e-2 and _maxdiff(got[2], ko.grad) < 2e-2
+    for a, b in ((got[4], fo.grad), (got[5], do_.grad), (ref[4], fo.grad), (ref[5], do_.grad)):
+        assert _maxdiff(a, b) / max(1.0, b.abs().max().item()) < 2e-2
