@@ -25,12 +25,15 @@ size_t esz(const pe_attn_params* p) { return p->dtype == PE_DTYPE_BF16 ? 2 : 4; 
 
 struct Layout {
   int dqk, dv;
-  size_t q_off, k_off, v_off, fwd_total;
+  size_t q_off, k_off, v_off, tab_off, fwd_total;
   size_t do_off, di_off, l2_off, dq_off, dk_off, pq_off, pk_off, pkd_off, ds_off, bwd_total;
   int sq_pad;
   int ds_nqt, ds_rows;
   int nq_blocks, nk_blocks;
 };
+
+// the query phases are shared by every batch and head, so PoPE evaluates them once per call
+bool use_qtab(const pe_attn_params* p) { return p->mode == PE_MODE_POPE && p->Dr > 0 && p->Dr % 8 == 0; }
 
 Layout layout(const pe_attn_params* p) {
   Layout L{};
@@ -41,7 +44,10 @@ Layout layout(const pe_attn_params* p) {
   L.q_off = 0;
   L.k_off = L.q_off + align_up(nq * L.dqk * e);
   L.v_off = L.k_off + align_up(nk * L.dqk * e);
-  L.fwd_total = L.v_off + align_up(nk * L.dv * e);
+  L.tab_off = L.v_off + align_up(nk * L.dv * e);
+  // query phase table (cos / sin of fl(pos * freq), fp32 [Sq][2][Dr]) for the PoPE prologue and the
+  // dQ epilogue
+  L.fwd_total = L.tab_off + (use_qtab(p) ? align_up((size_t)p->Sq * 2 * p->Dr * 4) : 0);
   // per-block partial sums of the phase gradient: blocks of the inverse-transform kernel (256
   // rows), or of the gradient kernels when the transform is fused into their epilogues (dQ GEMM:
   // 256 queries, dK/dV: 128 keys); the buffers are sized for the larger count
@@ -301,7 +307,10 @@ static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe
 
   pe::PrepArgs a;
   stage_mark(PE_STAGE_FWD_PREP, 0, s);
+  float* qtab = use_qtab(p) ? (float*)(ws + L.tab_off) : nullptr;
+  if (qtab && (rc = pe::launch_phase_table(freqs, p->start_pos_q, p->Sq, p->Dr, qtab, s))) return rc;
   fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
+  a.tab = qtab;
   if (nrm) {
     a.norm_w = nrm->q_weight; a.norm_w_dtype = nrm->weight_dtype; a.norm_eps = nrm->eps;
     if ((rc = pe::launch_prep_norm(a, s))) return rc;
@@ -419,6 +428,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   c.ds_rows = L.ds_rows;
   c.lse_in = lse;
   c.dq_t = (float*)(bws + L.dq_off);
+  c.qtab = use_qtab(p) ? (const float*)(fws + L.tab_off) : nullptr;
   c.dk_t = (float*)(bws + L.dk_off);
   c.dv = (void*)dv->data; c.dv_sb = dv->stride[0]; c.dv_sh = dv->stride[1]; c.dv_ss = dv->stride[2];
   c.dv_dtype = dv->dtype;

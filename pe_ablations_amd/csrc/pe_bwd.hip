@@ -643,10 +643,13 @@ __device__ __forceinline__ bool epi_vec_ok(const EpiPoPE& e) {
 // paid once, then reads the two gradient halves as 16-byte LDS vectors and stores 8 dx at a time.
 // Row r is sequence index base + r (valid below nidx).  With key set, dl (8 values) is the key
 // phase bias; sdl / sf accumulate sum(dphi) and sum(pos * dphi) per dim over the thread's rows.
-template <int DQK, int NT, int NR>
+// With TAB (query side) the sin / cos of each row's phases come from launch_phase_table's
+// [S][2][Dr] table, indexed by the row's sequence index, instead of being evaluated.
+template <int DQK, int NT, int NR, bool TAB>
 __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st, int tid, int64_t xb,
                                               int64_t dxb, int base, int nidx, const float (&fr)[8],
-                                              const float (&dl)[8], bool key, float (&sdl)[8], float (&sf)[8]) {
+                                              const float (&dl)[8], bool key, const float* tab,
+                                              float (&sdl)[8], float (&sf)[8]) {
   constexpr int Dr = DQK / 2, CG = Dr / 8, RPP = NT / CG, NI = NR / RPP;
   static_assert(NT % CG == 0 && NR % RPP == 0, "whole rows per thread");
   const int c0 = (tid % CG) * 8, rr = tid / CG;
@@ -669,12 +672,26 @@ __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st,
       const f32x4 s_lo = *(const f32x4*)(st + r * DQK + Dr + c0), s_hi = *(const f32x4*)(st + r * DQK + Dr + c0 + 4);
       const float pos = (float)(e.start_pos + idx);
       float dx[8];
+      if constexpr (TAB) {
+        const float* tr = tab + (int64_t)idx * DQK + c0;
+        const f32x4 tc0 = *(const f32x4*)tr, tc1 = *(const f32x4*)(tr + 4);
+        const f32x4 ts0 = *(const f32x4*)(tr + Dr), ts1 = *(const f32x4*)(tr + Dr + 4);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float gc = j < 4 ? c_lo[j] : c_hi[j - 4], gs = j < 4 ? s_lo[j] : s_hi[j - 4];
-        const float dph = inv_pope_elem(xv[i][j], pos, fr[j], dl[j], key, gc, gs, dx[j]);
-        sdl[j] += dph;
-        sf[j] += pos * dph;
+        for (int j = 0; j < 8; ++j) {
+          const float gc = j < 4 ? c_lo[j] : c_hi[j - 4], gs = j < 4 ? s_lo[j] : s_hi[j - 4];
+          const float cs = j < 4 ? tc0[j] : tc1[j - 4], sn = j < 4 ? ts0[j] : ts1[j - 4];
+          const float dph = inv_pope_elem_cs(xv[i][j], sn, cs, gc, gs, dx[j]);
+          sdl[j] += dph;
+          sf[j] += pos * dph;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float gc = j < 4 ? c_lo[j] : c_hi[j - 4], gs = j < 4 ? s_lo[j] : s_hi[j - 4];
+          const float dph = inv_pope_elem(xv[i][j], pos, fr[j], dl[j], key, gc, gs, dx[j]);
+          sdl[j] += dph;
+          sf[j] += pos * dph;
+        }
       }
       store8(e.dx, dxb + (int64_t)idx * e.dx_s[2] + c0, e.dx_dtype, dx);
     }
@@ -981,8 +998,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       sdl[j] = sf[j] = 0.f;
     }
     __syncthreads();  // every dk~ row staged
-    inv_pope_rows<DQK, NW * 64, BNK>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1], b * e.dx_s[0] + hk * e.dx_s[1],
-                                     k0, a.Sk, fr, dl, a.delta != nullptr, sdl, sf);
+    inv_pope_rows<DQK, NW * 64, BNK, false>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1], b * e.dx_s[0] + hk * e.dx_s[1],
+                                     k0, a.Sk, fr, dl, a.delta != nullptr, nullptr, sdl, sf);
     if (e.part_delta || e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
       __syncthreads();
       float* red = st_epi;  // [2][RPP][Dr]
@@ -1266,7 +1283,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
         }
         __syncthreads();
       };
-      if (epi_vec_ok(e)) {
+      if (epi_vec_ok(e) && a.qtab) {  // the host provides the query phase table with the fused form
         constexpr int CG = Dr_c / 8, RPP = NW * 64 / CG;
         const int c0 = (tid % CG) * 8, rr = tid / CG;
         float fr8[8], dl8[8], sdl8[8], sf8[8];
@@ -1277,8 +1294,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
         }
         for (int half = 0; half < 2; ++half) {
           stage(half);
-          inv_pope_rows<DQK, NW * 64, 128>(e, st, tid, b * e.x_s[0] + h * e.x_s[1], b * e.dx_s[0] + h * e.dx_s[1],
-                                           q0 + half * 128, a.Sq, fr8, dl8, false, sdl8, sf8);
+          inv_pope_rows<DQK, NW * 64, 128, true>(e, st, tid, b * e.x_s[0] + h * e.x_s[1], b * e.dx_s[0] + h * e.dx_s[1],
+                                           q0 + half * 128, a.Sq, fr8, dl8, false, a.qtab, sdl8, sf8);
         }
         if (e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
           __syncthreads();

@@ -555,16 +555,23 @@ __device__ __forceinline__ void pe_sincos(float x, float& sn, float& cs) {
 // Gradient of one PoPE element y = [mu cos phi, mu sin phi] (mu = softplus(x), phi = fl(pos*freq)
 // (+ delta, added after the product)): from the pair (gc, gs) writes dx = (gc cos + gs sin)
 // sigmoid(x) and returns dphi = mu (gs cos - gc sin).
-__device__ __forceinline__ float inv_pope_elem(float x, float pos, float freq, float dl, bool key,
-                                               float gc, float gs, float& dx) {
+// The same with sin / cos of the phase given.  The products and sums are written out (one fma
+// each, the other product unfused) so that every caller rounds them alike: left to the compiler,
+// the contraction of gc*cs + gs*sn depends on the surrounding code, and the element-wise and
+// vectorised epilogues would differ in the last bit.
+__device__ __forceinline__ float inv_pope_elem_cs(float x, float sn, float cs, float gc, float gs, float& dx) {
   float mu, sg;
   softplus_sigmoid(x, mu, sg);
+  dx = mul_nc(__builtin_fmaf(gc, cs, mul_nc(gs, sn)), sg);
+  return mul_nc(mu, __builtin_fmaf(gs, cs, -mul_nc(gc, sn)));
+}
+__device__ __forceinline__ float inv_pope_elem(float x, float pos, float freq, float dl, bool key,
+                                               float gc, float gs, float& dx) {
   float ph = mul_nc(pos, freq);
   if (key) ph = add_nc(ph, dl);
   float sn, cs;
   pe_sincos(ph, sn, cs);
-  dx = (gc * cs + gs * sn) * sg;
-  return mu * (gs * cs - gc * sn);
+  return inv_pope_elem_cs(x, sn, cs, gc, gs, dx);
 }
 
 // Launch-order remap.  Blocks are issued heaviest first (LPT for the causal triangle) and, when the

@@ -43,6 +43,7 @@ struct CoreArgs {
                     // block, key kl and query chunk r = (q%64)/8 at chunk ((r>>1)*64 + (r&1)*32 + kl)
   int ds_nqt;       // 64-query blocks per 32-key row (ceil(Sq / 256) * 4)
   int ds_rows;      // key rows per head (Sk rounded up to 128)
+  const float* qtab;  // query phase table of launch_phase_table ([Sq][2][Dr]) or null
   float* dq_t;      // (B, Hq, Sq, DQK) fp32, already multiplied by scale
   float* dk_t;      // (B, Hkv, Sk, DQK) fp32, already multiplied by scale (summed over the GQA group)
   void* dv; int64_t dv_sb, dv_sh, dv_ss; int dv_dtype;
@@ -68,8 +69,14 @@ struct PrepArgs {
   float mscale;
   // RMSNorm of xr over all H*Dr features of a token before the transform (launch_prep_norm only)
   const void* norm_w; int norm_w_dtype; float norm_eps;
+  // query side only: cos / sin of fl((start_pos + s) * freq) as [S][2][Dr] fp32 (launch_phase_table),
+  // read instead of evaluated by the vectorised PoPE prologue; null evaluates them
+  const float* tab;
 };
 int launch_prep(const PrepArgs& a, hipStream_t s);
+// cos / sin of the query phases fl((start + s) * freqs[c]) for s < S, c < Dr into tab [S][2][Dr]
+// (cos row then sin row), with the same routine and rounding as the prologue kernels
+int launch_phase_table(const float* freqs, int start, int S, int Dr, float* tab, hipStream_t s);
 // PoPE prologue with the RMSNorm fused in: one workgroup per token (all heads)
 int launch_prep_norm(const PrepArgs& a, hipStream_t s);
 

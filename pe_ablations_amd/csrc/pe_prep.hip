@@ -324,15 +324,27 @@ __global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
   float x[8];
   unpack8(xv, x);
   float cv[8], sv[8];
+  if (a.tab && !a.is_key) {  // query phases from the table (shared by every batch and head)
+    const float* tr = a.tab + (int64_t)s * 2 * a.Dr + t * 8;
+    const f32x4 c0 = *(const f32x4*)tr, c1 = *(const f32x4*)(tr + 4);
+    const f32x4 s0 = *(const f32x4*)(tr + a.Dr), s1 = *(const f32x4*)(tr + a.Dr + 4);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float mu = softplus_f(x[e]);
-    float ph = mul_nc(pos, e < 4 ? f0[e] : f1[e - 4]);
-    if (add) ph = add_nc(ph, e < 4 ? d0[e] : d1[e - 4]);
-    float sn, cs;
-    pe_sincos(ph, sn, cs);
-    cv[e] = mul_nc(mu, cs);
-    sv[e] = mul_nc(mu, sn);
+    for (int e = 0; e < 8; ++e) {
+      const float mu = softplus_f(x[e]);
+      cv[e] = mul_nc(mu, e < 4 ? c0[e] : c1[e - 4]);
+      sv[e] = mul_nc(mu, e < 4 ? s0[e] : s1[e - 4]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float mu = softplus_f(x[e]);
+      float ph = mul_nc(pos, e < 4 ? f0[e] : f1[e - 4]);
+      if (add) ph = add_nc(ph, e < 4 ? d0[e] : d1[e - 4]);
+      float sn, cs;
+      pe_sincos(ph, sn, cs);
+      cv[e] = mul_nc(mu, cs);
+      sv[e] = mul_nc(mu, sn);
+    }
   }
   *(u32x4*)(drow + a.Dc + t * 8) =
       u32x4{pack_bf2(cv[0], cv[1]), pack_bf2(cv[2], cv[3]), pack_bf2(cv[4], cv[5]), pack_bf2(cv[6], cv[7])};
@@ -395,6 +407,23 @@ int launch_prep(const PrepArgs& a, hipStream_t s) {
   } else {
     hipLaunchKernelGGL(prep_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
   }
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
+__global__ __launch_bounds__(256) void phase_table_kernel(const float* freqs, int start, int S, int Dr, float* tab) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (int64_t)S * Dr) return;
+  const int s = (int)(gid / Dr), c = (int)(gid % Dr);
+  float sn, cs;
+  pe_sincos(mul_nc((float)(start + s), freqs[c]), sn, cs);
+  tab[(int64_t)s * 2 * Dr + c] = cs;
+  tab[(int64_t)s * 2 * Dr + Dr + c] = sn;
+}
+
+int launch_phase_table(const float* freqs, int start, int S, int Dr, float* tab, hipStream_t s) {
+  const int64_t n = (int64_t)S * Dr;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(phase_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, freqs, start, S, Dr, tab);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
