@@ -1373,7 +1373,7 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
   if constexpr (DT == 0) {
     if (which == 0) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
-      if constexpr ((DQK == 128 || DQK == 256) && DV == 128) {
+      if constexpr ((DQK == 128 || DQK == 256) && (DV == 128 || DV == 64)) {
         // two waves per SIMD (role-split pairs); the one-wave kernel serves the other widths
         hipLaunchKernelGGL((dkdv_pair_kernel<DQK, DV>), dim3(nkb * a.B * a.Hkv), dim3(512), 0, s, a);
       } else {
