@@ -1392,8 +1392,11 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
 #ifndef DQ_NW
 #define DQ_NW 8
 #endif
-      constexpr int DNW = DQK == 256 ? DQ_NW : 8;
-      hipLaunchKernelGGL((dq_gemm_kernel<DQK, DNW, (DQK == 256 ? DQ_BK : 64), (DQK == 256 ? DQ_NSTG : 2)>), dim3(nqb * a.B * a.Hq), dim3(DNW * 64), 0, s, a);
+      // the 32-key ring for the wide operands (a 64-wide k~ tile of 32 keys is less than one DMA
+      // instruction per wave)
+      constexpr bool TW = DQK == 256 || DQK == 128;
+      constexpr int DNW = TW ? DQ_NW : 8;
+      hipLaunchKernelGGL((dq_gemm_kernel<DQK, DNW, (TW ? DQ_BK : 64), (TW ? DQ_NSTG : 2)>), dim3(nqb * a.B * a.Hq), dim3(DNW * 64), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {

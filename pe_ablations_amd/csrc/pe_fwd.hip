@@ -385,7 +385,7 @@ static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
 #ifndef FWD_NSTG
 #define FWD_NSTG 2
 #endif
-  constexpr int NDW = (DQK == 256 && DV == 128) ? FWD_NDW : 8, NSTG = (DQK == 256 && DV == 128) ? FWD_NSTG : 2;
+  constexpr int NDW = FWD_NDW, NSTG = (DQK == 256 && DV == 128) ? FWD_NSTG : 2;
   const int BM = NW * 32;
   const int nqb = (a.Sq + BM - 1) / BM;
   const int grid = nqb * a.B * a.Hq;
