@@ -1086,7 +1086,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 // workgroup owns 256 queries of one head; its 8 waves split them into 4 pairs of 32-query tiles x
 // 2 halves of the dq~ columns, so every fragment read from LDS feeds two MFMAs (A: dS for 32
 // queries x 16 keys, shared by the wave's column tiles; B: k~ for 16 keys x 32 columns, shared by
-// its two query tiles) and the 128 accumulators per wave leave room for two waves per SIMD.  Each
+// its two query tiles) and the 128 accumulators per wave leave room for two waves per SIMD.  (NW =
+// 4 gives each wave 128 queries x 128 columns in AGPRs at one wave per SIMD: one fragment per MFMA
+// instead of 1.5, but it measured 25 % slower, as each wave then waits on its own LDS reads and
+// loads.)  Each
 // BK-key step stages dS^T (BK keys x 256 queries) and k~ (BK x DQK) in one slot of an NSTAGE ring,
 // NSTAGE - 1 steps ahead: dS is read once from HBM, so the kernel streams it and needs several
 // tiles in flight to cover the memory latency.  Both operands are read with the transpose load.
@@ -1390,7 +1393,7 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       // wide operands: 32-key steps in a 4-deep ring (three steps of loads in flight) measured
       // 4 % faster than 64-key steps double-buffered or a 3-deep ring of 32-key steps
 #ifndef DQ_NW
-#define DQ_NW 8
+#define DQ_NW 8  // waves per workgroup (4 or 8)
 #endif
       // the 32-key ring for the wide operands (a 64-wide k~ tile of 32 keys is less than one DMA
       // instruction per wave)
