@@ -500,8 +500,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
       const int h = hk * grp + t / nper;
       char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * (a.ds_rows / 32) + (kw0 >> 5)) * a.ds_nqt * 4096 +
                   (int64_t)(q0 >> 6) * 4096;
-      *(u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16) = cdsf[0];
-      *(u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16) = cdsf[1];
+      __builtin_nontemporal_store(cdsf[0], (u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16));  // read once
+      __builtin_nontemporal_store(cdsf[1], (u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16));
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -962,8 +962,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
         char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * (a.ds_rows / 32) + (kw0 >> 5)) * a.ds_nqt * 4096 +
                     (int64_t)(q0 >> 6) * 4096;
         const int mt = (q0 >> 5) & 1;
-        *(u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16) = dsf[0];
-        *(u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16) = dsf[1];
+        // dS is read once, by the dQ GEMM after this kernel: non-temporal stores keep it from
+        // displacing the q~ / dO tiles that the other key blocks re-read (4 % of this kernel's
+        // time; non-temporal loads of it in the dQ GEMM measured 35 % slower there)
+        __builtin_nontemporal_store(dsf[0], (u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16));
+        __builtin_nontemporal_store(dsf[1], (u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16));
         products(dk, dsf, st + crq, cq);
       }
       if (t < niter) scores_dp(smem + (t % NSTG) * STAGE + SQ_BYTES + rro, vf, dp);
