@@ -393,8 +393,9 @@ def run_decoder(args, torch, dev) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 20; decoder 5)")
-    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 3; decoder 2)")
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default fwdbwd 50, fwd 100, decoder 5)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps (default fwdbwd 100, fwd 400, decoder 4: about 0.5 s of work)")
     ap.add_argument("--workload", choices=["fwdbwd", "fwd", "decoder"], default="fwdbwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=2)
@@ -402,8 +403,12 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="decoder CPU baseline: tokens of the sample")
     args = ap.parse_args()
     dec = args.workload == "decoder"
-    args.steps = args.steps if args.steps is not None else (5 if dec else 20)
-    args.warmup = args.warmup if args.warmup is not None else (2 if dec else 3)
+    # Defaults: about half a second of untimed work before the timed steps.  Under this load the
+    # chip runs at its socket power limit; after an idle host phase its clock and power state need
+    # a few hundred milliseconds to settle, and timing from a 3-step warm-up measured the forward
+    # 7-9 % and the fwd+bwd step 1.7 % slower than the settled state.
+    args.steps = args.steps if args.steps is not None else {"decoder": 5, "fwd": 100, "fwdbwd": 50}[args.workload]
+    args.warmup = args.warmup if args.warmup is not None else {"decoder": 4, "fwd": 400, "fwdbwd": 100}[args.workload]
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
