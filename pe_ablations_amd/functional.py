@@ -79,6 +79,60 @@ def _params(cfg, qr, kr, v, qc, delta) -> _lib.PeParams:
     return p
 
 
+def _shape_error(msg: str) -> ValueError:
+    return ValueError(f"pe_attention: {msg}")
+
+
+def check_operands(q, k, v, q_c=None, k_c=None, freqs=None, delta=None, *, mode: int,
+                   q_norm_weight=None, k_norm_weight=None) -> None:
+    """Shape and device agreement of every operand, checked before anything is enqueued.
+
+    The C ABI sees pointers and strides only, so a short freqs, a CPU delta or a v with fewer rows
+    than k would otherwise reach the kernels as an out-of-bounds read or write.  The reference's
+    torch ops raise on the same mismatches (src/model/fpope_attention.py:145-177 concatenates and
+    multiplies these tensors), so this raises ValueError instead.  q (B,Hq,Sq,Dr), k (B,Hkv,Sk,Dr),
+    v (B,Hkv,Sk,Dv), q_c (B,Hq,Sq,Dc) and k_c (B,Hkv,Sk,Dc) together or not at all; freqs (Dr,)
+    for PoPE / FoPE, (Dr/2,) for RoPE; delta (Dr,) or (Hkv,Dr); norm weights (Hq*Dr,) / (Hkv*Dr,).
+    Every tensor must sit on q's device."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("q_c", q_c), ("k_c", k_c)):
+        if t is not None and t.dim() != 4:
+            raise _shape_error(f"{name} must be (B, H, S, D), got shape {tuple(t.shape)}")
+    B, Hq, Sq, Dr = q.shape
+    if k.shape[0] != B or k.shape[3] != Dr:
+        raise _shape_error(f"k {tuple(k.shape)} must match q {tuple(q.shape)} in batch and width")
+    Hkv, Sk = k.shape[1], k.shape[2]
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise _shape_error(f"query heads {Hq} must be a multiple of key heads {Hkv}")
+    if tuple(v.shape[:3]) != (B, Hkv, Sk):
+        raise _shape_error(f"v {tuple(v.shape)} must be (B, Hkv, Sk, Dv) = ({B}, {Hkv}, {Sk}, Dv)")
+    if (q_c is None) != (k_c is None):
+        raise _shape_error("pass q_c and k_c together (content dims on both sides) or neither")
+    if q_c is not None:
+        if tuple(q_c.shape[:3]) != (B, Hq, Sq) or tuple(k_c.shape[:3]) != (B, Hkv, Sk):
+            raise _shape_error(f"q_c {tuple(q_c.shape)} / k_c {tuple(k_c.shape)} must share the rows of q / k")
+        if q_c.shape[3] != k_c.shape[3]:
+            raise _shape_error(f"q_c and k_c widths differ ({q_c.shape[3]} vs {k_c.shape[3]})")
+    if mode == _lib.PE_MODE_POPE or mode == _lib.PE_MODE_ROPE:
+        want = Dr if mode == _lib.PE_MODE_POPE else Dr // 2
+        if freqs is None or freqs.dim() != 1 or freqs.shape[0] != want:
+            got = None if freqs is None else tuple(freqs.shape)
+            raise _shape_error(f"freqs must have shape ({want},) for this mode, got {got}")
+    if delta is not None:
+        if mode != _lib.PE_MODE_POPE:
+            raise _shape_error("delta (phase bias) only applies to PoPE/FoPE")
+        if not (tuple(delta.shape) == (Dr,) or tuple(delta.shape) == (Hkv, Dr)):
+            raise _shape_error(f"delta must be ({Dr},) or ({Hkv}, {Dr}), got {tuple(delta.shape)}")
+    if q_norm_weight is not None and tuple(q_norm_weight.shape) != (Hq * Dr,):
+        raise _shape_error(f"qr_norm_weight must be ({Hq * Dr},), got {tuple(q_norm_weight.shape)}")
+    if k_norm_weight is not None and tuple(k_norm_weight.shape) != (Hkv * Dr,):
+        raise _shape_error(f"kr_norm_weight must be ({Hkv * Dr},), got {tuple(k_norm_weight.shape)}")
+    dev = q.device
+    for name, t in (("k", k), ("v", v), ("q_c", q_c), ("k_c", k_c), ("freqs", freqs), ("delta", delta),
+                    ("qr_norm_weight", q_norm_weight), ("kr_norm_weight", k_norm_weight)):
+        if t is not None and t.device != dev:
+            raise _shape_error(f"{name} is on {t.device}, q on {dev}: every operand must be on one device")
+
+
 def _stream(dev: torch.device):
     return torch.cuda.current_stream(dev).cuda_stream
 
@@ -190,11 +244,12 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
     Returns out (B,Hq,Sq,Dv) [and lse (B,Hq,Sq) fp32]."""
     if mode not in _MODES:
         raise ValueError(f"unknown PE mode {mode!r}")
-    for t in (q, k, v, q_c, k_c):
-        if t is not None and not t.is_cuda:
-            raise RuntimeError("pe_attention runs on the GPU only (got a CPU tensor); "
-                               "the HIP kernels have no CPU path")
+    if not q.is_cuda:
+        raise RuntimeError("pe_attention runs on the GPU only (got a CPU tensor); "
+                           "the HIP kernels have no CPU path")
     m = _MODES[mode]
+    check_operands(q, k, v, q_c, k_c, freqs if m != _lib.PE_MODE_NONE else None, delta, mode=m,
+                   q_norm_weight=qr_norm_weight, k_norm_weight=kr_norm_weight)
     half_in = q.dtype == torch.float16
     q, k, v, q_c, k_c = (_prep_in(t) for t in (q, k, v, q_c, k_c))
     if m != _lib.PE_MODE_NONE:

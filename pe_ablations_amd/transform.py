@@ -100,6 +100,29 @@ class PETransformFn(torch.autograd.Function):
         return dx.to(xdtype), dfreqs, ddelta, None, None, None, None
 
 
+def check_transform_operands(x, freqs, delta, *, mode: str, is_key: bool) -> None:
+    """x (B, S, H, D); freqs (D,) for PoPE or (D/2,) for RoPE; delta (D,) or (H, D) for PoPE keys;
+    all on x's device.  Raises ValueError before anything is enqueued (the library only sees
+    pointers, so a short freqs or delta would be read out of bounds)."""
+    if x.dim() != 4:
+        raise ValueError(f"pe_transform: x must be (B, S, H, D), got shape {tuple(x.shape)}")
+    H, D = x.shape[2], x.shape[3]
+    want = D if mode == "pope" else D // 2
+    if mode == "rope" and D % 2:
+        raise ValueError(f"pe_transform: RoPE needs an even width, got {D}")
+    if freqs is None or freqs.dim() != 1 or freqs.shape[0] != want:
+        got = None if freqs is None else tuple(freqs.shape)
+        raise ValueError(f"pe_transform: freqs must have shape ({want},), got {got}")
+    if delta is not None and is_key:
+        if mode != "pope":
+            raise ValueError("pe_transform: delta (phase bias) only applies to PoPE keys")
+        if not (tuple(delta.shape) == (D,) or tuple(delta.shape) == (H, D)):
+            raise ValueError(f"pe_transform: delta must be ({D},) or ({H}, {D}), got {tuple(delta.shape)}")
+    for name, t in (("freqs", freqs), ("delta", delta)):
+        if t is not None and t.device != x.device:
+            raise ValueError(f"pe_transform: {name} is on {t.device}, x on {x.device}")
+
+
 def pe_transform(x: torch.Tensor, freqs: torch.Tensor, delta: Optional[torch.Tensor], *, start_pos: int = 0,
                  is_key: bool = False, mode: str = "pope", mscale: float = 1.0) -> torch.Tensor:
     """x (B, S, H, D) -> PoPE [mu cos, mu sin] (B, S, H, 2D) or RoPE-rotated (B, S, H, D) on the GPU.
@@ -108,6 +131,9 @@ def pe_transform(x: torch.Tensor, freqs: torch.Tensor, delta: Optional[torch.Ten
     if not x.is_cuda:
         raise RuntimeError("the positional transform runs on the GPU only (got a CPU tensor); "
                            "the HIP library has no CPU path")
+    if mode not in ("pope", "rope"):
+        raise ValueError(f"pe_transform: unknown mode {mode!r}")
+    check_transform_operands(x, freqs, delta, mode=mode, is_key=is_key)
     m = {"pope": _lib.PE_MODE_POPE, "rope": _lib.PE_MODE_ROPE}[mode]
     freqs = freqs.float().contiguous()
     if delta is not None:

@@ -3,8 +3,8 @@
 Covers FoPE (gradient into the effective frequencies), RoPE / NTK / YaRN with and without the
 fused QKNorm, no-PE, the reference module's split form (content 64 | PoPE 2x32, value 64), GQA,
 bottom-right (KV-cache) and non-causal masks, start positions, fp32 and bf16.  Tolerances: 1e-5
-max-abs in fp32 mode and 2e-2 in bf16 mode for out / dq / dk / dv (a bf16 result
-is measured net of its own rounding to bf16, tests/_cmp.py); the
+max-abs in fp32 mode and 2e-2 in bf16 mode for out / dq / dk / dv (raw
+max-abs including the result's own rounding to bf16, tests/_cmp.py); the
 frequency and phase-bias gradients are sums over B*H*S rows and are compared relative to their
 largest entry.
 """
@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import pe_oracle as O
-from tests._cmp import err
+from tests._cmp import argmax_err, err, err_both
 from pe_ablations_amd.functional import pe_attention
 
 pytestmark = pytest.mark.gpu
@@ -51,7 +51,12 @@ def oracle_operands(mode, qc, kc, qr, kr, freqs, delta, start_q, start_k, mscale
 
 def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=64, Dc=0,
              dtype=torch.bfloat16, causal=True, freqs=None, delta=None, scale=None, mscale=1.0,
-             qk_norm=False, start_q=0, start_k=0, seed=0, grad_freqs=False, grad_delta=True):
+             qk_norm=False, start_q=0, start_k=0, seed=0, grad_freqs=False, grad_delta=True,
+             net_names=()):
+    """One case through pe_attention against the oracle.  Every listed error is the raw max-abs;
+    ``net_names`` lists results whose magnitude puts the raw bf16 bar out of reach of any bf16
+    number (the test names the magnitude): those are asserted net of their own rounding and their
+    raw figure and largest-error element are reported in the message."""
     Sk = Sq if Sk is None else Sk
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
     qr, kr = rnd(B, Hq, Sq, Dr, seed=seed), rnd(B, Hkv, Sk, Dr, seed=seed + 1)
@@ -84,11 +89,18 @@ def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=
     out.backward(dout.to(cuda))
     torch.cuda.synchronize()
     errs = {"out": md(out, ref), "lse": md(lse, ref_lse)}
+    pairs = {"out": (out, ref)}
     for name, a, b in zip(("dq", "dk", "dv", "dqc", "dkc"), g_in, o_in):
         if a is not None:
             errs[name] = md(a.grad, b.grad)
+            pairs[name] = (a.grad, b.grad)
     for name, e in errs.items():
-        assert e < tol, (name, errs)
+        if name in net_names:
+            a, b = pairs[name]
+            raw, net = err_both(a, b)
+            assert net < tol, (name, "net", net, "raw", raw, "at (index, |ref|, err)", argmax_err(a, b), errs)
+        else:
+            assert e < tol, (name, errs)
     for name, a, b in (("dfreqs", gf, of), ("ddelta", gd, od)):
         if a is not None and a.requires_grad:
             rel = md(a.grad, b.grad) / max(1.0, b.grad.abs().max().item())
@@ -126,9 +138,13 @@ def test_pope_shared_delta_start_pos_fp32(cuda):
 
 def test_split_form_reference_module_shape(cuda):
     """The reference module's contraction: [q_c (64) | PoPE(q_r) (2x32)], V 64, GQA 8 -> 4,
-    scale (64 + 64)^-1/2 (src/model/fpope_attention.py:107,166-177)."""
+    scale (64 + 64)^-1/2 (src/model/fpope_attention.py:107,166-177).
+
+    dv sums two query heads' gradients per key and reaches |dv| = 7.2 here, where the bf16
+    spacing is 2^-5: any bf16 dv is up to 0.0156 from the exact value there, so dv is held to
+    2e-2 net of its own rounding (raw measured 0.023 at an element of |dv| in [4, 8))."""
     run_case(cuda, Dc=64, Dr=32, Dv=64, Hq=8, Hkv=4, Sq=256, B=2, freqs=O.pope_freqs(32),
-             delta=-torch.rand(32) * 6, seed=50)
+             delta=-torch.rand(32) * 6, seed=50, net_names=("dv",))
 
 
 def test_split_form_fp32(cuda):

@@ -1,7 +1,8 @@
 """GPU parity of the HIP PE-attention path (libpe_attn.so through its C ABI) against the CPU oracle.
 
 Tolerances (north star): max-abs 1e-5 in fp32 mode, 2e-2 in bf16 mode for the output and
-dQ/dK/dV (a bf16 result net of its own rounding to bf16, tests/_cmp.py); the phase-bias / frequency gradients are sums over B*H*S rows and are compared relative
+dQ/dK/dV (raw max-abs, a bf16 result including its own rounding to bf16, tests/_cmp.py); the
+phase-bias / frequency gradients are sums over B*H*S rows and are compared relative
 to their own scale.  The oracle computes the transforms in fp32 exactly as the reference orders
 them and the attention core in fp64; in bf16 mode it rounds the transformed operands to bf16 the
 way autocast hands them to SDPA.
