@@ -62,7 +62,8 @@ enum {
   PE_ERR_STRIDE = -5,        /* last-dim stride != 1 or misaligned base pointer */
   PE_ERR_WORKSPACE = -6,     /* workspace NULL or smaller than pe_attn_*_workspace_bytes */
   PE_ERR_LAUNCH = -7,        /* a kernel launch failed (hipGetLastError) */
-  PE_ERR_NO_DEVICE = -8      /* no gfx950 device is current */
+  PE_ERR_NO_DEVICE = -8,     /* no gfx950 device is current */
+  PE_ERR_SCRATCH_LIMIT = -9  /* pe_attn_fwd_noalloc: workspace need exceeds the static scratch */
 };
 
 /* A (B, H, S, D) tensor view: device pointer, element type, element strides in (B, H, S, D)
@@ -136,6 +137,23 @@ typedef struct {
   int32_t weight_dtype;  /* PE_DTYPE_* of both */
   float eps;             /* RMSNorm eps (the module default is 1e-6) */
 } pe_norm_params;
+
+/* Forward that allocates nothing: pe_attn_fwd with the workspace taken from a static device array
+ * of PE_NOALLOC_SCRATCH_BYTES held by the library on each GPU (from code-object load to process
+ * exit).  No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Calls whose
+ * forward workspace (pe_attn_fwd_workspace_bytes) exceeds the scratch return PE_ERR_SCRATCH_LIMIT.
+ * All calls on one GPU share its scratch: calls that overlap in time on one GPU (different streams
+ * or threads) race and must be serialised by the caller.  Outputs are as for pe_attn_fwd; the
+ * scratch cannot serve pe_attn_bwd (use pe_attn_fwd with a caller workspace for training). */
+#define PE_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+size_t pe_attn_noalloc_scratch_bytes(void);
+int pe_attn_fwd_noalloc(const pe_attn_params* p,
+                        const pe_tensor_t* qc, const pe_tensor_t* qr,
+                        const pe_tensor_t* kc, const pe_tensor_t* kr,
+                        const pe_tensor_t* v,
+                        const float* freqs, const float* delta,
+                        const pe_tensor_t* out, float* lse, void* stream);
 
 /* Forward with the RMSNorm of the raw position projections fused into the PoPE prologue: qr / kr
  * are wq_r(x) / wk_r(x) as (B,H,S,Dr) views of (B,S,H*Dr) rows, and each token's H*Dr features are

@@ -20,6 +20,7 @@ PE_CAUSAL_NONE, PE_CAUSAL_TOP_LEFT, PE_CAUSAL_BOTTOM_RIGHT = 0, 1, 2
 ERRORS = {
     "PE_OK": 0, "PE_ERR_NULL": -1, "PE_ERR_SHAPE": -2, "PE_ERR_HEAD_DIM": -3, "PE_ERR_MODE": -4,
     "PE_ERR_STRIDE": -5, "PE_ERR_WORKSPACE": -6, "PE_ERR_LAUNCH": -7, "PE_ERR_NO_DEVICE": -8,
+    "PE_ERR_SCRATCH_LIMIT": -9,
 }
 
 # every symbol include/pe_attn.h declares
@@ -27,7 +28,7 @@ EXPORTED = [
     "pe_attn_check", "pe_attn_fwd_workspace_bytes", "pe_attn_bwd_workspace_bytes", "pe_attn_fwd",
     "pe_attn_bwd", "pe_attn_transform", "pe_attn_operand_width", "pe_attn_strerror", "pe_attn_version",
     "pe_attn_set_stage_events", "pe_attn_transform_bwd_workspace_bytes", "pe_attn_transform_bwd",
-    "pe_attn_fwd_normed", "pe_rmsnorm_fwd",
+    "pe_attn_fwd_normed", "pe_rmsnorm_fwd", "pe_attn_fwd_noalloc", "pe_attn_noalloc_scratch_bytes",
 ]
 
 # kernel stages bracketed by pe_attn_set_stage_events
@@ -112,6 +113,10 @@ def lib():
             i32, i64 = ctypes.c_int32, ctypes.c_int64
             L.pe_rmsnorm_fwd.argtypes = [vp, i32, i64, i64, i32, vp, i32, ctypes.c_float, vp, i32, i64, vp]
             L.pe_rmsnorm_fwd.restype = ctypes.c_int
+            L.pe_attn_fwd_noalloc.argtypes = [P, T, T, T, T, T, vp, vp, T, vp, vp]
+            L.pe_attn_fwd_noalloc.restype = ctypes.c_int
+            L.pe_attn_noalloc_scratch_bytes.argtypes = []
+            L.pe_attn_noalloc_scratch_bytes.restype = sz
             L.pe_attn_set_stage_events.argtypes = [vp]
             L.pe_attn_set_stage_events.restype = ctypes.c_int
             _lib = L

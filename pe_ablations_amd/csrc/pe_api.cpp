@@ -1,7 +1,8 @@
-// C-ABI entry points of libpe_attn.so (declared in include/pe_attn.h).  Host code only: validates
-// the parameter block, carves the caller's workspace and enqueues the kernels on the caller's
-// stream.  No allocation, no synchronisation, no global mutable state beyond a per-device
-// "is this a gfx950" flag computed once.
+// C-ABI entry points of libpe_attn.so (declared in include/pe_attn.h).  Host code only (plus the
+// static scratch array of pe_attn_fwd_noalloc): validates the parameter block, carves the
+// caller's workspace and enqueues the kernels on the caller's stream.  No allocation, no
+// synchronisation; the only global mutable state is a per-device "is this a gfx950" flag and the
+// per-device address of the static scratch, each computed once under a mutex.
 #include <hip/hip_runtime.h>
 #include <string.h>
 #include <atomic>
@@ -174,6 +175,7 @@ const char* pe_attn_strerror(int code) {
     case PE_ERR_WORKSPACE: return "pe_attn: workspace missing or too small";
     case PE_ERR_LAUNCH: return "pe_attn: kernel launch failed";
     case PE_ERR_NO_DEVICE: return "pe_attn: current device is not an MI355X (gfx950)";
+    case PE_ERR_SCRATCH_LIMIT: return "pe_attn: the call needs more than the library's static scratch (pe_attn_noalloc_scratch_bytes); use the workspace entry point";
     default: return "pe_attn: unknown error";
   }
 }
@@ -346,6 +348,55 @@ int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
                 const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,
                 void* fwd_workspace, size_t fwd_ws_bytes, void* stream) {
   return fwd_impl(p, nullptr, qc, qr, kc, kr, v, freqs, delta, out, lse, fwd_workspace, fwd_ws_bytes, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Library-owned scratch for pe_attn_fwd_noalloc: the forward workspace (transformed operands, value
+// repack, query phase table) of calls that may not allocate.  Each GPU the library runs on holds
+// its own copy from code-object load until the process ends.  In host code `scratch` names a
+// host-side stand-in, never the device memory: its address on the current device comes from
+// hipGetSymbolAddress, once per device, and only that pointer is handed to kernels.
+__device__ __align__(256) char scratch[PE_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];  // per device ordinal; nullptr until resolved
+
+// device address of `scratch` on the current device (resolved on the first call per device)
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return PE_ERR_NO_DEVICE;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return PE_ERR_LAUNCH;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return PE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t pe_attn_noalloc_scratch_bytes(void) { return PE_NOALLOC_SCRATCH_BYTES; }
+
+int pe_attn_fwd_noalloc(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                        const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                        const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,
+                        void* stream) {
+  int rc = pe_attn_check(p);
+  if (rc) return rc;
+  if (layout(p).fwd_total > PE_NOALLOC_SCRATCH_BYTES) return PE_ERR_SCRATCH_LIMIT;
+  if ((rc = device_ok())) return rc;
+  void* ws = nullptr;
+  if ((rc = scratch_on_current_device(&ws))) return rc;
+  // every byte the kernels read from the workspace is written earlier in the same call (operand
+  // rows including their zero padding, the phase table, the value repack), so nothing is cleared
+  return fwd_impl(p, nullptr, qc, qr, kc, kr, v, freqs, delta, out, lse, ws, PE_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int pe_attn_fwd_normed(const pe_attn_params* p, const pe_norm_params* n, const pe_tensor_t* qc,

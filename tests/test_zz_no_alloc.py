@@ -1,0 +1,78 @@
+"""pe_attn_fwd_noalloc: the forward with its workspace in the library's static device scratch.
+
+Called through the C ABI (ctypes) and compared with pe_attn_fwd on a caller workspace: both run the
+same kernels on the same operands, so out and lse must agree bit for bit.  Two calls in a row, the
+second on a smaller problem, check that the shared scratch carries nothing over from the last call;
+a problem whose workspace exceeds the scratch must be refused with PE_ERR_SCRATCH_LIMIT before any
+launch."""
+
+import ctypes
+import math
+
+import pytest
+import torch
+
+from pe_ablations_amd import _lib
+from pe_ablations_amd.functional import _params, _tensor
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(cuda, B, H, S, D, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, S, H, D, generator=g).to(dtype).to(cuda).transpose(1, 2) for _ in range(3))
+    freqs = (10000.0 ** (-(torch.arange(D, dtype=torch.float32) / D))).to(cuda)
+    delta = (torch.rand(H, D, generator=g) * (-2 * math.pi)).to(cuda)
+    cfg = dict(mode=_lib.PE_MODE_POPE, dtype=_lib.PE_DTYPE_BF16 if dtype == torch.bfloat16 else _lib.PE_DTYPE_FP32,
+               causal=_lib.PE_CAUSAL_TOP_LEFT, start_pos_q=0, start_pos_k=0, qk_norm=False,
+               scale=1.0 / math.sqrt(D), mscale=1.0)
+    return q, k, v, freqs, delta, cfg
+
+
+def _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc):
+    p = _params(cfg, q, k, v, None, delta)
+    B, H, S, D = q.shape
+    out = torch.empty((B, S, H, D), dtype=q.dtype, device=cuda).transpose(1, 2)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=cuda)
+    stream = torch.cuda.current_stream(cuda).cuda_stream
+    args = (ctypes.byref(p), ctypes.byref(_tensor(None)), ctypes.byref(_tensor(q)), ctypes.byref(_tensor(None)),
+            ctypes.byref(_tensor(k)), ctypes.byref(_tensor(v)), freqs.data_ptr(), delta.data_ptr(),
+            ctypes.byref(_tensor(out)), lse.data_ptr())
+    if noalloc:
+        rc = L.pe_attn_fwd_noalloc(*args, stream)
+    else:
+        nb = L.pe_attn_fwd_workspace_bytes(ctypes.byref(p))
+        ws = torch.empty(nb, dtype=torch.uint8, device=cuda)
+        rc = L.pe_attn_fwd(*args, ws.data_ptr(), nb, stream)
+    torch.cuda.synchronize()
+    return rc, out, lse
+
+
+def test_noalloc_forward_matches_workspace_forward(cuda):
+    L = _lib.lib()
+    limit = L.pe_attn_noalloc_scratch_bytes()
+    assert limit == 128 << 20
+    for B, H, S, D, seed in ((2, 4, 1000, 64, 1), (1, 2, 300, 128, 2)):   # the second call is smaller
+        q, k, v, freqs, delta, cfg = _case(cuda, B, H, S, D, seed)
+        rc0, out0, lse0 = _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc=False)
+        rc1, out1, lse1 = _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc=True)
+        assert rc0 == 0 and rc1 == 0, (rc0, rc1)
+        assert torch.equal(out0, out1), (B, H, S, D, (out0.float() - out1.float()).abs().max().item())
+        assert torch.equal(lse0, lse1)
+
+
+def test_noalloc_forward_fp32_and_limit(cuda):
+    L = _lib.lib()
+    q, k, v, freqs, delta, cfg = _case(cuda, 1, 3, 257, 64, 3, dtype=torch.float32)
+    rc0, out0, lse0 = _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc=False)
+    rc1, out1, lse1 = _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc=True)
+    assert rc0 == 0 and rc1 == 0
+    assert torch.equal(out0, out1) and torch.equal(lse0, lse1)
+    # a forward workspace above the scratch (16 heads of 16384 rows: 128 MiB each of q~ and k~) is
+    # refused before anything is enqueued; the tensors are real ones of that size
+    q, k, v, freqs, delta, cfg = _case(cuda, 1, 16, 16384, 128, 4)
+    big = _params(cfg, q, k, v, None, delta)
+    assert L.pe_attn_fwd_workspace_bytes(ctypes.byref(big)) > L.pe_attn_noalloc_scratch_bytes()
+    rc, _, _ = _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc=True)
+    assert rc == _lib.ERRORS["PE_ERR_SCRATCH_LIMIT"]
+    assert "static scratch" in L.pe_attn_strerror(rc).decode()
