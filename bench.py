@@ -29,8 +29,13 @@ Two more workloads, selected with ``--workload`` (the default is the headline ab
   logits have variance 0.02^2 * d_model).  Reported as tokens/s; the roofline entry is
   the attention kernel of the last layer.
 
+* ``decode``: one decoded token per step at the same attention shape (16 heads of D=128) against
+  a cache of 16384 transformed key rows: the new key row is appended to the cache and the new
+  query attends to every cached row (split-key decode kernel).  Reported as cache GB/s against
+  the 8 TB/s HBM peak, the bound of decode.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--workload fwdbwd|fwd|decoder]
+                       [--workload fwdbwd|fwd|decoder|decode]
 """
 
 from __future__ import annotations
@@ -390,13 +395,104 @@ def run_decoder(args, torch, dev) -> dict:
     }
 
 
+DECODE = dict(B=1, H=16, D=128, L=16384)
+
+
+def run_decode(args, torch, dev) -> dict:
+    """One decoded token per step at the 1B attention shape: the new key row is transformed into the
+    cache (pe_attn_cache_append) and the new query attends to all L cached rows (pe_attn_decode,
+    split-key kernel + merge).  Decode is bound by reading the cache, so the roofline entry is HBM
+    bandwidth over the cache bytes one step must read: L rows of transformed keys (2D bf16) and
+    values (D bf16) per head."""
+    from pe_ablations_amd.functional import cache_widths, pe_attention_decode, pe_cache_append
+
+    B, H, D, L = DECODE["B"], DECODE["H"], DECODE["D"], DECODE["L"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    k = torch.randn(B, H, L, D, generator=g, device=dev).to(bf)
+    v = torch.randn(B, H, L, D, generator=g, device=dev).to(bf)
+    q = torch.randn(B, H, 1, D, generator=g, device=dev).to(bf)
+    delta = torch.rand(H, D, generator=g, device=dev) * (-2 * math.pi)
+    freqs = (10000.0 ** (-(torch.arange(0, D, dtype=torch.float32) / D))).to(dev)
+    wk, wv = cache_widths(mode="pope", d_pe=D, d_v=D)
+    kc = torch.zeros(B, H, L, wk, dtype=bf, device=dev)
+    vc = torch.zeros(B, H, L, wv, dtype=bf, device=dev)
+    with torch.inference_mode():
+        pe_cache_append(k[:, :, :L - 1], v[:, :, :L - 1], kc, vc, start_pos=0, freqs=freqs, delta=delta)
+
+        def step():
+            pe_cache_append(k[:, :, L - 1:], v[:, :, L - 1:], kc, vc, start_pos=L - 1, freqs=freqs, delta=delta)
+            return pe_attention_decode(q, kc, vc, L, d_v=D, freqs=freqs, scale=1.0 / math.sqrt(D))
+
+        log(f"bench: decode warmup {args.warmup} steps (B={B} H={H} D={D}, {L} cached rows)")
+        for _ in range(args.warmup):
+            out = step()
+        torch.cuda.synchronize()
+        if not torch.isfinite(out.float()).all():
+            raise RuntimeError("non-finite decode output")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = B * H * L * (wk + wv) * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "fused PoPE KV-cache decode: cache GB/s per decoded token @16k cached rows, D=128; % of HBM peak",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "host_ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) keys / values / query, delta ~ U(-2pi,0) per head)",
+        "config": {"workload": "one decoded token: cache append + split-key decode attention", "B": B, "H": H,
+                   "D": D, "cached_rows": L, "parallelism": "single GPU"},
+        "roofline": {"kernel": "decode_split_kernel + decode_merge_kernel + cache append", "bound": "hbm",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": nbytes},
+    }
+
+
+def decode_cpu_baseline(torch) -> dict:
+    """The oracle's attention of one query against L cached rows (fp32 CPU, all host threads), one
+    pass per head: the same arithmetic the decode step performs."""
+    from oracle import pe_oracle as O
+    B, H, D, L = DECODE["B"], DECODE["H"], DECODE["D"], DECODE["L"]
+    g = torch.Generator().manual_seed(0)
+    k, v, q = torch.randn(L, D, generator=g), torch.randn(L, D, generator=g), torch.randn(1, D, generator=g)
+    delta = torch.rand(D, generator=g) * (-2 * math.pi)
+    freqs = O.pope_freqs(D)
+    O.pope_attention_chunked(q, k, v, freqs, delta, scale=1.0 / math.sqrt(D), start_q=L - 1)
+    t0 = time.perf_counter()
+    for _ in range(H):
+        O.pope_attention_chunked(q, k, v, freqs, delta, scale=1.0 / math.sqrt(D), start_q=L - 1)
+    dt = time.perf_counter() - t0
+    wk = 2 * D
+    return {"value": B * H * L * (wk + D) * 2 / dt / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle pope_attention_chunked of 1 query against {L} keys, fp32, {H} heads one after "
+                      f"another ({dt:.3f} s); bytes counted as the GPU cache bytes of the same step",
+            "seconds": dt}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default fwdbwd 50, fwd 100, decoder 5)")
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps (default fwdbwd 100, fwd 400, decoder 4: about 0.5 s of work)")
-    ap.add_argument("--workload", choices=["fwdbwd", "fwd", "decoder"], default="fwdbwd")
+    ap.add_argument("--workload", choices=["fwdbwd", "fwd", "decoder", "decode"], default="fwdbwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=2)
     ap.add_argument("--cpu-reps", type=int, default=4)
@@ -407,8 +503,10 @@ def main() -> int:
     # chip runs at its socket power limit; after an idle host phase its clock and power state need
     # a few hundred milliseconds to settle, and timing from a 3-step warm-up measured the forward
     # 7-9 % and the fwd+bwd step 1.7 % slower than the settled state.
-    args.steps = args.steps if args.steps is not None else {"decoder": 5, "fwd": 100, "fwdbwd": 50}[args.workload]
-    args.warmup = args.warmup if args.warmup is not None else {"decoder": 4, "fwd": 400, "fwdbwd": 100}[args.workload]
+    args.steps = args.steps if args.steps is not None else {"decoder": 5, "fwd": 100, "fwdbwd": 50,
+                                                            "decode": 200}[args.workload]
+    args.warmup = args.warmup if args.warmup is not None else {"decoder": 4, "fwd": 400, "fwdbwd": 100,
+                                                               "decode": 200}[args.workload]
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -425,6 +523,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if dec:
         res = run_decoder(args, torch, dev)
+    elif args.workload == "decode":
+        res = run_decode(args, torch, dev)
     else:
         res = run_attention(args, torch, dev, backward=args.workload == "fwdbwd")
     props = torch.cuda.get_device_properties(dev)
@@ -434,6 +534,9 @@ def main() -> int:
         if dec:
             log(f"bench: CPU baseline (decoder, {args.cpu_tokens} tokens)")
             cb = decoder_cpu_baseline(torch, model, ids, args.cpu_tokens)
+        elif args.workload == "decode":
+            log("bench: CPU baseline (decode)")
+            cb = decode_cpu_baseline(torch)
         else:
             log(f"bench: CPU baseline ({args.cpu_heads} heads)")
             cb = cpu_baseline(args.cpu_heads, args.cpu_reps, backward=args.workload == "fwdbwd")

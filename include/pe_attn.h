@@ -171,6 +171,38 @@ int pe_attn_fwd_normed(const pe_attn_params* p, const pe_norm_params* n,
                        const pe_tensor_t* out, float* lse,
                        void* fwd_workspace, size_t fwd_ws_bytes, void* stream);
 
+/* KV-cache decode: the cache path of FPoPEGroupedQueryAttentionWithCache.forward
+ * (src/model/fpope_attention.py:226-327).  The reference caches the transformed keys
+ * [k_c | PoPE(k_r)] and the values (:283-299) and attends to the first cache_len rows with SDPA under
+ * a bottom-right causal mask (:301-324).  Here the caches are caller-owned device buffers:
+ *   k_cache (B, Hkv, capacity, pe_attn_operand_width(p)) in p->dtype: the library's operand rows
+ *           [content | transform | zero pad], whose first Dc + 2*Dr (PoPE) columns are the
+ *           reference's cached key layout;
+ *   v_cache (B, Hkv, capacity, pe_attn_value_width(p)) in p->dtype, zero-padded.
+ *
+ * pe_attn_cache_append: transforms p->Sk new key rows (kc / kr / v views (B, Hkv, Sk, *), phases at
+ * positions start_pos_k + s, key phase bias delta) and writes them, with their values, to cache rows
+ * start_pos_k .. start_pos_k + Sk - 1 (the reference's k_cache[:, :, start_pos:start_pos+S] = k_new,
+ * :294-296).  start_pos_k + Sk must not exceed capacity.
+ *
+ * pe_attn_decode: p->Sq new query rows (qc / qr views (B, Hq, Sq, *), phases at start_pos_q + t)
+ * attend to the first p->Sk cached rows (Sk = the reference's cache_len, new rows included);
+ * p->causal BOTTOM_RIGHT gives the reference's mask, key s visible to query t iff
+ * s <= t + Sk - Sq.  out (B, Hq, Sq, Dv) and lse (B, Hq, Sq) as for pe_attn_fwd.  The work is split
+ * over key ranges whose partial results are merged in a fixed order (bitwise reproducible); the
+ * workspace holds the transformed queries and the partials.  Forward only. */
+int pe_attn_value_width(const pe_attn_params* p);
+int pe_attn_cache_append(const pe_attn_params* p,
+                         const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                         const float* freqs, const float* delta,
+                         void* k_cache, void* v_cache, int32_t capacity, void* stream);
+size_t pe_attn_decode_workspace_bytes(const pe_attn_params* p);
+int pe_attn_decode(const pe_attn_params* p,
+                   const pe_tensor_t* qc, const pe_tensor_t* qr,
+                   const void* k_cache, const void* v_cache, int32_t capacity,
+                   const float* freqs, const pe_tensor_t* out, float* lse,
+                   void* workspace, size_t ws_bytes, void* stream);
+
 /* RMSNorm forward over the last dim of a (rows, n) view with unit element stride
  * (src/model/normalization.py:7-27, the module on hidden states and on the position
  * projections): y = (x * rsqrt(mean(x^2) + eps)).type_as(x) * weight, in fp32; y_dtype must be

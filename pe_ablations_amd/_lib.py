@@ -29,6 +29,7 @@ EXPORTED = [
     "pe_attn_bwd", "pe_attn_transform", "pe_attn_operand_width", "pe_attn_strerror", "pe_attn_version",
     "pe_attn_set_stage_events", "pe_attn_transform_bwd_workspace_bytes", "pe_attn_transform_bwd",
     "pe_attn_fwd_normed", "pe_rmsnorm_fwd", "pe_attn_fwd_noalloc", "pe_attn_noalloc_scratch_bytes",
+    "pe_attn_value_width", "pe_attn_cache_append", "pe_attn_decode_workspace_bytes", "pe_attn_decode",
 ]
 
 # kernel stages bracketed by pe_attn_set_stage_events
@@ -117,6 +118,14 @@ def lib():
             L.pe_attn_fwd_noalloc.restype = ctypes.c_int
             L.pe_attn_noalloc_scratch_bytes.argtypes = []
             L.pe_attn_noalloc_scratch_bytes.restype = sz
+            L.pe_attn_value_width.argtypes = [P]
+            L.pe_attn_value_width.restype = ctypes.c_int
+            L.pe_attn_cache_append.argtypes = [P, T, T, T, vp, vp, vp, vp, ctypes.c_int32, vp]
+            L.pe_attn_cache_append.restype = ctypes.c_int
+            L.pe_attn_decode_workspace_bytes.argtypes = [P]
+            L.pe_attn_decode_workspace_bytes.restype = sz
+            L.pe_attn_decode.argtypes = [P, T, T, vp, vp, ctypes.c_int32, vp, T, vp, vp, sz, vp]
+            L.pe_attn_decode.restype = ctypes.c_int
             L.pe_attn_set_stage_events.argtypes = [vp]
             L.pe_attn_set_stage_events.restype = ctypes.c_int
             _lib = L

@@ -14,6 +14,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
+from .fpope_attention import KVCache, cached_attention
 from .functional import pe_attention
 from .normalization import QKNorm
 
@@ -34,10 +35,20 @@ class GroupedQueryAttention(nn.Module):
         self.wo = nn.Linear(num_heads * self.head_dim, hidden_dim, bias=False)
         self.qk_norm = QKNorm(self.head_dim) if use_qk_norm else None
         self.rope = rope
+        # KV cache for generation (an addition: the reference's RoPE / no-PE module has no cache and
+        # its generate re-runs the whole sequence, src/model/transformer.py:389-446)
+        self.max_cache_len = 2048
+        self.cache = KVCache()
 
-    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0) -> torch.Tensor:
+    def reset_cache(self) -> None:
+        self.cache.reset()
+
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0,
+                use_cache: bool = False) -> torch.Tensor:
         """``mask`` must be None (the reference's TransformerBlock passes None; an explicit dense
-        mask would need a masked kernel variant that this build does not provide)."""
+        mask would need a masked kernel variant that this build does not provide).  ``use_cache``
+        (inference only) keeps the rotated, normalised keys of earlier calls and attends the new
+        queries to all of them under the bottom-right causal mask."""
         if mask is not None:
             raise NotImplementedError("GroupedQueryAttention: only the causal (mask=None) path is fused")
         B, S, _ = x.shape
@@ -45,6 +56,14 @@ class GroupedQueryAttention(nn.Module):
         k = self.wk(x).view(B, S, self.num_kv_heads, self.head_dim).transpose(1, 2)
         v = self.wv(x).view(B, S, self.num_kv_heads, self.head_dim).transpose(1, 2)
         norm = self.qk_norm is not None
+        if use_cache:
+            rope = {} if self.rope is None else dict(freqs=self.rope.kernel_inv_freq(),
+                                                     rope_mscale=self.rope.kernel_mscale())
+            out = cached_attention(self.cache, self.max_cache_len, start_pos, q=q, k=k, v=v,
+                                   mode="rope" if self.rope is not None else "none", qk_norm=norm,
+                                   scale=1.0 / (self.head_dim ** 0.5), d_v=self.head_dim, **rope)
+            out = out.transpose(1, 2).reshape(B, S, -1)
+            return self.wo(out if torch.is_autocast_enabled() else out.to(x.dtype))
         if self.rope is not None:
             out = pe_attention(q, k, v, mode="rope", freqs=self.rope.kernel_inv_freq(),
                                rope_mscale=self.rope.kernel_mscale(), qk_norm=norm,

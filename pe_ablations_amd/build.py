@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libpe_attn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["pe_api.cpp", "pe_prep.hip", "pe_norm.hip", "pe_fwd.hip", "pe_bwd.hip"]
+SOURCES = ["pe_api.cpp", "pe_prep.hip", "pe_norm.hip", "pe_fwd.hip", "pe_bwd.hip", "pe_decode.hip"]
 ARCH = "gfx950"
 
 

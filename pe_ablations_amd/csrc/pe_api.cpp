@@ -5,6 +5,7 @@
 // per-device address of the static scratch, each computed once under a mutex.
 #include <hip/hip_runtime.h>
 #include <string.h>
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -397,6 +398,123 @@ int pe_attn_fwd_noalloc(const pe_attn_params* p, const pe_tensor_t* qc, const pe
   // every byte the kernels read from the workspace is written earlier in the same call (operand
   // rows including their zero padding, the phase table, the value repack), so nothing is cleared
   return fwd_impl(p, nullptr, qc, qr, kc, kr, v, freqs, delta, out, lse, ws, PE_NOALLOC_SCRATCH_BYTES, stream);
+}
+
+int pe_attn_value_width(const pe_attn_params* p) {
+  if (pe_attn_check(p) != PE_OK) return -1;
+  return pad_v(p->Dv);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Work split and workspace of pe_attn_decode: transformed queries, then the per-range partials.
+struct DecodePlan {
+  int nqt, nunit;
+  size_t q_bytes, po_off, pm_off, pl_off, total;
+};
+
+DecodePlan decode_plan(const pe_attn_params* p) {
+  DecodePlan d{};
+  const int grp = p->Hq / p->Hkv;
+  d.nqt = (int)(((int64_t)grp * p->Sq + 31) / 32);
+  const int64_t tiles = (int64_t)p->B * p->Hkv * d.nqt;
+  const int nkb = (p->Sk + 31) / 32;
+  // about 2048 waves over the GPU, at least two 32-key blocks per range, a multiple of 4 ranges
+  int64_t nu = (2048 + tiles - 1) / tiles;
+  nu = std::min<int64_t>(nu, (nkb + 1) / 2);
+  nu = std::max<int64_t>(4, std::min<int64_t>(512, (nu + 3) / 4 * 4));
+  d.nunit = (int)nu;
+  const size_t rows = (size_t)tiles * d.nunit * 32;
+  d.q_bytes = align_up((size_t)p->B * p->Hq * p->Sq * pad_qk(qk_width(p)) * esz(p));
+  d.po_off = d.q_bytes;
+  d.pm_off = d.po_off + align_up(rows * pad_v(p->Dv) * 4);
+  d.pl_off = d.pm_off + align_up(rows * 4);
+  d.total = d.pl_off + align_up(rows * 4);
+  return d;
+}
+
+// the parameter block of the new key rows written by pe_attn_cache_append: Sk rows per kv head
+int append_params(const pe_attn_params* p, pe_attn_params* q) {
+  *q = *p;
+  q->Hq = p->Hkv;
+  q->Sq = p->Sk;
+  q->causal = PE_CAUSAL_NONE;
+  return pe_attn_check(q);
+}
+
+}  // namespace
+
+extern "C" {
+
+int pe_attn_cache_append(const pe_attn_params* p, const pe_tensor_t* kc, const pe_tensor_t* kr,
+                         const pe_tensor_t* v, const float* freqs, const float* delta, void* k_cache,
+                         void* v_cache, int32_t capacity, void* stream) {
+  if (!p) return PE_ERR_NULL;
+  pe_attn_params pa;
+  int rc = append_params(p, &pa);
+  if (rc) return rc;
+  if (p->start_pos_k < 0 || capacity <= 0 || (int64_t)p->start_pos_k + p->Sk > capacity) return PE_ERR_SHAPE;
+  if ((rc = check_tensor(kr, p->Dr > 0)) || (rc = check_tensor(kc, p->Dc > 0)) || (rc = check_tensor(v, true)))
+    return rc;
+  if (!k_cache || !v_cache || (p->mode != PE_MODE_NONE && p->Dr > 0 && !freqs)) return PE_ERR_NULL;
+  if ((uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16) return PE_ERR_STRIDE;
+  if ((rc = device_ok())) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  pe::PrepArgs a;
+  fill_prep(a, &pa, 1, kc, kr, freqs, delta, k_cache, pad_qk(qk_width(&pa)));
+  a.dst_rows = capacity;
+  a.dst_row0 = p->start_pos_k;
+  if ((rc = pe::launch_prep(a, s))) return rc;
+  pe_attn_params pv = pa;
+  pv.mode = PE_MODE_NONE; pv.Dc = 0; pv.Dr = p->Dv; pv.qk_l2norm = 0;
+  fill_prep(a, &pv, 1, nullptr, v, nullptr, nullptr, v_cache, pad_v(p->Dv));
+  a.dst_rows = capacity;
+  a.dst_row0 = p->start_pos_k;
+  return pe::launch_prep(a, s);
+}
+
+size_t pe_attn_decode_workspace_bytes(const pe_attn_params* p) {
+  if (pe_attn_check(p) != PE_OK) return 0;
+  return decode_plan(p).total;
+}
+
+int pe_attn_decode(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                   const void* k_cache, const void* v_cache, int32_t capacity, const float* freqs,
+                   const pe_tensor_t* out, float* lse, void* workspace, size_t ws_bytes, void* stream) {
+  int rc = pe_attn_check(p);
+  if (rc) return rc;
+  if (capacity < p->Sk) return PE_ERR_SHAPE;
+  if ((rc = check_tensor(qr, p->Dr > 0)) || (rc = check_tensor(qc, p->Dc > 0)) || (rc = check_tensor(out, true)))
+    return rc;
+  if (!k_cache || !v_cache || !lse || (p->mode != PE_MODE_NONE && p->Dr > 0 && !freqs)) return PE_ERR_NULL;
+  if ((uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16) return PE_ERR_STRIDE;
+  if (out->dtype != p->dtype) return PE_ERR_MODE;
+  const DecodePlan d = decode_plan(p);
+  if (!workspace || ws_bytes < d.total) return PE_ERR_WORKSPACE;
+  if ((rc = device_ok())) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const int dqk = pad_qk(qk_width(p)), dv = pad_v(p->Dv);
+  pe::PrepArgs a;
+  fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws, dqk);
+  if ((rc = pe::launch_prep(a, s))) return rc;
+  pe::DecodeArgs da;
+  memset(&da, 0, sizeof(da));
+  da.q = ws; da.k = k_cache; da.v = v_cache;
+  da.B = p->B; da.Hq = p->Hq; da.Hkv = p->Hkv; da.Sq = p->Sq; da.L = p->Sk; da.cap = capacity;
+  da.causal = p->causal != PE_CAUSAL_NONE;
+  da.off = p->causal == PE_CAUSAL_BOTTOM_RIGHT ? p->Sk - p->Sq : 0;
+  da.scale = p->scale;
+  da.nqt = d.nqt; da.nunit = d.nunit;
+  da.part_o = (float*)(ws + d.po_off);
+  da.part_m = (float*)(ws + d.pm_off);
+  da.part_l = (float*)(ws + d.pl_off);
+  da.o = (void*)out->data; da.o_sb = out->stride[0]; da.o_sh = out->stride[1]; da.o_ss = out->stride[2];
+  da.o_dtype = out->dtype; da.dv_real = p->Dv;
+  da.lse = lse;
+  return pe::launch_decode(p->dtype == PE_DTYPE_BF16 ? 0 : 1, dqk, dv, da, s);
 }
 
 int pe_attn_fwd_normed(const pe_attn_params* p, const pe_norm_params* n, const pe_tensor_t* qc,

@@ -72,6 +72,10 @@ struct PrepArgs {
   // query side only: cos / sin of fl((start_pos + s) * freq) as [S][2][Dr] fp32 (launch_phase_table),
   // read instead of evaluated by the vectorised PoPE prologue; null evaluates them
   const float* tab;
+  // destination rows: (b, h, s) goes to row (b * H + h) * dst_rows + dst_row0 + s of dst; dst_rows
+  // 0 means S (a contiguous (B, H, S, width) buffer).  A KV cache of capacity C takes new rows at
+  // position p with dst_rows = C, dst_row0 = p.
+  int dst_rows, dst_row0;
 };
 int launch_prep(const PrepArgs& a, hipStream_t s);
 // cos / sin of the query phases fl((start + s) * freqs[c]) for s < S, c < Dr into tab [S][2][Dr]
@@ -79,6 +83,26 @@ int launch_prep(const PrepArgs& a, hipStream_t s);
 int launch_phase_table(const float* freqs, int start, int S, int Dr, float* tab, hipStream_t s);
 // PoPE prologue with the RMSNorm fused in: one workgroup per token (all heads)
 int launch_prep_norm(const PrepArgs& a, hipStream_t s);
+
+// Attention of Sq new query rows (transformed, (B, Hq, Sq, DQK) contiguous) against the first L
+// rows of a cache of transformed keys (B, Hkv, cap, DQK) and values (B, Hkv, cap, DV), split over
+// `nunit` key ranges per (b, kv head, 32-row query tile) and merged in range order.
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  int B, Hq, Hkv, Sq, L, cap;
+  int causal, off;  // with causal, key s is visible to query i iff s <= i + off
+  float scale;
+  int nqt;          // 32-row tiles of the (Hq / Hkv) * Sq query rows of one kv head
+  int nunit;        // key ranges per tile, a multiple of 4 (one per wave)
+  float* part_o;    // [B*Hkv][nqt][nunit][32][DV] unnormalised O relative to part_m
+  float* part_m;    // [B*Hkv][nqt][nunit][32] running max of the scaled scores, log2 units
+  float* part_l;    // [B*Hkv][nqt][nunit][32] sum of 2^(score - part_m)
+  void* o; int64_t o_sb, o_sh, o_ss; int o_dtype; int dv_real;
+  float* lse;       // (B, Hq, Sq)
+};
+int launch_decode(int dt, int dqk, int dv, const DecodeArgs& a, hipStream_t s);
 
 // Stand-alone RMSNorm over the last dim of a (rows, n) view.
 struct NormArgs {

@@ -162,6 +162,7 @@ int launch_rmsnorm(const NormArgs& a, hipStream_t s) {
 
 int launch_prep_norm(const PrepArgs& a, hipStream_t s) {
   if (a.mode != 0 || !a.norm_w || ((a.norm_w_dtype | a.xr_dtype | a.dst_dtype) & ~1)) return -4;
+  if (a.dst_rows != 0 || a.dst_row0 != 0) return -2;  // writes contiguous (B, H, S, width) rows only
   if (a.Dr <= 0 || a.Dr % 8 != 0 || a.Dc % 8 != 0 || a.width % 8 != 0 || a.H * (a.Dr / 8) > NT * MAXC) return -3;
   if ((int64_t)a.B * a.S > 0x7fffffff) return -2;
   const bool ok = a.xr_s[3] == 1 && rows_aligned(a.xr, a.xr_dtype, a.xr_s[0], a.xr_s[1], a.xr_s[2]) &&

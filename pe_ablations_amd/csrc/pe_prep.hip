@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
   const int bh = (int)(row / a.S);
   const int h = bh % a.H, b = bh / a.H;
   const float pos = (float)(a.start_pos + s);
-  const int64_t dbase = row * a.width;
+  const int64_t dbase = ((int64_t)bh * (a.dst_rows ? a.dst_rows : a.S) + a.dst_row0 + s) * a.width;
 
   for (int c = lane; c < a.Dc; c += 64) {
     const float x = load_as_float(a.xc, b * a.xc_s[0] + h * a.xc_s[1] + (int64_t)s * a.xc_s[2] + c * a.xc_s[3], a.xc_dtype);
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
   const int bh = (int)(row / a.S);
   const int h = bh % a.H, b = bh / a.H;
   const float pos = (float)(a.start_pos + s);
-  uint16_t* drow = (uint16_t*)a.dst + row * a.width;
+  uint16_t* drow = (uint16_t*)a.dst + ((int64_t)bh * (a.dst_rows ? a.dst_rows : a.S) + a.dst_row0 + s) * a.width;
   const u32x4 xv = *(const u32x4*)((const uint16_t*)a.xr + b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + t * 8);
   const f32x4 f0 = *(const f32x4*)(a.freqs + t * 8), f1 = *(const f32x4*)(a.freqs + t * 8 + 4);
   f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;

@@ -17,7 +17,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .functional import pe_attention
+from .functional import cache_widths, pe_attention, pe_attention_decode, pe_cache_append
 from .normalization import RMSNorm
 
 
@@ -116,11 +116,77 @@ class FPoPEGroupedQueryAttention(nn.Module):
         return self.wo(out.transpose(1, 2).reshape(B, S, -1))
 
 
+class KVCache:
+    """Per-layer cache of transformed keys and values for the decode path.
+
+    ``k_cache`` (B, Hkv, capacity, Wk) holds the library's operand rows [content | transform | zero
+    pad] in the compute dtype (its first Dc + 2*Dr columns are the reference's cached
+    [k_c | PoPE(k_r)], src/model/fpope_attention.py:283-296); ``v_cache`` (B, Hkv, capacity, Wv)
+    the zero-padded values.  New rows are transformed once, when appended; every later step reads
+    them as they are."""
+
+    def __init__(self):
+        self.k = None
+        self.v = None
+        self.length = 0
+
+    def ensure(self, B: int, Hkv: int, capacity: int, wk: int, wv: int, dtype, device) -> None:
+        shape_k, shape_v = (B, Hkv, capacity, wk), (B, Hkv, capacity, wv)
+        if (self.k is None or tuple(self.k.shape) != shape_k or tuple(self.v.shape) != shape_v
+                or self.k.dtype != dtype or self.k.device != device):
+            self.k = torch.zeros(shape_k, dtype=dtype, device=device)
+            self.v = torch.zeros(shape_v, dtype=dtype, device=device)
+
+    def reset(self) -> None:
+        self.k = None
+        self.v = None
+        self.length = 0
+
+
+def cache_compute_dtype(x: torch.Tensor) -> torch.dtype:
+    """bf16 under autocast or for bf16 / fp16 activations, else fp32 (as pe_attention decides)."""
+    if torch.is_autocast_enabled() or x.dtype in (torch.bfloat16, torch.float16):
+        return torch.bfloat16
+    return torch.float32
+
+
+def cached_attention(cache: KVCache, capacity: int, start_pos: int, *, q, k, v, q_c=None, k_c=None, mode: str,
+                     freqs=None, delta=None, scale: float, rope_mscale: float = 1.0, qk_norm: bool = False,
+                     d_v: int) -> torch.Tensor:
+    """Append the new key / value rows at ``start_pos`` and attend the new queries to every cached
+    row with the bottom-right causal mask (src/model/fpope_attention.py:294-324).  The first chunk
+    (start_pos 0) runs the regular causal forward on the same operands; later chunks run the
+    split-key decode kernel over the cache.  Inference only.  Returns (B, Hq, S, d_v)."""
+    if torch.is_grad_enabled():
+        raise RuntimeError("use_cache=True is an inference path: run it under torch.no_grad() / inference_mode")
+    B, Hkv, S = k.shape[0], k.shape[1], k.shape[2]
+    if start_pos < 0 or start_pos + S > capacity:
+        raise ValueError(f"cache rows {start_pos}..{start_pos + S - 1} exceed max_cache_len {capacity}")
+    cdt = cache_compute_dtype(k)
+    wk, wv = cache_widths(mode=mode, d_content=0 if k_c is None else k_c.shape[-1], d_pe=k.shape[-1], d_v=d_v)
+    cache.ensure(B, Hkv, capacity, wk, wv, cdt, k.device)
+    if start_pos == 0:
+        cache.length = 0
+    elif start_pos != cache.length:
+        raise ValueError(f"the cache holds {cache.length} rows; the next chunk must start there, not at {start_pos}")
+    pe_cache_append(k, v, cache.k, cache.v, start_pos=start_pos, mode=mode, k_c=k_c, freqs=freqs, delta=delta,
+                    rope_mscale=rope_mscale, qk_norm=qk_norm)
+    cache.length = start_pos + S
+    if start_pos == 0:
+        return pe_attention(q, k, v, mode=mode, q_c=q_c, k_c=k_c, freqs=freqs, delta=delta, scale=scale, causal=True,
+                            rope_mscale=rope_mscale, qk_norm=qk_norm, compute_dtype=cdt)
+    return pe_attention_decode(q, cache.k, cache.v, cache.length, d_v=d_v, mode=mode, q_c=q_c, freqs=freqs,
+                               scale=scale, causal="bottom_right", start_pos_q=start_pos, rope_mscale=rope_mscale,
+                               qk_norm=qk_norm)
+
+
 class FPoPEGroupedQueryAttentionWithCache(FPoPEGroupedQueryAttention):
-    """KV-cache variant (src/model/fpope_attention.py:184-327).  The cache holds the raw content
-    keys, normalised position keys and values; the kernel re-applies the key transform with
-    absolute positions 0..L-1, which reproduces the reference's cached [k_c | PoPE(k_r)] exactly,
-    and masks bottom-right (query i sees keys <= L - S + i)."""
+    """KV-cache variant (src/model/fpope_attention.py:184-327): same constructor, ``k_cache`` /
+    ``v_cache`` / ``cache_len`` / ``reset_cache`` and ``forward(x, mask, start_pos, use_cache)``.
+    With ``use_cache`` the new keys are transformed once into the cache (pe_attn_cache_append) and
+    the new queries attend to all ``cache_len`` cached rows under the bottom-right mask
+    (pe_attn_decode); chunks must arrive in order (start_pos = the current cache length, or 0 to
+    start over)."""
 
     def __init__(self, hidden_dim: int, num_heads: int, num_kv_heads: int, head_dim: int = 64,
                  d_rope: int = 32, use_qk_norm: bool = True, fpope: Optional[nn.Module] = None,
@@ -128,16 +194,22 @@ class FPoPEGroupedQueryAttentionWithCache(FPoPEGroupedQueryAttention):
         super().__init__(hidden_dim, num_heads, num_kv_heads, head_dim, d_rope, use_qk_norm, fpope,
                          d_content=d_content)
         self.max_cache_len = max_cache_len
-        self.register_buffer("k_cache", None, persistent=False)
-        self.register_buffer("v_cache", None, persistent=False)
-        self.kr_cache: Optional[torch.Tensor] = None
-        self.cache_len = 0
+        self.cache = KVCache()
+
+    @property
+    def k_cache(self) -> Optional[torch.Tensor]:
+        return self.cache.k
+
+    @property
+    def v_cache(self) -> Optional[torch.Tensor]:
+        return self.cache.v
+
+    @property
+    def cache_len(self) -> int:
+        return self.cache.length
 
     def reset_cache(self) -> None:
-        self.k_cache = None
-        self.v_cache = None
-        self.kr_cache = None
-        self.cache_len = 0
+        self.cache.reset()
 
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0,
                 use_cache: bool = False) -> torch.Tensor:
@@ -145,21 +217,16 @@ class FPoPEGroupedQueryAttentionWithCache(FPoPEGroupedQueryAttention):
             return super().forward(x, mask, start_pos)
         B, S, _ = x.shape
         q_c, k_c, q_r, k_r, v = self._project(x)
-        if self.kr_cache is None:
-            if k_c is not None:
-                self.k_cache = torch.zeros(B, self.num_kv_heads, self.max_cache_len, self.d_content,
-                                           dtype=k_c.dtype, device=x.device)
-            self.kr_cache = torch.zeros(B, self.num_kv_heads, self.max_cache_len, self.d_rope,
-                                        dtype=k_r.dtype, device=x.device)
-            self.v_cache = torch.zeros(B, self.num_kv_heads, self.max_cache_len, self.head_dim,
-                                       dtype=v.dtype, device=x.device)
-        if k_c is not None:
-            self.k_cache[:, :, start_pos:start_pos + S] = k_c
-        self.kr_cache[:, :, start_pos:start_pos + S] = k_r
-        self.v_cache[:, :, start_pos:start_pos + S] = v
-        self.cache_len = start_pos + S
-        L = self.cache_len
-        k_c_all = self.k_cache[:, :, :L] if k_c is not None else None
-        out = self._attend(q_c, k_c_all, q_r, self.kr_cache[:, :, :L], self.v_cache[:, :, :L],
-                           start_pos, 0, "bottom_right")
-        return self.wo(out.transpose(1, 2).reshape(B, S, -1))
+        if self.fpope is None:
+            # the reference's no-PE fallback keys [k_c | k_r | k_r] (:148-151), untransformed
+            dt = v.dtype
+            qa = torch.cat(([q_c] if q_c is not None else []) + [q_r.to(dt), q_r.to(dt)], dim=-1)
+            ka = torch.cat(([k_c] if k_c is not None else []) + [k_r.to(dt), k_r.to(dt)], dim=-1)
+            out = cached_attention(self.cache, self.max_cache_len, start_pos, q=qa, k=ka, v=v, mode="none",
+                                   scale=self.scale, d_v=self.head_dim)
+        else:
+            out = cached_attention(self.cache, self.max_cache_len, start_pos, q=q_r, k=k_r, v=v, q_c=q_c, k_c=k_c,
+                                   mode="pope", freqs=self.fpope.kernel_freqs(), delta=self.fpope.kernel_delta(),
+                                   scale=self.scale, d_v=self.head_dim)
+        out = out.transpose(1, 2).reshape(B, S, -1)
+        return self.wo(out if torch.is_autocast_enabled() else out.to(x.dtype))

@@ -346,3 +346,132 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
                               y.stride(0), _stream(x.device))
     _lib.check(rc)
     return y.view(*x.shape[:-1], n)
+
+
+# ------------------------------------------------------------------------------------------------
+# KV cache (src/model/fpope_attention.py:226-327): caches of transformed keys and values, and the
+# split-key decode attention over them.  Inference only.
+
+def _cache_params(*, B, Hq, Hkv, Sq, Sk, Dc, Dr, Dv, mode, dtype, causal, start_q, start_k, scale,
+                  mscale, qk_norm, delta) -> _lib.PeParams:
+    p = _lib.PeParams()
+    p.B, p.Hq, p.Hkv, p.Sq, p.Sk = B, Hq, Hkv, Sq, Sk
+    p.Dc, p.Dr, p.Dv = Dc, Dr, Dv
+    p.mode, p.dtype, p.causal = mode, dtype, causal
+    p.start_pos_q, p.start_pos_k = int(start_q), int(start_k)
+    p.qk_l2norm = int(qk_norm)
+    p.scale, p.rope_mscale = float(scale), float(mscale)
+    p.delta_head_stride = 0 if (delta is None or delta.dim() == 1) else delta.shape[-1]
+    return p
+
+
+def cache_widths(*, mode: str = "pope", d_content: int = 0, d_pe: int, d_v: int) -> tuple[int, int]:
+    """(key width, value width) of the cache rows pe_cache_append writes: the library's transformed
+    operand rows [content | transform | zero pad] and the zero-padded value rows."""
+    m = _MODES[mode]
+    p = _cache_params(B=1, Hq=1, Hkv=1, Sq=1, Sk=1, Dc=d_content, Dr=d_pe, Dv=d_v, mode=m,
+                      dtype=_lib.PE_DTYPE_BF16, causal=_lib.PE_CAUSAL_NONE, start_q=0, start_k=0, scale=1.0,
+                      mscale=1.0, qk_norm=False, delta=None)
+    L = _lib.lib()
+    _lib.check(L.pe_attn_check(ref(p)))
+    return L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p))
+
+
+def _check_cache(k_cache, v_cache, B, Hkv, wk, wv, cdt, dev):
+    for name, c, wdt in (("k_cache", k_cache, wk), ("v_cache", v_cache, wv)):
+        if c.dim() != 4 or tuple(c.shape[:2]) != (B, Hkv) or c.shape[3] != wdt:
+            raise ValueError(f"{name} must be (B, Hkv, capacity, {wdt}) = ({B}, {Hkv}, C, {wdt}), got {tuple(c.shape)}")
+        if not c.is_contiguous() or c.dtype != cdt or c.device != dev or c.data_ptr() % 16:
+            raise ValueError(f"{name} must be a contiguous, 16-byte aligned {cdt} tensor on {dev}")
+    if k_cache.shape[2] != v_cache.shape[2]:
+        raise ValueError("k_cache and v_cache capacities differ")
+
+
+def pe_cache_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *,
+                    start_pos: int, mode: str = "pope", k_c: Optional[torch.Tensor] = None,
+                    freqs: Optional[torch.Tensor] = None, delta: Optional[torch.Tensor] = None,
+                    rope_mscale: float = 1.0, qk_norm: bool = False) -> None:
+    """Write the transformed key rows of k (B, Hkv, S, Dr) [with content k_c (B, Hkv, S, Dc)] and
+    the value rows v (B, Hkv, S, Dv) to cache rows start_pos .. start_pos + S - 1, phases at those
+    positions (the reference's k_cache[:, :, start_pos:start_pos+S] = [k_c | PoPE(k_r)],
+    src/model/fpope_attention.py:294-296).  The caches are (B, Hkv, capacity, width) in the compute
+    dtype with the widths of ``cache_widths``."""
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (k, v, k_c, freqs, delta)):
+        raise RuntimeError("the KV-cache path is inference only (run it under torch.no_grad())")
+    if not k.is_cuda:
+        raise RuntimeError("pe_cache_append runs on the GPU only (got a CPU tensor)")
+    m = _MODES[mode]
+    check_operands(k, k, v, k_c, k_c, freqs if m != _lib.PE_MODE_NONE else None, delta, mode=m)
+    k, v, k_c = (_prep_in(t) for t in (k, v, k_c))
+    freqs = freqs.float().contiguous() if m != _lib.PE_MODE_NONE else None
+    delta = None if delta is None else delta.float().contiguous()
+    B, Hkv, S, Dr = k.shape
+    Dc = 0 if k_c is None else k_c.shape[-1]
+    cdt = k_cache.dtype
+    dt = _dtype_code(cdt)
+    p = _cache_params(B=B, Hq=Hkv, Hkv=Hkv, Sq=S, Sk=S, Dc=Dc, Dr=Dr, Dv=v.shape[-1], mode=m, dtype=dt,
+                      causal=_lib.PE_CAUSAL_NONE, start_q=start_pos, start_k=start_pos, scale=1.0,
+                      mscale=rope_mscale, qk_norm=qk_norm, delta=delta)
+    L = _lib.lib()
+    _lib.check(L.pe_attn_check(ref(p)))
+    _check_cache(k_cache, v_cache, B, Hkv, L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p)), cdt,
+                 k.device)
+    if start_pos < 0 or start_pos + S > k_cache.shape[2]:
+        raise ValueError(f"rows {start_pos}..{start_pos + S - 1} do not fit a cache of capacity {k_cache.shape[2]}")
+    with torch.cuda.device(k.device):
+        rc = L.pe_attn_cache_append(ref(p), ref(_tensor(k_c)), ref(_tensor(k)), ref(_tensor(v)), _ptr(freqs),
+                                    _ptr(delta), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2],
+                                    _stream(k.device))
+    _lib.check(rc)
+
+
+def pe_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_len: int, *,
+                        d_v: int, mode: str = "pope", q_c: Optional[torch.Tensor] = None,
+                        freqs: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                        causal="bottom_right", start_pos_q: Optional[int] = None, rope_mscale: float = 1.0,
+                        qk_norm: bool = False, return_lse: bool = False):
+    """Attention of the new queries q (B, Hq, Sq, Dr) [content q_c] against the first ``cache_len``
+    rows of caches filled by pe_cache_append (src/model/fpope_attention.py:301-324): bottom-right
+    causal mask by default, query phases at start_pos_q (default cache_len - Sq), GQA by index.
+    Returns out (B, Hq, Sq, d_v) in the cache dtype [and lse (B, Hq, Sq)]."""
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, q_c, freqs)):
+        raise RuntimeError("the KV-cache path is inference only (run it under torch.no_grad())")
+    if not q.is_cuda:
+        raise RuntimeError("pe_attention_decode runs on the GPU only (got a CPU tensor)")
+    m = _MODES[mode]
+    if q.dim() != 4:
+        raise ValueError(f"q must be (B, Hq, Sq, D), got shape {tuple(q.shape)}")
+    if m != _lib.PE_MODE_NONE:
+        want = q.shape[-1] if m == _lib.PE_MODE_POPE else q.shape[-1] // 2
+        if freqs is None or freqs.dim() != 1 or freqs.shape[0] != want or freqs.device != q.device:
+            raise ValueError(f"freqs must be a ({want},) tensor on {q.device}")
+    if q_c is not None and (q_c.dim() != 4 or tuple(q_c.shape[:3]) != tuple(q.shape[:3]) or q_c.device != q.device):
+        raise ValueError(f"q_c {tuple(q_c.shape)} must share the rows of q {tuple(q.shape)}")
+    q, q_c = _prep_in(q), _prep_in(q_c)
+    freqs = freqs.float().contiguous() if m != _lib.PE_MODE_NONE else None
+    B, Hq, Sq, Dr = q.shape
+    Hkv = k_cache.shape[1]
+    Dc = 0 if q_c is None else q_c.shape[-1]
+    dqk = Dc + (2 * Dr if m == _lib.PE_MODE_POPE else Dr)
+    scale = dqk ** -0.5 if scale is None else scale
+    cdt = k_cache.dtype
+    start_q = cache_len - Sq if start_pos_q is None else start_pos_q
+    p = _cache_params(B=B, Hq=Hq, Hkv=Hkv, Sq=Sq, Sk=cache_len, Dc=Dc, Dr=Dr, Dv=d_v, mode=m,
+                      dtype=_dtype_code(cdt), causal=_CAUSAL[causal], start_q=start_q, start_k=0, scale=scale,
+                      mscale=rope_mscale, qk_norm=qk_norm, delta=None)
+    L = _lib.lib()
+    _lib.check(L.pe_attn_check(ref(p)))
+    _check_cache(k_cache, v_cache, B, Hkv, L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p)), cdt,
+                 q.device)
+    if cache_len > k_cache.shape[2]:
+        raise ValueError(f"cache_len {cache_len} exceeds the cache capacity {k_cache.shape[2]}")
+    out = torch.empty((B, Sq, Hq, d_v), dtype=cdt, device=q.device).transpose(1, 2)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device)
+    nb = L.pe_attn_decode_workspace_bytes(ref(p))
+    ws = torch.empty(nb, dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = L.pe_attn_decode(ref(p), ref(_tensor(q_c)), ref(_tensor(q)), k_cache.data_ptr(), v_cache.data_ptr(),
+                              k_cache.shape[2], _ptr(freqs), ref(_tensor(out)), lse.data_ptr(), ws.data_ptr(), nb,
+                              _stream(q.device))
+    _lib.check(rc)
+    return (out, lse) if return_lse else out

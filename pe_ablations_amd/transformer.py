@@ -26,7 +26,7 @@ from .attention import GroupedQueryAttention
 from .embeddings import TokenEmbedding
 from .ffn import FeedForward
 from .fpope import FoPEPoPEEmbedding
-from .fpope_attention import FPoPEGroupedQueryAttention
+from .fpope_attention import FPoPEGroupedQueryAttentionWithCache
 from .normalization import RMSNorm
 from .pope import PoPEEmbedding
 from .rope import NTKAwareRotaryEmbedding, RotaryEmbedding, YaRNRotaryEmbedding
@@ -112,13 +112,13 @@ class TransformerBlock(nn.Module):
         self.attention_norm = RMSNorm(config.hidden_dim, eps=config.norm_eps)
         mode = config.pe_mode
         if mode == "fpope":
-            self.attention = FPoPEGroupedQueryAttention(
+            self.attention = FPoPEGroupedQueryAttentionWithCache(
                 hidden_dim=config.hidden_dim, num_heads=config.num_heads, num_kv_heads=config.num_kv_heads,
                 head_dim=config.head_dim, d_rope=config.fpope_d_rope, use_qk_norm=config.use_qk_norm,
                 fpope=fpope)
         elif mode in ("pope", "pope_floor"):
             d_rope, d_content = _pope_dims(config)
-            self.attention = FPoPEGroupedQueryAttention(
+            self.attention = FPoPEGroupedQueryAttentionWithCache(
                 hidden_dim=config.hidden_dim, num_heads=config.num_heads, num_kv_heads=config.num_kv_heads,
                 head_dim=config.head_dim, d_rope=d_rope, use_qk_norm=config.use_qk_norm, fpope=pope,
                 d_content=d_content)
@@ -138,8 +138,12 @@ class TransformerBlock(nn.Module):
         self.feed_forward = FeedForward(hidden_dim=config.hidden_dim, ffn_dim=config.ffn_dim,
                                         multiple_of=config.ffn_multiple_of)
 
-    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0) -> torch.Tensor:
-        x = x + self.attention(self.attention_norm(x), mask, start_pos)
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0,
+                use_cache: bool = False) -> torch.Tensor:
+        """``use_cache`` (inference only) routes the attention through its KV cache."""
+        h = self.attention_norm(x)
+        a = self.attention(h, mask, start_pos, use_cache=True) if use_cache else self.attention(h, mask, start_pos)
+        x = x + a
         x = x + self.feed_forward(self.ffn_norm(x))
         return x
 
@@ -204,15 +208,17 @@ class Transformer(nn.Module):
                 torch.nn.init.normal_(module.weight, mean=0.0, std=0.02)
 
     def forward(self, input_ids: torch.Tensor, labels: Optional[torch.Tensor] = None,
-                start_pos: int = 0) -> dict:
+                start_pos: int = 0, use_cache: bool = False) -> dict:
         """{'logits'} and, with ``labels``, {'loss'}: next-token cross entropy over the shifted
-        sequence with ignore_index -100 (src/model/transformer.py:313-364)."""
+        sequence with ignore_index -100 (src/model/transformer.py:313-364).  ``use_cache``
+        (inference only, an addition) feeds the tokens at absolute positions start_pos.. through
+        every layer's KV cache, which must hold exactly start_pos earlier rows."""
         x = self.token_embedding(input_ids)
         for layer in self.layers:
             if self.gradient_checkpointing and self.training:
                 x = torch.utils.checkpoint.checkpoint(layer, x, None, start_pos, use_reentrant=False)
             else:
-                x = layer(x, mask=None, start_pos=start_pos)
+                x = layer(x, mask=None, start_pos=start_pos, use_cache=use_cache)
         x = self.norm(x)
         logits = self.output(x)
         out = {"logits": logits}
@@ -230,30 +236,56 @@ class Transformer(nn.Module):
                 pe.extend_seq_len(new_max_seq_len)
         self.config.max_seq_len = new_max_seq_len
 
+    def reset_caches(self) -> None:
+        for layer in self.layers:
+            layer.attention.reset_cache()
+
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 100, temperature: float = 1.0,
                  top_k: Optional[int] = None, top_p: Optional[float] = None) -> torch.Tensor:
-        """Autoregressive sampling by full re-forward per token, greedy at temperature 0, with
-        top-k / nucleus filtering (src/model/transformer.py:380-446)."""
+        """Autoregressive continuation of ``input_ids`` (B, P) by ``max_new_tokens`` tokens, with the
+        reference's sampling semantics (src/model/transformer.py:389-446): greedy at temperature 0;
+        otherwise logits / temperature, optional top-k, optional nucleus (top-p) filtering that
+        always keeps the most likely token, then one multinomial draw.
+
+        Unlike the reference, which re-runs the whole sequence for every new token, the prompt is
+        run once (prefill) and every layer keeps a cache of transformed keys and values sized for
+        P + max_new_tokens; each further step feeds one token through the caches (the split-key
+        decode kernel).  The caches are freed on return."""
         self.eval()
-        for _ in range(max_new_tokens):
-            if input_ids.shape[1] > self.config.max_seq_len:
-                self.extend_context_length(input_ids.shape[1])
-            logits = self.forward(input_ids)["logits"][:, -1, :]
-            if temperature == 0.0:
-                input_ids = torch.cat([input_ids, logits.argmax(dim=-1, keepdim=True)], dim=1)
-                continue
-            logits = logits / temperature
-            if top_k is not None:
-                v, _ = torch.topk(logits, min(top_k, logits.size(-1)))
-                logits[logits < v[:, [-1]]] = float("-inf")
-            if top_p is not None:
-                sorted_logits, sorted_indices = torch.sort(logits, descending=True)
-                cum = torch.cumsum(F.softmax(sorted_logits, dim=-1), dim=-1)
-                remove = cum > top_p
-                remove[:, 1:] = remove[:, :-1].clone()
-                remove[:, 0] = False
-                logits[remove.scatter(1, sorted_indices, remove)] = float("-inf")
-            probs = F.softmax(logits, dim=-1)
-            input_ids = torch.cat([input_ids, torch.multinomial(probs, num_samples=1)], dim=1)
-        return input_ids
+        B, P = input_ids.shape
+        total = P + max_new_tokens
+        if total > self.config.max_seq_len:
+            self.extend_context_length(total)
+        for layer in self.layers:
+            layer.attention.max_cache_len = max(layer.attention.max_cache_len, total)
+        self.reset_caches()
+        tokens = [input_ids]
+        try:
+            logits = self.forward(input_ids, start_pos=0, use_cache=True)["logits"][:, -1, :]
+            for step in range(max_new_tokens):
+                nxt = _next_token(logits, temperature, top_k, top_p)
+                tokens.append(nxt)
+                if step + 1 < max_new_tokens:
+                    logits = self.forward(nxt, start_pos=P + step, use_cache=True)["logits"][:, -1, :]
+        finally:
+            self.reset_caches()
+        return torch.cat(tokens, dim=1)
+
+
+def _next_token(logits: torch.Tensor, temperature: float, top_k: Optional[int], top_p: Optional[float]) -> torch.Tensor:
+    """(B, V) logits of the last position -> (B, 1) next token ids."""
+    if temperature == 0.0:
+        return logits.argmax(dim=-1, keepdim=True)
+    z = logits / temperature
+    if top_k is not None:
+        kth = torch.topk(z, min(top_k, z.shape[-1]), dim=-1).values[:, -1:]
+        z = z.masked_fill(z < kth, float("-inf"))
+    if top_p is not None:
+        # a token is dropped when the probability mass of the tokens ranked above it already
+        # exceeds top_p, so the most likely token always survives
+        probs, order = torch.sort(F.softmax(z, dim=-1), dim=-1, descending=True)
+        mass_before = torch.cumsum(probs, dim=-1) - probs
+        drop = torch.zeros_like(mass_before, dtype=torch.bool).scatter(-1, order, mass_before > top_p)
+        z = z.masked_fill(drop, float("-inf"))
+    return torch.multinomial(F.softmax(z, dim=-1), num_samples=1)

@@ -248,3 +248,23 @@ def test_oracle_decoder_causal_prefix():
     la, lb = O.decoder_forward(sd, c, a)["logits"], O.decoder_forward(sd, c, b)["logits"]
     assert torch.allclose(la[:, :12], lb[:, :12], atol=1e-6)
     assert not torch.allclose(la[:, 12:], lb[:, 12:], atol=1e-3)
+
+
+def test_next_token_sampling_rules():
+    """The sampling rules of generate (src/model/transformer.py:389-446): temperature 0 is argmax;
+    top-k keeps the k largest logits; nucleus filtering drops a token once the probability mass
+    ranked above it exceeds top_p, so the most likely token always survives."""
+    from pe_ablations_amd.transformer import _next_token
+    torch.manual_seed(0)
+    logits = torch.tensor([[0.0, 3.0, 1.0, 2.9, -1.0], [5.0, 0.0, 0.0, 0.0, 4.0]])
+    assert _next_token(logits, 0.0, None, None).tolist() == [[1], [0]]
+    for _ in range(20):
+        assert _next_token(logits, 1.0, 1, None).tolist() == [[1], [0]]
+        assert _next_token(logits, 1.0, None, 1e-6).tolist() == [[1], [0]]
+        assert _next_token(logits, 0.7, 2, None)[0].item() in (1, 3)
+    # top_p = 0.6: row 0 mass is (0.45, 0.41, ...) -> tokens 1 and 3 survive, nothing else
+    picks = {int(_next_token(logits[:1], 1.0, None, 0.6).item()) for _ in range(200)}
+    assert picks <= {1, 3} and len(picks) == 2
+    counts = torch.bincount(torch.cat([_next_token(logits[1:], 1.0, None, None) for _ in range(400)]).flatten(),
+                            minlength=5)
+    assert counts[0] > counts[4] > 0 and counts[1:4].sum() < 40

@@ -99,13 +99,18 @@ def test_kv_cache_decode_equals_full_forward(cuda):
     pe = PoPEEmbedding(32, 512, delta_init="uniform")
     m = FPoPEGroupedQueryAttentionWithCache(256, 4, 2, 64, 32, fpope=pe, max_cache_len=128).to(cuda)
     x = torch.randn(1, 43, 256, device=cuda)
-    full = m(x)
-    outs = [m(x[:, :40], use_cache=True)]
-    for t in range(40, 43):
-        outs.append(m(x[:, t:t + 1], start_pos=t, use_cache=True))
+    with torch.no_grad():
+        full = m(x)
+        outs = [m(x[:, :40], use_cache=True)]
+        for t in range(40, 43):
+            outs.append(m(x[:, t:t + 1], start_pos=t, use_cache=True))
     inc = torch.cat(outs, 1)
     assert m.cache_len == 43
+    # the cache holds the transformed key rows [k_c | mu cos | mu sin] (width 64 + 2 * 32)
+    assert tuple(m.k_cache.shape) == (1, 2, 128, 128) and tuple(m.v_cache.shape) == (1, 2, 128, 64)
     assert md(inc, full) < 1e-5
+    with pytest.raises(RuntimeError, match="inference"):
+        m(x[:, 43:], start_pos=43, use_cache=True)   # gradients enabled: the cache path refuses
     m.reset_cache()
     assert m.k_cache is None and m.v_cache is None and m.cache_len == 0
 
