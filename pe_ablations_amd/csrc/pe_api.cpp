@@ -30,12 +30,21 @@ struct Layout {
   size_t q_off, k_off, v_off, tab_off, fwd_total;
   size_t do_off, di_off, l2_off, dq_off, dk_off, pq_off, pk_off, pkd_off, ds_off, bwd_total;
   int sq_pad;
-  int ds_nqt, ds_rows;
+  int ds_nqt, ds_rows, ds_e;
+  int64_t ds_head;
   int nq_blocks, nk_blocks;
 };
 
 // the query phases are shared by every batch and head, so PoPE evaluates them once per call
 bool use_qtab(const pe_attn_params* p) { return p->mode == PE_MODE_POPE && p->Dr > 0 && p->Dr % 8 == 0; }
+
+// bf16 fused PoPE form whose transformed width is exactly 2*Dr of 128 or 256: the gradient kernels
+// apply the inverse transform in their epilogues and write dq / dk directly, so the backward needs
+// no fp32 dq~ / dk~ buffers (pe_attn_bwd's input checks require the q / k views whenever Dr > 0)
+bool fused_bwd(const pe_attn_params* p) {
+  return p->dtype == PE_DTYPE_BF16 && p->mode == PE_MODE_POPE && p->Dc == 0 && (p->Dr == 64 || p->Dr == 128) &&
+         pad_qk(qk_width(p)) == 2 * p->Dr;
+}
 
 Layout layout(const pe_attn_params* p) {
   Layout L{};
@@ -61,17 +70,24 @@ Layout layout(const pe_attn_params* p) {
   L.di_off = L.do_off + align_up(nq * L.dv * e);
   L.l2_off = L.di_off + align_up(nq_pad * 4);
   L.dq_off = L.l2_off + align_up(nq_pad * 4);
-  L.dk_off = L.dq_off + align_up(nq * L.dqk * 4);
-  L.pq_off = L.dk_off + align_up(nk * L.dqk * 4);
+  const bool fb = fused_bwd(p);
+  L.dk_off = L.dq_off + (fb ? 0 : align_up(nq * L.dqk * 4));
+  L.pq_off = L.dk_off + (fb ? 0 : align_up(nk * L.dqk * 4));
   L.pk_off = L.pq_off + align_up((size_t)L.nq_blocks * p->Dr * 4);
   L.pkd_off = L.pk_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
   L.ds_off = L.pkd_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
-  // bf16 path: dS in fragment order (B, Hq, Sk_pad/32, ds_nqt blocks of 4 KiB) stored by the
-  // dK/dV kernel for the dQ GEMM
+  // bf16 path: dS in fragment order, 4 KiB blocks packed per (b, h) to the blocks the causal
+  // dK/dV kernel stores (pe::ds_row_base), written by it for the dQ GEMM.  The dQ GEMM's masked
+  // edge steps also load up to four blocks before a key row's first stored one; those lie in the
+  // earlier rows of the same or the previous (b, h), never before the buffer or past its end.
   L.ds_nqt = (p->Sq + 255) / 256 * 4;
   L.ds_rows = (p->Sk + 127) / 128 * 128;
+  const int causal = p->causal != PE_CAUSAL_NONE;
+  const int off = p->causal == PE_CAUSAL_BOTTOM_RIGHT ? p->Sk - p->Sq : 0;
+  L.ds_e = causal ? (off + 63) / 64 : 0;
+  L.ds_head = pe::ds_row_base(L.ds_rows / 32, L.ds_e, L.ds_nqt, causal);
   const size_t ds_bytes =
-      p->dtype == PE_DTYPE_BF16 ? (size_t)p->B * p->Hq * (L.ds_rows / 32) * L.ds_nqt * 4096 : 0;
+      p->dtype == PE_DTYPE_BF16 ? (size_t)p->B * p->Hq * L.ds_head * 4096 : 0;
   L.bwd_total = L.ds_off + align_up(ds_bytes);
   return L;
 }
@@ -595,6 +611,8 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   c.dS = (uint16_t*)(bws + L.ds_off);
   c.ds_nqt = L.ds_nqt;
   c.ds_rows = L.ds_rows;
+  c.ds_e = L.ds_e;
+  c.ds_head = L.ds_head;
   c.lse_in = lse;
   c.dq_t = (float*)(bws + L.dq_off);
   c.qtab = use_qtab(p) ? (const float*)(fws + L.tab_off) : nullptr;
@@ -604,9 +622,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   stage_mark(PE_STAGE_BWD_DKDV, 0, s);
   // fused form in bf16 with both halves of a column in one wave: the gradient kernels apply the
   // inverse PoPE transform in their epilogues
-  const bool fuse = dt == 0 && p->mode == PE_MODE_POPE && p->Dc == 0 && L.dqk == 2 * p->Dr &&
-                    (p->Dr == 64 || p->Dr == 128) && qr && qr->data && kr && kr->data &&
-                    dqr && dqr->data && dkr && dkr->data;
+  const bool fuse = fused_bwd(p);
   const int nqg = (p->Sq + 255) / 256, nkg = (p->Sk + 127) / 128;
   if (fuse) {
     c.fuse_inv = 1;

@@ -498,8 +498,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     // contiguous (block (key/32, q0/64), chunks (mt*2 + h2)*64 + lane); rows past Sk are padding
     {
       const int h = hk * grp + t / nper;
-      char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * (a.ds_rows / 32) + (kw0 >> 5)) * a.ds_nqt * 4096 +
-                  (int64_t)(q0 >> 6) * 4096;
+      char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * a.ds_head + ds_row_base(kw0 >> 5, a.ds_e, a.ds_nqt, a.causal) +
+                                 (q0 >> 6) - ds_first(kb, a.ds_e, a.causal)) * 4096;
       __builtin_nontemporal_store(cdsf[0], (u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16));  // read once
       __builtin_nontemporal_store(cdsf[1], (u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16));
     }
@@ -748,10 +748,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const int64_t qrs = (int64_t)DQK * 2;
 
   // tiles are issued in loop order: query tile qt of query head h advances qt, then h
-#ifndef DKDV_SWZ
-#define DKDV_SWZ 1
-#endif
-  constexpr int SZ = DKDV_SWZ;  // swizzle kind of the q~ and dO tiles
+  constexpr int SZ = 1;  // swizzle kind of the q~ and dO tiles (both take transpose reads)
   const DmaPlan<BMQ, NCQ, NA, SZ> plan_q(pw, lane, (uint32_t)qrs);
   const DmaPlan<BMQ, NCO, NA, SZ> plan_o(pw, lane, (uint32_t)(a.do_ss * 2));
   const uint32_t smem_l = lds_addr(smem);
@@ -778,10 +775,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     }
   };
 
-#ifndef DKDV_FD
-#define DKDV_FD 3
-#endif
-  constexpr int FD = DKDV_FD;
+  constexpr int FD = 3;  // fragment read-ahead depth (depths 2, 4, 6 and 8 measured within 1 %)
   const RowX<NCQ, SZ> rq(perm_row<0>(l32), g);
   const RowX<NCO, SZ> ro(perm_row<0>(l32), g);
   const ColX<NCQ, SZ> cq(lane);
@@ -932,12 +926,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       for (int j = 0; j < 16; ++j) dk[t][j] = 0.f;
     f32x16 dp;
     int prev_h = hk * grp, prev_qt = qb0;  // head and query tile of step t - 1
+    // the wave's key row in the packed dS (pe_internal.h), less its first stored 64-query block
+    const int64_t ds_row = ds_row_base(kw0 >> 5, a.ds_e, a.ds_nqt, a.causal) - ds_first(kb, a.ds_e, a.causal);
     // role B is the critical path of every step: its instructions go first when both waves of a
     // SIMD are ready to issue
-#ifndef DKDV_PRIO
-#define DKDV_PRIO 2
-#endif
-    __builtin_amdgcn_s_setprio(DKDV_PRIO);
+    __builtin_amdgcn_s_setprio(2);
     for (int t = 0; t <= niter; ++t) {
       if (t >= 1) {  // dS of tile t - 1 from A's fp32 P; store it; dK~ += dS^T q~
         const char* st = smem + ((t - 1) % NSTG) * STAGE;
@@ -959,8 +952,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           prev_qt = qb0;
           ++prev_h;
         }
-        char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * (a.ds_rows / 32) + (kw0 >> 5)) * a.ds_nqt * 4096 +
-                    (int64_t)(q0 >> 6) * 4096;
+        char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * a.ds_head + ds_row + (q0 >> 6)) * 4096;
         const int mt = (q0 >> 5) & 1;
         // dS is read once, by the dQ GEMM after this kernel: non-temporal stores keep it from
         // displacing the q~ / dO tiles that the other key blocks re-read (4 % of this kernel's
@@ -1089,11 +1081,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 // workgroup owns 256 queries of one head; its 8 waves split them into 4 pairs of 32-query tiles x
 // 2 halves of the dq~ columns, so every fragment read from LDS feeds two MFMAs (A: dS for 32
 // queries x 16 keys, shared by the wave's column tiles; B: k~ for 16 keys x 32 columns, shared by
-// its two query tiles) and the 128 accumulators per wave leave room for two waves per SIMD.  (NW =
-// 4 gives each wave 128 queries x 128 columns in AGPRs at one wave per SIMD: one fragment per MFMA
-// instead of 1.5, but it measured 25 % slower, as each wave then waits on its own LDS reads and
-// loads.)  Each
-// BK-key step stages dS^T (BK keys x 256 queries) and k~ (BK x DQK) in one slot of an NSTAGE ring,
+// its two query tiles) and the 128 accumulators per wave leave room for two waves per SIMD.  (Four
+// waves of 128 queries x 128 columns in AGPRs at one wave per SIMD read one fragment per MFMA
+// instead of 1.5, but measured 25 % slower, as each wave then waits on its own LDS reads and
+// loads; that variant is not built.)  Each BK-key step stages dS^T (BK keys x 256 queries) and k~ (BK x DQK) in one slot of an NSTAGE ring,
 // NSTAGE - 1 steps ahead: dS is read once from HBM, so the kernel streams it and needs several
 // tiles in flight to cover the memory latency.  Both operands are read with the transpose load.
 // Keys past a query's causal limit or past Sk hold no valid dS (never written), so on those tiles
@@ -1105,11 +1096,8 @@ __device__ __forceinline__ uint32_t keep_bf2(uint32_t v, bool lo, bool hi) {
 template <int DQK, int NW, int BK, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   using M = MT<0>;
-  static_assert(NW == 8 || NW == 4, "NW/2 query groups x 2 column halves");
-#ifndef DQ_SWZ
-#define DQ_SWZ 1
-#endif
-  constexpr int SZ = DQ_SWZ;  // tile swizzle kind (both tiles are only read with the transpose load)
+  static_assert(NW == 8, "4 query groups x 2 column halves");
+  constexpr int SZ = 1;  // tile swizzle kind (both tiles are only read with the transpose load)
   constexpr int NQG = NW / 2, QT = 8 / NQG;  // query groups; 32-query tiles per wave
   static_assert(NSTAGE >= 2 && NSTAGE <= 4, "ring depth");
   constexpr int BQ = 256;
@@ -1163,13 +1151,17 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   if (a.causal) kend = min(a.Sk, q0 + BQ + off);
   const int nkb = kend > 0 ? (kend + BK - 1) / BK : 0;
   const char* kbase = (const char*)((const uint16_t*)a.k + (int64_t)(b * a.Hkv + hk) * a.Sk * DQK);
-  const char* sbase = (const char*)a.dS + (int64_t)(b * a.Hq + h) * (a.ds_rows / 32) * a.ds_nqt * 4096;
+  // the packed dS of this (b, h) (pe_internal.h): key row r of the block's 64-query blocks
+  // j0 .. j0 + 3 (j0 = q0 / 64) starts at block ds_row_base(r) + j0 - ds_first(r / 4)
+  const int j0 = q0 >> 6;
+  const char* sbase = (const char*)a.dS + ((int64_t)(b * a.Hq + h) * a.ds_head + j0) * 4096;
   const int64_t krs = (int64_t)DQK * 2;
-  // dS window for keys k0 .. k0+63 and this block's 256 queries: LDS slot (row kl, physical chunk
-  // pc) holds query chunk lc = pc ^ swz(kl) of key k0 + kl; its source is that key's 32-key block
-  // at 64-query block (q0/8 + lc)/8, chunk ((r>>1)*64 + (r&1)*32 + kl%32), r = (q0/8 + lc) % 8.
-  // k0 is a multiple of 32, so a lane's source offset is (k0/32) * ds_nqt * 4096 (wave-uniform)
-  // plus a per-lane constant, computed once
+  // dS window for keys k0 .. k0+BK-1 and this block's 256 queries: LDS slot (row kl, physical chunk
+  // pc) holds query chunk lc = pc ^ swz(kl) of key k0 + kl; its source is key row r = (k0 + kl) / 32
+  // at 64-query block j0 + lc/8, chunk ((q>>1)*64 + (q&1)*32 + kl%32), q = lc % 8.  A DMA
+  // instruction covers 64 / (BK / 8) = 256 / BK key rows of one 32-key row, so per instruction the
+  // row base is wave-uniform (computed per step) and a lane's offset (lc/8) * 4096 + chunk is a
+  // per-lane constant, computed once
   constexpr int NDS = BK * NCS / (64 * NW);
   uint32_t ds_off[NDS];
 #pragma unroll
@@ -1177,21 +1169,38 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
     const int slot = (i * NW + w) * 64 + lane;
     const int kl = slot / NCS, pc = slot % NCS;
     const int lc = pc ^ swz<NCS, SZ>(kl);
-    const int qc = (q0 >> 3) + lc, r = qc & 7;
-    ds_off[i] = ((uint32_t)(kl >> 5) * a.ds_nqt + (qc >> 3)) * 4096u +
-                (uint32_t)(((r >> 1) * 64 + (r & 1) * 32 + (kl & 31)) * 16);
+    const int q = lc & 7;
+    ds_off[i] = (uint32_t)((lc >> 3) * 4096 + ((q >> 1) * 64 + (q & 1) * 32 + (kl & 31)) * 16);
   }
+  // key row (within the step) of DMA instruction i: slots (i * NW + w) * 64 .. +63 hold key rows
+  // kl = slot / NCS of one 32-row group, (i * NW + w) * 64 / NCS / 32, the same for every wave when
+  // NW * 64 / NCS divides 32
+  static_assert((NW * 64 / NCS) <= 32 && 32 % (NW * 64 / NCS) == 0, "one 32-key row per DMA instruction");
   const DmaPlan<BK, NCK, NW, SZ> plan_k(w, lane, (uint32_t)krs);
   const uint32_t smem_l = lds_addr(smem);
+  // tiles are issued in key order, so the packed row start ds_row_base(r) - ds_first(r / 4) of the
+  // next tile's first key row is carried forward: row r + 1 starts nqt - ds_first((r + 1) / 4)
+  // blocks after row r
+  int iss_r = 0;
+  int64_t iss_rs = 0;
+  auto next_rs = [&](int r, int64_t rs) -> int64_t { return rs + a.ds_nqt - ds_first((r + 1) >> 2, a.ds_e, a.causal); };
   auto issue = [&](int kb) {
     char* st = smem + (kb % NSTAGE) * STAGE;
     const uint32_t stl = smem_l + (uint32_t)((kb % NSTAGE) * STAGE);
     const char* ksrc = kbase + (int64_t)kb * BK * krs;
     if (a.Sk - kb * BK >= BK) plan_k.full(ksrc, stl, w, (uint32_t)krs);
     else dma_tile<BK, NCK, NW, SZ>(st, ksrc, krs, a.Sk - kb * BK, w, lane);
-    const char* dsrc = sbase + (int64_t)((kb * BK) >> 5) * a.ds_nqt * 4096;
+    int64_t rs[BK / 32];  // row starts of the step's key rows iss_r .. iss_r + BK/32 - 1 (= kb * BK / 32 ..)
+    rs[0] = iss_rs;
 #pragma unroll
-    for (int i = 0; i < NDS; ++i) dma16s(ds_off[i], dsrc, stl + SK_BYTES + (uint32_t)((i * NW + w) * 64 * 16));
+    for (int j = 1; j < BK / 32; ++j) rs[j] = next_rs(iss_r + j - 1, rs[j - 1]);
+#pragma unroll
+    for (int i = 0; i < NDS; ++i) {
+      const int rr = ((i * NW + w) * 64 / NCS) / 32;  // key row of instruction i within the step
+      dma16s(ds_off[i], sbase + rs[rr] * 4096, stl + SK_BYTES + (uint32_t)((i * NW + w) * 64 * 16));
+    }
+    iss_rs = next_rs(iss_r + BK / 32 - 1, rs[BK / 32 - 1]);
+    iss_r += BK / 32;
   };
 #pragma unroll
   for (int i = 0; i < NSTAGE - 1; ++i)
@@ -1387,22 +1396,12 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       }
     } else {
       const int nqb = (a.Sq + 255) / 256;
-#ifndef DQ_BK
-#define DQ_BK 32
-#endif
-#ifndef DQ_NSTG
-#define DQ_NSTG 4
-#endif
       // wide operands: 32-key steps in a 4-deep ring (three steps of loads in flight) measured
-      // 4 % faster than 64-key steps double-buffered or a 3-deep ring of 32-key steps
-#ifndef DQ_NW
-#define DQ_NW 8  // waves per workgroup (4 or 8)
-#endif
-      // the 32-key ring for the wide operands (a 64-wide k~ tile of 32 keys is less than one DMA
-      // instruction per wave)
+      // 4 % faster than 64-key steps double-buffered or a 3-deep ring of 32-key steps; the narrow
+      // 64-wide k~ (a 32-key tile of it is less than one DMA instruction per wave) keeps 64-key
+      // steps double-buffered
       constexpr bool TW = DQK == 256 || DQK == 128;
-      constexpr int DNW = TW ? DQ_NW : 8;
-      hipLaunchKernelGGL((dq_gemm_kernel<DQK, DNW, (TW ? DQ_BK : 64), (TW ? DQ_NSTG : 2)>), dim3(nqb * a.B * a.Hq), dim3(DNW * 64), 0, s, a);
+      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8, (TW ? 32 : 64), (TW ? 4 : 2)>), dim3(nqb * a.B * a.Hq), dim3(8 * 64), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {

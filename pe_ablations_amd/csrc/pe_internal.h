@@ -17,6 +17,24 @@ struct EpiPoPE {
   float* part_freq;
 };
 
+// Packed bf16 dS of one (batch, head): 4 KiB blocks of 32 keys x 64 queries, key-row major.  Key
+// row r (32 keys) of key block kb = r / 4 (128 keys) holds the 64-query blocks ds_first(kb) ..
+// nqt - 1 that the causal dK/dV kernels store for it, contiguously, so block (r, j) sits at
+// ds_row_base(r) + j - ds_first(r / 4).  Causal: ds_first(kb) = max(0, 2 kb - e) with
+// e = ceil(causal_off / 64) (the kernels start at query max(0, 128 kb - causal_off)); without the
+// mask every row holds all nqt blocks.  ds_row_base(r) = r nqt - 4 F(r / 4) - (r % 4) ds_first(r / 4)
+// with F(K) = sum_{kb < K} ds_first(kb) = n (K - 1 + m - e), m = ceil(e / 2), n = max(0, K - m).
+// Half the square at Sq = Sk.
+__host__ __device__ inline int ds_first(int kb, int e, int causal) {
+  const int f = 2 * kb - e;
+  return causal && f > 0 ? f : 0;
+}
+__host__ __device__ inline int64_t ds_row_base(int r, int e, int nqt, int causal) {
+  if (!causal) return (int64_t)r * nqt;
+  const int64_t K = r / 4, m = (e + 1) / 2, n = K > m ? K - m : 0;
+  return (int64_t)r * nqt - 4 * n * (K - 1 + m - e) - (int64_t)(r % 4) * ds_first(r / 4, e, causal);
+}
+
 // Attention core over transformed operands.
 struct CoreArgs {
   const void* q;    // (B, Hq, Sq, DQK) contiguous, compute dtype
@@ -39,10 +57,13 @@ struct CoreArgs {
   int sq_pad;       // Sq rounded up to a multiple of 64
   const float* lse_in;
   uint16_t* dS;     // bf16 dS per (b, h) in MFMA fragment order: 4 KiB blocks of 32 keys x 64
-                    // queries, block (k/32, q/64) at ((k/32) * ds_nqt + q/64) * 4096 bytes; inside a
-                    // block, key kl and query chunk r = (q%64)/8 at chunk ((r>>1)*64 + (r&1)*32 + kl)
-  int ds_nqt;       // 64-query blocks per 32-key row (ceil(Sq / 256) * 4)
+                    // queries, block (k/32, q/64) at (ds_row_base(k/32) + q/64 - ds_first(k/128)) *
+                    // 4096 bytes within the (b, h) region of ds_head blocks; inside a block, key kl
+                    // and query chunk r = (q%64)/8 at chunk ((r>>1)*64 + (r&1)*32 + kl)
+  int ds_nqt;       // 64-query blocks per head (ceil(Sq / 256) * 4)
   int ds_rows;      // key rows per head (Sk rounded up to 128)
+  int ds_e;         // ceil(causal_off / 64) (causal only)
+  int64_t ds_head;  // blocks per (b, h) region: ds_row_base(ds_rows / 32)
   const float* qtab;  // query phase table of launch_phase_table ([Sq][2][Dr]) or null
   float* dq_t;      // (B, Hq, Sq, DQK) fp32, already multiplied by scale
   float* dk_t;      // (B, Hkv, Sk, DQK) fp32, already multiplied by scale (summed over the GQA group)

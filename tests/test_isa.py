@@ -18,7 +18,7 @@ import pytest
 
 from pe_ablations_amd import build as B
 
-DMA_SOURCES = ["pe_fwd.hip", "pe_bwd.hip"]
+DMA_SOURCES = ["pe_fwd.hip", "pe_bwd.hip", "pe_decode.hip"]
 
 
 def device_asm(src: str, out_dir: str) -> subprocess.Popen:
