@@ -18,10 +18,20 @@ The CPU baseline times this repository's CPU restatement of the reference's eage
 (oracle/pe_oracle.py, fp32) on a bounded sample of the same workload: ``--cpu-heads`` of the 16
 heads at the full S=16384, forward + backward.
 
-Two more workloads, selected with ``--workload`` (the default is the headline above):
+More workloads, selected with ``--workload`` (the default is the headline above):
 
 * ``fwd``: the long-context evaluation forward (the same shape, forward only, under
-  ``torch.inference_mode``; 3*B*H*S^2*D FLOPs per step).
+  ``torch.inference_mode``; 3*B*H*S^2*D FLOPs per step); ``fwd32`` the same in fp32, the
+  precision of the reference's 16k evaluation, against the fp32 MFMA peak.
+* ``c2``: PoPE fwd+bwd at B=8, H=12, S=2048, D=64 (~125M GPT shape).
+* ``c3``: FoPE fwd+bwd at B=4, H=16, S=4096, D=128, M=4 frequencies per dim; the FoPE collapse
+  (FoPEPoPEEmbedding) runs in each step and the Fourier coefficients get gradients.
+* ``split``: the reference's training module shape, split form [content 64 | PoPE 2x32], V 64,
+  8 query heads on 4 kv heads, B=8, S=512, one shared (Dr,) phase bias.
+
+Every attention line carries a ``prologue`` entry: the algorithmic bytes of the q / k transform
+stage (read raw rows, write transformed rows), its time from the stage events, GB/s against the
+8 TB/s HBM peak and, for the headline, the PMC-measured bytes of its kernels.
 * ``decoder``: the whole ~1B decoder forward of the long-context configuration: 24 layers,
   d_model 2048, 16 fused-PoPE heads of D=128, SwiGLU 5632, RMSNorm, vocab 32000, bf16 weights
   ~ N(0, 0.02^2), one sequence of 16384 uniform token ids, with the next-token cross entropy
@@ -35,7 +45,7 @@ Two more workloads, selected with ``--workload`` (the default is the headline ab
   the 8 TB/s HBM peak, the bound of decode.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--workload fwdbwd|fwd|decoder|decode]
+                       [--workload fwdbwd|fwd|fwd32|c2|c3|split|decoder|decode]
 """
 
 from __future__ import annotations
@@ -49,9 +59,38 @@ import sys
 import time
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA (published)
 HBM_PEAK_GBS = 8000.0
 
 WORKLOAD = dict(B=1, H=16, S=16384, D=128)
+
+# Attention workloads.  Hq / Hkv heads, S queries and keys (causal), content width Dc (passed
+# through), positional width Dr (PoPE: 2*Dr after the transform), value width Dv.  delta: "head" =
+# per-head (Hkv, Dr) phase bias, "shared" = one (Dr,) bias (the reference module's parameter).
+# fope: (M, coefficient sigma, training length) of a FoPE collapse computed per step by the
+# FoPEPoPEEmbedding module (base frequency plus M - 1 extra frequencies ~ U(0, theta_0)).
+ATTN_WORKLOADS = {
+    "fwdbwd": dict(B=1, Hq=16, Hkv=16, S=16384, Dc=0, Dr=128, Dv=128, dtype="bf16", backward=True, delta="head",
+                   name="PoPE causal attention fwd+bwd",
+                   metric="fused PoPE attn fwd+bwd TFLOP/s @S=16k,D=128; % of bf16 MFMA peak"),
+    "fwd": dict(B=1, Hq=16, Hkv=16, S=16384, Dc=0, Dr=128, Dv=128, dtype="bf16", backward=False, delta="head",
+                name="PoPE causal attention forward (long-context eval)",
+                metric="fused PoPE attn fwd TFLOP/s @S=16k,D=128 (long-context eval forward); % of bf16 MFMA peak"),
+    "fwd32": dict(B=1, Hq=16, Hkv=16, S=16384, Dc=0, Dr=128, Dv=128, dtype="fp32", backward=False, delta="head",
+                  name="PoPE causal attention forward in fp32 (the reference's 16k evaluation precision)",
+                  metric="fused PoPE attn fwd TFLOP/s @S=16k,D=128, fp32; % of fp32 MFMA peak"),
+    "c2": dict(B=8, Hq=12, Hkv=12, S=2048, Dc=0, Dr=64, Dv=64, dtype="bf16", backward=True, delta="head",
+               name="PoPE causal attention fwd+bwd, ~125M GPT shape",
+               metric="fused PoPE attn fwd+bwd TFLOP/s @B=8,H=12,S=2048,D=64; % of bf16 MFMA peak"),
+    "c3": dict(B=4, Hq=16, Hkv=16, S=4096, Dc=0, Dr=128, Dv=128, dtype="bf16", backward=True, delta="head",
+               fope=(4, 0.1, 2048), name="FoPE causal attention fwd+bwd (M=4 frequencies per dim)",
+               metric="fused FoPE attn fwd+bwd TFLOP/s @B=4,H=16,S=4096,D=128; % of bf16 MFMA peak"),
+    "split": dict(B=8, Hq=8, Hkv=4, S=512, Dc=64, Dr=32, Dv=64, dtype="bf16", backward=True, delta="shared",
+                  name="split-form PoPE attention fwd+bwd at the reference's training shape "
+                       "([content 64 | PoPE 2x32], V 64, GQA 8 -> 4)",
+                  metric="split-form PoPE attn fwd+bwd TFLOP/s @B=8,S=512,Hq=8,Hkv=4,Dc=64,Dr=32; "
+                         "% of bf16 MFMA peak"),
+}
 
 # HBM bytes per dispatch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this workload,
 # scaled by a calibration copy (python -m pe_ablations_amd.profiling traffic ...); the file records
@@ -78,45 +117,104 @@ def measured_traffic(stage: str):
 
 def flops(B, H, S, D):
     """Algorithmic FLOPs of fused PoPE causal attention (Dqk = 2D, Dv = D, c = 1/2)."""
-    base = B * H * S * S * D
+    return attn_flops(dict(B=B, Hq=H, S=S, Dc=0, Dr=D, Dv=D))
+
+
+def attn_flops(w: dict) -> dict:
+    """Algorithmic FLOPs of causal attention over transformed operands of width Wqk = Dc + 2*Dr and
+    values of width Dv, with B*Hq*S^2/2 query-key pairs: forward S~ (Wqk) + PV (Dv); backward S~
+    recompute (Wqk), dP (Dv), dV (Dv), dK~ (Wqk) and dQ~ (Wqk).  At Dc = 0, Dr = Dv = D this is
+    3, 8 and 11 * B*H*S^2*D."""
+    pairs = w["B"] * w["Hq"] * w["S"] * w["S"] / 2.0
+    wqk, dv = w["Dc"] + 2 * w["Dr"], w["Dv"]
     return {
-        "fwd": 3.0 * base,
-        "bwd": 8.0 * base,
-        "total": 11.0 * base,
-        "fa_convention": 7.0 * base,
+        "fwd": 2.0 * pairs * (wqk + dv),
+        "bwd": 2.0 * pairs * (3 * wqk + 2 * dv),
+        "total": 2.0 * pairs * (4 * wqk + 3 * dv),
+        # flash-attention convention at head width Dv: forward 4*B*H*S^2*Dv/2, backward 2.5 times that
+        "fa_convention": 2.0 * pairs * 7 * dv,
         # per kernel stage: GEMMs each kernel must perform
-        "fwd_core": 3.0 * base,      # S = q~k~^T (2D) + O = PV (D)
-        "bwd_dkdv": 6.0 * base,      # S (2D) + dP (D) + dV (D) + dK~ (2D)
-        "bwd_dq": 2.0 * base,        # dQ~ (2D); its S/dP recompute (3*base) is not algorithmic
+        "fwd_core": 2.0 * pairs * (wqk + dv),
+        "bwd_dkdv": 2.0 * pairs * (2 * wqk + 2 * dv),
+        "bwd_dq": 2.0 * pairs * wqk,   # its S/dP recompute is not algorithmic
     }
+
+
+def prologue_bytes(w: dict) -> int:
+    """Algorithmic HBM bytes of the forward's PE prologue: read the raw q and k rows (content and
+    positional parts), write the transformed rows of width Dc + 2*Dr."""
+    es = 4 if w["dtype"] == "fp32" else 2
+    rows = w["B"] * (w["Hq"] + w["Hkv"]) * w["S"]
+    return rows * (w["Dc"] + w["Dr"]) * es + rows * (w["Dc"] + 2 * w["Dr"]) * es
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(heads: int, reps: int, backward: bool = True):
-    """Oracle forward (+ backward) (fp32, torch eager, all host threads) on `heads` heads of the
-    workload: one untimed warm-up pass, then the median of `reps` timed passes."""
+def fope_module(torch, w: dict, D: int, seed: int = 33):
+    """FoPEPoPEEmbedding with the workload's frequency table (base theta_c plus M - 1 frequencies
+    ~ U(0, theta_0)) and coefficients ~ N(0, sigma^2)."""
+    from pe_ablations_amd.fpope import FoPEPoPEEmbedding
+    M, sigma, tl = w["fope"]
+    g = torch.Generator().manual_seed(seed)
+    base = 10000.0 ** (-(torch.arange(0, D, dtype=torch.float32) / D))
+    table = torch.cat([base.unsqueeze(1), torch.rand(D, M - 1, generator=g) * float(base[0])], 1)
+    m = FoPEPoPEEmbedding(D, max_seq_len=w["S"], num_fourier_terms=M, fourier_sigma=sigma, training_length=tl,
+                          freq_table=table)
+    with torch.no_grad():
+        m.fourier_coeffs.copy_(torch.randn(D, M, generator=g) * sigma)
+    return m
+
+
+def cpu_baseline(w: dict, heads: int, reps: int):
+    """The oracle's eager path (fp32, torch eager, all host threads) forward (+ backward) on `heads`
+    query heads of one batch entry of the workload at its full S: one untimed warm-up pass, then
+    the median of `reps` timed passes."""
     import torch
     from oracle import pe_oracle as O
 
-    B, H, S, D = WORKLOAD["B"], WORKLOAD["H"], WORKLOAD["S"], WORKLOAD["D"]
+    backward = w["backward"]
+    S, Dc, Dr, Dv = w["S"], w["Dc"], w["Dr"], w["Dv"]
+    hkv = max(1, heads * w["Hkv"] // w["Hq"])
     g = torch.Generator().manual_seed(0)
-    q = torch.randn(1, heads, S, D, generator=g).requires_grad_(backward)
-    k = torch.randn(1, heads, S, D, generator=g).requires_grad_(backward)
-    v = torch.randn(1, heads, S, D, generator=g).requires_grad_(backward)
-    dO = torch.randn(1, heads, S, D, generator=g)
-    delta = (torch.rand(heads, D, generator=g) * (-2 * math.pi)).requires_grad_(backward)
-    freqs = O.pope_freqs(D)
+    qr = torch.randn(1, heads, S, Dr, generator=g).requires_grad_(backward)
+    kr = torch.randn(1, hkv, S, Dr, generator=g).requires_grad_(backward)
+    v = torch.randn(1, hkv, S, Dv, generator=g).requires_grad_(backward)
+    qc = torch.randn(1, heads, S, Dc, generator=g).requires_grad_(backward) if Dc else None
+    kc = torch.randn(1, hkv, S, Dc, generator=g).requires_grad_(backward) if Dc else None
+    dO = torch.randn(1, heads, S, Dv, generator=g)
+    dshape = (hkv, Dr) if w["delta"] == "head" else (Dr,)
+    delta = (torch.rand(*dshape, generator=g) * (-2 * math.pi)).requires_grad_(backward)
+    fm = fope_module(torch, w, Dr) if w.get("fope") else None
+    freqs = None if fm else O.pope_freqs(Dr)
+    scale = 1.0 / math.sqrt(Dc + 2 * Dr) if Dc else 1.0 / math.sqrt(Dr)
+    leaves = [t for t in (qr, kr, v, qc, kc, delta) if t is not None]
+    if fm is not None:
+        leaves.append(fm.fourier_coeffs)
 
     def one_pass():
-        for t in (q, k, v, delta):
+        for t in leaves:
             t.grad = None
         t0 = time.perf_counter()
         with torch.set_grad_enabled(backward):
-            out, _ = O.pope_attention(q, k, v, freqs, delta, scale=1.0 / math.sqrt(D), clamp=False,
-                                      core_dtype=torch.float32)
+            f = freqs if fm is None else O.fope_effective_freqs(
+                fm.base_freqs, fm.fourier_coeffs, freq_table=fm.freq_table, training_length=fm.training_length)
+            if Dc:
+                out, _ = O.split_pope_attention(qc, kc, qr, kr, v, f, delta, scale=scale, core_dtype=torch.float32)
+            else:
+                out, _ = O.pope_attention(qr, kr, v, f, delta, scale=scale, clamp=False, core_dtype=torch.float32)
             if backward:
                 out.backward(dO.to(out.dtype))
         return time.perf_counter() - t0
@@ -124,36 +222,43 @@ def cpu_baseline(heads: int, reps: int, backward: bool = True):
     one_pass()
     times = sorted(one_pass() for _ in range(reps))
     dt = times[len(times) // 2]
-    f = flops(1, heads, S, D)["total" if backward else "fwd"]
+    f = attn_flops(dict(w, B=1, Hq=heads))["total" if backward else "fwd"]
     what = "fwd+bwd" if backward else "fwd"
+    fn = "split_pope_attention" if Dc else "pope_attention"
     return {
         "value": f / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
+        "cpu": cpu_model(),
         "kind": "port",
-        "sample": f"oracle/pe_oracle.py pope_attention {what}, fp32 torch eager, {heads} of {H} heads "
-                  f"(B=1, S={S}, D={D}); 1 warm-up + median of {reps} passes, {dt:.2f} s per pass, "
-                  f"{sum(times):.1f} s timed",
+        "sample": f"oracle/pe_oracle.py {fn} {what}, fp32 torch eager, {heads} of {w['Hq']} query heads "
+                  f"of one batch entry (S={S}, Dc={Dc}, Dr={Dr}, Dv={Dv}); 1 warm-up + median of {reps} "
+                  f"passes, {dt:.2f} s per pass, {sum(times):.1f} s timed",
         "seconds": dt,
     }
 
 
 def stage_events(torch, steps: int, stream):
-    """Per timed step, a ctypes array of 2 events per library stage (start, end), each recorded
-    once up front so the HIP event exists before the library records into it."""
+    """Stage events for the timed steps: a ctypes array of 2 events per library stage (start, end)
+    for every `every`-th step (at most about 50 sampled steps), None for the others.  Each event is
+    recorded once up front so the HIP event exists before the library records into it.  Sampling
+    keeps the event records (12 per step) from adding host time to short, host-bound steps."""
     from pe_ablations_amd import _lib
     nst = len(_lib.STAGES)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nst)] for _ in range(steps)]
+    every = max(1, steps // 50)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nst)] for _ in range(0, steps, every)]
     for row in evs:
         for e in row:
             e.record(stream)
     torch.cuda.synchronize()
-    arrays = [(ctypes.c_void_p * (2 * nst))(*[e.cuda_event for e in row]) for row in evs]
+    arrays = [None] * steps
+    for j, row in enumerate(evs):
+        arrays[j * every] = (ctypes.c_void_p * (2 * nst))(*[e.cuda_event for e in row])
     return evs, arrays
 
 
 def stage_times(evs, names):
-    """Average ms of each named stage over the timed steps."""
+    """Average ms of each named stage over the sampled timed steps."""
     from pe_ablations_amd import _lib
     out = {}
     for si, name in enumerate(_lib.STAGES):
@@ -164,64 +269,105 @@ def stage_times(evs, names):
 
 
 def timed_loop(torch, L, step, arrays, steps):
-    """Run `steps` steps between two device synchronisations, handing the library one event array
-    per step; returns ms per step."""
+    """Run `steps` steps between two device synchronisations, handing the library the step's event
+    array (or none); returns ms per step."""
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        L.pe_attn_set_stage_events(ctypes.cast(arrays[i], ctypes.c_void_p))
+        a = arrays[i]
+        L.pe_attn_set_stage_events(None if a is None else ctypes.cast(a, ctypes.c_void_p))
         step()
     L.pe_attn_set_stage_events(None)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def roofline(stage: str, flop: float, ms: float) -> dict:
-    traffic, traffic_kernel = measured_traffic(stage)
+def roofline(stage: str, flop: float, ms: float, peak: float = PEAK_BF16_TFLOPS, headline: bool = True) -> dict:
+    """Roofline entry of a kernel stage.  The measured HBM traffic comes from the committed PMC
+    summary of the headline workload, so other workloads report it as null."""
+    traffic, traffic_kernel = measured_traffic(stage) if headline else (None, None)
     achieved = flop / (ms * 1e-3) / 1e12
     return {
         "kernel": stage,
         "bound": "mfma",
         "achieved": round(achieved, 2),
-        "peak": PEAK_BF16_TFLOPS,
+        "peak": peak,
         "unit": "TFLOP/s",
-        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "frac": round(achieved / peak, 4),
         "traffic": None if traffic is None else int(traffic),
         "traffic_unit": "bytes per launch (HBM read + write)",
         "traffic_source": None if traffic is None else f"profiles/{os.path.basename(TRAFFIC_FILE)}: {traffic_kernel}",
     }
 
 
-def run_attention(args, torch, dev, backward: bool) -> dict:
-    """Headline (fwd+bwd) or evaluation-forward step on the attention workload."""
+def prologue_entry(w: dict, ms: float, headline: bool) -> dict:
+    """The forward's PE prologue stage (q / k transforms, plus the query phase table where the
+    backward uses one) against the HBM peak: algorithmic bytes / stage time, and, for the headline
+    workload, the PMC-measured bytes of its kernels."""
+    nbytes = prologue_bytes(w)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"stage": "fwd_prep", "bytes": nbytes, "ms": round(ms, 4), "achieved": round(gbs, 1),
+           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+    if headline:
+        try:
+            with open(TRAFFIC_FILE) as f:
+                kern = json.load(f).get("kernels", {})
+            # per step: one prep dispatch per operand (q, k) and one phase-table dispatch
+            t = 0.0
+            for name, per in (("prep_pope_vec_kernel", 2), ("phase_table_kernel", 1)):
+                v = kern[name]
+                t += per * (v["fetch_bytes"] + v["write_bytes"])
+            out["traffic"] = int(t)
+            out["traffic_source"] = f"profiles/{os.path.basename(TRAFFIC_FILE)}: prep_pope_vec_kernel x2 + phase_table_kernel"
+        except (OSError, ValueError, KeyError, TypeError):
+            pass
+    return out
+
+
+def run_attention(args, torch, dev, wname: str) -> dict:
+    """One step of an attention workload: forward (+ backward) through pe_attention and the C-ABI."""
     from pe_ablations_amd import _lib
     from pe_ablations_amd.functional import pe_attention
 
-    B, H, S, D = WORKLOAD["B"], WORKLOAD["H"], WORKLOAD["S"], WORKLOAD["D"]
-    F = flops(B, H, S, D)
+    w = ATTN_WORKLOADS[wname]
+    backward = w["backward"]
+    B, Hq, Hkv, S, Dc, Dr, Dv = (w[k] for k in ("B", "Hq", "Hkv", "S", "Dc", "Dr", "Dv"))
+    F = attn_flops(w)
     g = torch.Generator(device=dev).manual_seed(0)
-    bf = torch.bfloat16
-    q = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(backward)
-    k = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(backward)
-    v = torch.randn(B, H, S, D, generator=g, device=dev).to(bf).requires_grad_(backward)
-    dO = torch.randn(B, H, S, D, generator=g, device=dev).to(bf)
-    delta = (torch.rand(H, D, generator=g, device=dev) * (-2 * math.pi)).requires_grad_(backward)
-    freqs = (10000.0 ** (-(torch.arange(0, D, dtype=torch.float32) / D))).to(dev)
-    scale = 1.0 / math.sqrt(D)
+    dt = torch.float32 if w["dtype"] == "fp32" else torch.bfloat16
+
+    def rnd(h, d):
+        return torch.randn(B, h, S, d, generator=g, device=dev).to(dt).requires_grad_(backward)
+
+    q, k, v = rnd(Hq, Dr), rnd(Hkv, Dr), rnd(Hkv, Dv)
+    qc, kc = (rnd(Hq, Dc), rnd(Hkv, Dc)) if Dc else (None, None)
+    dO = torch.randn(B, Hq, S, Dv, generator=g, device=dev).to(dt)
+    dshape = (Hkv, Dr) if w["delta"] == "head" else (Dr,)
+    delta = (torch.rand(*dshape, generator=g, device=dev) * (-2 * math.pi)).requires_grad_(backward)
+    fm = fope_module(torch, w, Dr).to(dev) if w.get("fope") else None
+    freqs = (10000.0 ** (-(torch.arange(0, Dr, dtype=torch.float32) / Dr))).to(dev)
+    scale = 1.0 / math.sqrt(Dc + 2 * Dr) if Dc else 1.0 / math.sqrt(Dr)
+    leaves = [t for t in (q, k, v, qc, kc, delta) if t is not None]
+    if fm is not None:
+        leaves.append(fm.fourier_coeffs)
+
+    def attn():
+        f = freqs if fm is None else fm.kernel_freqs()
+        return pe_attention(q, k, v, mode="pope", q_c=qc, k_c=kc, freqs=f, delta=delta, scale=scale)
 
     if backward:
         def step():
-            out = pe_attention(q, k, v, mode="pope", freqs=freqs, delta=delta, scale=scale)
-            return torch.autograd.grad(out, (q, k, v, delta), dO)
+            return torch.autograd.grad(attn(), leaves, dO)
     else:
         def step():
             with torch.inference_mode():
-                return (pe_attention(q, k, v, mode="pope", freqs=freqs, delta=delta, scale=scale),)
+                return (attn(),)
 
     L = _lib.lib()
     stream = torch.cuda.current_stream(dev)
     what = "fwd+bwd" if backward else "fwd"
-    log(f"bench: warmup {args.warmup} steps ({what}, B={B} H={H} S={S} D={D} bf16)")
+    log(f"bench: warmup {args.warmup} steps ({wname}: {what}, B={B} Hq={Hq} Hkv={Hkv} S={S} Dc={Dc} Dr={Dr} "
+        f"Dv={Dv} {w['dtype']})")
     for _ in range(args.warmup):
         res = step()
     torch.cuda.synchronize()
@@ -239,14 +385,20 @@ def run_attention(args, torch, dev, backward: bool) -> dict:
     dom = max(core, key=lambda n: stage_ms[n])
     total = F["total"] if backward else F["fwd"]
     value = total / (ms * 1e-3) / 1e12
-    if backward:
-        metric = "fused PoPE attn fwd+bwd TFLOP/s @S=16k,D=128; % of bf16 MFMA peak"
-        workload = "PoPE causal attention fwd+bwd"
+    peak = PEAK_FP32_TFLOPS if w["dtype"] == "fp32" else PEAK_BF16_TFLOPS
+    headline = wname == "fwdbwd"
+    config = {"workload": w["name"], "B": B, "S": S}
+    if Dc or Hq != Hkv:
+        config.update(Hq=Hq, Hkv=Hkv, Dc=Dc, Dr=Dr, Dv=Dv)
     else:
-        metric = "fused PoPE attn fwd TFLOP/s @S=16k,D=128 (long-context eval forward); % of bf16 MFMA peak"
-        workload = "PoPE causal attention forward (long-context eval)"
+        config.update(H=Hq, D=Dr)
+    config.update(delta="per-head (Hkv, Dr)" if w["delta"] == "head" else "shared (Dr,)",
+                  grads=("q,k,v,delta" + (",q_c,k_c" if Dc else "") + (",fourier_coeffs" if fm else ""))
+                  if backward else "none", parallelism="single GPU")
+    if fm is not None:
+        config["fope"] = {"M": w["fope"][0], "coeff_sigma": w["fope"][1], "training_length": w["fope"][2]}
     return {
-        "metric": metric,
+        "metric": w["metric"],
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -256,15 +408,15 @@ def run_attention(args, torch, dev, backward: bool) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) q/k/v/dO, delta ~ U(-2pi,0) per head)",
-        "config": {"workload": workload, "B": B, "H": H, "S": S, "D": D, "delta": "per-head (H, D)",
-                   "grads": "q,k,v,delta" if backward else "none", "parallelism": "single GPU"},
-        "frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
-        "fa_convention_tflops": round((F["fa_convention"] if backward else 2.0 * B * H * S * S * D)
+        "dtype": w["dtype"],
+        "data": "synthetic (seeded N(0,1) q/k/v/dO, delta ~ U(-2pi,0))",
+        "config": config,
+        "frac_of_peak": round(value / peak, 4),
+        "fa_convention_tflops": round((F["fa_convention"] if backward else 2.0 * F["fa_convention"] / 7.0)
                                       / (ms * 1e-3) / 1e12, 2),
         "stage_ms": {k2: round(v2, 4) for k2, v2 in stage_ms.items()},
-        "roofline": roofline(dom, F[dom], stage_ms[dom]),
+        "roofline": roofline(dom, F[dom], stage_ms[dom], peak, headline),
+        "prologue": prologue_entry(w, stage_ms["fwd_prep"], headline),
     }
 
 
@@ -321,6 +473,7 @@ def decoder_cpu_baseline(torch, model, ids, tokens: int):
         "value": tokens / dt,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
+        "cpu": cpu_model(),
         "kind": "port",
         "sample": f"oracle/pe_oracle.py decoder_forward (fp32 weights, fp64 attention), all 24 layers, "
                   f"first {tokens} of the {DECODER['S']} tokens, one pass of {dt:.1f} s (loss {loss:.3f}); "
@@ -479,23 +632,32 @@ def decode_cpu_baseline(torch) -> dict:
         O.pope_attention_chunked(q, k, v, freqs, delta, scale=1.0 / math.sqrt(D), start_q=L - 1)
     dt = time.perf_counter() - t0
     wk = 2 * D
-    return {"value": B * H * L * (wk + D) * 2 / dt / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+    return {"value": B * H * L * (wk + D) * 2 / dt / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "cpu": cpu_model(),
             "kind": "port",
             "sample": f"oracle pope_attention_chunked of 1 query against {L} keys, fp32, {H} heads one after "
                       f"another ({dt:.3f} s); bytes counted as the GPU cache bytes of the same step",
             "seconds": dt}
 
 
+# (timed steps, warm-up steps) per workload: about half a second of untimed work, and timed work
+# well under a minute
+# query heads of one batch entry in the CPU baseline's sample (about 10-30 s of CPU work)
+CPU_HEADS = {"fwdbwd": 2, "fwd": 2, "fwd32": 2, "c2": 12, "c3": 16, "split": 8}
+CPU_REPS = {"c2": 40, "c3": 10, "fwd32": 12, "split": 1000}
+DEFAULT_STEPS = {"fwdbwd": (50, 100), "fwd": (100, 400), "fwd32": (10, 40), "c2": (200, 600), "c3": (100, 250),
+                 "split": (500, 2000), "decoder": (5, 4), "decode": (200, 200)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="timed steps (default fwdbwd 50, fwd 100, decoder 5)")
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default per workload, DEFAULT_STEPS)")
     ap.add_argument("--warmup", type=int, default=None,
-                    help="untimed steps (default fwdbwd 100, fwd 400, decoder 4: about 0.5 s of work)")
-    ap.add_argument("--workload", choices=["fwdbwd", "fwd", "decoder", "decode"], default="fwdbwd")
+                    help="untimed steps (default per workload: about 0.5 s of work or more)")
+    ap.add_argument("--workload", choices=list(ATTN_WORKLOADS) + ["decoder", "decode"], default="fwdbwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=2)
-    ap.add_argument("--cpu-reps", type=int, default=4)
+    ap.add_argument("--cpu-heads", type=int, default=None, help="CPU baseline sample: query heads at full S")
+    ap.add_argument("--cpu-reps", type=int, default=None, help="CPU baseline: timed passes (default per workload)")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="decoder CPU baseline: tokens of the sample")
     args = ap.parse_args()
     dec = args.workload == "decoder"
@@ -503,10 +665,8 @@ def main() -> int:
     # chip runs at its socket power limit; after an idle host phase its clock and power state need
     # a few hundred milliseconds to settle, and timing from a 3-step warm-up measured the forward
     # 7-9 % and the fwd+bwd step 1.7 % slower than the settled state.
-    args.steps = args.steps if args.steps is not None else {"decoder": 5, "fwd": 100, "fwdbwd": 50,
-                                                            "decode": 200}[args.workload]
-    args.warmup = args.warmup if args.warmup is not None else {"decoder": 4, "fwd": 400, "fwdbwd": 100,
-                                                               "decode": 200}[args.workload]
+    args.steps = args.steps if args.steps is not None else DEFAULT_STEPS[args.workload][0]
+    args.warmup = args.warmup if args.warmup is not None else DEFAULT_STEPS[args.workload][1]
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -526,7 +686,7 @@ def main() -> int:
     elif args.workload == "decode":
         res = run_decode(args, torch, dev)
     else:
-        res = run_attention(args, torch, dev, backward=args.workload == "fwdbwd")
+        res = run_attention(args, torch, dev, args.workload)
     props = torch.cuda.get_device_properties(dev)
     res["device"] = {"name": props.name, "cus": props.multi_processor_count}
     model, ids = res.pop("_model", None), res.pop("_ids", None)
@@ -538,8 +698,10 @@ def main() -> int:
             log("bench: CPU baseline (decode)")
             cb = decode_cpu_baseline(torch)
         else:
-            log(f"bench: CPU baseline ({args.cpu_heads} heads)")
-            cb = cpu_baseline(args.cpu_heads, args.cpu_reps, backward=args.workload == "fwdbwd")
+            w = ATTN_WORKLOADS[args.workload]
+            heads = args.cpu_heads if args.cpu_heads is not None else CPU_HEADS[args.workload]
+            log(f"bench: CPU baseline ({heads} heads)")
+            cb = cpu_baseline(w, min(heads, w["Hq"]), args.cpu_reps or CPU_REPS.get(args.workload, 4))
         res["cpu_baseline"] = {k2: v2 for k2, v2 in cb.items() if k2 != "seconds"}
         res["cpu_baseline"]["value"] = round(cb["value"], 5)
     print(json.dumps(res), flush=True)

@@ -342,7 +342,7 @@ def pope_attention_backward_closed_form(q, k, v, freqs, delta, dout, scale=None,
 # --------------------------------------------------------------------------------------------
 
 def split_pope_attention(qc, kc, qr, kr, v, freqs, delta, scale=None, causal=True, start: int = 0,
-                         operand_dtype=None):
+                         operand_dtype=None, core_dtype=torch.float64):
     """The reference module's contraction: Q = [q_c | PoPE(q_r)], K = [k_c | PoPE(k_r, delta)]
     (src/model/fpope_attention.py:128-177).  q_c/q_r (B,Hq,S,Dc/Dr), k_c/k_r/v (B,Hkv,S,.).
     delta is the (already clamped) key phase bias.  scale defaults to (Dc + 2 Dr)^-1/2
@@ -353,7 +353,7 @@ def split_pope_attention(qc, kc, qr, kr, v, freqs, delta, scale=None, causal=Tru
     kt = torch.cat([kc.float(), pope_transform(kr, freqs, start, delta)], -1)
     qt, kt = round_ste(qt, operand_dtype), round_ste(kt, operand_dtype)
     vv = round_ste(v.float(), operand_dtype)
-    return attention(qt, kt, vv, scale, causal)
+    return attention(qt, kt, vv, scale, causal, core_dtype)
 
 
 def rope_attention(q, k, v, inv_freq, mscale: float = 1.0, qk_norm: bool = True, causal=True,

@@ -16,7 +16,14 @@ namespace {
 
 constexpr size_t ALIGN = 256;
 inline size_t align_up(size_t x) { return (x + ALIGN - 1) / ALIGN * ALIGN; }
-constexpr int INV_ROWS = 256;  // rows per inverse-transform block
+// Rows per inverse-transform block: 256, halved (down to 16) until the grid has 2048 blocks.  A
+// thread walks rows_per_block / (256 / threads per row) rows one after another, each a dependent
+// global round trip, so short sequences need short blocks to spread over the chip.
+int inv_rows(int B, int H, int S) {
+  int r = 256;
+  while (r > 16 && (int64_t)B * H * ((S + r - 1) / r) < 2048) r /= 2;
+  return r;
+}
 
 int qk_width(const pe_attn_params* p) {
   return p->Dc + (p->mode == PE_MODE_POPE ? 2 * p->Dr : p->Dr);
@@ -59,11 +66,12 @@ Layout layout(const pe_attn_params* p) {
   // query phase table (cos / sin of fl(pos * freq), fp32 [Sq][2][Dr]) for the PoPE prologue and the
   // dQ epilogue
   L.fwd_total = L.tab_off + (use_qtab(p) ? align_up((size_t)p->Sq * 2 * p->Dr * 4) : 0);
-  // per-block partial sums of the phase gradient: blocks of the inverse-transform kernel (256
-  // rows), or of the gradient kernels when the transform is fused into their epilogues (dQ GEMM:
-  // 256 queries, dK/dV: 128 keys); the buffers are sized for the larger count
-  L.nq_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hq, p->Sq, INV_ROWS) : 0;
-  L.nk_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hkv, p->Sk, 128) : 0;
+  // per-block partial sums of the phase gradient: blocks of the inverse-transform kernel
+  // (inv_rows rows, at most 256), or of the gradient kernels when the transform is fused into their
+  // epilogues (dQ GEMM: 256 queries, dK/dV: 128 keys); the buffers are sized for the larger count
+  L.nq_blocks = p->mode == PE_MODE_POPE ? pe::inv_blocks(p->B, p->Hq, p->Sq, inv_rows(p->B, p->Hq, p->Sq)) : 0;
+  L.nk_blocks = p->mode == PE_MODE_POPE
+                    ? pe::inv_blocks(p->B, p->Hkv, p->Sk, std::min(128, inv_rows(p->B, p->Hkv, p->Sk))) : 0;
   L.do_off = 0;
   L.sq_pad = (p->Sq + 127) / 128 * 128;
   const size_t nq_pad = (size_t)p->B * p->Hq * L.sq_pad;
@@ -244,7 +252,8 @@ int pe_attn_transform(const pe_attn_params* p, int is_key, const pe_tensor_t* xc
 size_t pe_attn_transform_bwd_workspace_bytes(const pe_attn_params* p, int is_key) {
   if (pe_attn_check(p) != PE_OK) return 0;
   if (p->mode != PE_MODE_POPE) return ALIGN;
-  const int nb = pe::inv_blocks(p->B, is_key ? p->Hkv : p->Hq, is_key ? p->Sk : p->Sq, INV_ROWS);
+  const int H = is_key ? p->Hkv : p->Hq, S = is_key ? p->Sk : p->Sq;
+  const int nb = pe::inv_blocks(p->B, H, S, inv_rows(p->B, H, S));
   return 2 * align_up((size_t)nb * (p->Dr > 0 ? p->Dr : 1) * 4);
 }
 
@@ -263,7 +272,8 @@ int pe_attn_transform_bwd(const pe_attn_params* p, int is_key, const float* g, c
   if ((rc = device_ok())) return rc;
   hipStream_t s = (hipStream_t)stream;
   const int H = is_key ? p->Hkv : p->Hq, S = is_key ? p->Sk : p->Sq;
-  const int nb = pe::inv_blocks(p->B, H, S, INV_ROWS);
+  const int rows = inv_rows(p->B, H, S);
+  const int nb = pe::inv_blocks(p->B, H, S, rows);
   float* part_f = (float*)workspace;
   float* part_d = (float*)((char*)workspace + need / 2);
   pe::InvArgs ia;
@@ -281,7 +291,7 @@ int pe_attn_transform_bwd(const pe_attn_params* p, int is_key, const float* g, c
   ia.mscale = p->rope_mscale;
   ia.part_delta = (is_key && p->mode == PE_MODE_POPE) ? part_d : nullptr;
   ia.part_freq = p->mode == PE_MODE_POPE ? part_f : nullptr;
-  ia.rows_per_block = INV_ROWS;
+  ia.rows_per_block = rows;
   if (ia.Dr == 0 && ia.Dc > 0) ia.mode = PE_MODE_NONE;
   if ((rc = pe::launch_inv(ia, nullptr, s))) return rc;
   if (p->mode == PE_MODE_POPE && p->Dr > 0 && (dfreqs || (is_key && ddelta))) {
@@ -292,7 +302,7 @@ int pe_attn_transform_bwd(const pe_attn_params* p, int is_key, const float* g, c
     } else {
       ra.part_q_freq = part_f; ra.nq = nb;
     }
-    ra.k_blocks_per_head = (S + INV_ROWS - 1) / INV_ROWS;
+    ra.k_blocks_per_head = (S + rows - 1) / rows;
     ra.Hkv = H; ra.B = p->B; ra.Dr = p->Dr;
     ra.delta_per_head = p->delta_head_stride != 0;
     ra.dfreqs = dfreqs; ra.ddelta = is_key ? ddelta : nullptr;
@@ -669,7 +679,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     ia.mscale = p->rope_mscale;
     ia.part_delta = key ? (float*)(bws + L.pkd_off) : nullptr;
     ia.part_freq = (float*)(bws + (key ? L.pk_off : L.pq_off));
-    ia.rows_per_block = INV_ROWS;
+    ia.rows_per_block = inv_rows(ia.B, ia.H, ia.S);
     if (ia.Dr == 0 && ia.Dc > 0) ia.mode = PE_MODE_NONE;
     int nb = 0;
     if ((rc = pe::launch_inv(ia, &nb, s))) return rc;
@@ -680,13 +690,15 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     ra.part_q_freq = (const float*)(bws + L.pq_off); ra.nq = L.nq_blocks;
     ra.part_k_freq = (const float*)(bws + L.pk_off); ra.part_k_delta = (const float*)(bws + L.pkd_off);
     ra.nk = L.nk_blocks;
-    ra.k_blocks_per_head = (p->Sk + INV_ROWS - 1) / INV_ROWS;
     if (fuse) {
       ra.nq = p->B * p->Hq * nqg;
       ra.nk = p->B * p->Hkv * nkg;
       ra.k_blocks_per_head = nkg;
     } else {
-      ra.nk = pe::inv_blocks(p->B, p->Hkv, p->Sk, INV_ROWS);
+      const int kr_rows = inv_rows(p->B, p->Hkv, p->Sk);
+      ra.nq = pe::inv_blocks(p->B, p->Hq, p->Sq, inv_rows(p->B, p->Hq, p->Sq));
+      ra.nk = pe::inv_blocks(p->B, p->Hkv, p->Sk, kr_rows);
+      ra.k_blocks_per_head = (p->Sk + kr_rows - 1) / kr_rows;
     }
     ra.Hkv = p->Hkv; ra.B = p->B; ra.Dr = p->Dr;
     ra.delta_per_head = p->delta_head_stride != 0;

@@ -452,7 +452,8 @@ int launch_inv(const InvArgs& a, int* nblocks_out, hipStream_t s) {
   if (a.mode == 0) {
     const int nb = inv_blocks(a.B, a.H, a.S, a.rows_per_block);
     if (nblocks_out) *nblocks_out = nb;
-    if (a.Dr <= 64) hipLaunchKernelGGL(inv_pope_kernel<64>, dim3(nb), dim3(256), 0, s, a);
+    if (a.Dr <= 32) hipLaunchKernelGGL(inv_pope_kernel<32>, dim3(nb), dim3(256), 0, s, a);
+    else if (a.Dr <= 64) hipLaunchKernelGGL(inv_pope_kernel<64>, dim3(nb), dim3(256), 0, s, a);
     else if (a.Dr <= 128) hipLaunchKernelGGL(inv_pope_kernel<128>, dim3(nb), dim3(256), 0, s, a);
     else hipLaunchKernelGGL(inv_pope_kernel<256>, dim3(nb), dim3(256), 0, s, a);
   } else {

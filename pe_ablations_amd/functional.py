@@ -13,7 +13,10 @@ autocast training path and its fp32 eval path).  Only GPU tensors are accepted.
 
 from __future__ import annotations
 
+import contextlib
+import ctypes
 import math
+import threading
 from typing import Optional
 
 import torch
@@ -133,12 +136,86 @@ def check_operands(q, k, v, q_c=None, k_c=None, freqs=None, delta=None, *, mode:
             raise _shape_error(f"{name} is on {t.device}, q on {dev}: every operand must be on one device")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(dev: torch.device):
+    """The current stream of dev as a raw hipStream_t (torch's raw-stream query when it has one)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index)
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _on(dev: torch.device):
+    """Make dev current for the library call (a no-op context when it already is)."""
+    if dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
+
+
+def _sig(t: Optional[torch.Tensor]):
+    return None if t is None else (tuple(t.shape), t.stride(), t.dtype, t.device)
+
+
+class _Desc:
+    """A PeTensor descriptor whose shape, strides and dtype are fixed by a launch plan's key; only
+    the data pointer changes from call to call."""
+    __slots__ = ("t", "ref")
+
+    def __init__(self, t: Optional[torch.Tensor]):
+        self.t = _tensor(t)
+        self.ref = ctypes.byref(self.t)
+
+    def bind(self, x: Optional[torch.Tensor]):
+        if x is not None:
+            self.t.data = x.data_ptr()
+        return self.ref
+
+
+class _FwdPlan:
+    """Per-signature launch state of PEAttentionFn: the parameter block (checked once), the
+    workspace sizes and the tensor descriptors.  Backward plans hang off it, keyed by dout's
+    signature and the gradients needed."""
+    __slots__ = ("p", "pref", "ws", "cdt", "out_shape", "d", "bwd")
+
+    def __init__(self, cfg, qr, kr, v, qc, kc, delta):
+        L = _lib.lib()
+        self.p = _params(cfg, qr, kr, v, qc, delta)
+        self.pref = ctypes.byref(self.p)
+        _lib.check(L.pe_attn_check(self.pref))
+        self.ws = L.pe_attn_fwd_workspace_bytes(self.pref)
+        self.cdt = torch.bfloat16 if cfg["dtype"] == _lib.PE_DTYPE_BF16 else torch.float32
+        B, Hq, Sq, Dv = qr.shape[0], qr.shape[1], qr.shape[2], v.shape[3]
+        self.out_shape = (B, Sq, Hq, Dv)
+        out = torch.empty(self.out_shape, dtype=self.cdt, device=qr.device).transpose(1, 2)
+        self.d = [_Desc(t) for t in (qc, qr, kc, kr, v, out)]
+        self.bwd = {}
+
+
+class _BwdPlan:
+    __slots__ = ("bws", "d")
+
+    def __init__(self, fp: _FwdPlan, tensors):
+        self.bws = _lib.lib().pe_attn_bwd_workspace_bytes(fp.pref)
+        self.d = [_Desc(t) for t in tensors]
+
+
+# Launch plans per thread (torch runs backward passes on its own device thread), keyed by the
+# operands' shapes, strides, dtypes and devices and the call's options; rebuilt from scratch when
+# the table grows past _PLAN_LIMIT (e.g. many distinct KV-cache start positions).
+_tls = threading.local()
+_PLAN_LIMIT = 256
+
+
+def _plans() -> dict:
+    d = getattr(_tls, "plans", None)
+    if d is None or len(d) > _PLAN_LIMIT:
+        d = _tls.plans = {}
+    return d
 
 
 class PEAttentionFn(torch.autograd.Function):
@@ -151,21 +228,23 @@ class PEAttentionFn(torch.autograd.Function):
     def forward(ctx, qr, kr, v, qc, kc, freqs, delta, cfg):
         L = _lib.lib()
         dev = qr.device
-        p = _params(cfg, qr, kr, v, qc, delta)
-        _lib.check(L.pe_attn_check(ctypes_ref(p)))
-        cdt = torch.bfloat16 if cfg["dtype"] == _lib.PE_DTYPE_BF16 else torch.float32
-        B, Hq, Sq, Dv = qr.shape[0], qr.shape[1], qr.shape[2], v.shape[3]
-        ws_bytes = L.pe_attn_fwd_workspace_bytes(ctypes_ref(p))
-        fws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        out = torch.empty((B, Sq, Hq, Dv), dtype=cdt, device=dev).transpose(1, 2)
-        lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
-            rc = L.pe_attn_fwd(ctypes_ref(p), ref(_tensor(qc)), ref(_tensor(qr)), ref(_tensor(kc)),
-                               ref(_tensor(kr)), ref(_tensor(v)), _ptr(freqs), _ptr(delta),
-                               ref(_tensor(out)), lse.data_ptr(), fws.data_ptr(), ws_bytes, _stream(dev))
+        key = (cfg["key"], _sig(qr), _sig(kr), _sig(v), _sig(qc), _sig(kc),
+               None if delta is None else delta.dim())
+        plans = _plans()
+        fp = plans.get(key)
+        if fp is None:
+            fp = plans[key] = _FwdPlan(cfg, qr, kr, v, qc, kc, delta)
+        fws = torch.empty(fp.ws, dtype=torch.uint8, device=dev)
+        out = torch.empty(fp.out_shape, dtype=fp.cdt, device=dev).transpose(1, 2)
+        lse = torch.empty((fp.out_shape[0], fp.out_shape[2], fp.out_shape[1]), dtype=torch.float32, device=dev)
+        d = fp.d
+        with _on(dev):
+            rc = L.pe_attn_fwd(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr), d[4].bind(v),
+                               _ptr(freqs), _ptr(delta), d[5].bind(out), lse.data_ptr(), fws.data_ptr(), fp.ws,
+                               _stream(dev))
         _lib.check(rc)
         ctx.cfg = cfg
-        ctx.ws_bytes = ws_bytes
+        ctx.key = key
         ctx.save_for_backward(qr, kr, v, qc, kc, freqs, delta, out, lse, fws)
         ctx.mark_non_differentiable(lse)
         return out, lse
@@ -176,28 +255,35 @@ class PEAttentionFn(torch.autograd.Function):
         qr, kr, v, qc, kc, freqs, delta, out, lse, fws = ctx.saved_tensors
         cfg = ctx.cfg
         dev = qr.device
-        p = _params(cfg, qr, kr, v, qc, delta)
-        dout = dout if dout.stride(-1) == 1 else dout.contiguous()
+        plans = _plans()
+        fp = plans.get(ctx.key)
+        if fp is None:
+            fp = plans[ctx.key] = _FwdPlan(cfg, qr, kr, v, qc, kc, delta)
+        if dout.stride(-1) != 1:
+            dout = dout.contiguous()
         if dout.dtype not in (torch.bfloat16, torch.float32):
             dout = dout.float()
         dqr, dkr = torch.empty_like(qr), torch.empty_like(kr)
         dqc = None if qc is None else torch.empty_like(qc)
         dkc = None if kc is None else torch.empty_like(kc)
-        cdt = torch.bfloat16 if cfg["dtype"] == _lib.PE_DTYPE_BF16 else torch.float32
+        cdt = fp.cdt
         dv = torch.empty_like(v, dtype=cdt) if v.dtype != cdt else torch.empty_like(v)
         need_f = freqs is not None and ctx.needs_input_grad[5]
         need_d = delta is not None and ctx.needs_input_grad[6]
         dfreqs = torch.empty(freqs.shape, dtype=torch.float32, device=dev) if need_f else None
         ddelta = torch.empty(delta.shape, dtype=torch.float32, device=dev) if need_d else None
-        bws_bytes = L.pe_attn_bwd_workspace_bytes(ctypes_ref(p))
-        bws = torch.empty(bws_bytes, dtype=torch.uint8, device=dev)
-        with torch.cuda.device(dev):
-            rc = L.pe_attn_bwd(ctypes_ref(p), ref(_tensor(qc)), ref(_tensor(qr)), ref(_tensor(kc)),
-                               ref(_tensor(kr)), ref(_tensor(v)), _ptr(freqs), _ptr(delta),
-                               ref(_tensor(out)), lse.data_ptr(), ref(_tensor(dout)),
-                               ref(_tensor(dqc)), ref(_tensor(dqr)), ref(_tensor(dkc)), ref(_tensor(dkr)),
-                               ref(_tensor(dv)), _ptr(dfreqs), _ptr(ddelta), fws.data_ptr(), ctx.ws_bytes,
-                               bws.data_ptr(), bws_bytes, _stream(dev))
+        bkey = (_sig(dout), _sig(dqr), _sig(dkr), _sig(dqc), _sig(dkc), _sig(dv))
+        bp = fp.bwd.get(bkey)
+        if bp is None:
+            bp = fp.bwd[bkey] = _BwdPlan(fp, (qc, qr, kc, kr, v, out, dout, dqc, dqr, dkc, dkr, dv))
+        bws = torch.empty(bp.bws, dtype=torch.uint8, device=dev)
+        d = bp.d
+        with _on(dev):
+            rc = L.pe_attn_bwd(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr), d[4].bind(v),
+                               _ptr(freqs), _ptr(delta), d[5].bind(out), lse.data_ptr(), d[6].bind(dout),
+                               d[7].bind(dqc), d[8].bind(dqr), d[9].bind(dkc), d[10].bind(dkr), d[11].bind(dv),
+                               _ptr(dfreqs), _ptr(ddelta), fws.data_ptr(), fp.ws, bws.data_ptr(), bp.bws,
+                               _stream(dev))
         _lib.check(rc)
         if dv.dtype != v.dtype:
             dv = dv.to(v.dtype)
@@ -273,6 +359,7 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
     cfg = dict(mode=m, dtype=dt, causal=_CAUSAL[causal], start_pos_q=int(start_pos_q),
                start_pos_k=int(start_pos_k), qk_norm=bool(qk_norm), scale=float(scale),
                mscale=float(rope_mscale))
+    cfg["key"] = tuple(cfg.values())
     if qr_norm_weight is not None or kr_norm_weight is not None:
         out, lse = _fwd_normed(q, k, v, q_c, k_c, freqs, delta, cfg, qr_norm_weight, kr_norm_weight, norm_eps)
     else:

@@ -117,7 +117,15 @@ def test_workspace_sizes(lib):
     rows = 2 * 3 * 100
     assert fws >= 2 * rows * 128 * 2 + rows * 64 * 2
     bws = lib.pe_attn_bwd_workspace_bytes(ctypes.byref(p))
-    assert bws >= rows * 64 * 2 + rows * 4 + 2 * rows * 128 * 4
+    # bf16 fused PoPE (Dc = 0, Dr = 64): dO repack, Di and L2, and the packed causal dS (at least
+    # the triangle's 100 * 101 / 2 bf16 elements per head, at most the padded 128 x 256 square);
+    # no fp32 dq~ / dk~ buffers
+    assert bws >= rows * 64 * 2 + 2 * rows * 4 + 6 * (100 * 101 // 2) * 2
+    assert bws < rows * 64 * 2 + 2 * rows * 4 + 2 * rows * 128 * 4 + 6 * 128 * 256 * 2 + 8 * 4096
+    # the fp32 path and the split form keep them
+    for kw in (dict(dtype=_lib.PE_DTYPE_FP32), dict(Dc=64, Dr=32)):
+        q = params(**dict(dict(B=2, Hq=3, Hkv=3, Sq=100, Sk=100, Dr=64, Dv=64), **kw))
+        assert lib.pe_attn_bwd_workspace_bytes(ctypes.byref(q)) >= 2 * rows * 128 * 4, kw
     assert lib.pe_attn_fwd_workspace_bytes(ctypes.byref(params(B=0))) == 0
     assert lib.pe_attn_operand_width(ctypes.byref(p)) == 128
     assert lib.pe_attn_operand_width(ctypes.byref(params(Dc=64, Dr=32))) == 128

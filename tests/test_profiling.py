@@ -39,3 +39,34 @@ def test_committed_traffic_covers_the_attention_kernels():
     # the dK/dV kernel writes the bf16 dS of the causal triangle, B*H*S^2/2 * 2 bytes at S = 16384
     dk = next(v for k, v in data["kernels"].items() if k.startswith(("dkdv_pair_kernel<", "dkdv_bf16_kernel<")))
     assert dk["write_bytes"] > 16 * 16384 * 16384 // 2 * 2 * 0.95
+
+
+def test_workload_flops_and_prologue_bytes():
+    """The general FLOP count reduces to 3 / 8 / 11 * B*H*S^2*D in the fused form, counts the split
+    form's content width once and its positional width twice, and the prologue moves raw rows in
+    and transformed rows out."""
+    bench = _bench()
+    w = bench.ATTN_WORKLOADS["fwdbwd"]
+    F = bench.attn_flops(w)
+    base = 1 * 16 * 16384 ** 2 * 128
+    assert (F["fwd"], F["bwd"], F["total"], F["fa_convention"]) == (3 * base, 8 * base, 11 * base, 7 * base)
+    assert F["fwd_core"] + F["bwd_dkdv"] + F["bwd_dq"] == F["total"]
+    assert bench.flops(1, 16, 16384, 128) == F
+    # q and k: 16 heads x 16384 rows of 128 bf16 in, 256 bf16 out
+    assert bench.prologue_bytes(w) == 2 * 16 * 16384 * (128 + 256) * 2
+    sp = bench.ATTN_WORKLOADS["split"]
+    Fs = bench.attn_flops(sp)
+    pairs = 8 * 8 * 512 * 512 / 2
+    assert Fs["fwd"] == 2 * pairs * ((64 + 64) + 64)          # S~ over [content | cos | sin], PV over 64
+    assert Fs["bwd"] == 2 * pairs * (3 * 128 + 2 * 64)
+    assert bench.prologue_bytes(sp) == 8 * (8 + 4) * 512 * ((64 + 32) + (64 + 64)) * 2
+    assert bench.prologue_bytes(bench.ATTN_WORKLOADS["fwd32"]) == 2 * bench.prologue_bytes(w)
+
+
+def test_cpu_baseline_runs_every_form():
+    """The cpu_baseline leg on tiny copies of the workloads (fused, FoPE, split form with GQA)."""
+    bench = _bench()
+    for name in ("fwdbwd", "c3", "split", "fwd"):
+        w = dict(bench.ATTN_WORKLOADS[name], S=64)
+        cb = bench.cpu_baseline(w, heads=2, reps=1)
+        assert cb["value"] > 0 and cb["kind"] == "port" and cb["cores"] >= 1 and cb["cpu"]
