@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 1
+#define PE_ATTN_ABI_VERSION 2
 
 /* positional-encoding mode */
 enum {
@@ -44,6 +44,14 @@ enum {
 
 /* element types of tensors crossing the boundary */
 enum { PE_DTYPE_BF16 = 0, PE_DTYPE_FP32 = 1 };
+
+/* how the PoPE / FoPE phase product sees a position p (pe_attn_params.position_rounding) */
+enum {
+  PE_POS_EXACT = 0, /* fl(p * freq) with p exact in fp32 (PoPEEmbedding, src/model/pope.py:110-119)  */
+  PE_POS_BF16 = 1,  /* p rounded to bf16 first: FoPE's arange(..., dtype=x.dtype) for bf16 x
+                       (src/model/fpope.py:285,322) */
+  PE_POS_FP16 = 2   /* p rounded to fp16 first (the same under fp16 autocast; inf beyond 65519) */
+};
 
 /* causal masking: key s visible to query t iff s <= t + off */
 enum {
@@ -88,6 +96,8 @@ typedef struct {
   float scale;                      /* softmax scale applied to q~ . k~                              */
   float rope_mscale;                /* YaRN mscale multiplying rotated q and k (1 otherwise)         */
   int64_t delta_head_stride;        /* PoPE key phase bias: 0 = (Dr,) shared, else per kv head     */
+  int32_t position_rounding;        /* PE_POS_* (PoPE mode only; 0 = exact positions)              */
+  int32_t reserved;                 /* 0                                                           */
 } pe_attn_params;
 
 /* Host-only validation of a parameter block (no device work). */

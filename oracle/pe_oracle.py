@@ -124,17 +124,26 @@ def yarn_inv_freq(dim: int, theta: float, scale: float, original_max_seq_len: in
 # PE transforms (float32, reference operation order)
 # --------------------------------------------------------------------------------------------
 
-def positions(n: int, start: int = 0) -> torch.Tensor:
-    return torch.arange(start, start + n, dtype=torch.float32)
+def positions(n: int, start: int = 0, pos_dtype=None) -> torch.Tensor:
+    """start .. start + n - 1 as float32.  ``pos_dtype`` bf16 / fp16 builds them as the reference
+    FoPE does on the GPU, torch.arange(..., dtype=x.dtype) (src/model/fpope.py:285,322): ATen's GPU
+    arange forms each value start + i in fp32 and casts it to the dtype, so every position is
+    rounded to nearest, ties to even (fp16: inf from 65520 on).  Torch's CPU arange for fp16 rounds
+    the start first and differs, so the positions are cast here rather than built by a CPU arange
+    of that dtype.  None keeps them exact (PoPE, src/model/pope.py:110-119)."""
+    pos = torch.arange(start, start + n, dtype=torch.float32)
+    if pos_dtype is None or pos_dtype == torch.float32:
+        return pos
+    return pos.to(pos_dtype).float()
 
 
 def pope_phases(n: int, freqs: torch.Tensor, start: int = 0,
-                delta: Optional[torch.Tensor] = None, dtype=torch.float32) -> torch.Tensor:
+                delta: Optional[torch.Tensor] = None, dtype=torch.float32, pos_dtype=None) -> torch.Tensor:
     """phi = fl(pos * theta) (+ delta): torch.outer then add, float32 (src/model/pope.py:88-90,172-176).
 
     delta: None, (D,) shared, or (H, D) per head.  Returns (S, D) or (H, S, D).  ``dtype`` float64
     evaluates the same expression in double precision (used by gradient checks)."""
-    ph = torch.outer(positions(n, start).to(dtype), freqs.to(dtype))
+    ph = torch.outer(positions(n, start, pos_dtype).to(dtype), freqs.to(dtype))
     if delta is None:
         return ph
     delta = delta.to(dtype)
@@ -144,14 +153,14 @@ def pope_phases(n: int, freqs: torch.Tensor, start: int = 0,
 
 
 def pope_transform(x: torch.Tensor, freqs: torch.Tensor, start: int = 0,
-                   delta: Optional[torch.Tensor] = None, dtype=torch.float32) -> torch.Tensor:
+                   delta: Optional[torch.Tensor] = None, dtype=torch.float32, pos_dtype=None) -> torch.Tensor:
     """x (B, H, S, D) -> [mu cos phi, mu sin phi] (B, H, S, 2D), float32 math (or ``dtype``).
 
     Query: delta None (src/model/pope.py:124-149).  Key: delta already clamped by the caller
     (src/model/pope.py:151-183).  mu = softplus (beta 1, threshold 20)."""
     B, H, S, D = x.shape
     mu = F.softplus(x.to(dtype))
-    ph = pope_phases(S, freqs, start, delta, dtype)
+    ph = pope_phases(S, freqs, start, delta, dtype, pos_dtype)
     if ph.dim() == 2:
         ph = ph.view(1, 1, S, D)
     else:
@@ -405,19 +414,20 @@ def brute_force_pope(q, k, v, freqs, delta, scale, causal=True):
 
 def pope_attention_chunked(q, k, v, freqs, delta, dout=None, scale=None, causal=True,
                            start_q: int = 0, start_k: int = 0, chunk: int = 1024,
-                           core_dtype=torch.float32, operand_dtype=None):
+                           core_dtype=torch.float32, operand_dtype=None, pos_dtype=None):
     """Fused-form PoPE attention forward (and, with ``dout``, the closed-form backward of
     pope_attention_backward_closed_form) evaluated in query-row chunks so the (S, S) score
     matrix never exists whole.  Single (b, h): q (Sq, D), k/v (Sk, D), delta (D,) as used.
     Transforms in fp32 in the reference order; ``operand_dtype`` rounds q~, k~, v as autocast
     would; the GEMMs run in ``core_dtype``.  Causal alignment: top-left when Sq == Sk, else
-    bottom-right.  Returns dict(out, lse[, dq, dk, dv, dfreqs, ddelta])."""
+    bottom-right.  ``pos_dtype`` rounds the positions as in ``positions`` (FoPE's x.dtype), in the
+    phases and in the frequency gradient.  Returns dict(out, lse[, dq, dk, dv, dfreqs, ddelta])."""
     Sq, D = q.shape
     Sk = k.shape[0]
     scale = (1.0 / math.sqrt(D)) if scale is None else scale
     ct = core_dtype
-    qt = pope_transform(q.view(1, 1, Sq, D), freqs, start_q)[0, 0]
-    kt = pope_transform(k.view(1, 1, Sk, D), freqs, start_k, delta)[0, 0]
+    qt = pope_transform(q.view(1, 1, Sq, D), freqs, start_q, pos_dtype=pos_dtype)[0, 0]
+    kt = pope_transform(k.view(1, 1, Sk, D), freqs, start_k, delta, pos_dtype=pos_dtype)[0, 0]
     vv = v.float()
     if operand_dtype is not None:
         qt, kt, vv = (t.to(operand_dtype).float() for t in (qt, kt, vv))
@@ -454,10 +464,10 @@ def pope_attention_chunked(q, k, v, freqs, delta, dout=None, scale=None, causal=
         dkt += dS.T @ qt[r0:r1]
         dv += P.T @ do[r0:r1]
     f64 = torch.float64
-    tq = torch.arange(start_q, start_q + Sq, dtype=f64)
-    tk = torch.arange(start_k, start_k + Sk, dtype=f64)
-    phq = pope_phases(Sq, freqs, start_q).to(f64)
-    phk = pope_phases(Sk, freqs, start_k, delta).to(f64)
+    tq = positions(Sq, start_q, pos_dtype).to(f64)
+    tk = positions(Sk, start_k, pos_dtype).to(f64)
+    phq = pope_phases(Sq, freqs, start_q, pos_dtype=pos_dtype).to(f64)
+    phk = pope_phases(Sk, freqs, start_k, delta, pos_dtype=pos_dtype).to(f64)
     mq, mk = F.softplus(q.double()), F.softplus(k.double())
 
     def inv(g, mu, ph):

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(PKG_DIR, "libpe_attn.so")
 PE_MODE_POPE, PE_MODE_ROPE, PE_MODE_NONE = 0, 1, 2
 PE_DTYPE_BF16, PE_DTYPE_FP32 = 0, 1
 PE_CAUSAL_NONE, PE_CAUSAL_TOP_LEFT, PE_CAUSAL_BOTTOM_RIGHT = 0, 1, 2
+PE_POS_EXACT, PE_POS_BF16, PE_POS_FP16 = 0, 1, 2
 
 ERRORS = {
     "PE_OK": 0, "PE_ERR_NULL": -1, "PE_ERR_SHAPE": -2, "PE_ERR_HEAD_DIM": -3, "PE_ERR_MODE": -4,
@@ -49,7 +50,8 @@ class PeParams(ctypes.Structure):
                 ("start_pos_q", ctypes.c_int32), ("start_pos_k", ctypes.c_int32),
                 ("qk_l2norm", ctypes.c_int32),
                 ("scale", ctypes.c_float), ("rope_mscale", ctypes.c_float),
-                ("delta_head_stride", ctypes.c_int64)]
+                ("delta_head_stride", ctypes.c_int64),
+                ("position_rounding", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class PeNormParams(ctypes.Structure):

@@ -154,6 +154,7 @@ void fill_prep(pe::PrepArgs& a, const pe_attn_params* p, int is_key, const pe_te
   a.B = p->B; a.H = is_key ? p->Hkv : p->Hq; a.S = is_key ? p->Sk : p->Sq;
   a.Dc = p->Dc; a.Dr = p->Dr; a.mode = p->mode;
   a.start_pos = is_key ? p->start_pos_k : p->start_pos_q;
+  a.pos_round = p->position_rounding;
   a.l2norm = p->qk_l2norm; a.is_key = is_key;
   a.freqs = freqs; a.delta = delta; a.delta_hs = p->delta_head_stride;
   a.mscale = p->rope_mscale;
@@ -213,6 +214,9 @@ int pe_attn_check(const pe_attn_params* p) {
   if (p->mode < 0 || p->mode > 2 || (p->dtype != PE_DTYPE_BF16 && p->dtype != PE_DTYPE_FP32) || p->causal < 0 || p->causal > 2)
     return PE_ERR_MODE;
   if (p->mode != PE_MODE_POPE && (p->Dr % 2) != 0) return PE_ERR_MODE;
+  if (p->position_rounding < PE_POS_EXACT || p->position_rounding > PE_POS_FP16 ||
+      (p->position_rounding != PE_POS_EXACT && p->mode != PE_MODE_POPE))
+    return PE_ERR_MODE;
   if (p->causal == PE_CAUSAL_BOTTOM_RIGHT && p->Sq > p->Sk) return PE_ERR_SHAPE;
   if (p->causal == PE_CAUSAL_TOP_LEFT && p->Sq != p->Sk) return PE_ERR_SHAPE;
   if (qk_width(p) <= 0 || pad_qk(qk_width(p)) < 0 || pad_v(p->Dv) < 0) return PE_ERR_HEAD_DIM;
@@ -286,6 +290,7 @@ int pe_attn_transform_bwd(const pe_attn_params* p, int is_key, const float* g, c
   ia.B = p->B; ia.H = H; ia.S = S;
   ia.Dc = p->Dc; ia.Dr = p->Dr; ia.mode = p->mode;
   ia.start_pos = is_key ? p->start_pos_k : p->start_pos_q;
+  ia.pos_round = p->position_rounding;
   ia.l2norm = p->qk_l2norm; ia.is_key = is_key;
   ia.freqs = freqs; ia.delta = is_key ? delta : nullptr; ia.delta_hs = p->delta_head_stride;
   ia.mscale = p->rope_mscale;
@@ -337,7 +342,8 @@ static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe
   pe::PrepArgs a;
   stage_mark(PE_STAGE_FWD_PREP, 0, s);
   float* qtab = use_qtab(p) ? (float*)(ws + L.tab_off) : nullptr;
-  if (qtab && (rc = pe::launch_phase_table(freqs, p->start_pos_q, p->Sq, p->Dr, qtab, s))) return rc;
+  if (qtab && (rc = pe::launch_phase_table(freqs, p->start_pos_q, p->Sq, p->Dr, p->position_rounding, qtab, s)))
+    return rc;
   fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
   a.tab = qtab;
   if (nrm) {
@@ -640,11 +646,12 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     c.freqs = freqs;
     c.delta = delta;
     c.delta_hs = p->delta_head_stride;
-    auto view = [](pe::EpiPoPE& e, const pe_tensor_t* x, const pe_tensor_t* dx, int start) {
+    auto view = [p](pe::EpiPoPE& e, const pe_tensor_t* x, const pe_tensor_t* dx, int start) {
       e.x = x->data; e.x_dtype = x->dtype;
       e.dx = (void*)dx->data; e.dx_dtype = dx->dtype;
       for (int i = 0; i < 4; ++i) { e.x_s[i] = x->stride[i]; e.dx_s[i] = dx->stride[i]; }
       e.start_pos = start;
+      e.pos_round = p->position_rounding;
     };
     view(c.eq, qr, dqr, p->start_pos_q);
     view(c.ek, kr, dkr, p->start_pos_k);
@@ -674,6 +681,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     ia.B = p->B; ia.H = key ? p->Hkv : p->Hq; ia.S = key ? p->Sk : p->Sq;
     ia.Dc = p->Dc; ia.Dr = p->Dr; ia.mode = p->mode;
     ia.start_pos = key ? p->start_pos_k : p->start_pos_q;
+    ia.pos_round = p->position_rounding;
     ia.l2norm = p->qk_l2norm; ia.is_key = key;
     ia.freqs = freqs; ia.delta = key ? delta : nullptr; ia.delta_hs = p->delta_head_stride;
     ia.mscale = p->rope_mscale;

@@ -578,7 +578,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
       for (int u = 0; u < EU; ++u) {
         const int r = r0 + u * rstep, key = k0 + r;
         if (r < BNK && key < a.Sk) {
-          const float pos = (float)(e.start_pos + key);
+          const float pos = pe_pos(e.start_pos + key, e.pos_round);
           float dx;
           const float dph = inv_pope_elem(xv[u], pos, fr, dl, a.delta != nullptr, st[r * DQK + c],
                                           st[r * DQK + Dr + c], dx);
@@ -670,7 +670,7 @@ __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st,
     if (idx < nidx) {
       const f32x4 c_lo = *(const f32x4*)(st + r * DQK + c0), c_hi = *(const f32x4*)(st + r * DQK + c0 + 4);
       const f32x4 s_lo = *(const f32x4*)(st + r * DQK + Dr + c0), s_hi = *(const f32x4*)(st + r * DQK + Dr + c0 + 4);
-      const float pos = (float)(e.start_pos + idx);
+      const float pos = pe_pos(e.start_pos + idx, e.pos_round);
       float dx[8];
       if constexpr (TAB) {
         const float* tr = tab + (int64_t)idx * DQK + c0;
@@ -1043,7 +1043,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       for (int u = 0; u < EU; ++u) {
         const int r = r0 + u * rstep, key = k0 + r;
         if (r < BNK && key < a.Sk) {
-          const float pos = (float)(e.start_pos + key);
+          const float pos = pe_pos(e.start_pos + key, e.pos_round);
           float dx;
           const float dph = inv_pope_elem(xv[u], pos, fr, dl, a.delta != nullptr, st[r * DQK + c],
                                           st[r * DQK + Dr + c], dx);
@@ -1343,7 +1343,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
           const int R = R0 + u * rstep, q = q0 + R;
           if (q < a.Sq) {
             const int r = R & 127;
-            const float pos = (float)(e.start_pos + q);
+            const float pos = pe_pos(e.start_pos + q, e.pos_round);
             float dx;
             const float dph = inv_pope_elem(xv[u], pos, fr, 0.f, false, st[r * DQK + c], st[r * DQK + Dr + c], dx);
             store_from_float(e.dx, b * e.dx_s[0] + h * e.dx_s[1] + (int64_t)q * e.dx_s[2] + c * e.dx_s[3],

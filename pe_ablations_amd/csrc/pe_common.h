@@ -53,6 +53,16 @@ __device__ __forceinline__ float bf2f(uint16_t h) {
 
 __device__ __forceinline__ float round_bf16(float x) { return bf2f(f2bf(x)); }
 
+// A position as the phase product sees it (PE_POS_*): exact (0), or first rounded to the nearest
+// bf16 (1) or fp16 (2), ties to even, which is what torch.arange(..., dtype=x.dtype) holds for a
+// bf16 / fp16 x (fp16 overflows to inf past 65519)
+__device__ __forceinline__ float pe_pos(int p, int rounding) {
+  const float x = (float)p;
+  if (rounding == 1) return round_bf16(x);
+  if (rounding == 2) return (float)(_Float16)x;
+  return x;
+}
+
 __device__ __forceinline__ void unpack8(const u32x4& v, float (&x)[8]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {

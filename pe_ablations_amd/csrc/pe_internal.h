@@ -13,6 +13,7 @@ struct EpiPoPE {
   const void* x; int x_dtype; int64_t x_s[4];
   void* dx; int dx_dtype; int64_t dx_s[4];
   int start_pos;
+  int pos_round;  // PE_POS_* rounding of positions
   float* part_delta;
   float* part_freq;
 };
@@ -86,6 +87,7 @@ struct PrepArgs {
   const void* xr; int xr_dtype; int64_t xr_s[4];
   void* dst; int dst_dtype; int width;           // (B, H, S, width) contiguous
   int B, H, S, Dc, Dr, mode, start_pos, l2norm, is_key;
+  int pos_round;  // PE_POS_* rounding of positions (PoPE)
   const float* freqs; const float* delta; int64_t delta_hs;
   float mscale;
   // RMSNorm of xr over all H*Dr features of a token before the transform (launch_prep_norm only)
@@ -99,9 +101,9 @@ struct PrepArgs {
   int dst_rows, dst_row0;
 };
 int launch_prep(const PrepArgs& a, hipStream_t s);
-// cos / sin of the query phases fl((start + s) * freqs[c]) for s < S, c < Dr into tab [S][2][Dr]
-// (cos row then sin row), with the same routine and rounding as the prologue kernels
-int launch_phase_table(const float* freqs, int start, int S, int Dr, float* tab, hipStream_t s);
+// cos / sin of the query phases fl(pe_pos(start + s) * freqs[c]) for s < S, c < Dr into tab
+// [S][2][Dr] (cos row then sin row), with the same routine and rounding as the prologue kernels
+int launch_phase_table(const float* freqs, int start, int S, int Dr, int pos_round, float* tab, hipStream_t s);
 // PoPE prologue with the RMSNorm fused in: one workgroup per token (all heads)
 int launch_prep_norm(const PrepArgs& a, hipStream_t s);
 
@@ -153,6 +155,7 @@ struct InvArgs {
   void* dxc; int dxc_dtype; int64_t dxc_s[4];
   void* dxr; int dxr_dtype; int64_t dxr_s[4];
   int B, H, S, Dc, Dr, mode, start_pos, l2norm, is_key;
+  int pos_round;  // PE_POS_* rounding of positions (PoPE)
   const float* freqs; const float* delta; int64_t delta_hs;
   float mscale;
   float* part_delta;   // (nblocks, Dr) or NULL

@@ -81,7 +81,7 @@ __global__ __launch_bounds__(NT) void prep_pope_norm_kernel(PrepArgs a) {
   const int nch = a.H * tpr;
   const int tok = blockIdx.x;
   const int b = tok / a.S, s = tok - b * a.S;
-  const float pos = (float)(a.start_pos + s);
+  const float pos = pe_pos(a.start_pos + s, a.pos_round);
   float x[MAXC][8];
   float ss = 0.f;
 #pragma unroll

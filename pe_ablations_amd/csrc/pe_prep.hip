@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
   const int s = (int)(row % a.S);
   const int bh = (int)(row / a.S);
   const int h = bh % a.H, b = bh / a.H;
-  const float pos = (float)(a.start_pos + s);
+  const float pos = pe_pos(a.start_pos + s, a.pos_round);
   const int64_t dbase = ((int64_t)bh * (a.dst_rows ? a.dst_rows : a.S) + a.dst_row0 + s) * a.width;
 
   for (int c = lane; c < a.Dc; c += 64) {
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void inv_pope_kernel(InvArgs a) {
     for (int cc = c; cc < a.Dc; cc += TPR)
       store_from_float(a.dxc, b * a.dxc_s[0] + h * a.dxc_s[1] + (int64_t)s * a.dxc_s[2] + cc * a.dxc_s[3], a.dxc_dtype, a.g[grow + cc]);
     if (c < a.Dr) {
-      const float pos = (float)(a.start_pos + s);
+      const float pos = pe_pos(a.start_pos + s, a.pos_round);
       const float x = load_as_float(a.xr, b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + c * a.xr_s[3], a.xr_dtype);
       float mu, sg;
       softplus_sigmoid(x, mu, sg);
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void inv_row_kernel(InvArgs a) {
   const int s = (int)(row % a.S);
   const int bh = (int)(row / a.S);
   const int h = bh % a.H, b = bh / a.H;
-  const float pos = (float)(a.start_pos + s);
+  const float pos = pe_pos(a.start_pos + s, a.pos_round);
   const int64_t grow = row * a.width;
   for (int c = lane; c < a.Dc; c += 64)
     store_from_float(a.dxc, b * a.dxc_s[0] + h * a.dxc_s[1] + (int64_t)s * a.dxc_s[2] + c * a.dxc_s[3], a.dxc_dtype, a.g[grow + c]);
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
   const int s = (int)(row % a.S);
   const int bh = (int)(row / a.S);
   const int h = bh % a.H, b = bh / a.H;
-  const float pos = (float)(a.start_pos + s);
+  const float pos = pe_pos(a.start_pos + s, a.pos_round);
   uint16_t* drow = (uint16_t*)a.dst + ((int64_t)bh * (a.dst_rows ? a.dst_rows : a.S) + a.dst_row0 + s) * a.width;
   const u32x4 xv = *(const u32x4*)((const uint16_t*)a.xr + b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + t * 8);
   const f32x4 f0 = *(const f32x4*)(a.freqs + t * 8), f1 = *(const f32x4*)(a.freqs + t * 8 + 4);
@@ -410,20 +410,22 @@ int launch_prep(const PrepArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
-__global__ __launch_bounds__(256) void phase_table_kernel(const float* freqs, int start, int S, int Dr, float* tab) {
+__global__ __launch_bounds__(256) void phase_table_kernel(const float* freqs, int start, int S, int Dr, int pos_round,
+                                                          float* tab) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (int64_t)S * Dr) return;
   const int s = (int)(gid / Dr), c = (int)(gid % Dr);
   float sn, cs;
-  pe_sincos(mul_nc((float)(start + s), freqs[c]), sn, cs);
+  pe_sincos(mul_nc(pe_pos(start + s, pos_round), freqs[c]), sn, cs);
   tab[(int64_t)s * 2 * Dr + c] = cs;
   tab[(int64_t)s * 2 * Dr + Dr + c] = sn;
 }
 
-int launch_phase_table(const float* freqs, int start, int S, int Dr, float* tab, hipStream_t s) {
+int launch_phase_table(const float* freqs, int start, int S, int Dr, int pos_round, float* tab, hipStream_t s) {
   const int64_t n = (int64_t)S * Dr;
   if (n == 0) return 0;
-  hipLaunchKernelGGL(phase_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, freqs, start, S, Dr, tab);
+  hipLaunchKernelGGL(phase_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, freqs, start, S, Dr, pos_round,
+                     tab);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 

@@ -104,8 +104,14 @@ class FoPEPoPEEmbedding(nn.Module):
                                                         device=self.positions.device), persistent=False)
         self.max_seq_len = new_max_seq_len
 
+    # the reference builds the positions of forward_query / forward_key with
+    # torch.arange(..., dtype=x.dtype) (src/model/fpope.py:285,322): rounded to bf16 for a bf16 x
+    positions_in_input_dtype = True
+
     def forward_query(self, x: torch.Tensor, start_pos: int = 0) -> torch.Tensor:
-        return pe_transform(x, self.kernel_freqs(), None, start_pos=start_pos, is_key=False)
+        return pe_transform(x, self.kernel_freqs(), None, start_pos=start_pos, is_key=False,
+                            position_dtype=x.dtype)
 
     def forward_key(self, x: torch.Tensor, start_pos: int = 0) -> torch.Tensor:
-        return pe_transform(x, self.kernel_freqs(), self.kernel_delta(), start_pos=start_pos, is_key=True)
+        return pe_transform(x, self.kernel_freqs(), self.kernel_delta(), start_pos=start_pos, is_key=True,
+                            position_dtype=x.dtype)

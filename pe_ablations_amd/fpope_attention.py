@@ -100,12 +100,17 @@ class FPoPEGroupedQueryAttention(nn.Module):
             return pe_attention(qc, kc, v, mode="none", scale=self.scale, causal=causal,
                                 start_pos_q=start_q, start_pos_k=start_k)
         norm = {}
+        x_dtype = q_r.dtype  # what the reference's forward_query / forward_key receive
         if fuse_norm:
             norm = dict(qr_norm_weight=self.qr_norm.weight, kr_norm_weight=self.kr_norm.weight,
                         norm_eps=self.qr_norm.eps)
+            # RMSNorm's output: bf16 only when the projection and the weight are both bf16
+            both_bf16 = q_r.dtype == torch.bfloat16 and self.qr_norm.weight.dtype == torch.bfloat16
+            x_dtype = torch.bfloat16 if both_bf16 else torch.float32
         return pe_attention(q_r, k_r, v, mode="pope", q_c=q_c, k_c=k_c, freqs=self.fpope.kernel_freqs(),
                             delta=self.fpope.kernel_delta(), scale=self.scale, causal=causal,
-                            start_pos_q=start_q, start_pos_k=start_k, **norm)
+                            start_pos_q=start_q, start_pos_k=start_k,
+                            position_dtype=kernel_position_dtype(self.fpope, x_dtype), **norm)
 
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0) -> torch.Tensor:
         """(B, S, hidden) -> (B, S, hidden); ``mask`` is ignored (causal always, as the reference)."""
@@ -150,9 +155,18 @@ def cache_compute_dtype(x: torch.Tensor) -> torch.dtype:
     return torch.float32
 
 
+def kernel_position_dtype(embedding, x_dtype):
+    """The dtype the embedding's phase product takes positions in for an input of x_dtype: FoPE
+    builds them with torch.arange(..., dtype=x.dtype) (src/model/fpope.py:285,322), PoPE in fp32
+    (src/model/pope.py:110-119).  None means exact positions."""
+    if getattr(embedding, "positions_in_input_dtype", False) and x_dtype in (torch.bfloat16, torch.float16):
+        return x_dtype
+    return None
+
+
 def cached_attention(cache: KVCache, capacity: int, start_pos: int, *, q, k, v, q_c=None, k_c=None, mode: str,
                      freqs=None, delta=None, scale: float, rope_mscale: float = 1.0, qk_norm: bool = False,
-                     d_v: int) -> torch.Tensor:
+                     d_v: int, position_dtype=None) -> torch.Tensor:
     """Append the new key / value rows at ``start_pos`` and attend the new queries to every cached
     row with the bottom-right causal mask (src/model/fpope_attention.py:294-324).  The first chunk
     (start_pos 0) runs the regular causal forward on the same operands; later chunks run the
@@ -170,14 +184,15 @@ def cached_attention(cache: KVCache, capacity: int, start_pos: int, *, q, k, v, 
     elif start_pos != cache.length:
         raise ValueError(f"the cache holds {cache.length} rows; the next chunk must start there, not at {start_pos}")
     pe_cache_append(k, v, cache.k, cache.v, start_pos=start_pos, mode=mode, k_c=k_c, freqs=freqs, delta=delta,
-                    rope_mscale=rope_mscale, qk_norm=qk_norm)
+                    rope_mscale=rope_mscale, qk_norm=qk_norm, position_dtype=position_dtype)
     cache.length = start_pos + S
     if start_pos == 0:
         return pe_attention(q, k, v, mode=mode, q_c=q_c, k_c=k_c, freqs=freqs, delta=delta, scale=scale, causal=True,
-                            rope_mscale=rope_mscale, qk_norm=qk_norm, compute_dtype=cdt)
+                            rope_mscale=rope_mscale, qk_norm=qk_norm, compute_dtype=cdt,
+                            position_dtype=position_dtype)
     return pe_attention_decode(q, cache.k, cache.v, cache.length, d_v=d_v, mode=mode, q_c=q_c, freqs=freqs,
                                scale=scale, causal="bottom_right", start_pos_q=start_pos, rope_mscale=rope_mscale,
-                               qk_norm=qk_norm)
+                               qk_norm=qk_norm, position_dtype=position_dtype)
 
 
 class FPoPEGroupedQueryAttentionWithCache(FPoPEGroupedQueryAttention):
@@ -227,6 +242,7 @@ class FPoPEGroupedQueryAttentionWithCache(FPoPEGroupedQueryAttention):
         else:
             out = cached_attention(self.cache, self.max_cache_len, start_pos, q=q_r, k=k_r, v=v, q_c=q_c, k_c=k_c,
                                    mode="pope", freqs=self.fpope.kernel_freqs(), delta=self.fpope.kernel_delta(),
-                                   scale=self.scale, d_v=self.head_dim)
+                                   scale=self.scale, d_v=self.head_dim,
+                                   position_dtype=kernel_position_dtype(self.fpope, q_r.dtype))
         out = out.transpose(1, 2).reshape(B, S, -1)
         return self.wo(out if torch.is_autocast_enabled() else out.to(x.dtype))

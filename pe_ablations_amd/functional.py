@@ -79,7 +79,25 @@ def _params(cfg, qr, kr, v, qc, delta) -> _lib.PeParams:
     p.scale = cfg["scale"]
     p.rope_mscale = cfg["mscale"]
     p.delta_head_stride = 0 if (delta is None or delta.dim() == 1) else delta.shape[-1]
+    p.position_rounding = cfg["pos_round"]
     return p
+
+
+def position_rounding(position_dtype, mode: int) -> int:
+    """PE_POS_* for a ``position_dtype``: None / torch.float32 keep positions exact; torch.bfloat16
+    / torch.float16 round them to that type before the phase product, as the reference FoPE's
+    torch.arange(..., dtype=x.dtype) does for a bf16 / fp16 x (src/model/fpope.py:285,322).
+    Rounding applies to PoPE / FoPE only."""
+    if position_dtype is None or position_dtype == torch.float32:
+        return _lib.PE_POS_EXACT
+    if mode != _lib.PE_MODE_POPE:
+        raise ValueError("position_dtype applies to PoPE / FoPE only")
+    if position_dtype == torch.bfloat16:
+        return _lib.PE_POS_BF16
+    if position_dtype == torch.float16:
+        return _lib.PE_POS_FP16
+    raise ValueError(f"position_dtype must be None, torch.float32, torch.bfloat16 or torch.float16, "
+                     f"got {position_dtype}")
 
 
 def _shape_error(msg: str) -> ValueError:
@@ -314,7 +332,7 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
                  start_pos_k: int = 0, rope_mscale: float = 1.0, qk_norm: bool = False,
                  return_lse: bool = False, compute_dtype: Optional[torch.dtype] = None,
                  qr_norm_weight: Optional[torch.Tensor] = None, kr_norm_weight: Optional[torch.Tensor] = None,
-                 norm_eps: float = 1e-6):
+                 norm_eps: float = 1e-6, position_dtype: Optional[torch.dtype] = None):
     """Fused PE attention on one GPU.
 
     q (B,Hq,Sq,Dr), k (B,Hkv,Sk,Dr): positional parts, transformed inside the kernel library;
@@ -327,6 +345,9 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
     qr_norm_weight / kr_norm_weight (PoPE only, forward only): q / k are the raw position
     projections and the library applies the modules' RMSNorm over each token's H*Dr features in
     the transform kernel (pe_attn_fwd_normed); raises when a gradient would be needed.
+    position_dtype (PoPE / FoPE): None or torch.float32 keeps positions exact; torch.bfloat16 /
+    torch.float16 rounds each position to that type before the phase product (and in the phase
+    gradient), reproducing FoPE's positions in x.dtype (src/model/fpope.py:285,322).
     Returns out (B,Hq,Sq,Dv) [and lse (B,Hq,Sq) fp32]."""
     if mode not in _MODES:
         raise ValueError(f"unknown PE mode {mode!r}")
@@ -358,7 +379,7 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
         dt = _dtype_code(compute_dtype)
     cfg = dict(mode=m, dtype=dt, causal=_CAUSAL[causal], start_pos_q=int(start_pos_q),
                start_pos_k=int(start_pos_k), qk_norm=bool(qk_norm), scale=float(scale),
-               mscale=float(rope_mscale))
+               mscale=float(rope_mscale), pos_round=position_rounding(position_dtype, m))
     cfg["key"] = tuple(cfg.values())
     if qr_norm_weight is not None or kr_norm_weight is not None:
         out, lse = _fwd_normed(q, k, v, q_c, k_c, freqs, delta, cfg, qr_norm_weight, kr_norm_weight, norm_eps)
@@ -440,7 +461,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
 # split-key decode attention over them.  Inference only.
 
 def _cache_params(*, B, Hq, Hkv, Sq, Sk, Dc, Dr, Dv, mode, dtype, causal, start_q, start_k, scale,
-                  mscale, qk_norm, delta) -> _lib.PeParams:
+                  mscale, qk_norm, delta, pos_round=0) -> _lib.PeParams:
     p = _lib.PeParams()
     p.B, p.Hq, p.Hkv, p.Sq, p.Sk = B, Hq, Hkv, Sq, Sk
     p.Dc, p.Dr, p.Dv = Dc, Dr, Dv
@@ -449,6 +470,7 @@ def _cache_params(*, B, Hq, Hkv, Sq, Sk, Dc, Dr, Dv, mode, dtype, causal, start_
     p.qk_l2norm = int(qk_norm)
     p.scale, p.rope_mscale = float(scale), float(mscale)
     p.delta_head_stride = 0 if (delta is None or delta.dim() == 1) else delta.shape[-1]
+    p.position_rounding = pos_round
     return p
 
 
@@ -477,7 +499,8 @@ def _check_cache(k_cache, v_cache, B, Hkv, wk, wv, cdt, dev):
 def pe_cache_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *,
                     start_pos: int, mode: str = "pope", k_c: Optional[torch.Tensor] = None,
                     freqs: Optional[torch.Tensor] = None, delta: Optional[torch.Tensor] = None,
-                    rope_mscale: float = 1.0, qk_norm: bool = False) -> None:
+                    rope_mscale: float = 1.0, qk_norm: bool = False,
+                    position_dtype: Optional[torch.dtype] = None) -> None:
     """Write the transformed key rows of k (B, Hkv, S, Dr) [with content k_c (B, Hkv, S, Dc)] and
     the value rows v (B, Hkv, S, Dv) to cache rows start_pos .. start_pos + S - 1, phases at those
     positions (the reference's k_cache[:, :, start_pos:start_pos+S] = [k_c | PoPE(k_r)],
@@ -498,7 +521,8 @@ def pe_cache_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_c
     dt = _dtype_code(cdt)
     p = _cache_params(B=B, Hq=Hkv, Hkv=Hkv, Sq=S, Sk=S, Dc=Dc, Dr=Dr, Dv=v.shape[-1], mode=m, dtype=dt,
                       causal=_lib.PE_CAUSAL_NONE, start_q=start_pos, start_k=start_pos, scale=1.0,
-                      mscale=rope_mscale, qk_norm=qk_norm, delta=delta)
+                      mscale=rope_mscale, qk_norm=qk_norm, delta=delta,
+                      pos_round=position_rounding(position_dtype, m))
     L = _lib.lib()
     _lib.check(L.pe_attn_check(ref(p)))
     _check_cache(k_cache, v_cache, B, Hkv, L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p)), cdt,
@@ -516,10 +540,12 @@ def pe_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
                         d_v: int, mode: str = "pope", q_c: Optional[torch.Tensor] = None,
                         freqs: Optional[torch.Tensor] = None, scale: Optional[float] = None,
                         causal="bottom_right", start_pos_q: Optional[int] = None, rope_mscale: float = 1.0,
-                        qk_norm: bool = False, return_lse: bool = False):
+                        qk_norm: bool = False, return_lse: bool = False,
+                        position_dtype: Optional[torch.dtype] = None):
     """Attention of the new queries q (B, Hq, Sq, Dr) [content q_c] against the first ``cache_len``
     rows of caches filled by pe_cache_append (src/model/fpope_attention.py:301-324): bottom-right
     causal mask by default, query phases at start_pos_q (default cache_len - Sq), GQA by index.
+    position_dtype as for pe_attention (the cached keys must have been appended with the same).
     Returns out (B, Hq, Sq, d_v) in the cache dtype [and lse (B, Hq, Sq)]."""
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, q_c, freqs)):
         raise RuntimeError("the KV-cache path is inference only (run it under torch.no_grad())")
@@ -545,7 +571,8 @@ def pe_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     start_q = cache_len - Sq if start_pos_q is None else start_pos_q
     p = _cache_params(B=B, Hq=Hq, Hkv=Hkv, Sq=Sq, Sk=cache_len, Dc=Dc, Dr=Dr, Dv=d_v, mode=m,
                       dtype=_dtype_code(cdt), causal=_CAUSAL[causal], start_q=start_q, start_k=0, scale=scale,
-                      mscale=rope_mscale, qk_norm=qk_norm, delta=None)
+                      mscale=rope_mscale, qk_norm=qk_norm, delta=None,
+                      pos_round=position_rounding(position_dtype, m))
     L = _lib.lib()
     _lib.check(L.pe_attn_check(ref(p)))
     _check_cache(k_cache, v_cache, B, Hkv, L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p)), cdt,

@@ -16,9 +16,10 @@ from typing import Optional
 import torch
 
 from . import _lib
+from .functional import position_rounding
 
 
-def _params(B, H, S, D, mode, dtype, start_pos, delta, mscale) -> _lib.PeParams:
+def _params(B, H, S, D, mode, dtype, start_pos, delta, mscale, pos_round) -> _lib.PeParams:
     p = _lib.PeParams()
     p.B, p.Hq, p.Hkv, p.Sq, p.Sk = B, H, H, S, S
     p.Dc, p.Dr, p.Dv = 0, D, 64
@@ -27,6 +28,7 @@ def _params(B, H, S, D, mode, dtype, start_pos, delta, mscale) -> _lib.PeParams:
     p.qk_l2norm = 0
     p.scale, p.rope_mscale = 1.0, float(mscale)
     p.delta_head_stride = 0 if (delta is None or delta.dim() == 1) else D
+    p.position_rounding = pos_round
     return p
 
 
@@ -45,7 +47,7 @@ def _view(t: Optional[torch.Tensor]) -> _lib.PeTensor:
 
 class PETransformFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, freqs, delta, mode, start_pos, is_key, mscale):
+    def forward(ctx, x, freqs, delta, mode, start_pos, is_key, mscale, pos_round):
         L = _lib.lib()
         if x.dtype not in (torch.float32, torch.bfloat16):
             x = x.float()
@@ -54,7 +56,7 @@ class PETransformFn(torch.autograd.Function):
             xv = xv.contiguous()
         B, H, S, D = xv.shape
         cdt = _lib.PE_DTYPE_FP32 if x.dtype == torch.float32 else _lib.PE_DTYPE_BF16
-        p = _params(B, H, S, D, mode, cdt, start_pos, delta if is_key else None, mscale)
+        p = _params(B, H, S, D, mode, cdt, start_pos, delta if is_key else None, mscale, pos_round)
         _lib.check(L.pe_attn_check(ctypes.byref(p)))
         width = L.pe_attn_operand_width(ctypes.byref(p))
         out_w = 2 * D if mode == _lib.PE_MODE_POPE else D
@@ -67,21 +69,21 @@ class PETransformFn(torch.autograd.Function):
                                      dst.data_ptr(), torch.cuda.current_stream(x.device).cuda_stream)
         _lib.check(rc)
         ctx.save_for_backward(xv, freqs, delta)
-        ctx.cfg = (mode, start_pos, is_key, mscale, cdt, width, x.dtype)
+        ctx.cfg = (mode, start_pos, is_key, mscale, cdt, width, x.dtype, pos_round)
         return dst[..., :out_w].transpose(1, 2)
 
     @staticmethod
     def backward(ctx, grad):
         L = _lib.lib()
         xv, freqs, delta = ctx.saved_tensors
-        mode, start_pos, is_key, mscale, cdt, width, xdtype = ctx.cfg
+        mode, start_pos, is_key, mscale, cdt, width, xdtype, pos_round = ctx.cfg
         B, H, S, D = xv.shape
         out_w = 2 * D if mode == _lib.PE_MODE_POPE else D
         g = torch.zeros((B, H, S, width), dtype=torch.float32, device=xv.device)
         g[..., :out_w] = grad.transpose(1, 2)
         dx = torch.empty((B, S, H, D), dtype=xv.dtype, device=xv.device)
         dxv = dx.transpose(1, 2)
-        p = _params(B, H, S, D, mode, cdt, start_pos, delta if is_key else None, mscale)
+        p = _params(B, H, S, D, mode, cdt, start_pos, delta if is_key else None, mscale, pos_round)
         need_f = freqs is not None and ctx.needs_input_grad[1] and mode == _lib.PE_MODE_POPE
         need_d = delta is not None and is_key and ctx.needs_input_grad[2]
         dfreqs = torch.empty(freqs.shape, dtype=torch.float32, device=xv.device) if need_f else None
@@ -97,7 +99,7 @@ class PETransformFn(torch.autograd.Function):
                                          None if ddelta is None else ddelta.data_ptr(),
                                          ws.data_ptr(), ws_bytes, torch.cuda.current_stream(xv.device).cuda_stream)
         _lib.check(rc)
-        return dx.to(xdtype), dfreqs, ddelta, None, None, None, None
+        return dx.to(xdtype), dfreqs, ddelta, None, None, None, None, None
 
 
 def check_transform_operands(x, freqs, delta, *, mode: str, is_key: bool) -> None:
@@ -124,10 +126,13 @@ def check_transform_operands(x, freqs, delta, *, mode: str, is_key: bool) -> Non
 
 
 def pe_transform(x: torch.Tensor, freqs: torch.Tensor, delta: Optional[torch.Tensor], *, start_pos: int = 0,
-                 is_key: bool = False, mode: str = "pope", mscale: float = 1.0) -> torch.Tensor:
+                 is_key: bool = False, mode: str = "pope", mscale: float = 1.0,
+                 position_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """x (B, S, H, D) -> PoPE [mu cos, mu sin] (B, S, H, 2D) or RoPE-rotated (B, S, H, D) on the GPU.
 
-    fp32 inputs are transformed in fp32; bf16 / fp16 inputs produce bf16."""
+    fp32 inputs are transformed in fp32; bf16 / fp16 inputs produce bf16.  position_dtype (PoPE):
+    None / torch.float32 exact positions, torch.bfloat16 / torch.float16 positions rounded to that
+    type (FoPE's torch.arange(..., dtype=x.dtype), src/model/fpope.py:285,322)."""
     if not x.is_cuda:
         raise RuntimeError("the positional transform runs on the GPU only (got a CPU tensor); "
                            "the HIP library has no CPU path")
@@ -140,4 +145,5 @@ def pe_transform(x: torch.Tensor, freqs: torch.Tensor, delta: Optional[torch.Ten
         delta = delta.float().contiguous()
     if x.dtype == torch.float16:
         x = x.to(torch.bfloat16)
-    return PETransformFn.apply(x, freqs, delta, m, int(start_pos), bool(is_key), float(mscale))
+    pr = position_rounding(position_dtype, m)
+    return PETransformFn.apply(x, freqs, delta, m, int(start_pos), bool(is_key), float(mscale), pr)

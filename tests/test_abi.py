@@ -50,13 +50,16 @@ def test_enums_match_header():
     assert val("PE_DTYPE_BF16") == _lib.PE_DTYPE_BF16
     assert val("PE_DTYPE_FP32") == _lib.PE_DTYPE_FP32
     assert val("PE_CAUSAL_BOTTOM_RIGHT") == _lib.PE_CAUSAL_BOTTOM_RIGHT
+    assert (val("PE_POS_EXACT"), val("PE_POS_BF16"), val("PE_POS_FP16")) == \
+        (_lib.PE_POS_EXACT, _lib.PE_POS_BF16, _lib.PE_POS_FP16)
     assert val("PE_STAGE_COUNT") == len(_lib.STAGES)
 
 
 def test_params_struct_layout():
-    # int32 x 14, float x 2, int64: 72 bytes, int64 at offset 64
-    assert ctypes.sizeof(_lib.PeParams) == 72
+    # int32 x 14, float x 2, int64, int32 x 2: 80 bytes, int64 at offset 64
+    assert ctypes.sizeof(_lib.PeParams) == 80
     assert _lib.PeParams.delta_head_stride.offset == 64
+    assert _lib.PeParams.position_rounding.offset == 72
     assert ctypes.sizeof(_lib.PeTensor) == 48
 
 
@@ -98,6 +101,8 @@ def test_valid_configs(lib):
     (dict(mode=7), "PE_ERR_MODE"),
     (dict(dtype=3), "PE_ERR_MODE"),
     (dict(causal=5), "PE_ERR_MODE"),
+    (dict(position_rounding=3), "PE_ERR_MODE"),
+    (dict(mode=_lib.PE_MODE_ROPE, position_rounding=1), "PE_ERR_MODE"),   # rounding is PoPE / FoPE only
     (dict(mode=_lib.PE_MODE_ROPE, Dr=63), "PE_ERR_MODE"),        # RoPE pairs need an even width
 ])
 def test_invalid_configs(lib, kw, code):
@@ -138,7 +143,7 @@ def test_strerror_and_version(lib):
         assert msg
         if code:
             assert msg.startswith("pe_attn:")
-    assert lib.pe_attn_version() == 1
+    assert lib.pe_attn_version() == 2
     with pytest.raises(_lib.PEAttnError) as ei:
         _lib.check(_lib.ERRORS["PE_ERR_WORKSPACE"])
     assert ei.value.code == _lib.ERRORS["PE_ERR_WORKSPACE"]

@@ -31,11 +31,11 @@ def md(a, b):
     return err(a, b)
 
 
-def oracle_operands(mode, qc, kc, qr, kr, freqs, delta, start_q, start_k, mscale, qk_norm):
+def oracle_operands(mode, qc, kc, qr, kr, freqs, delta, start_q, start_k, mscale, qk_norm, pos_dtype=None):
     """[content | transform] operands in fp32 the way the reference builds them."""
     if mode == "pope":
-        tq = O.pope_transform(qr, freqs, start_q)
-        tk = O.pope_transform(kr, freqs, start_k, delta)
+        tq = O.pope_transform(qr, freqs, start_q, pos_dtype=pos_dtype)
+        tk = O.pope_transform(kr, freqs, start_k, delta, pos_dtype=pos_dtype)
     elif mode == "rope":
         tq = O.rope_rotate(qr, freqs, start_q) * mscale
         tk = O.rope_rotate(kr, freqs, start_k) * mscale
@@ -52,7 +52,7 @@ def oracle_operands(mode, qc, kc, qr, kr, freqs, delta, start_q, start_k, mscale
 def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=64, Dc=0,
              dtype=torch.bfloat16, causal=True, freqs=None, delta=None, scale=None, mscale=1.0,
              qk_norm=False, start_q=0, start_k=0, seed=0, grad_freqs=False, grad_delta=True,
-             net_names=()):
+             net_names=(), pos_dtype=None):
     """One case through pe_attention against the oracle.  Every listed error is the raw max-abs;
     ``net_names`` lists results whose magnitude puts the raw bf16 bar out of reach of any bf16
     number (the test names the magnitude): those are asserted net of their own rounding and their
@@ -74,7 +74,8 @@ def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=
     o_in = [None if t is None else t.float().clone().requires_grad_(True) for t in ins]
     of = None if freqs is None else freqs.clone().requires_grad_(grad_freqs)
     od = None if delta is None else delta.clone().requires_grad_(grad_delta)
-    tq, tk = oracle_operands(mode, o_in[3], o_in[4], o_in[0], o_in[1], of, od, start_q, start_k, mscale, qk_norm)
+    tq, tk = oracle_operands(mode, o_in[3], o_in[4], o_in[0], o_in[1], of, od, start_q, start_k, mscale, qk_norm,
+                             pos_dtype)
     rd = torch.bfloat16 if dtype == torch.bfloat16 else None
     tq, tk, vv = O.round_ste(tq, rd), O.round_ste(tk, rd), O.round_ste(o_in[2].float(), rd)
     ref, ref_lse = O.attention(tq, tk, vv, scale, causal=bool(causal))
@@ -85,7 +86,7 @@ def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=
     gd = None if delta is None else delta.to(cuda).requires_grad_(grad_delta)
     out, lse = pe_attention(g_in[0], g_in[1], g_in[2], mode=mode, q_c=g_in[3], k_c=g_in[4], freqs=gf, delta=gd,
                             scale=scale, causal=causal_flag, start_pos_q=start_q, start_pos_k=start_k,
-                            rope_mscale=mscale, qk_norm=qk_norm, return_lse=True)
+                            rope_mscale=mscale, qk_norm=qk_norm, return_lse=True, position_dtype=pos_dtype)
     out.backward(dout.to(cuda))
     torch.cuda.synchronize()
     errs = {"out": md(out, ref), "lse": md(lse, ref_lse)}
@@ -105,6 +106,13 @@ def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=
         if a is not None and a.requires_grad:
             rel = md(a.grad, b.grad) / max(1.0, b.grad.abs().max().item())
             assert rel < (2e-2 if dtype == torch.bfloat16 else 1e-4), (name, rel, errs)
+    if pos_dtype is not None:
+        # not vacuous: with exact positions the oracle's output is far from the kernel's
+        eq, ek = oracle_operands(mode, *(None if t is None else t.detach() for t in (o_in[3], o_in[4], o_in[0], o_in[1])),
+                                 freqs, None if delta is None else delta, start_q, start_k, mscale, qk_norm)
+        exact, _ = O.attention(O.round_ste(eq, rd), O.round_ste(ek, rd), vv.detach(), scale, causal=bool(causal))
+        errs["vs_exact_positions"] = md(out, exact)
+        assert errs["vs_exact_positions"] > 5 * tol, errs
     return errs
 
 
@@ -194,3 +202,36 @@ def test_yarn_mscale(cuda):
 
 def test_nope_qknorm(cuda):
     run_case(cuda, mode="none", Dr=64, Dv=64, Hq=4, Hkv=4, Sq=96, qk_norm=True, scale=1 / 8, seed=120)
+
+
+# ------------------------------------------------------------- FoPE positions in the input dtype
+
+def test_fope_positions_bf16_fused(cuda):
+    """FoPE without QK norm under bf16 autocast builds its positions with
+    torch.arange(..., dtype=bf16) (src/model/fpope.py:285,322): above 256 they are rounded (to
+    multiples of 4 in 512..1023).  The fused bf16 path (prologue, dK/dV and dQ epilogues, query
+    phase table, frequency gradient) with position_dtype=bf16 against the oracle built the same
+    way, positions 300..1019."""
+    D = 64
+    omega = O.fope_effective_freqs(O.pope_freqs(D), rnd(D, 4, seed=40, scale=0.4)).detach()
+    delta = -torch.rand(2, D, generator=torch.Generator().manual_seed(41)) * 2 * math.pi
+    run_case(cuda, Dr=D, Dv=D, Sq=720, freqs=omega, delta=delta, grad_freqs=True, start_q=300, start_k=300,
+             pos_dtype=torch.bfloat16, seed=42)
+
+
+def test_fope_positions_bf16_split_form_gqa(cuda):
+    """The same rounding through the split form (content 64 | PoPE 2 x 32, GQA 4 -> 2), whose
+    backward takes the stand-alone inverse-transform kernels."""
+    D = 32
+    omega = O.fope_effective_freqs(O.pope_freqs(D), rnd(D, 4, seed=43, scale=0.4)).detach()
+    run_case(cuda, Dr=D, Dv=64, Dc=64, Hq=4, Hkv=2, Sq=600, freqs=omega, delta=-torch.rand(D) * 6,
+             grad_freqs=True, start_q=400, start_k=400, pos_dtype=torch.bfloat16, seed=44)
+
+
+def test_positions_fp16_fp32_mode(cuda):
+    """fp16 rounding (fp16 autocast; spacing 4 between 4096 and 8191) checked at the fp32 bar, so
+    every phase must match the oracle's to fp32 accuracy."""
+    D = 32
+    omega = O.fope_effective_freqs(O.pope_freqs(D), rnd(D, 4, seed=45, scale=0.4)).detach()
+    run_case(cuda, Dr=D, Dv=64, Sq=160, dtype=torch.float32, freqs=omega, delta=-torch.rand(D) * 6,
+             grad_freqs=True, start_q=5000, start_k=5000, pos_dtype=torch.float16, seed=46)

@@ -234,3 +234,92 @@ def test_transform_phase_range(cuda, start_pos):
     rr = O.rope_rotate(x.transpose(1, 2), inv, start_pos).transpose(1, 2)
     rg = pe_transform(x.to(cuda), inv.to(cuda), None, start_pos=start_pos, mode="rope")
     assert md(rg, rr) < 1e-5
+
+
+# ------------------------------------------------------------- FoPE positions in the input dtype
+
+def _fope(dim, max_len, seed):
+    torch.manual_seed(seed)
+    return FoPEPoPEEmbedding(dim, max_len, num_fourier_terms=4, fourier_sigma=0.4, delta_init="uniform")
+
+
+def _omega(pe):
+    return O.fope_effective_freqs(pe.base_freqs, pe.fourier_coeffs, pe.fourier_indices,
+                                  training_length=pe.training_length, normalize=pe.normalize_coeffs,
+                                  use_ceiling=pe.use_ceiling)
+
+
+def test_fope_embedding_bf16_input_rounds_positions(cuda):
+    """forward_query / forward_key on a bf16 x take positions in bf16, as the reference's
+    torch.arange(..., dtype=x.dtype) (src/model/fpope.py:285,322): against the oracle transform
+    with bf16 positions (forward and input gradient at the bf16 bar, coefficient gradient relative),
+    and far from the exact-position transform.  PoPEEmbedding keeps exact positions."""
+    pe = _fope(48, 1024, seed=50)
+    x = torch.randn(2, 200, 3, 48).to(torch.bfloat16)
+    for is_key in (False, True):
+        pg = clone_to(pe, cuda)
+        xo = x.float().requires_grad_(True)
+        delta = O.clamp_delta(pe.phase_bias) if is_key else None
+        ref = O.pope_transform(xo.transpose(1, 2), _omega(pe), 400, delta, pos_dtype=torch.bfloat16).transpose(1, 2)
+        gout = torch.randn_like(ref)
+        ref.backward(gout)
+        xg = x.to(cuda).requires_grad_(True)
+        out = pg.forward_key(xg, 400) if is_key else pg.forward_query(xg, 400)
+        out.backward(gout.to(cuda).to(out.dtype))
+        torch.cuda.synchronize()
+        assert md(out, ref) < 2e-2
+        assert md(xg.grad, xo.grad) / max(1.0, xo.grad.abs().max().item()) < 1e-2
+        assert md(pg.fourier_coeffs.grad, pe.fourier_coeffs.grad) / max(1.0, pe.fourier_coeffs.grad.abs().max().item()) < 2e-2
+        exact = O.pope_transform(x.float().transpose(1, 2), _omega(pe).detach(), 400,
+                                 None if delta is None else delta.detach()).transpose(1, 2)
+        assert md(out, exact) > 0.5
+        pe.zero_grad()
+    pp = PoPEEmbedding(48, 1024, delta_init="uniform").to(cuda)
+    out = pp.forward_query(x.to(cuda), 400)
+    assert md(out, O.pope_transform(x.float().transpose(1, 2), pp.effective_freqs.cpu(), 400).transpose(1, 2)) < 2e-2
+
+
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_fpope_module_autocast_position_dtype(cuda, qk_norm):
+    """The FoPE module under bf16 autocast: without QK norm the position projections are bf16, so
+    the reference's positions are bf16 (rounded past 256); with the norm its fp32 weight makes them
+    fp32 and the positions stay exact.  The module's attention (before wo) against the oracle built
+    each way, on the projections the module itself computed."""
+    pe = _fope(32, 1024, seed=51)
+    m = FPoPEGroupedQueryAttention(256, 8, 4, 64, 32, use_qk_norm=qk_norm, fpope=pe).to(cuda)
+    # without the norm, larger inputs sharpen attention so that the positions visibly matter
+    x = torch.randn(1, 640, 256, device=cuda) * (1 if qk_norm else 3)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        q_c, k_c, q_r, k_r, v = m._project(x)
+        out = m._attend(q_c, k_c, q_r, k_r, v, 0, 0, True)
+    assert q_r.dtype == (torch.float32 if qk_norm else torch.bfloat16)
+    pos_dt = None if qk_norm else torch.bfloat16
+    import copy
+    pc = copy.deepcopy(m.fpope).cpu()
+    omega, delta = _omega(pc).detach(), O.clamp_delta(pc.phase_bias).detach()
+    c = [t.float().cpu() for t in (q_c, k_c, q_r, k_r, v)]
+
+    def oracle(pd):
+        tq = torch.cat([c[0], O.pope_transform(c[2], omega, 0, pos_dtype=pd)], -1).to(torch.bfloat16).float()
+        tk = torch.cat([c[1], O.pope_transform(c[3], omega, 0, delta, pos_dtype=pd)], -1).to(torch.bfloat16).float()
+        return O.attention(tq, tk, c[4].to(torch.bfloat16).float(), m.scale, causal=True)[0]
+
+    e = md(out, oracle(pos_dt))
+    assert e < 2e-2
+    if not qk_norm:   # the kernel is far closer to the rounded positions than to exact ones
+        assert md(out, oracle(None)) > max(4 * e, 0.02), (e, md(out, oracle(None)))
+
+
+def test_fope_cache_decode_bf16_positions(cuda):
+    """KV-cache decode with the FoPE module under bf16 autocast and no QK norm: keys appended and
+    queries decoded at bf16-rounded positions agree with the full forward's last rows."""
+    pe = _fope(32, 1024, seed=52)
+    m = FPoPEGroupedQueryAttentionWithCache(256, 4, 2, 64, 32, use_qk_norm=False, fpope=pe,
+                                            max_cache_len=640).to(cuda)
+    x = torch.randn(1, 603, 256, device=cuda)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        full = m(x)
+        outs = [m(x[:, :600], use_cache=True)]
+        for t in range(600, 603):
+            outs.append(m(x[:, t:t + 1], start_pos=t, use_cache=True))
+    assert md(torch.cat(outs, 1), full) < 2e-2

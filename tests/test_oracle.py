@@ -322,3 +322,41 @@ def test_chunked_oracle_matches_closed_form():
     # bottom-right alignment for Sq < Sk equals the tail rows of the full causal problem
     sub = O.pope_attention_chunked(q[30:], k, v, fr, de, scale=0.3, chunk=7, core_dtype=f64, start_q=30)
     assert (sub["out"] - ch["out"][30:]).abs().max().item() < 1e-5
+
+
+def _round_to_bits(p: int, bits: int, max_finite: float) -> float:
+    """p rounded to `bits` significant bits, ties to even, by integer arithmetic alone (inf past
+    the type's largest finite value, rounding first): the value a bf16 (bits 8) or fp16 (bits 11)
+    holds for the integer p."""
+    if p == 0:
+        return 0.0
+    e = p.bit_length() - 1
+    shift = e - (bits - 1)
+    if shift <= 0:
+        r = p
+    else:
+        q, rem = divmod(p, 1 << shift)
+        half = 1 << (shift - 1)
+        if rem > half or (rem == half and q % 2 == 1):
+            q += 1
+        r = q << shift
+    return float("inf") if r > max_finite else float(r)
+
+
+@pytest.mark.parametrize("dtype, bits, top", [(torch.bfloat16, 8, 3.3895313892515355e38), (torch.float16, 11, 65504.0)])
+def test_positions_in_input_dtype(dtype, bits, top):
+    """The oracle's FoPE positions (torch.arange(..., dtype=x.dtype), src/model/fpope.py:285,322)
+    against round-to-nearest-even computed on integers: exact below 2^bits, then multiples of 2,
+    4, ... with ties to the even multiple (257 -> 256, 259 -> 260 in bf16); fp16 overflows to inf
+    from 65520 on."""
+    for start, n in ((0, 600), (250, 20), (16370, 40), (65500, 40), (1 << 20, 50)):
+        got = O.positions(n, start, dtype)
+        want = torch.tensor([_round_to_bits(p, bits, top) for p in range(start, start + n)])
+        assert torch.equal(got, want), (dtype, start)
+    assert O.positions(3, 256, torch.bfloat16).tolist() == [256.0, 256.0, 258.0]
+    assert O.positions(2, 259, torch.bfloat16).tolist() == [260.0, 260.0]
+    assert torch.equal(O.positions(10, 7, None), torch.arange(7, 17, dtype=torch.float32))
+    # the phases use the rounded positions, the frequency gradient too (pope_attention_chunked)
+    f = O.pope_freqs(8)
+    assert torch.equal(O.pope_phases(20, f, 300, pos_dtype=torch.bfloat16),
+                       torch.outer(O.positions(20, 300, torch.bfloat16), f))

@@ -25,7 +25,7 @@ def _case(cuda, B, H, S, D, seed, dtype=torch.bfloat16):
     delta = (torch.rand(H, D, generator=g) * (-2 * math.pi)).to(cuda)
     cfg = dict(mode=_lib.PE_MODE_POPE, dtype=_lib.PE_DTYPE_BF16 if dtype == torch.bfloat16 else _lib.PE_DTYPE_FP32,
                causal=_lib.PE_CAUSAL_TOP_LEFT, start_pos_q=0, start_pos_k=0, qk_norm=False,
-               scale=1.0 / math.sqrt(D), mscale=1.0)
+               scale=1.0 / math.sqrt(D), mscale=1.0, pos_round=_lib.PE_POS_EXACT)
     return q, k, v, freqs, delta, cfg
 
 
