@@ -53,6 +53,26 @@ bool fused_bwd(const pe_attn_params* p) {
          pad_qk(qk_width(p)) == 2 * p->Dr;
 }
 
+// a view the vectorised epilogues can read or write 8 elements at a time: unit dim stride and
+// every row 16-byte aligned
+bool vec16(const pe_tensor_t* t) {
+  if (!t || !t->data) return false;
+  const int64_t e = t->dtype == PE_DTYPE_BF16 ? 2 : 4;
+  return t->stride[3] == 1 && (uintptr_t)t->data % 16 == 0 && (t->stride[0] * e) % 16 == 0 &&
+         (t->stride[1] * e) % 16 == 0 && (t->stride[2] * e) % 16 == 0;
+}
+
+// the reference module's split form [content 64 | PoPE 2 x 32] (QK width 128, value width 64 or
+// 128) in bf16: the gradient kernels' epilogues also apply its inverse transform and copy the
+// content gradient, when every view they touch takes 16-byte vector access
+bool fused_split_bwd(const pe_attn_params* p, const pe_tensor_t* qr, const pe_tensor_t* kr,
+                     const pe_tensor_t* dqc, const pe_tensor_t* dqr, const pe_tensor_t* dkc,
+                     const pe_tensor_t* dkr) {
+  return p->dtype == PE_DTYPE_BF16 && p->mode == PE_MODE_POPE && p->Dc == 64 && p->Dr == 32 &&
+         (p->Dv == 64 || p->Dv == 128) && vec16(qr) && vec16(kr) && vec16(dqc) && vec16(dqr) && vec16(dkc) &&
+         vec16(dkr);
+}
+
 Layout layout(const pe_attn_params* p) {
   Layout L{};
   L.dqk = pad_qk(qk_width(p));
@@ -638,11 +658,13 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   stage_mark(PE_STAGE_BWD_DKDV, 0, s);
   // fused form in bf16 with both halves of a column in one wave: the gradient kernels apply the
   // inverse PoPE transform in their epilogues
-  const bool fuse = fused_bwd(p);
+  const bool split = fused_split_bwd(p, qr, kr, dqc, dqr, dkc, dkr);
+  const bool fuse = fused_bwd(p) || split;
   const int nqg = (p->Sq + 255) / 256, nkg = (p->Sk + 127) / 128;
   if (fuse) {
     c.fuse_inv = 1;
     c.Dr = p->Dr;
+    c.Dc = p->Dc;
     c.freqs = freqs;
     c.delta = delta;
     c.delta_hs = p->delta_head_stride;
@@ -655,6 +677,14 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     };
     view(c.eq, qr, dqr, p->start_pos_q);
     view(c.ek, kr, dkr, p->start_pos_k);
+    if (split) {
+      auto cview = [](pe::EpiPoPE& e, const pe_tensor_t* dxc) {
+        e.dxc = (void*)dxc->data; e.dxc_dtype = dxc->dtype;
+        for (int i = 0; i < 4; ++i) e.dxc_s[i] = dxc->stride[i];
+      };
+      cview(c.eq, dqc);
+      cview(c.ek, dkc);
+    }
     c.eq.part_freq = dfreqs ? (float*)(bws + L.pq_off) : nullptr;
     c.ek.part_freq = dfreqs ? (float*)(bws + L.pk_off) : nullptr;
     c.ek.part_delta = ddelta ? (float*)(bws + L.pkd_off) : nullptr;

@@ -629,28 +629,32 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     }
 }
 
-// Vectorised form of the fused inverse PoPE epilogue.  It needs x and dx with a unit dim stride
-// and every row 16-byte aligned (true of the projections' (B, S, H, D) views).
-__device__ __forceinline__ bool epi_vec_ok(const EpiPoPE& e) {
-  const int64_t xe = e.x_dtype == 0 ? 2 : 4, de = e.dx_dtype == 0 ? 2 : 4;
-  return e.x_s[3] == 1 && e.dx_s[3] == 1 && (uintptr_t)e.x % 16 == 0 && (uintptr_t)e.dx % 16 == 0 &&
+// Vectorised form of the fused inverse PoPE epilogue.  It needs x and dx (and, with a content part,
+// dxc) with a unit dim stride and every row 16-byte aligned (true of the projections'
+// (B, S, H, D) views).
+__device__ __forceinline__ bool epi_vec_ok(const EpiPoPE& e, int dc) {
+  const int64_t xe = e.x_dtype == 0 ? 2 : 4, de = e.dx_dtype == 0 ? 2 : 4, ce = e.dxc_dtype == 0 ? 2 : 4;
+  const bool c_ok = dc == 0 || (e.dxc_s[3] == 1 && (uintptr_t)e.dxc % 16 == 0 && (e.dxc_s[0] * ce) % 16 == 0 &&
+                                (e.dxc_s[1] * ce) % 16 == 0 && (e.dxc_s[2] * ce) % 16 == 0);
+  return c_ok && e.x_s[3] == 1 && e.dx_s[3] == 1 && (uintptr_t)e.x % 16 == 0 && (uintptr_t)e.dx % 16 == 0 &&
          (e.x_s[0] * xe) % 16 == 0 && (e.x_s[1] * xe) % 16 == 0 && (e.x_s[2] * xe) % 16 == 0 &&
          (e.dx_s[0] * de) % 16 == 0 && (e.dx_s[1] * de) % 16 == 0 && (e.dx_s[2] * de) % 16 == 0;
 }
-// Inverse transform of NR staged rows (st: fp32 [NR][DQK], cos half then sin half of each row's
-// gradient).  Thread (cg, rr) of the NT threads takes dims 8cg .. 8cg+7 of rows rr + RPP*i, with
-// RPP = NT / (DQK/16): it loads all its x rows first (16 or 32 bytes each), so their latency is
-// paid once, then reads the two gradient halves as 16-byte LDS vectors and stores 8 dx at a time.
-// Row r is sequence index base + r (valid below nidx).  With key set, dl (8 values) is the key
-// phase bias; sdl / sf accumulate sum(dphi) and sum(pos * dphi) per dim over the thread's rows.
-// With TAB (query side) the sin / cos of each row's phases come from launch_phase_table's
-// [S][2][Dr] table, indexed by the row's sequence index, instead of being evaluated.
-template <int DQK, int NT, int NR, bool TAB>
+// Inverse transform of NR staged rows (st: fp32 [NR][DQK]; each row's gradient is the content part
+// [0, DC), then the cos half [DC, DC + DR) and the sin half [DC + DR, DQK), DR = (DQK - DC) / 2).
+// Thread (cg, rr) of the NT threads takes dims 8cg .. 8cg+7 of rows rr + RPP*i, with
+// RPP = NT / (DR/8): it loads all its x rows first (16 or 32 bytes each), so their latency is paid
+// once, then reads the two gradient halves as 16-byte LDS vectors and stores 8 dx at a time.  Row r
+// is sequence index base + r (valid below nidx).  With key set, dl (8 values) is the key phase
+// bias; sdl / sf accumulate sum(dphi) and sum(pos * dphi) per dim over the thread's rows.  With TAB
+// (query side) the sin / cos of each row's phases come from launch_phase_table's [S][2][DR] table,
+// indexed by the row's sequence index, instead of being evaluated.
+template <int DQK, int DC, int NT, int NR, bool TAB>
 __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st, int tid, int64_t xb,
                                               int64_t dxb, int base, int nidx, const float (&fr)[8],
                                               const float (&dl)[8], bool key, const float* tab,
                                               float (&sdl)[8], float (&sf)[8]) {
-  constexpr int Dr = DQK / 2, CG = Dr / 8, RPP = NT / CG, NI = NR / RPP;
+  constexpr int Dr = (DQK - DC) / 2, CG = Dr / 8, RPP = NT / CG, NI = NR / RPP;
   static_assert(NT % CG == 0 && NR % RPP == 0, "whole rows per thread");
   const int c0 = (tid % CG) * 8, rr = tid / CG;
   float xv[NI][8];
@@ -668,12 +672,13 @@ __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st,
   for (int i = 0; i < NI; ++i) {
     const int r = rr + RPP * i, idx = base + r;
     if (idx < nidx) {
-      const f32x4 c_lo = *(const f32x4*)(st + r * DQK + c0), c_hi = *(const f32x4*)(st + r * DQK + c0 + 4);
-      const f32x4 s_lo = *(const f32x4*)(st + r * DQK + Dr + c0), s_hi = *(const f32x4*)(st + r * DQK + Dr + c0 + 4);
+      const float* gr = st + r * DQK + DC;
+      const f32x4 c_lo = *(const f32x4*)(gr + c0), c_hi = *(const f32x4*)(gr + c0 + 4);
+      const f32x4 s_lo = *(const f32x4*)(gr + Dr + c0), s_hi = *(const f32x4*)(gr + Dr + c0 + 4);
       const float pos = pe_pos(e.start_pos + idx, e.pos_round);
       float dx[8];
       if constexpr (TAB) {
-        const float* tr = tab + (int64_t)idx * DQK + c0;
+        const float* tr = tab + (int64_t)idx * (2 * Dr) + c0;
         const f32x4 tc0 = *(const f32x4*)tr, tc1 = *(const f32x4*)(tr + 4);
         const f32x4 ts0 = *(const f32x4*)(tr + Dr), ts1 = *(const f32x4*)(tr + Dr + 4);
 #pragma unroll
@@ -694,6 +699,24 @@ __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st,
         }
       }
       store8(e.dx, dxb + (int64_t)idx * e.dx_s[2] + c0, e.dx_dtype, dx);
+    }
+  }
+}
+// The content part [0, DC) of NR staged rows, copied to dxc 8 dims at a time (no transform: the
+// content dims enter the scores unchanged, so their gradient is the staged one).
+template <int DQK, int DC, int NT, int NR>
+__device__ __forceinline__ void content_rows(const EpiPoPE& e, const float* st, int tid, int64_t dxcb, int base,
+                                             int nidx) {
+  constexpr int CG = DC / 8, RPP = NT / CG;
+  static_assert(DC % 8 == 0 && NT % CG == 0 && NR % RPP == 0, "whole rows per thread");
+  const int c0 = (tid % CG) * 8, rr = tid / CG;
+#pragma unroll
+  for (int i = 0; i < NR / RPP; ++i) {
+    const int r = rr + RPP * i, idx = base + r;
+    if (idx < nidx) {
+      const f32x4 lo = *(const f32x4*)(st + r * DQK + c0), hi = *(const f32x4*)(st + r * DQK + c0 + 4);
+      const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      store8(e.dxc, dxcb + (int64_t)idx * e.dxc_s[2] + c0, e.dxc_dtype, v);
     }
   }
 }
@@ -981,9 +1004,12 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     }
   }
 
-  if (a.fuse_inv && epi_vec_ok(a.ek)) {  // inverse PoPE transform of the staged dk~ rows, all 8 waves
+  // inverse PoPE transform of the staged dk~ rows (and the content part's copy), all 8 waves; DC is
+  // the content width, 0, or DQK / 2 at DQK = 128 (the host fuses no other split)
+  auto epi_vec = [&](auto dc_tag) {
+    constexpr int DC = decltype(dc_tag)::value;
     const EpiPoPE& e = a.ek;
-    constexpr int Dr = DQK / 2, CG = Dr / 8, RPP = NW * 64 / CG;
+    constexpr int Dr = (DQK - DC) / 2, CG = Dr / 8, RPP = NW * 64 / CG;
     const int c0 = (tid % CG) * 8, rr = tid / CG;
     float fr[8], dl[8], sdl[8], sf[8];
 #pragma unroll
@@ -993,8 +1019,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       sdl[j] = sf[j] = 0.f;
     }
     __syncthreads();  // every dk~ row staged
-    inv_pope_rows<DQK, NW * 64, BNK, false>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1], b * e.dx_s[0] + hk * e.dx_s[1],
-                                     k0, a.Sk, fr, dl, a.delta != nullptr, nullptr, sdl, sf);
+    if constexpr (DC > 0)
+      content_rows<DQK, DC, NW * 64, BNK>(e, st_epi, tid, b * e.dxc_s[0] + hk * e.dxc_s[1], k0, a.Sk);
+    inv_pope_rows<DQK, DC, NW * 64, BNK, false>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1],
+                                                b * e.dx_s[0] + hk * e.dx_s[1], k0, a.Sk, fr, dl,
+                                                a.delta != nullptr, nullptr, sdl, sf);
     if (e.part_delta || e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
       __syncthreads();
       float* red = st_epi;  // [2][RPP][Dr]
@@ -1015,6 +1044,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
         if (e.part_freq) e.part_freq[blk * Dr + tid] = f0;
       }
     }
+  };
+  if (DQK == 128 && a.fuse_inv && a.Dc == DQK / 2) {  // split form: fused only at width 128, vector views
+    if constexpr (DQK == 128) epi_vec(std::integral_constant<int, DQK / 2>{});
+  } else if (a.fuse_inv && epi_vec_ok(a.ek, 0)) {
+    epi_vec(std::integral_constant<int, 0>{});
   } else if (a.fuse_inv) {  // the same, element by element, for strided x / dx
     const EpiPoPE& e = a.ek;
     const int Dr = DQK / 2;
@@ -1298,8 +1332,11 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
         }
         __syncthreads();
       };
-      if (epi_vec_ok(e) && a.qtab) {  // the host provides the query phase table with the fused form
-        constexpr int CG = Dr_c / 8, RPP = NW * 64 / CG;
+      // vectorised rows; DC is the content width, 0, or DQK / 2 at DQK = 128 (the host fuses no other
+      // split, and the split form only with vector views)
+      auto epi_vec = [&](auto dc_tag) {
+        constexpr int DC = decltype(dc_tag)::value;
+        constexpr int Drv = (DQK - DC) / 2, CG = Drv / 8, RPP = NW * 64 / CG;
         const int c0 = (tid % CG) * 8, rr = tid / CG;
         float fr8[8], dl8[8], sdl8[8], sf8[8];
 #pragma unroll
@@ -1309,22 +1346,34 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
         }
         for (int half = 0; half < 2; ++half) {
           stage(half);
-          inv_pope_rows<DQK, NW * 64, 128, true>(e, st, tid, b * e.x_s[0] + h * e.x_s[1], b * e.dx_s[0] + h * e.dx_s[1],
-                                           q0 + half * 128, a.Sq, fr8, dl8, false, a.qtab, sdl8, sf8);
+          if constexpr (DC > 0)
+            content_rows<DQK, DC, NW * 64, 128>(e, st, tid, b * e.dxc_s[0] + h * e.dxc_s[1], q0 + half * 128, a.Sq);
+          inv_pope_rows<DQK, DC, NW * 64, 128, true>(e, st, tid, b * e.x_s[0] + h * e.x_s[1],
+                                                     b * e.dx_s[0] + h * e.dx_s[1], q0 + half * 128, a.Sq, fr8,
+                                                     dl8, false, a.qtab, sdl8, sf8);
         }
         if (e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
           __syncthreads();
           float* red = st;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) red[rr * Dr_c + c0 + j] = sf8[j];
+          for (int j = 0; j < 8; ++j) red[rr * Drv + c0 + j] = sf8[j];
           __syncthreads();
           const int64_t blk = (int64_t)bh * nqb + qb;
-          if (tid < Dr_c) {
+          if (tid < Drv) {
             float f0 = 0.f;
-            for (int i = 0; i < RPP; ++i) f0 += red[i * Dr_c + tid];
-            e.part_freq[blk * Dr_c + tid] = f0;
+            for (int i = 0; i < RPP; ++i) f0 += red[i * Drv + tid];
+            e.part_freq[blk * Drv + tid] = f0;
           }
         }
+      };
+      if constexpr (DQK == 128) {  // split form: fused only at width 128, with vector views
+        if (a.qtab && a.Dc == DQK / 2) {
+          epi_vec(std::integral_constant<int, DQK / 2>{});
+          return;
+        }
+      }
+      if (epi_vec_ok(e, 0) && a.qtab) {  // the host provides the query phase table with the fused form
+        epi_vec(std::integral_constant<int, 0>{});
         return;
       }
       float xv[EU], xn[EU];

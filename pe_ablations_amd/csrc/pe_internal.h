@@ -12,6 +12,7 @@ namespace pe {
 struct EpiPoPE {
   const void* x; int x_dtype; int64_t x_s[4];
   void* dx; int dx_dtype; int64_t dx_s[4];
+  void* dxc; int dxc_dtype; int64_t dxc_s[4];  // content-part gradient (split form, Dc > 0)
   int start_pos;
   int pos_round;  // PE_POS_* rounding of positions
   float* part_delta;
@@ -69,9 +70,10 @@ struct CoreArgs {
   float* dq_t;      // (B, Hq, Sq, DQK) fp32, already multiplied by scale
   float* dk_t;      // (B, Hkv, Sk, DQK) fp32, already multiplied by scale (summed over the GQA group)
   void* dv; int64_t dv_sb, dv_sh, dv_ss; int dv_dtype;
-  // fused inverse transform (bf16 fused PoPE form: Dc = 0, DQK = 2*Dr): when set the gradient
-  // kernels write dq / dk through eq / ek instead of dq_t / dk_t
-  int fuse_inv; int Dr;
+  // fused inverse transform (bf16 PoPE with DQK = Dc + 2*Dr, Dc = 0 or Dc = DQK/2): when set the
+  // gradient kernels write dq / dk (and the content parts dq_c / dk_c) through eq / ek instead of
+  // dq_t / dk_t
+  int fuse_inv; int Dr; int Dc;
   const float* freqs; const float* delta; int64_t delta_hs;
   EpiPoPE eq, ek;
 };

@@ -235,3 +235,49 @@ def test_positions_fp16_fp32_mode(cuda):
     omega = O.fope_effective_freqs(O.pope_freqs(D), rnd(D, 4, seed=45, scale=0.4)).detach()
     run_case(cuda, Dr=D, Dv=64, Sq=160, dtype=torch.float32, freqs=omega, delta=-torch.rand(D) * 6,
              grad_freqs=True, start_q=5000, start_k=5000, pos_dtype=torch.float16, seed=46)
+
+
+def test_split_form_fused_epilogue_matches_unfused_path(cuda):
+    """The split form [content 64 | PoPE 2 x 32] in bf16 applies its inverse transform and copies
+    the content gradient in the gradient kernels' epilogues when every view is 16-byte aligned.
+    The same call with a q_c view that starts 2 bytes off alignment takes the stand-alone inverse
+    kernels instead.  Both evaluate the same per-element function on the same fp32 gradients, so
+    every gradient agrees bit for bit; the phase-gradient partial sums run over different blocks."""
+    B, Hq, Hkv, S, Dc, Dr, Dv = 2, 8, 4, 700, 64, 32, 64
+    g = torch.Generator().manual_seed(60)
+    mk = lambda h, d: torch.randn(B, h, S, d, generator=g).to(torch.bfloat16)
+    qr, kr, qc, kc, v, do = mk(Hq, Dr), mk(Hkv, Dr), mk(Hq, Dc), mk(Hkv, Dc), mk(Hkv, Dv), mk(Hq, Dv)
+    freqs = O.fope_effective_freqs(O.pope_freqs(Dr), rnd(Dr, 4, seed=61, scale=0.4)).detach()
+    delta = -torch.rand(Dr, generator=g) * 6
+
+    def run(unaligned):
+        wide = torch.zeros(B, Hq, S, Dc + 1, dtype=torch.bfloat16)
+        wide[..., 1:] = qc
+        qcv = wide.to(cuda)[..., 1:] if unaligned else qc.to(cuda)
+        ins = [t.to(cuda) for t in (qr, kr, v, kc)]
+        leaves = [ins[0], ins[1], ins[2], qcv, ins[3]]
+        for t in leaves:
+            t.requires_grad_(True)
+        f, d = freqs.to(cuda).requires_grad_(True), delta.to(cuda).requires_grad_(True)
+        out = pe_attention(ins[0], ins[1], ins[2], mode="pope", q_c=qcv, k_c=ins[3], freqs=f, delta=d)
+        grads = torch.autograd.grad(out, leaves + [f, d], do.to(cuda))
+        torch.cuda.synchronize()
+        return [out] + list(grads)
+
+    fused, plain = run(False), run(True)
+    names = ["out", "dqr", "dkr", "dv", "dqc", "dkc", "dfreqs", "ddelta"]
+    for n, a, b in zip(names, fused, plain):
+        if n in ("dfreqs", "ddelta"):
+            assert md(a, b) / max(1.0, b.abs().max().item()) < 1e-5, n
+        else:
+            assert torch.equal(a, b), (n, md(a, b))
+    # and the fused path against the oracle (the reference module's contraction, fp64 core)
+    o = [t.float().requires_grad_(True) for t in (qc, kc, qr, kr, v)]
+    of, od = freqs.clone().requires_grad_(True), delta.clone().requires_grad_(True)
+    ref, _ = O.split_pope_attention(o[0], o[1], o[2], o[3], o[4], of, od, operand_dtype=torch.bfloat16)
+    rg = torch.autograd.grad(ref, [o[2], o[3], o[4], o[0], o[1], of, od], do.double())
+    for n, a, b in zip(names, fused, [ref] + list(rg)):
+        if n in ("dfreqs", "ddelta"):
+            assert md(a, b) / max(1.0, b.abs().max().item()) < 2e-2, n
+        else:
+            assert md(a, b) < 2e-2, n
