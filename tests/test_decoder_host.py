@@ -268,3 +268,48 @@ def test_next_token_sampling_rules():
     counts = torch.bincount(torch.cat([_next_token(logits[1:], 1.0, None, None) for _ in range(400)]).flatten(),
                             minlength=5)
     assert counts[0] > counts[4] > 0 and counts[1:4].sum() < 40
+
+
+def test_oracle_decoder_gate_order_and_prenorm_by_numbers():
+    """The decoder oracle's SwiGLU gate order and pre-norm residuals pinned by numbers, not by a
+    restated formula.  One layer, one token with embedding 2 * ones (RMS 2); with one key the
+    attention output is wo wv h.  Every weight is zero except the final norm, the sub-layer norms
+    (ones) and, in two separate runs:
+      attention run: wv row 0 = ones / d (v0 = mean of h), wo[1, 0] = 1  -> adds v0 to dim 1;
+      FFN run: w1 row 0 = 2 ones / d, w3 row 0 = 3 ones / d, w2[0, 0] = 0.5 -> adds 0.5 g to dim 0;
+    output rows 0, 1, 2 = unit vectors 0, 1, 2 (the final RMSNorm keeps ratios).  The reference
+    (src/model/transformer.py:205-206, src/model/ffn.py:27,68) normalises before each sub-layer and
+    adds to the raw residual, so h = ones: v0 = 1, logit1 / logit2 = 3 / 2; g = silu(3) * 2 (silu on
+    the w3 branch), logit0 / logit2 = (2 + silu(3)) / 2 with silu(3) = 3 / (1 + e^-3) =
+    2.857722380...  A swapped gate gives (2 + 1.5 silu(2)) / 2; a sub-layer that reads the raw
+    stream (no pre-norm, or a post-norm block) sees h = 2 ones and gives logit1 / logit2 = 2 and
+    (2 + 2 silu(6)) / 2."""
+    c, sd = _tiny("pope", num_layers=1, pope_fused=True)
+    d = c.hidden_dim
+    p, f = "layers.0.", "layers.0.feed_forward."
+
+    def run(attn: bool):
+        w = {k: torch.zeros_like(v) for k, v in sd.items()}
+        for k in w:
+            if k.endswith("norm.weight"):
+                w[k] = torch.ones_like(w[k])
+        w["token_embedding.embedding.weight"][7] = 2.0
+        if attn:
+            w[p + "attention.wv.weight"][0] = 1.0 / d
+            w[p + "attention.wo.weight"][1, 0] = 1.0
+        else:
+            w[f + "w1.weight"][0] = 2.0 / d
+            w[f + "w3.weight"][0] = 3.0 / d
+            w[f + "w2.weight"][0, 0] = 0.5
+        for i in range(3):
+            w["output.weight"][i, i] = 1.0
+        return O.decoder_forward(w, c, torch.tensor([[7]]))["logits"][0, 0].double()
+
+    silu = lambda t: t / (1.0 + math.exp(-t))
+    assert abs(silu(3.0) - 2.8577223804673) < 1e-12
+    la, lf = run(True), run(False)
+    # h = 2 / sqrt(4 + eps) per dim: the RMSNorm eps moves the ratios by < 1e-6
+    assert abs(la[1] / la[2] - 1.5) < 1e-5
+    assert abs(lf[0] / lf[2] - (2.0 + 0.5 * 2.0 * silu(3.0)) / 2.0) < 1e-5
+    for wrong in ((2.0 + 0.5 * 3.0 * silu(2.0)) / 2.0, (2.0 + 0.5 * 4.0 * silu(6.0)) / 2.0):
+        assert abs(lf[0] / lf[2] - wrong) > 0.1
