@@ -239,8 +239,12 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
       plan_k.full(ksrc, nl, dw, (uint32_t)krs);
       plan_v.full(vsrc, nl + SK_BYTES, dw, (uint32_t)vrs);
     } else {
-      dma_tile<BN, NCK, NDW, KSZ>(nK, ksrc, krs, a.Sk - k0, dw, lane);
-      dma_tile<BN, NCV, NDW, VSZ>(nK + SK_BYTES, vsrc, vrs, a.Sk - k0, dw, lane);
+      // the last, partial tile: an opaque copy of the lane index keeps this path's offsets from
+      // being hoisted out of the loop (they would hold registers for the whole loop)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      dma_tile<BN, NCK, NDW, KSZ>(nK, ksrc, krs, a.Sk - k0, dw, ln);
+      dma_tile<BN, NCV, NDW, VSZ>(nK + SK_BYTES, vsrc, vrs, a.Sk - k0, dw, ln);
     }
   };
 #pragma unroll
@@ -248,7 +252,11 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
     if (i < nkb) issue(i);
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * BN;
-    char* sK = smem + (kb % NSTG) * STAGE;
+    // the slot offset is opaque to the compiler, which would otherwise keep a set of per-lane
+    // fragment addresses for each slot
+    int slot = (kb % NSTG) * STAGE;
+    asm volatile("" : "+s"(slot));
+    char* sK = smem + slot;
     char* sV = sK + SK_BYTES;
     // tile kb has landed once at most the loads of the tiles issued after it are outstanding
     if (NSTG == 3 && kb + 1 < nkb) wait_vmcnt<PER>();
@@ -372,7 +380,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_
 
 template <int DQK, int DV>
 static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
-  constexpr int NW = 8, BN = 64;
+  constexpr int NW = 8;
   // four DMA waves, a double-buffered ring (a 3-tile ring measured 1.44 against 1.41 ms)
   constexpr int NDW = 4, NSTG = 2;
   const int BM = NW * 32;
@@ -380,7 +388,13 @@ static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
   const int grid = nqb * a.B * a.Hq;
   const int o_vec = (a.dv_real == DV) && ((uintptr_t)a.o % 16 == 0) && ((a.o_ss * 2) % 16 == 0) &&
                     ((a.o_sh * 2) % 16 == 0) && ((a.o_sb * 2) % 16 == 0);
-  hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, BN, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
+  // 96-key tiles spread each step's barrier and tile wait over 1.5 times the products (forward
+  // 1.37 vs 1.40 ms at S = 16384, 3 % faster at S = 2048); on short sequences the wider diagonal
+  // tiles waste more than that saves (S = 512: 0.023 vs 0.021 ms), so they keep 64-key tiles
+  if (a.Sk >= 2048)
+    hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, 96, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
+  else
+    hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, 64, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
