@@ -265,6 +265,9 @@ class PEAttentionFn(torch.autograd.Function):
         ctx.key = key
         ctx.save_for_backward(qr, kr, v, qc, kc, freqs, delta, out, lse, fws)
         ctx.mark_non_differentiable(lse)
+        # lse carries no gradient: without this, autograd fills a zero (B, Hq, Sq) tensor for it in
+        # every backward
+        ctx.set_materialize_grads(False)
         return out, lse
 
     @staticmethod
@@ -277,6 +280,8 @@ class PEAttentionFn(torch.autograd.Function):
         fp = plans.get(ctx.key)
         if fp is None:
             fp = plans[ctx.key] = _FwdPlan(cfg, qr, kr, v, qc, kc, delta)
+        if dout is None:  # out was not used by the loss either
+            dout = torch.zeros_like(out)
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
         if dout.dtype not in (torch.bfloat16, torch.float32):
