@@ -1,4 +1,4 @@
-// RMSNorm kernels (HBM-bound, one workgroup per row / token).
+// RMSNorm kernels (HBM-bound, one wave per row / token, WPB rows per workgroup).
 //
 //   rmsnorm_kernel         y = (x * rsqrt(mean(x^2) + eps)).type_as(x) * w over the last dim
 //                          (src/model/normalization.py:7-27): statistics and products in fp32, the
@@ -10,26 +10,23 @@
 //                          (src/model/pope.py:124-183), written straight into the attention
 //                          kernels' operand rows [content | mu cos | mu sin | 0]
 //
-// Each thread owns up to MAXC 8-element chunks of the row in registers, so the row is read from
-// HBM once; the sum of squares is reduced per wave (butterfly) and across the 4 waves in a fixed
-// order, so results do not depend on scheduling.
+// Each lane owns CPL 8-element chunks of its wave's row in registers (chunk c = lane + 64 k), so
+// the row is read from HBM once and all of a lane's loads are in flight together.  The sum of
+// squares is reduced by the wave's xor butterfly, which leaves the same value in every lane and
+// depends on nothing but the row, so no LDS and no barrier are involved and the waves of a
+// workgroup (rows of their own) never wait for each other.
 #include "pe_common.h"
 #include "pe_internal.h"
 
 namespace pe {
 
-constexpr int NT = 256;   // threads per workgroup
-constexpr int MAXC = 4;   // chunks per thread: rows up to NT * MAXC * 8 = 8192 elements
+constexpr int WPB = 4;      // waves, i.e. rows, per workgroup
+constexpr int MAXCPL = 16;  // chunks per lane: rows up to 64 * MAXCPL * 8 = 8192 elements
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
+__device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int i = 0; i < NT / 64; ++i) t += red[i];
-  return t;
+  return v;
 }
 
 // normalise one chunk in place: n = fl(x * r) rounded to x's dtype, y = fl(n * w) (bf16 if both are)
@@ -47,15 +44,17 @@ __device__ __forceinline__ void norm_chunk(float (&x)[8], float r, bool x_bf, co
   }
 }
 
-__global__ __launch_bounds__(NT) void rmsnorm_kernel(NormArgs a) {
-  __shared__ float red[NT / 64];
-  const int64_t row = blockIdx.x;
+template <int CPL>
+__global__ __launch_bounds__(WPB * 64) void rmsnorm_kernel(NormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // whole waves: the kernel has no barrier
   const int nch = a.n >> 3;
-  float x[MAXC][8];
+  float x[CPL][8];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < MAXC; ++k) {
-    const int c = threadIdx.x + k * NT;
+  for (int k = 0; k < CPL; ++k) {
+    const int c = lane + k * 64;
     if (c < nch) {
       load8(a.x, row * a.x_rs + c * 8, a.x_dtype, x[k]);
 #pragma unroll
@@ -63,10 +62,10 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(NormArgs a) {
     }
   }
   // torch: mean = sum * (1/n), then rsqrt(mean + eps)
-  const float r = rsqrtf(block_sum(ss, red) * (1.0f / (float)a.n) + a.eps);
+  const float r = rsqrtf(wave_sum(ss) * (1.0f / (float)a.n) + a.eps);
 #pragma unroll
-  for (int k = 0; k < MAXC; ++k) {
-    const int c = threadIdx.x + k * NT;
+  for (int k = 0; k < CPL; ++k) {
+    const int c = lane + k * 64;
     if (c < nch) {
       norm_chunk(x[k], r, a.x_dtype == 0, a.w, a.w_dtype, c * 8);
       store8(a.y, row * a.y_rs + c * 8, a.y_dtype, x[k]);
@@ -74,19 +73,20 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(NormArgs a) {
   }
 }
 
-template <int DDT>
-__global__ __launch_bounds__(NT) void prep_pope_norm_kernel(PrepArgs a) {
-  __shared__ float red[NT / 64];
+template <int DDT, int CPL>
+__global__ __launch_bounds__(WPB * 64) void prep_pope_norm_kernel(PrepArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (tok >= a.B * a.S) return;  // whole waves: the kernel has no barrier
   const int tpr = a.Dr >> 3;
   const int nch = a.H * tpr;
-  const int tok = blockIdx.x;
   const int b = tok / a.S, s = tok - b * a.S;
   const float pos = pe_pos(a.start_pos + s, a.pos_round);
-  float x[MAXC][8];
+  float x[CPL][8];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < MAXC; ++k) {
-    const int c = threadIdx.x + k * NT;
+  for (int k = 0; k < CPL; ++k) {
+    const int c = lane + k * 64;
     if (c < nch) {
       const int h = c / tpr, t = c - h * tpr;
       load8(a.xr, b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + t * 8, a.xr_dtype, x[k]);
@@ -94,11 +94,11 @@ __global__ __launch_bounds__(NT) void prep_pope_norm_kernel(PrepArgs a) {
       for (int e = 0; e < 8; ++e) ss += x[k][e] * x[k][e];
     }
   }
-  const float r = rsqrtf(block_sum(ss, red) * (1.0f / (float)(a.H * a.Dr)) + a.norm_eps);
+  const float r = rsqrtf(wave_sum(ss) * (1.0f / (float)(a.H * a.Dr)) + a.norm_eps);
   const bool add = a.is_key && a.delta;
 #pragma unroll
-  for (int k = 0; k < MAXC; ++k) {
-    const int c = threadIdx.x + k * NT;
+  for (int k = 0; k < CPL; ++k) {
+    const int c = lane + k * 64;
     if (c < nch) {
       const int h = c / tpr, t = c - h * tpr;
       norm_chunk(x[k], r, a.xr_dtype == 0, a.norm_w, a.norm_w_dtype, c * 8);
@@ -109,15 +109,27 @@ __global__ __launch_bounds__(NT) void prep_pope_norm_kernel(PrepArgs a) {
         d1 = *(const f32x4*)(a.delta + h * a.delta_hs + t * 8 + 4);
       }
       float cv[8], sv[8];
+      if (a.tab && !a.is_key) {  // query phases from the table (the same values pe_sincos gives)
+        const float* tr = a.tab + (int64_t)s * 2 * a.Dr + t * 8;
+        const f32x4 c0 = *(const f32x4*)tr, c1 = *(const f32x4*)(tr + 4);
+        const f32x4 s0 = *(const f32x4*)(tr + a.Dr), s1 = *(const f32x4*)(tr + a.Dr + 4);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float mu = softplus_f(x[k][e]);
-        float ph = mul_nc(pos, e < 4 ? f0[e] : f1[e - 4]);
-        if (add) ph = add_nc(ph, e < 4 ? d0[e] : d1[e - 4]);
-        float sn, cs;
-        pe_sincos(ph, sn, cs);
-        cv[e] = mul_nc(mu, cs);
-        sv[e] = mul_nc(mu, sn);
+        for (int e = 0; e < 8; ++e) {
+          const float mu = softplus_f(x[k][e]);
+          cv[e] = mul_nc(mu, e < 4 ? c0[e] : c1[e - 4]);
+          sv[e] = mul_nc(mu, e < 4 ? s0[e] : s1[e - 4]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float mu = softplus_f(x[k][e]);
+          float ph = mul_nc(pos, e < 4 ? f0[e] : f1[e - 4]);
+          if (add) ph = add_nc(ph, e < 4 ? d0[e] : d1[e - 4]);
+          float sn, cs;
+          pe_sincos(ph, sn, cs);
+          cv[e] = mul_nc(mu, cs);
+          sv[e] = mul_nc(mu, sn);
+        }
       }
       const int64_t drow = ((int64_t)(b * a.H + h) * a.S + s) * a.width;
       store8(a.dst, drow + a.Dc + t * 8, DDT, cv);
@@ -126,7 +138,7 @@ __global__ __launch_bounds__(NT) void prep_pope_norm_kernel(PrepArgs a) {
   }
   if (a.Dc > 0) {  // content part: converted copy
     const int cpr = a.Dc >> 3;
-    for (int c = threadIdx.x; c < a.H * cpr; c += NT) {
+    for (int c = lane; c < a.H * cpr; c += 64) {
       const int h = c / cpr, j = c - h * cpr;
       float v[8];
       load8(a.xc, b * a.xc_s[0] + h * a.xc_s[1] + (int64_t)s * a.xc_s[2] + j * 8, a.xc_dtype, v);
@@ -135,10 +147,29 @@ __global__ __launch_bounds__(NT) void prep_pope_norm_kernel(PrepArgs a) {
   }
   const int used = a.Dc + 2 * a.Dr;
   const int ppr = (a.width - used) >> 3;
-  for (int c = threadIdx.x; c < a.H * ppr; c += NT) {
+  for (int c = lane; c < a.H * ppr; c += 64) {
     const int h = c / ppr, j = c - h * ppr;
     const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     store8(a.dst, ((int64_t)(b * a.H + h) * a.S + s) * a.width + used + j * 8, DDT, z);
+  }
+}
+
+// chunks per lane for a row of nch 8-element chunks: the smallest instantiated count that covers it
+static int chunks_per_lane(int nch) {
+  int c = 1;
+  while (c < MAXCPL && 64 * c < nch) c *= 2;
+  return c;
+}
+
+// calls f with the chunk count as a compile-time constant (a power of two up to MAXCPL)
+template <typename F>
+static void with_cpl(int cpl, F&& f) {
+  switch (cpl) {
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    case 8: f(std::integral_constant<int, 8>{}); break;
+    default: f(std::integral_constant<int, 16>{}); break;
   }
 }
 
@@ -150,29 +181,35 @@ static bool rows_aligned(const void* p, int dtype, int64_t s0, int64_t s1, int64
 
 int launch_rmsnorm(const NormArgs& a, hipStream_t s) {
   if (a.rows <= 0 || a.rows > 0x7fffffff || a.n <= 0) return -2;
-  if (a.n % 8 != 0 || a.n > NT * MAXC * 8) return -3;
+  if (a.n % 8 != 0 || a.n > 64 * MAXCPL * 8) return -3;
   if ((a.x_dtype | a.w_dtype | a.y_dtype) & ~1) return -4;
   if (a.y_dtype != ((a.x_dtype == 0 && a.w_dtype == 0) ? 0 : 1)) return -4;
   if (!rows_aligned(a.x, a.x_dtype, a.x_rs, 0, 0) || !rows_aligned(a.y, a.y_dtype, a.y_rs, 0, 0) ||
       ((uintptr_t)a.w % 16) != 0)
     return -5;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)a.rows), dim3(NT), 0, s, a);
+  const dim3 grid((unsigned)((a.rows + WPB - 1) / WPB));
+  with_cpl(chunks_per_lane(a.n >> 3), [&](auto c) {
+    hipLaunchKernelGGL((rmsnorm_kernel<decltype(c)::value>), grid, dim3(WPB * 64), 0, s, a);
+  });
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
 int launch_prep_norm(const PrepArgs& a, hipStream_t s) {
   if (a.mode != 0 || !a.norm_w || ((a.norm_w_dtype | a.xr_dtype | a.dst_dtype) & ~1)) return -4;
   if (a.dst_rows != 0 || a.dst_row0 != 0) return -2;  // writes contiguous (B, H, S, width) rows only
-  if (a.Dr <= 0 || a.Dr % 8 != 0 || a.Dc % 8 != 0 || a.width % 8 != 0 || a.H * (a.Dr / 8) > NT * MAXC) return -3;
+  if (a.Dr <= 0 || a.Dr % 8 != 0 || a.Dc % 8 != 0 || a.width % 8 != 0 || a.H * (a.Dr / 8) > 64 * MAXCPL) return -3;
   if ((int64_t)a.B * a.S > 0x7fffffff) return -2;
   const bool ok = a.xr_s[3] == 1 && rows_aligned(a.xr, a.xr_dtype, a.xr_s[0], a.xr_s[1], a.xr_s[2]) &&
                   ((uintptr_t)a.dst % 16) == 0 && ((uintptr_t)a.freqs % 16) == 0 && ((uintptr_t)a.norm_w % 16) == 0 &&
                   (!a.is_key || !a.delta || (((uintptr_t)a.delta % 16) == 0 && a.delta_hs % 4 == 0)) &&
                   (a.Dc == 0 || (a.xc_s[3] == 1 && rows_aligned(a.xc, a.xc_dtype, a.xc_s[0], a.xc_s[1], a.xc_s[2])));
   if (!ok) return -5;
-  const dim3 grid((unsigned)((int64_t)a.B * a.S));
-  if (a.dst_dtype == 0) hipLaunchKernelGGL(prep_pope_norm_kernel<0>, grid, dim3(NT), 0, s, a);
-  else hipLaunchKernelGGL(prep_pope_norm_kernel<1>, grid, dim3(NT), 0, s, a);
+  const dim3 grid((unsigned)(((int64_t)a.B * a.S + WPB - 1) / WPB));
+  with_cpl(chunks_per_lane(a.H * (a.Dr / 8)), [&](auto c) {
+    constexpr int C = decltype(c)::value;
+    if (a.dst_dtype == 0) hipLaunchKernelGGL((prep_pope_norm_kernel<0, C>), grid, dim3(WPB * 64), 0, s, a);
+    else hipLaunchKernelGGL((prep_pope_norm_kernel<1, C>), grid, dim3(WPB * 64), 0, s, a);
+  });
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 

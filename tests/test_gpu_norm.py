@@ -30,7 +30,7 @@ def ulp_bf16(x):
 
 
 @pytest.mark.parametrize("xd,wd", [("bf16", "bf16"), ("bf16", "fp32"), ("fp32", "fp32"), ("fp32", "bf16")])
-@pytest.mark.parametrize("rows,n", [(1, 64), (37, 2048), (513, 8192), (9, 1000)])
+@pytest.mark.parametrize("rows,n", [(1, 64), (37, 2048), (5, 4096), (513, 8192), (9, 1000)])
 def test_rmsnorm_matches_oracle(cuda, xd, wd, rows, n):
     g = torch.Generator().manual_seed(rows * 7 + n)
     x = (torch.randn(rows, n, generator=g) * 3).to(DT[xd])
@@ -138,7 +138,7 @@ def test_fused_norm_refuses_grad(cuda):
 
 def test_fused_norm_fused_form_decoder_shape(cuda):
     """Fused form at the 1B shape's head layout (16 heads x 128, H*Dr = 2048 features per token,
-    one workgroup of 256 threads per token) against the oracle, fp32."""
+    one wave per token with four chunks per lane) against the oracle, fp32."""
     torch.manual_seed(5)
     pe = PoPEEmbedding(128, 512, delta_init="uniform")
     m = FPoPEGroupedQueryAttention(256, 16, 16, 128, 128, fpope=pe, d_content=0)
