@@ -397,15 +397,17 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     u32x4 ring[FD];
 #pragma unroll
     for (int i = 0; i < FD; ++i) ring[i] = rd(i);
-    // fences for MFMA / LDS reads only (0x417 lets ALU, VALU, SALU, transcendental and global
-    // memory instructions cross), so the next tile's DMA issue, which precedes the scores at a tile
-    // boundary, can be spread between the products
+    // fences for MFMA / LDS reads only (0x416 lets VALU, SALU, transcendental and global memory
+    // instructions cross; the ALU bit 0x1 would let MFMAs cross as well, and under register pressure
+    // the scheduler then pulls each product up to its own read, which leaves no read-ahead), so the
+    // next tile's DMA issue, which precedes the scores at a tile boundary, can be spread between the
+    // products
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      __builtin_amdgcn_sched_barrier(0x417);
+      __builtin_amdgcn_sched_barrier(0x416);
       const u32x4 cur = ring[i % FD];
       if (i + FD < NS) ring[i % FD] = rd(i + FD);
-      __builtin_amdgcn_sched_barrier(0x417);
+      __builtin_amdgcn_sched_barrier(0x416);
       if (i < NKF) s = M::mma(cur, kf[i], s);
       else dp = M::mma(cur, vf[i - NKF], dp);
     }
@@ -473,9 +475,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     constexpr int NR = NP > 16 ? NP : 16;
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      // fence for MFMA / LDS reads only (mask 0x407 lets ALU, VALU, SALU and transcendental
-      // instructions cross), so the softmax chains of consecutive elements overlap
-      __builtin_amdgcn_sched_barrier(0x407);
+      // fence for MFMA / LDS reads only (mask 0x406 lets VALU, SALU and transcendental
+      // instructions cross, but not MFMAs), so the softmax chains of consecutive elements overlap
+      __builtin_amdgcn_sched_barrier(0x406);
       const u32x4 cur = ring[i % FD];
       if (i + FD < NP) ring[i % FD] = rdp(pq, po, i + FD);
       if (i % 4 == 2 && i + 2 < 16) load_ld((i + 2) / 4);
@@ -798,7 +800,12 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     }
   };
 
-  constexpr int FD = 3;  // fragment read-ahead depth (depths 2, 4, 6 and 8 measured within 1 %)
+  // fragment read-ahead depth: fragment i + FD is read while product i runs.  The fences below
+  // (masks 0x416 / 0x406) pin LDS reads and MFMAs in program order and let vector, scalar and
+  // transcendental work cross; with the ALU bit 0x1 MFMAs may cross too, and role B (at the register
+  // limit) then had each product scheduled right after its own read.  Depths 3 and 4 with the ring
+  // intact measured alike.
+  constexpr int FD = 3;
   const RowX<NCQ, SZ> rq(perm_row<0>(l32), g);
   const RowX<NCO, SZ> ro(perm_row<0>(l32), g);
   const ColX<NCQ, SZ> cq(lane);
@@ -815,10 +822,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     for (int i = 0; i < FD; ++i) ring[i] = rq.read(sq, 0, i);
 #pragma unroll
     for (int i = 0; i < NKF; ++i) {
-      __builtin_amdgcn_sched_barrier(0x417);
+      __builtin_amdgcn_sched_barrier(0x416);
       const u32x4 cur = ring[i % FD];
       if (i + FD < NKF) ring[i % FD] = rq.read(sq, 0, i + FD);
-      __builtin_amdgcn_sched_barrier(0x417);
+      __builtin_amdgcn_sched_barrier(0x416);
       s = M::mma(cur, kf[i], s);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -832,10 +839,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     for (int i = 0; i < FD; ++i) ring[i] = ro.read(so, 0, i);
 #pragma unroll
     for (int i = 0; i < NVF; ++i) {
-      __builtin_amdgcn_sched_barrier(0x417);
+      __builtin_amdgcn_sched_barrier(0x416);
       const u32x4 cur = ring[i % FD];
       if (i + FD < NVF) ring[i % FD] = ro.read(so, 0, i + FD);
-      __builtin_amdgcn_sched_barrier(0x417);
+      __builtin_amdgcn_sched_barrier(0x416);
       dp = M::mma(cur, vf[i], dp);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -851,10 +858,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     for (int i = 0; i < FD; ++i) ring[i] = cx.read(base, (i / NT) * 16, (i % NT) * 32);
 #pragma unroll
     for (int i = 0; i < NPR; ++i) {
-      __builtin_amdgcn_sched_barrier(0x407);
+      __builtin_amdgcn_sched_barrier(0x406);
       const u32x4 cur = ring[i % FD];
       if (i + FD < NPR) ring[i % FD] = cx.read(base, ((i + FD) / NT) * 16, ((i + FD) % NT) * 32);
-      __builtin_amdgcn_sched_barrier(0x407);
+      __builtin_amdgcn_sched_barrier(0x406);
       acc[i % NT] = M::mma(af[i / NT], cur, acc[i % NT]);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -879,6 +886,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       const uint16_t* krow = (const uint16_t*)a.k + ((int64_t)(b * a.Hkv + hk) * a.Sk + kr) * DQK;
 #pragma unroll
       for (int kk = 0; kk < NKF; ++kk) kf[kk] = *(const u32x4*)(krow + kk * 16 + g * 8);
+      // a wait the compiler sees (the inline-asm waits for the tile loads are opaque to it):
+      // without it these loads stay pending in its accounting, and it inserts vmcnt(15) .. vmcnt(0)
+      // into the score products of every step, which also drains the tile loads issued a step
+      // earlier.  Here it costs one wait for tile 1's loads.
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
     }
     f32x16 dv[NDV];
 #pragma unroll
