@@ -1,8 +1,9 @@
 // C-ABI entry points of libpe_attn.so (declared in include/pe_attn.h).  Host code only (plus the
 // static scratch array of pe_attn_fwd_noalloc): validates the parameter block, carves the
 // caller's workspace and enqueues the kernels on the caller's stream.  No allocation, no
-// synchronisation; the only global mutable state is a per-device "is this a gfx950" flag and the
-// per-device address of the static scratch, each computed once under a mutex.
+// synchronisation; the only global mutable state is a per-device "is this a gfx950" flag with the
+// device's CU count, and the per-device address of the static scratch, each computed once under a
+// mutex.
 #include <hip/hip_runtime.h>
 #include <string.h>
 #include <algorithm>
@@ -140,19 +141,31 @@ int check_tensor(const pe_tensor_t* t, bool required) {
   return PE_OK;
 }
 
+int dev_flags[64];  // 0 unknown, 1 gfx950, 2 other
+int dev_cus[64];    // compute units of the device (set with its flag)
+std::mutex dev_mu;
+
 int device_ok() {
-  static int flags[64];  // 0 unknown, 1 gfx950, 2 other
-  static std::mutex mu;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return PE_ERR_NO_DEVICE;
   if (dev >= 64) return PE_OK;
-  std::lock_guard<std::mutex> lk(mu);
-  if (flags[dev] == 0) {
+  std::lock_guard<std::mutex> lk(dev_mu);
+  if (dev_flags[dev] == 0) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return PE_ERR_NO_DEVICE;
-    flags[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+    dev_cus[dev] = prop.multiProcessorCount;
+    dev_flags[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
   }
-  return flags[dev] == 1 ? PE_OK : PE_ERR_NO_DEVICE;
+  return dev_flags[dev] == 1 ? PE_OK : PE_ERR_NO_DEVICE;
+}
+
+// CU count of the current device (MI355X: 256), for launch shapes that must fill the chip; every
+// entry point calls device_ok first, which records it
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lk(dev_mu);
+  return dev_cus[dev] > 0 ? dev_cus[dev] : 256;
 }
 
 bool v_direct(const pe_attn_params* p, const pe_tensor_t* v, int dvp) {
@@ -192,6 +205,7 @@ pe::CoreArgs core_args(const pe_attn_params* p, const Layout& L, const char* ws,
     c.v = ws + L.v_off; c.v_ss = L.dv; c.v_sh = (int64_t)p->Sk * L.dv; c.v_sb = (int64_t)p->Hkv * p->Sk * L.dv;
   }
   c.B = p->B; c.Hq = p->Hq; c.Hkv = p->Hkv; c.Sq = p->Sq; c.Sk = p->Sk;
+  c.n_cu = device_cus();
   c.dv_real = p->Dv;
   c.causal = p->causal != PE_CAUSAL_NONE;
   c.causal_off = p->causal == PE_CAUSAL_BOTTOM_RIGHT ? p->Sk - p->Sq : 0;

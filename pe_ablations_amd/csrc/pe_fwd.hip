@@ -172,7 +172,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) 
 // MFMAs.  The running max is raised lazily: O and l are rescaled only when some query's block
 // max exceeds the current one by more than TAU (in log2 units), which bounds p by 2^TAU.
 template <int DQK, int DV, int BN, int NW, int NDW, int NSTG>
-__global__ __launch_bounds__(NW * 64, 1) void fwd_bf16_kernel(CoreArgs a, int o_vec) {
+__global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(CoreArgs a, int o_vec) {
   using M = MT<0>;
   constexpr int BM = NW * 32;
   constexpr int NCK = DQK / 8, NCV = DV / 8;
@@ -386,12 +386,18 @@ static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
   const int BM = NW * 32;
   const int nqb = (a.Sq + BM - 1) / BM;
   const int grid = nqb * a.B * a.Hq;
+  // a grid of 256-query blocks that leaves CUs idle (short sequences, few heads): 128-query blocks
+  // of four waves, two workgroups per CU, double the workgroups and halve the longest causal block
+  const bool small = (int64_t)grid < a.n_cu;
+  const int grid4 = ((a.Sq + 127) / 128) * a.B * a.Hq;
   const int o_vec = (a.dv_real == DV) && ((uintptr_t)a.o % 16 == 0) && ((a.o_ss * 2) % 16 == 0) &&
                     ((a.o_sh * 2) % 16 == 0) && ((a.o_sb * 2) % 16 == 0);
   // 96-key tiles spread each step's barrier and tile wait over 1.5 times the products (forward
   // 1.37 vs 1.40 ms at S = 16384, 3 % faster at S = 2048); on short sequences the wider diagonal
   // tiles waste more than that saves (S = 512: 0.023 vs 0.021 ms), so they keep 64-key tiles
-  if (a.Sk >= 2048)
+  if (small)
+    hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, 64, 4, 4, NSTG>), dim3(grid4), dim3(4 * 64), 0, s, a, o_vec);
+  else if (a.Sk >= 2048)
     hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, 96, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
   else
     hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, 64, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);

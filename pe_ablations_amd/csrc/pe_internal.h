@@ -76,6 +76,7 @@ struct CoreArgs {
   int fuse_inv; int Dr; int Dc;
   const float* freqs; const float* delta; int64_t delta_hs;
   EpiPoPE eq, ek;
+  int n_cu;  // compute units of the device: launchers pick smaller blocks when a grid would not fill them
 };
 
 int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
