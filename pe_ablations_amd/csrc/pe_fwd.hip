@@ -198,6 +198,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
     const uint16_t* qrow = (const uint16_t*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + (myq < a.Sq ? myq : a.Sq - 1)) * DQK;
 #pragma unroll
     for (int kk = 0; kk < NQF; ++kk) qf[kk] = *(const u32x4*)(qrow + kk * 16 + g * 8);
+    // a wait the compiler sees, before any tile load is in flight (it costs only the q~ loads).  The
+    // tile waits are inline asm, opaque to the compiler's wait-count pass; without this the q~
+    // loads stay pending in its accounting and it puts vmcnt(18) .. vmcnt(3) ahead of the score
+    // products of every tile, right after the DMA waves have issued the next tile, so those waves
+    // stalled until that tile had almost landed (0.27 ms of the headline forward)
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
   }
 
   int kend = a.Sk;
