@@ -727,12 +727,23 @@ __device__ __forceinline__ void content_rows(const EpiPoPE& e, const float* st, 
 // keys of pair p are shared by wave p (role A: scores S, P = softmax numerator, dV += P^T dO) and
 // wave p + 4 (role B: dP = dO v^T, dS = P (dP - Di), the dS store, dK~ += dS^T q~), which land on
 // the same SIMD, so each SIMD interleaves two instruction streams of 24 products per 32-query tile
-// and neither wave's exponentials, loads or waits leave the matrix core idle.  B keeps the fp32 P
-// it needs from an LDS exchange buffer, so dS is formed from unrounded P exactly as in the
-// one-wave kernel.  Each loop step t runs A's S / P of tile t, the loads of tile t+2 and dV of
+// and neither wave's exponentials, loads or waits leave the matrix core idle.  B gets the P it
+// needs through an LDS exchange buffer in fp16 (11 significant bits, 2 KiB per wave per tile): dS
+// = P (dP - Di) is rounded to bf16 (8 bits) right after, so the hand-off adds about an eighth of
+// dS's own rounding error, where a bf16 hand-off would double it.  Each loop step t runs A's S / P of tile t, the loads of tile t+2 and dV of
 // tile t-1 (so A starts the step on products while B forms dS), and B's dS / dK~ of tile t-1 and
 // dP of tile t, then one barrier; the 32-query tiles stream through a ring of
 // 4 LDS stages (q~ 32 x DQK, dO 32 x DV, the rows' log2 lse and Di) loaded two steps ahead.
+// two floats <-> one dword of fp16 (lo in bits 0-15), round-to-nearest-even (v_cvt_pk_f16_f32)
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, h2_t));
+}
+__device__ __forceinline__ void unpack_h2(uint32_t v, float& lo, float& hi) {
+  const f32x2_t f = __builtin_convertvector(__builtin_bit_cast(h2_t, v), f32x2_t);
+  lo = f[0];
+  hi = f[1];
+}
 template <int DQK, int DV>
 __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   using M = MT<0>;
@@ -741,7 +752,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   constexpr int NKF = DQK / 16, NVF = DV / 16, NDK = DQK / 32, NDV = DV / 32;
   constexpr int SQ_BYTES = BMQ * NCQ * 16, SO_BYTES = BMQ * NCO * 16;
   constexpr int STAGE = SQ_BYTES + SO_BYTES + 2 * BMQ * 4;
-  constexpr int XB_BYTES = 2 * 4 * 4096;  // P exchange: [step parity][pair] 16 floats x 64 lanes
+  constexpr int XB_BYTES = 2 * 4 * 2048;  // P exchange: [step parity][pair] 16 fp16 x 64 lanes
   constexpr int RING = NSTG * STAGE + XB_BYTES;
   constexpr int EPI = BNK * DQK * 4;
   constexpr int SMEM = RING > EPI ? RING : EPI;
@@ -915,17 +926,21 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           for (int i = 0; i < 16; ++i) s[i] = masked_row(kd, i) ? -INFINITY : s[i];
         }
         const float* sL = (const float*)(st + SQ_BYTES + SO_BYTES);
-        float* xb = (float*)(xbuf + ((t & 1) * 4 + pw) * 4096);
+        char* xb = xbuf + ((t & 1) * 4 + pw) * 2048;
+        u32x4 ph[2];
 #pragma unroll
         for (int G = 0; G < 4; ++G) {
           const f32x4 lv = *(const f32x4*)(sL + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
           f32x4 p;
 #pragma unroll
           for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[4 * G + e] * sl2 - lv[e]);
-          *(f32x4*)(xb + (G * 64 + lane) * 4) = p;
+          ph[G >> 1][(G & 1) * 2] = pack_h2(p[0], p[1]);
+          ph[G >> 1][(G & 1) * 2 + 1] = pack_h2(p[2], p[3]);
           pn[G >> 1][(G & 1) * 2] = pack_bf2(p[0], p[1]);
           pn[G >> 1][(G & 1) * 2 + 1] = pack_bf2(p[2], p[3]);
         }
+        *(u32x4*)(xb + (0 * 64 + lane) * 16) = ph[0];
+        *(u32x4*)(xb + (1 * 64 + lane) * 16) = ph[1];
       }
       if (t + 2 < niter) issue(t + 2);  // its stage held tile t - 2, released by the last barrier
       if (t >= 1) products(dv, pp, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);
@@ -970,11 +985,15 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       if (t >= 1) {  // dS of tile t - 1 from A's fp32 P; store it; dK~ += dS^T q~
         const char* st = smem + ((t - 1) % NSTG) * STAGE;
         const float* sD = (const float*)(st + SQ_BYTES + SO_BYTES) + BMQ;
-        const float* xb = (const float*)(xbuf + (((t - 1) & 1) * 4 + pw) * 4096);
+        const char* xb = xbuf + (((t - 1) & 1) * 4 + pw) * 2048;
         u32x4 dsf[2];
+        const u32x4 ph[2] = {*(const u32x4*)(xb + (0 * 64 + lane) * 16), *(const u32x4*)(xb + (1 * 64 + lane) * 16)};
 #pragma unroll
         for (int G = 0; G < 4; ++G) {
-          const f32x4 p = *(const f32x4*)(xb + (G * 64 + lane) * 4);
+          float p0, p1, p2, p3;
+          unpack_h2(ph[G >> 1][(G & 1) * 2], p0, p1);
+          unpack_h2(ph[G >> 1][(G & 1) * 2 + 1], p2, p3);
+          const f32x4 p = {p0, p1, p2, p3};
           const f32x4 dd = *(const f32x4*)(sD + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
           float ds[4];
 #pragma unroll
