@@ -744,15 +744,16 @@ __device__ __forceinline__ void unpack_h2(uint32_t v, float& lo, float& hi) {
   lo = f[0];
   hi = f[1];
 }
-template <int DQK, int DV>
+template <int DQK, int DV, int QT>
 __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   using M = MT<0>;
-  constexpr int NW = 8, BMQ = 32, BNK = 128, NSTG = 4;
+  constexpr int NW = 8, BMQ = 32 * QT, BNK = 128, NSTG = 4;
   constexpr int NCQ = DQK / 8, NCO = DV / 8;
   constexpr int NKF = DQK / 16, NVF = DV / 16, NDK = DQK / 32, NDV = DV / 32;
   constexpr int SQ_BYTES = BMQ * NCQ * 16, SO_BYTES = BMQ * NCO * 16;
   constexpr int STAGE = SQ_BYTES + SO_BYTES + 2 * BMQ * 4;
-  constexpr int XB_BYTES = 2 * 4 * 2048;  // P exchange: [step parity][pair] 16 fp16 x 64 lanes
+  constexpr int XBP = 2048 * QT;          // one pair's fp16 P of a step: [sub-tile][half][lane] 8 fp16
+  constexpr int XB_BYTES = 2 * 4 * XBP;   // P exchange: [step parity][pair]
   constexpr int RING = NSTG * STAGE + XB_BYTES;
   constexpr int EPI = BNK * DQK * 4;
   constexpr int SMEM = RING > EPI ? RING : EPI;
@@ -802,9 +803,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       dma_tile<BMQ, NCQ, NA, SZ>(st, qsrc, qrs, a.Sq - q0, pw, lane);
       dma_tile<BMQ, NCO, NA, SZ>(st + SQ_BYTES, osrc, a.do_ss * 2, a.Sq - q0, pw, lane);
     }
-    // every A wave issues the same 16-lane load of the tile's L2 (lanes 0-7) and Di (lanes 8-15)
+    // every A wave issues the same load of the tile's L2 (lanes 0 .. NL-1) and Di (lanes NL ..
+    // 2 NL-1), NL = BMQ / 4 lanes of 4 floats each
+    constexpr int NL = BMQ / 4;
     const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
-    if (lane < 16) dma16((lane < 8 ? a.L2 : a.Di) + p0 + (lane & 7) * 4, stl + SQ_BYTES + SO_BYTES);
+    if (lane < 2 * NL) dma16((lane < NL ? a.L2 : a.Di) + p0 + (lane % NL) * 4, stl + SQ_BYTES + SO_BYTES);
     if (++iss_qt == nqt) {
       iss_qt = qb0;
       ++iss_h;
@@ -824,46 +827,53 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const uint32_t rrq = (uint32_t)perm_row<0>(l32) * NCQ * 16, rro = (uint32_t)perm_row<0>(l32) * NCO * 16;
   const uint32_t crq = ColX<NCQ>::row_term(lane), cro = ColX<NCO>::row_term(lane);
 
-  // A: S of tile t into s (16 k-steps of the q~ rows against the wave's k~)
-  auto scores_s = [&](const char* sq, const u32x4 (&kf)[NKF], f32x16& s) {
+  // A: S of the tile's QT 32-query sub-tiles into s[m] (the q~ rows of sub-tile m against the
+  // wave's k~; fragment r of the read order is k-step r / QT of sub-tile r % QT)
+  constexpr int NSS = NKF * QT;
+  auto scores_s = [&](const char* sq, const u32x4 (&kf)[NKF], f32x16 (&s)[QT]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s[j] = 0.f;
+    for (int m = 0; m < QT; ++m)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s[m][j] = 0.f;
     u32x4 ring[FD];
 #pragma unroll
-    for (int i = 0; i < FD; ++i) ring[i] = rq.read(sq, 0, i);
+    for (int i = 0; i < FD; ++i) ring[i] = rq.read(sq, (i % QT) * 32, i / QT);
 #pragma unroll
-    for (int i = 0; i < NKF; ++i) {
+    for (int i = 0; i < NSS; ++i) {
       __builtin_amdgcn_sched_barrier(0x416);
       const u32x4 cur = ring[i % FD];
-      if (i + FD < NKF) ring[i % FD] = rq.read(sq, 0, i + FD);
+      if (i + FD < NSS) ring[i % FD] = rq.read(sq, ((i + FD) % QT) * 32, (i + FD) / QT);
       __builtin_amdgcn_sched_barrier(0x416);
-      s = M::mma(cur, kf[i], s);
+      s[i % QT] = M::mma(cur, kf[i / QT], s[i % QT]);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // B: dP of tile t into dp
-  auto scores_dp = [&](const char* so, const u32x4 (&vf)[NVF], f32x16& dp) {
+  // B: dP of the tile's sub-tiles into dp[m]
+  constexpr int NSP = NVF * QT;
+  auto scores_dp = [&](const char* so, const u32x4 (&vf)[NVF], f32x16 (&dp)[QT]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) dp[j] = 0.f;
+    for (int m = 0; m < QT; ++m)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) dp[m][j] = 0.f;
     u32x4 ring[FD];
 #pragma unroll
-    for (int i = 0; i < FD; ++i) ring[i] = ro.read(so, 0, i);
+    for (int i = 0; i < FD; ++i) ring[i] = ro.read(so, (i % QT) * 32, i / QT);
 #pragma unroll
-    for (int i = 0; i < NVF; ++i) {
+    for (int i = 0; i < NSP; ++i) {
       __builtin_amdgcn_sched_barrier(0x416);
       const u32x4 cur = ring[i % FD];
-      if (i + FD < NVF) ring[i % FD] = ro.read(so, 0, i + FD);
+      if (i + FD < NSP) ring[i % FD] = ro.read(so, ((i + FD) % QT) * 32, (i + FD) / QT);
       __builtin_amdgcn_sched_barrier(0x416);
-      dp = M::mma(cur, vf[i], dp);
+      dp[i % QT] = M::mma(cur, vf[i / QT], dp[i % QT]);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // products of one 32-query tile: NPR = 2 * NT MFMAs over accumulators acc[0..NT), B operands by
-  // the transpose load from the tile at `base` (k-step major, so the two products of one
-  // accumulator are NT apart)
-  auto products = [&](auto& acc, const u32x4 (&af)[2], const char* base, const auto& cx) {
+  // products of one tile: NPR = 2 * QT * NT MFMAs over accumulators acc[0..NT), B operands by the
+  // transpose load from the tile at `base` (k-step major, so the products of one accumulator are
+  // NT apart; k-step ks covers query rows 16 ks .. 16 ks + 15)
+  auto products = [&](auto& acc, const u32x4 (&af)[2 * QT], const char* base, const auto& cx) {
     constexpr int NT = sizeof(acc) / sizeof(acc[0]);
-    constexpr int NPR = 2 * NT;
+    constexpr int NPR = 2 * QT * NT;
     u32x4 ring[FD];
 #pragma unroll
     for (int i = 0; i < FD; ++i) ring[i] = cx.read(base, (i / NT) * 16, (i % NT) * 32);
@@ -908,39 +918,47 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     for (int t = 0; t < NDV; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) dv[t][j] = 0.f;
-    u32x4 pa0[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};  // bf16 P, alternating tiles
-    u32x4 pa1[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
-    f32x16 s;
+    u32x4 pa0[2 * QT], pa1[2 * QT];  // bf16 P, alternating tiles
+#pragma unroll
+    for (int i = 0; i < 2 * QT; ++i) pa0[i] = pa1[i] = u32x4{0u, 0u, 0u, 0u};
+    f32x16 s[QT];
     int cur_qt = qb0;  // query tile of step t
     // step t: S and P of tile t (products right after the barrier), the loads of tile t + 2, then
     // dV of tile t - 1 from the other P buffer
-    auto astep = [&](int t, u32x4 (&pn)[2], u32x4 (&pp)[2]) {
+    auto astep = [&](int t, u32x4 (&pn)[2 * QT], u32x4 (&pp)[2 * QT]) {
       if (t < niter) {
         const char* st = smem + (t % NSTG) * STAGE;
         scores_s(st + rrq, kf, s);
         const int q0 = cur_qt * BMQ;
         if (++cur_qt == nqt) cur_qt = qb0;
-        if (__builtin_amdgcn_readfirstlane(a.causal && kw0 + 31 - off - q0 > 0)) {
-          const int kd = myk - off - q0 - g * 8;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) s[i] = masked_row(kd, i) ? -INFINITY : s[i];
+        for (int m = 0; m < QT; ++m) {
+          const int q0m = q0 + 32 * m;
+          if (__builtin_amdgcn_readfirstlane(a.causal && kw0 + 31 - off - q0m > 0)) {
+            const int kd = myk - off - q0m - g * 8;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[m][i] = masked_row(kd, i) ? -INFINITY : s[m][i];
+          }
         }
         const float* sL = (const float*)(st + SQ_BYTES + SO_BYTES);
-        char* xb = xbuf + ((t & 1) * 4 + pw) * 2048;
-        u32x4 ph[2];
+        char* xb = xbuf + ((t & 1) * 4 + pw) * XBP;
 #pragma unroll
-        for (int G = 0; G < 4; ++G) {
-          const f32x4 lv = *(const f32x4*)(sL + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
-          f32x4 p;
+        for (int m = 0; m < QT; ++m) {
+          u32x4 ph[2];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[4 * G + e] * sl2 - lv[e]);
-          ph[G >> 1][(G & 1) * 2] = pack_h2(p[0], p[1]);
-          ph[G >> 1][(G & 1) * 2 + 1] = pack_h2(p[2], p[3]);
-          pn[G >> 1][(G & 1) * 2] = pack_bf2(p[0], p[1]);
-          pn[G >> 1][(G & 1) * 2 + 1] = pack_bf2(p[2], p[3]);
+          for (int G = 0; G < 4; ++G) {
+            const f32x4 lv = *(const f32x4*)(sL + m * 32 + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
+            f32x4 p;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[m][4 * G + e] * sl2 - lv[e]);
+            ph[G >> 1][(G & 1) * 2] = pack_h2(p[0], p[1]);
+            ph[G >> 1][(G & 1) * 2 + 1] = pack_h2(p[2], p[3]);
+            pn[2 * m + (G >> 1)][(G & 1) * 2] = pack_bf2(p[0], p[1]);
+            pn[2 * m + (G >> 1)][(G & 1) * 2 + 1] = pack_bf2(p[2], p[3]);
+          }
+          *(u32x4*)(xb + ((2 * m + 0) * 64 + lane) * 16) = ph[0];
+          *(u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16) = ph[1];
         }
-        *(u32x4*)(xb + (0 * 64 + lane) * 16) = ph[0];
-        *(u32x4*)(xb + (1 * 64 + lane) * 16) = ph[1];
       }
       if (t + 2 < niter) issue(t + 2);  // its stage held tile t - 2, released by the last barrier
       if (t >= 1) products(dv, pp, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);
@@ -974,7 +992,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     for (int t = 0; t < NDK; ++t)
 #pragma unroll
       for (int j = 0; j < 16; ++j) dk[t][j] = 0.f;
-    f32x16 dp;
+    f32x16 dp[QT];
     int prev_h = hk * grp, prev_qt = qb0;  // head and query tile of step t - 1
     // the wave's key row in the packed dS (pe_internal.h), less its first stored 64-query block
     const int64_t ds_row = ds_row_base(kw0 >> 5, a.ds_e, a.ds_nqt, a.causal) - ds_first(kb, a.ds_e, a.causal);
@@ -985,21 +1003,25 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       if (t >= 1) {  // dS of tile t - 1 from A's fp32 P; store it; dK~ += dS^T q~
         const char* st = smem + ((t - 1) % NSTG) * STAGE;
         const float* sD = (const float*)(st + SQ_BYTES + SO_BYTES) + BMQ;
-        const char* xb = xbuf + (((t - 1) & 1) * 4 + pw) * 2048;
-        u32x4 dsf[2];
-        const u32x4 ph[2] = {*(const u32x4*)(xb + (0 * 64 + lane) * 16), *(const u32x4*)(xb + (1 * 64 + lane) * 16)};
+        const char* xb = xbuf + (((t - 1) & 1) * 4 + pw) * XBP;
+        u32x4 dsf[2 * QT];
 #pragma unroll
-        for (int G = 0; G < 4; ++G) {
-          float p0, p1, p2, p3;
-          unpack_h2(ph[G >> 1][(G & 1) * 2], p0, p1);
-          unpack_h2(ph[G >> 1][(G & 1) * 2 + 1], p2, p3);
-          const f32x4 p = {p0, p1, p2, p3};
-          const f32x4 dd = *(const f32x4*)(sD + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
-          float ds[4];
+        for (int m = 0; m < QT; ++m) {
+          const u32x4 ph[2] = {*(const u32x4*)(xb + ((2 * m + 0) * 64 + lane) * 16),
+                               *(const u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16)};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) ds[e] = p[e] * (dp[4 * G + e] - dd[e]);
-          dsf[G >> 1][(G & 1) * 2] = pack_bf2(ds[0], ds[1]);
-          dsf[G >> 1][(G & 1) * 2 + 1] = pack_bf2(ds[2], ds[3]);
+          for (int G = 0; G < 4; ++G) {
+            float p0, p1, p2, p3;
+            unpack_h2(ph[G >> 1][(G & 1) * 2], p0, p1);
+            unpack_h2(ph[G >> 1][(G & 1) * 2 + 1], p2, p3);
+            const f32x4 p = {p0, p1, p2, p3};
+            const f32x4 dd = *(const f32x4*)(sD + m * 32 + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
+            float ds[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ds[e] = p[e] * (dp[m][4 * G + e] - dd[e]);
+            dsf[2 * m + (G >> 1)][(G & 1) * 2] = pack_bf2(ds[0], ds[1]);
+            dsf[2 * m + (G >> 1)][(G & 1) * 2 + 1] = pack_bf2(ds[2], ds[3]);
+          }
         }
         const int h = prev_h, q0 = prev_qt * BMQ;
         if (++prev_qt == nqt) {
@@ -1007,12 +1029,13 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           ++prev_h;
         }
         char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * a.ds_head + ds_row + (q0 >> 6)) * 4096;
-        const int mt = (q0 >> 5) & 1;
+        const int mt = (q0 >> 5) & 1;  // 0 for 64-query tiles, which fill their block
         // dS is read once, by the dQ GEMM after this kernel: non-temporal stores keep it from
         // displacing the q~ / dO tiles that the other key blocks re-read (4 % of this kernel's
         // time; non-temporal loads of it in the dQ GEMM measured 35 % slower there)
-        __builtin_nontemporal_store(dsf[0], (u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16));
-        __builtin_nontemporal_store(dsf[1], (u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16));
+#pragma unroll
+        for (int i = 0; i < 2 * QT; ++i)
+          __builtin_nontemporal_store(dsf[i], (u32x4*)(blk + ((mt * 2 + i) * 64 + lane) * 16));
         products(dk, dsf, st + crq, cq);
       }
       if (t < niter) scores_dp(smem + (t % NSTG) * STAGE + SQ_BYTES + rro, vf, dp);
@@ -1470,7 +1493,10 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
       if constexpr ((DQK == 128 || DQK == 256) && (DV == 128 || DV == 64)) {
         // two waves per SIMD (role-split pairs); the one-wave kernel serves the other widths
-        hipLaunchKernelGGL((dkdv_pair_kernel<DQK, DV>), dim3(nkb * a.B * a.Hkv), dim3(512), 0, s, a);
+        // 64-query tiles where they fit the LDS (QK width 128, V width 64: the ~125M GPT shape and the
+        // split training form), which halves the per-step barriers and waits per product
+        constexpr int QT = DQK == 128 && DV == 64 ? 2 : 1;
+        hipLaunchKernelGGL((dkdv_pair_kernel<DQK, DV, QT>), dim3(nkb * a.B * a.Hkv), dim3(512), 0, s, a);
       } else {
         hipLaunchKernelGGL((dkdv_bf16_kernel<DQK, DV, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
       }

@@ -2,9 +2,9 @@
 
 The bf16 backward stores dS in 4 KiB blocks (32 keys x 64 queries), key-row major, packed per
 (batch, head) to the blocks the causal dK/dV kernels write; the dQ GEMM reads them back.  This
-replays, on the CPU, the loop bounds of the writers (dkdv_pair_kernel: 32-query tiles from
-max(0, k0 - off) / 32; dkdv_bf16_kernel: 64-query tiles from max(0, k0 - off) / 64; both per
-128-key block) and of the reader (dq_gemm_kernel: 256-query blocks, key steps up to
+replays, on the CPU, the loop bounds of the writers (32-query tiles from max(0, k0 - off) / 32:
+dkdv_pair_kernel; 64-query tiles from max(0, k0 - off) / 64: dkdv_pair_kernel at QK width 128 and V
+width 64, and dkdv_bf16_kernel; all per 128-key block) and of the reader (dq_gemm_kernel: 256-query blocks, key steps up to
 min(Sk, q0 + 256 + off), unmasked steps below min(Sk, q0 + off + 1), masked fragments elsewhere),
 and checks that
 
@@ -57,7 +57,7 @@ def geometry(Sq, Sk, causal, bottom_right):
 
 
 def written(Sq, Sk, causal, bottom_right, pair):
-    """{(row, j, half)} stored by the dK/dV kernel of one (b, h)."""
+    """{(row, j, half)} stored by the dK/dV kernel of one (b, h): 32-query tiles (pair) or 64."""
     off, _, R, _ = geometry(Sq, Sk, causal, bottom_right)
     out = set()
     for kb in range(R):
