@@ -532,6 +532,12 @@ int pe_attn_cache_append(const pe_attn_params* p, const pe_tensor_t* kc, const p
   fill_prep(a, &pa, 1, kc, kr, freqs, delta, k_cache, pad_qk(qk_width(&pa)));
   a.dst_rows = capacity;
   a.dst_row0 = p->start_pos_k;
+  // the value rows go out in the key rows' launch when both take the vectorised path (bf16 PoPE
+  // rows, 16-byte aligned, unit inner stride), otherwise in a launch of their own
+  a.cv = v->data; a.cv_cols = p->Dv; a.cdst = v_cache; a.cwidth = pad_v(p->Dv);
+  for (int i = 0; i < 4; ++i) a.cv_s[i] = v->stride[i];
+  if (v->dtype == PE_DTYPE_BF16 && p->dtype == PE_DTYPE_BF16 && pe::prep_vec_copy_ok(a)) return pe::launch_prep(a, s);
+  a.cv = nullptr; a.cdst = nullptr;
   if ((rc = pe::launch_prep(a, s))) return rc;
   pe_attn_params pv = pa;
   pv.mode = PE_MODE_NONE; pv.Dc = 0; pv.Dr = p->Dv; pv.qk_l2norm = 0;

@@ -102,8 +102,16 @@ struct PrepArgs {
   // 0 means S (a contiguous (B, H, S, width) buffer).  A KV cache of capacity C takes new rows at
   // position p with dst_rows = C, dst_row0 = p.
   int dst_rows, dst_row0;
+  // optional rows copied alongside (launch_prep's vectorised PoPE path only, see prep_vec_copy_ok):
+  // row (b, h, s) of cv (bf16, unit inner stride, cv_cols values) goes to row
+  // (b * H + h) * dst_rows + dst_row0 + s of cdst (width cwidth, zero padded); the KV-cache append
+  // writes the new value rows in the launch that transforms the new key rows
+  const void* cv; int64_t cv_s[4]; int cv_cols; void* cdst; int cwidth;
 };
 int launch_prep(const PrepArgs& a, hipStream_t s);
+// whether launch_prep takes the vectorised PoPE path for `a` and can copy the rows described by
+// its cv / cdst fields in the same launch
+bool prep_vec_copy_ok(const PrepArgs& a);
 // cos / sin of the query phases fl(pe_pos(start + s) * freqs[c]) for s < S, c < Dr into tab
 // [S][2][Dr] (cos row then sin row), with the same routine and rounding as the prologue kernels
 int launch_phase_table(const float* freqs, int start, int S, int Dr, int pos_round, float* tab, hipStream_t s);

@@ -355,6 +355,12 @@ __global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
     for (int j = t; j < a.Dc / 8; j += tpr) *(u32x4*)(drow + j * 8) = *(const u32x4*)(xc + j * 8);
   }
   for (int j = (a.Dc + 2 * a.Dr) / 8 + t; j < a.width / 8; j += tpr) *(u32x4*)(drow + j * 8) = u32x4{0u, 0u, 0u, 0u};
+  if (a.cdst) {  // the row's companion copy (KV-cache append: the value row)
+    const uint16_t* crow = (const uint16_t*)a.cv + b * a.cv_s[0] + h * a.cv_s[1] + (int64_t)s * a.cv_s[2];
+    uint16_t* cd = (uint16_t*)a.cdst + ((int64_t)bh * (a.dst_rows ? a.dst_rows : a.S) + a.dst_row0 + s) * a.cwidth;
+    for (int j = t; j < a.cwidth / 8; j += tpr)
+      *(u32x4*)(cd + j * 8) = j * 8 < a.cv_cols ? *(const u32x4*)(crow + j * 8) : u32x4{0u, 0u, 0u, 0u};
+  }
 }
 
 // one group of TPR = Dv / 8 lanes per padded row (TPR a power of two, groups never straddle a
@@ -393,14 +399,24 @@ bool aligned16(const void* p, int64_t s0, int64_t s1, int64_t s2) {
   return ((uintptr_t)p % 16) == 0 && s0 % 8 == 0 && s1 % 8 == 0 && s2 % 8 == 0;
 }
 
+static bool prep_vec_ok(const PrepArgs& a) {
+  return a.mode == 0 && a.dst_dtype == 0 && a.xr_dtype == 0 && a.Dr > 0 && a.Dr % 8 == 0 &&
+         a.Dc % 8 == 0 && a.width % 8 == 0 && a.xr_s[3] == 1 &&
+         aligned16(a.xr, a.xr_s[0], a.xr_s[1], a.xr_s[2]) && ((uintptr_t)a.dst % 16) == 0 &&
+         ((uintptr_t)a.freqs % 16) == 0 &&
+         (!a.is_key || !a.delta || (((uintptr_t)a.delta % 16) == 0 && a.delta_hs % 4 == 0)) &&
+         (a.Dc == 0 || (a.xc_dtype == 0 && a.xc_s[3] == 1 && aligned16(a.xc, a.xc_s[0], a.xc_s[1], a.xc_s[2])));
+}
+
+bool prep_vec_copy_ok(const PrepArgs& a) {
+  return prep_vec_ok(a) && a.cv && a.cdst && a.cv_s[3] == 1 && aligned16(a.cv, a.cv_s[0], a.cv_s[1], a.cv_s[2]) &&
+         ((uintptr_t)a.cdst % 16) == 0 && a.cv_cols % 8 == 0 && a.cwidth % 8 == 0 && a.cv_cols <= a.cwidth;
+}
+
 int launch_prep(const PrepArgs& a, hipStream_t s) {
   const int64_t nrows = (int64_t)a.B * a.H * a.S;
-  const bool vec = a.mode == 0 && a.dst_dtype == 0 && a.xr_dtype == 0 && a.Dr > 0 && a.Dr % 8 == 0 &&
-                   a.Dc % 8 == 0 && a.width % 8 == 0 && a.xr_s[3] == 1 &&
-                   aligned16(a.xr, a.xr_s[0], a.xr_s[1], a.xr_s[2]) && ((uintptr_t)a.dst % 16) == 0 &&
-                   ((uintptr_t)a.freqs % 16) == 0 &&
-                   (!a.is_key || !a.delta || (((uintptr_t)a.delta % 16) == 0 && a.delta_hs % 4 == 0)) &&
-                   (a.Dc == 0 || (a.xc_dtype == 0 && a.xc_s[3] == 1 && aligned16(a.xc, a.xc_s[0], a.xc_s[1], a.xc_s[2])));
+  const bool vec = prep_vec_ok(a);
+  if (a.cdst && !(vec && prep_vec_copy_ok(a))) return -2;  // the caller checks prep_vec_copy_ok first
   if (vec) {
     const int64_t nthr = nrows * (a.Dr / 8);
     hipLaunchKernelGGL(prep_pope_vec_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, a);
