@@ -501,6 +501,18 @@ def _check_cache(k_cache, v_cache, B, Hkv, wk, wv, cdt, dev):
         raise ValueError("k_cache and v_cache capacities differ")
 
 
+class _AppendPlan:
+    """Per-signature launch state of pe_cache_append: the parameter block (checked once against the
+    caches) and the tensor descriptors; a call sets the start position and swaps the pointers."""
+    __slots__ = ("p", "pref", "dk", "dv", "dkc", "S", "cap")
+
+    def __init__(self, p, k, v, k_c, S, cap):
+        self.p = p
+        self.pref = ref(p)
+        self.dk, self.dv, self.dkc = _Desc(k), _Desc(v), _Desc(k_c)
+        self.S, self.cap = S, cap
+
+
 def pe_cache_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *,
                     start_pos: int, mode: str = "pope", k_c: Optional[torch.Tensor] = None,
                     freqs: Optional[torch.Tensor] = None, delta: Optional[torch.Tensor] = None,
@@ -510,35 +522,61 @@ def pe_cache_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_c
     the value rows v (B, Hkv, S, Dv) to cache rows start_pos .. start_pos + S - 1, phases at those
     positions (the reference's k_cache[:, :, start_pos:start_pos+S] = [k_c | PoPE(k_r)],
     src/model/fpope_attention.py:294-296).  The caches are (B, Hkv, capacity, width) in the compute
-    dtype with the widths of ``cache_widths``."""
+    dtype with the widths of ``cache_widths``.  Shapes, strides, dtypes and devices are checked
+    once per operand signature (one token per step keeps the same signature), the rows to write
+    on every call."""
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (k, v, k_c, freqs, delta)):
         raise RuntimeError("the KV-cache path is inference only (run it under torch.no_grad())")
     if not k.is_cuda:
         raise RuntimeError("pe_cache_append runs on the GPU only (got a CPU tensor)")
     m = _MODES[mode]
-    check_operands(k, k, v, k_c, k_c, freqs if m != _lib.PE_MODE_NONE else None, delta, mode=m)
     k, v, k_c = (_prep_in(t) for t in (k, v, k_c))
-    freqs = freqs.float().contiguous() if m != _lib.PE_MODE_NONE else None
+    freqs = freqs.float().contiguous() if m != _lib.PE_MODE_NONE and freqs is not None else None
     delta = None if delta is None else delta.float().contiguous()
-    B, Hkv, S, Dr = k.shape
-    Dc = 0 if k_c is None else k_c.shape[-1]
-    cdt = k_cache.dtype
-    dt = _dtype_code(cdt)
-    p = _cache_params(B=B, Hq=Hkv, Hkv=Hkv, Sq=S, Sk=S, Dc=Dc, Dr=Dr, Dv=v.shape[-1], mode=m, dtype=dt,
-                      causal=_lib.PE_CAUSAL_NONE, start_q=start_pos, start_k=start_pos, scale=1.0,
-                      mscale=rope_mscale, qk_norm=qk_norm, delta=delta,
-                      pos_round=position_rounding(position_dtype, m))
+    pos_round = position_rounding(position_dtype, m)
+    key = ("append", m, _sig(k), _sig(v), _sig(k_c), _sig(freqs), _sig(delta), _sig(k_cache), _sig(v_cache),
+           float(rope_mscale), bool(qk_norm), pos_round)
+    plans = _plans()
+    ap = plans.get(key)
     L = _lib.lib()
-    _lib.check(L.pe_attn_check(ref(p)))
-    _check_cache(k_cache, v_cache, B, Hkv, L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p)), cdt,
-                 k.device)
-    if start_pos < 0 or start_pos + S > k_cache.shape[2]:
-        raise ValueError(f"rows {start_pos}..{start_pos + S - 1} do not fit a cache of capacity {k_cache.shape[2]}")
-    with torch.cuda.device(k.device):
-        rc = L.pe_attn_cache_append(ref(p), ref(_tensor(k_c)), ref(_tensor(k)), ref(_tensor(v)), _ptr(freqs),
-                                    _ptr(delta), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2],
-                                    _stream(k.device))
+    if ap is None:
+        check_operands(k, k, v, k_c, k_c, freqs if m != _lib.PE_MODE_NONE else None, delta, mode=m)
+        if m != _lib.PE_MODE_NONE and freqs is None:
+            raise ValueError("freqs is required for a positional mode")
+        B, Hkv, S, Dr = k.shape
+        Dc = 0 if k_c is None else k_c.shape[-1]
+        cdt = k_cache.dtype
+        p = _cache_params(B=B, Hq=Hkv, Hkv=Hkv, Sq=S, Sk=S, Dc=Dc, Dr=Dr, Dv=v.shape[-1], mode=m,
+                          dtype=_dtype_code(cdt), causal=_lib.PE_CAUSAL_NONE, start_q=0, start_k=0, scale=1.0,
+                          mscale=rope_mscale, qk_norm=qk_norm, delta=delta, pos_round=pos_round)
+        _lib.check(L.pe_attn_check(ref(p)))
+        _check_cache(k_cache, v_cache, B, Hkv, L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p)), cdt,
+                     k.device)
+        ap = plans[key] = _AppendPlan(p, k, v, k_c, S, k_cache.shape[2])
+    if start_pos < 0 or start_pos + ap.S > ap.cap:
+        raise ValueError(f"rows {start_pos}..{start_pos + ap.S - 1} do not fit a cache of capacity {ap.cap}")
+    ap.p.start_pos_q = ap.p.start_pos_k = int(start_pos)
+    with _on(k.device):
+        rc = L.pe_attn_cache_append(ap.pref, ap.dkc.bind(k_c), ap.dk.bind(k), ap.dv.bind(v), _ptr(freqs),
+                                    _ptr(delta), k_cache.data_ptr(), v_cache.data_ptr(), ap.cap, _stream(k.device))
     _lib.check(rc)
+
+
+class _DecodePlan:
+    """Per-signature launch state of pe_attention_decode: the parameter block, the descriptors and a
+    workspace sized for the whole cache (the largest any cache length needs), reused by every call
+    on the same stream; a call sets the cache length and the query position and swaps pointers."""
+    __slots__ = ("p", "pref", "dq", "dqc", "dout", "lse", "ws", "nb", "cap", "out_shape", "cdt")
+
+    def __init__(self, p, q, q_c, out, cap, out_shape, cdt, L):
+        self.p = p
+        self.pref = ref(p)
+        self.dq, self.dqc, self.dout = _Desc(q), _Desc(q_c), _Desc(out)
+        self.cap, self.out_shape, self.cdt = cap, out_shape, cdt
+        p.Sk = cap
+        self.nb = L.pe_attn_decode_workspace_bytes(self.pref)
+        self.ws = torch.empty(self.nb, dtype=torch.uint8, device=q.device)
+        self.lse = torch.empty((out_shape[0], out_shape[2], out_shape[1]), dtype=torch.float32, device=q.device)
 
 
 def pe_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_len: int, *,
@@ -551,46 +589,58 @@ def pe_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     rows of caches filled by pe_cache_append (src/model/fpope_attention.py:301-324): bottom-right
     causal mask by default, query phases at start_pos_q (default cache_len - Sq), GQA by index.
     position_dtype as for pe_attention (the cached keys must have been appended with the same).
-    Returns out (B, Hq, Sq, d_v) in the cache dtype [and lse (B, Hq, Sq)]."""
+    Returns out (B, Hq, Sq, d_v) in the cache dtype [and lse (B, Hq, Sq)].  Shapes, strides, dtypes
+    and devices are checked once per operand signature and stream, whose workspace is then reused;
+    cache_len and the query position on every call."""
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, q_c, freqs)):
         raise RuntimeError("the KV-cache path is inference only (run it under torch.no_grad())")
     if not q.is_cuda:
         raise RuntimeError("pe_attention_decode runs on the GPU only (got a CPU tensor)")
     m = _MODES[mode]
-    if q.dim() != 4:
-        raise ValueError(f"q must be (B, Hq, Sq, D), got shape {tuple(q.shape)}")
-    if m != _lib.PE_MODE_NONE:
-        want = q.shape[-1] if m == _lib.PE_MODE_POPE else q.shape[-1] // 2
-        if freqs is None or freqs.dim() != 1 or freqs.shape[0] != want or freqs.device != q.device:
-            raise ValueError(f"freqs must be a ({want},) tensor on {q.device}")
-    if q_c is not None and (q_c.dim() != 4 or tuple(q_c.shape[:3]) != tuple(q.shape[:3]) or q_c.device != q.device):
-        raise ValueError(f"q_c {tuple(q_c.shape)} must share the rows of q {tuple(q.shape)}")
     q, q_c = _prep_in(q), _prep_in(q_c)
-    freqs = freqs.float().contiguous() if m != _lib.PE_MODE_NONE else None
-    B, Hq, Sq, Dr = q.shape
-    Hkv = k_cache.shape[1]
-    Dc = 0 if q_c is None else q_c.shape[-1]
-    dqk = Dc + (2 * Dr if m == _lib.PE_MODE_POPE else Dr)
-    scale = dqk ** -0.5 if scale is None else scale
-    cdt = k_cache.dtype
-    start_q = cache_len - Sq if start_pos_q is None else start_pos_q
-    p = _cache_params(B=B, Hq=Hq, Hkv=Hkv, Sq=Sq, Sk=cache_len, Dc=Dc, Dr=Dr, Dv=d_v, mode=m,
-                      dtype=_dtype_code(cdt), causal=_CAUSAL[causal], start_q=start_q, start_k=0, scale=scale,
-                      mscale=rope_mscale, qk_norm=qk_norm, delta=None,
-                      pos_round=position_rounding(position_dtype, m))
+    freqs = freqs.float().contiguous() if m != _lib.PE_MODE_NONE and freqs is not None else None
+    pos_round = position_rounding(position_dtype, m)
+    dev = q.device
+    stream = _stream(dev)
+    key = ("decode", m, _sig(q), _sig(q_c), _sig(freqs), _sig(k_cache), _sig(v_cache), int(d_v),
+           None if scale is None else float(scale), causal, float(rope_mscale), bool(qk_norm), pos_round, stream)
+    plans = _plans()
+    dp = plans.get(key)
     L = _lib.lib()
-    _lib.check(L.pe_attn_check(ref(p)))
-    _check_cache(k_cache, v_cache, B, Hkv, L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p)), cdt,
-                 q.device)
-    if cache_len > k_cache.shape[2]:
-        raise ValueError(f"cache_len {cache_len} exceeds the cache capacity {k_cache.shape[2]}")
-    out = torch.empty((B, Sq, Hq, d_v), dtype=cdt, device=q.device).transpose(1, 2)
-    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device)
-    nb = L.pe_attn_decode_workspace_bytes(ref(p))
-    ws = torch.empty(nb, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
-        rc = L.pe_attn_decode(ref(p), ref(_tensor(q_c)), ref(_tensor(q)), k_cache.data_ptr(), v_cache.data_ptr(),
-                              k_cache.shape[2], _ptr(freqs), ref(_tensor(out)), lse.data_ptr(), ws.data_ptr(), nb,
-                              _stream(q.device))
+    if dp is None:
+        if q.dim() != 4:
+            raise ValueError(f"q must be (B, Hq, Sq, D), got shape {tuple(q.shape)}")
+        if m != _lib.PE_MODE_NONE:
+            want = q.shape[-1] if m == _lib.PE_MODE_POPE else q.shape[-1] // 2
+            if freqs is None or freqs.dim() != 1 or freqs.shape[0] != want or freqs.device != dev:
+                raise ValueError(f"freqs must be a ({want},) tensor on {dev}")
+        if q_c is not None and (q_c.dim() != 4 or tuple(q_c.shape[:3]) != tuple(q.shape[:3]) or q_c.device != dev):
+            raise ValueError(f"q_c {tuple(q_c.shape)} must share the rows of q {tuple(q.shape)}")
+        B, Hq, Sq, Dr = q.shape
+        Hkv = k_cache.shape[1]
+        Dc = 0 if q_c is None else q_c.shape[-1]
+        dqk = Dc + (2 * Dr if m == _lib.PE_MODE_POPE else Dr)
+        sc = dqk ** -0.5 if scale is None else scale
+        cdt = k_cache.dtype
+        p = _cache_params(B=B, Hq=Hq, Hkv=Hkv, Sq=Sq, Sk=max(Sq, 1), Dc=Dc, Dr=Dr, Dv=d_v, mode=m,
+                          dtype=_dtype_code(cdt), causal=_CAUSAL[causal], start_q=0, start_k=0, scale=sc,
+                          mscale=rope_mscale, qk_norm=qk_norm, delta=None, pos_round=pos_round)
+        _lib.check(L.pe_attn_check(ref(p)))
+        _check_cache(k_cache, v_cache, B, Hkv, L.pe_attn_operand_width(ref(p)), L.pe_attn_value_width(ref(p)), cdt,
+                     dev)
+        out_shape = (B, Sq, Hq, d_v)
+        probe = torch.empty(out_shape, dtype=cdt, device=dev).transpose(1, 2)
+        dp = plans[key] = _DecodePlan(p, q, q_c, probe, k_cache.shape[2], out_shape, cdt, L)
+    Sq = dp.out_shape[1]
+    if cache_len > dp.cap:
+        raise ValueError(f"cache_len {cache_len} exceeds the cache capacity {dp.cap}")
+    dp.p.Sk = int(cache_len)
+    dp.p.start_pos_q = int(cache_len - Sq if start_pos_q is None else start_pos_q)
+    out = torch.empty(dp.out_shape, dtype=dp.cdt, device=dev).transpose(1, 2)
+    lse = torch.empty_like(dp.lse) if return_lse else dp.lse
+    with _on(dev):
+        rc = L.pe_attn_decode(dp.pref, dp.dqc.bind(q_c), dp.dq.bind(q), k_cache.data_ptr(), v_cache.data_ptr(),
+                              dp.cap, _ptr(freqs), dp.dout.bind(out), lse.data_ptr(), dp.ws.data_ptr(), dp.nb,
+                              stream)
     _lib.check(rc)
     return (out, lse) if return_lse else out
