@@ -4,9 +4,10 @@
 //
 // Decode is bound by reading the cache, not by the matrix cores, so the work is split over the
 // keys: a (batch, kv head, 32-row query tile) is cut into `nunit` key ranges of 32-key blocks, one
-// per wave.  Each wave keeps the tile's q~ rows in registers as the MFMA B operand, reads its k~
-// rows straight from HBM as A operands (16 contiguous bytes per lane and k-step), stages each
-// 32-key v block in its own LDS slot for the transpose read, and keeps an online softmax.  Its
+// per wave.  The tile's q~ rows (the MFMA B operand) sit in LDS, shared by the workgroup's 4 waves.
+// A wave reads its k~ rows straight from HBM as A operands (16 contiguous bytes per lane and
+// k-step), stages each 32-key v block in one of its two LDS slots for the transpose read, loads the
+// next block while it computes the current one, and keeps an online softmax.  Its
 // unnormalised O^T, running max and row sum go to a partials buffer; a second kernel merges the
 // ranges of every row in a fixed order (no atomics, bitwise reproducible).
 //
@@ -25,10 +26,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == 0 ? 2
   constexpr int KC = M::KC, EPL = M::EPL, ESZ = M::ESZ;
   constexpr int NQF = DQK / KC, NCV = DV * ESZ / 16, NOT = DV / 32, NPF = 32 / KC;
   constexpr int SV = 32 * NCV * 16;  // one 32-key v block
-  __shared__ __attribute__((aligned(1024))) char smem[4 * SV];
+  constexpr int NV = 32 * NCV / 64;  // DMA instructions per v block
+  constexpr int NCQ = 2 * NQF;       // 16-byte chunks per q~ row (fragment kk of lane half g is chunk 2 kk + g)
+  constexpr int QROW = NCQ * 16;
+  // [4 waves][2 slots] v blocks, then the tile's 32 q~ rows (shared by the 4 waves)
+  __shared__ __attribute__((aligned(1024))) char smem[8 * SV + 32 * QROW];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
-  char* vt = smem + w * SV;
+  char* const vslot[2] = {smem + (2 * w) * SV, smem + (2 * w + 1) * SV};  // this wave's two v slots
   const int ubs = a.nunit / 4;
   int bid = blockIdx.x;
   const int ub = bid % ubs;
@@ -41,12 +46,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == 0 ? 2
   const int rr = r < nrows ? r : nrows - 1;
   const int h = hk * grp + rr / a.Sq, qi = rr % a.Sq;
 
-  u32x4 qf[NQF];
-  {
-    const E* qrow = (const E*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + qi) * DQK;
-#pragma unroll
-    for (int kk = 0; kk < NQF; ++kk) qf[kk] = *(const u32x4*)(qrow + kk * KC + g * EPL);
-  }
   // this wave's 32-key blocks [kb0, kb1); keys past the tile's last visible key are skipped
   const int nkb = (a.L + 31) / 32;
   const int kb0 = (int)((int64_t)u * nkb / a.nunit), kb1 = (int)((int64_t)(u + 1) * nkb / a.nunit);
@@ -70,18 +69,69 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == 0 ? 2
   float m = -1e30f, l = 0.f;
   const float sl2 = a.scale * LOG2E;
 
-  for (int kb = kb0; kb < kend; ++kb) {
-    const int k0 = kb * 32;
-    // v rows k0 .. k0+31 into this wave's slot (rows at or past L re-read row L - 1)
-    dma_tile<32, NCV, 1>(vt, vbase + (int64_t)k0 * DV * ESZ, (int64_t)DV * ESZ, a.L - k0, 0, lane);
-    // S^T = k~ q~^T: A row of lane (l32, g) is key k0 + perm_row(l32), clamped into the cache
-    const int ka = min(k0 + perm_row<DT>(l32), a.L - 1);
-    const E* krow = kbase + (int64_t)ka * DQK;
+  // The next block's loads are in flight while a block is computed.  The k~ rows go straight to
+  // registers as A operands (lane (l32, g) takes key k0 + perm_row(l32), clamped into the cache), and
+  // each fragment is refilled with the next block's row right after its score product.  The v rows go
+  // by DMA into the wave's other LDS slot (rows at or past L re-read row L - 1).  Issue order per
+  // block: the refill loads, then the next v block; the wait before the PV products leaves exactly
+  // those outstanding.  The compiler does not see the DMA, so its waits for a refilled fragment in the
+  // next block may also drain that block's own v loads (issued after the refills), which its PV
+  // products need anyway, but never loads of a later block.
+  auto krow_of = [&](int kb) {
+    return kbase + (int64_t)min(kb * 32 + perm_row<DT>(l32), a.L - 1) * DQK;
+  };
+  auto issue_v = [&](int kb, char* slot) {
+    dma_tile<32, NCV, 1>(slot, vbase + (int64_t)kb * 32 * DV * ESZ, (int64_t)DV * ESZ, a.L - kb * 32, 0, lane);
+  };
+  u32x4 kf[NQF];
+  if (kb0 < kend) {
+    const E* krow = krow_of(kb0);
+#pragma unroll
+    for (int kk = 0; kk < NQF; ++kk) kf[kk] = *(const u32x4*)(krow + kk * KC + g * EPL);
+    issue_v(kb0, vslot[0]);
+  }
+  // The 4 waves of a workgroup share the tile's query rows, so wave 0 stages them in LDS once (while
+  // the first block's loads are in flight) and every wave reads its B fragments from there per block
+  // (64 registers fewer than holding them).  Chunk c of row x is stored at chunk c ^ (x % NCQ), so
+  // the 32 rows of one fragment read spread over the banks.  The barrier waits only for the LDS
+  // writes: __syncthreads() would also drain the block loads in flight.
+  char* const qlds = smem + 8 * SV;
+  const uint32_t qrd = (uint32_t)l32 * QROW;
+  const uint32_t qsw = (uint32_t)(l32 & (NCQ - 1));
+  if (w == 0) {
+    const E* qrow = (const E*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + qi) * DQK;
+    u32x4 qv[NQF];
+#pragma unroll
+    for (int kk = 0; kk < NQF; ++kk) qv[kk] = *(const u32x4*)(qrow + kk * KC + g * EPL);
+#pragma unroll
+    for (int kk = 0; kk < NQF; ++kk) *(u32x4*)(qlds + qrd + (((uint32_t)(2 * kk + g) ^ qsw) << 4)) = qv[kk];
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  auto qfrag = [&](int kk) { return *(const u32x4*)(qlds + qrd + (((uint32_t)(2 * kk + g) ^ qsw) << 4)); };
+  constexpr int FD = 3;  // q~ fragments read ahead of their product
+  auto block = [&](const int kb, auto next_tag) {
+    constexpr bool NEXT = decltype(next_tag)::value;
+    const int k0 = kb * 32, sl = (kb - kb0) & 1;
+    const E* krn = krow_of(kb + 1);
     f32x16 s;
 #pragma unroll
     for (int j = 0; j < 16; ++j) s[j] = 0.f;
+    // q~ fragments read FD products ahead; the fences (mask 0x406: vector, scalar and transcendental
+    // work may cross) keep the LDS reads, the refill loads and the products in program order, so the
+    // compiler neither hoists every read nor issues the refills early, which would need registers
+    u32x4 qr[FD];
 #pragma unroll
-    for (int kk = 0; kk < NQF; ++kk) s = M::mma(*(const u32x4*)(krow + kk * KC + g * EPL), qf[kk], s);
+    for (int i = 0; i < FD; ++i) qr[i] = qfrag(i);
+#pragma unroll
+    for (int kk = 0; kk < NQF; ++kk) {
+      __builtin_amdgcn_sched_barrier(0x406);
+      const u32x4 cur = qr[kk % FD];
+      if (kk + FD < NQF) qr[kk % FD] = qfrag(kk + FD);
+      __builtin_amdgcn_sched_barrier(0x406);
+      s = M::mma(kf[kk], cur, s);
+      if constexpr (NEXT) kf[kk] = *(const u32x4*)(krn + kk * KC + g * EPL);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float mx = m;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -109,12 +159,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == 0 ? 2
     u32x4 pf[NPF];
 #pragma unroll
     for (int ks = 0; ks < NPF; ++ks) pf[ks] = M::pack(s, ks * EPL);
-    wait_vmcnt<0>();  // the v block has landed (each wave reads only its own slot)
+    // the slot of block kb + 1 held block kb - 1, whose PV products have read it
+    if constexpr (NEXT) {
+      issue_v(kb + 1, vslot[sl ^ 1]);
+      wait_vmcnt<NQF + NV>();  // v block kb has landed; the refills and v block kb + 1 may not have
+    } else {
+      wait_vmcnt<0>();
+    }
+    const char* vt = vslot[sl];
 #pragma unroll
     for (int t = 0; t < NOT; ++t)
 #pragma unroll
       for (int ks = 0; ks < NPF; ++ks) o[t] = M::mma(lds_col_frag<DT, NCV>(vt, ks * KC, t * 32, lane), pf[ks], o[t]);
-  }
+  };
+  int kb = kb0;
+  for (; kb + 1 < kend; ++kb) block(kb, std::true_type{});
+  if (kb < kend) block(kb, std::false_type{});
 
   // partials of this wave's range: [bh][qt][u] blocks of 32 rows (rows past the tile's query rows
   // are neither written nor read)
