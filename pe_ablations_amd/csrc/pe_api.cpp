@@ -571,9 +571,18 @@ int pe_attn_decode(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tens
   const int dqk = pad_qk(qk_width(p)), dv = pad_v(p->Dv);
   pe::PrepArgs a;
   fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws, dqk);
-  if ((rc = pe::launch_prep(a, s))) return rc;
+  // a tile of few query rows (one decoded token of a small GQA group) is transformed inside the
+  // split kernel, with the prologue's arithmetic, instead of in a launch of its own
+  const bool fuse_q = p->dtype == PE_DTYPE_BF16 && (int64_t)(p->Hq / p->Hkv) * p->Sq <= pe::DECODE_FUSED_ROWS &&
+                      pe::prep_vec_query_ok(a);
+  if (!fuse_q && (rc = pe::launch_prep(a, s))) return rc;
   pe::DecodeArgs da;
   memset(&da, 0, sizeof(da));
+  if (fuse_q) {
+    da.qraw = qr->data;
+    for (int i = 0; i < 4; ++i) da.qr_s[i] = qr->stride[i];
+    da.freqs = freqs; da.Dr = p->Dr; da.start_pos = p->start_pos_q; da.pos_round = p->position_rounding;
+  }
   da.q = ws; da.k = k_cache; da.v = v_cache;
   da.B = p->B; da.Hq = p->Hq; da.Hkv = p->Hkv; da.Sq = p->Sq; da.L = p->Sk; da.cap = capacity;
   da.causal = p->causal != PE_CAUSAL_NONE;

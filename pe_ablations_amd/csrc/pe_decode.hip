@@ -98,7 +98,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == 0 ? 2
   char* const qlds = smem + 8 * SV;
   const uint32_t qrd = (uint32_t)l32 * QROW;
   const uint32_t qsw = (uint32_t)(l32 & (NCQ - 1));
-  if (w == 0) {
+  bool staged = false;
+  if constexpr (DT == 0) {
+    if (a.qraw) {
+      // the raw rows transformed here, element by element with the vectorised prologue's arithmetic
+      // (softplus magnitude times cos / sin of fl(pos * freq), rounded to bf16), so the operand
+      // rows are bitwise those the prologue would write; tile rows past the query rows are zero
+      // (their columns are never stored).  Element (x, d) of the tile goes to column d (cos) and
+      // Dr + d (sin) of row x, chunk-swizzled as above.
+      const int tid = threadIdx.x, Dr = a.Dr;
+      const int nreal = min(32, nrows - qt * 32);
+      for (int i = tid; i < (32 - nreal) * NCQ; i += 256) {
+        const int x = nreal + i / NCQ, c = i % NCQ;
+        *(u32x4*)(qlds + x * QROW + ((c ^ (x & (NCQ - 1))) << 4)) = u32x4{0u, 0u, 0u, 0u};
+      }
+      for (int i = tid; i < nreal * Dr; i += 256) {
+        const int x = i / Dr, d = i % Dr;
+        const int rq = qt * 32 + x, hq = hk * grp + rq / a.Sq, iq = rq % a.Sq;
+        const uint16_t raw = ((const uint16_t*)a.qraw)[b * a.qr_s[0] + hq * a.qr_s[1] + (int64_t)iq * a.qr_s[2] + d];
+        const float mu = softplus_f(__builtin_bit_cast(float, (uint32_t)raw << 16));
+        float sn, cs;
+        pe_sincos(mul_nc(pe_pos(a.start_pos + iq, a.pos_round), a.freqs[d]), sn, cs);
+        const uint32_t pr = pack_bf2(mul_nc(mu, cs), mul_nc(mu, sn));
+        const int cc = d, cs_ = Dr + d;
+        *(uint16_t*)(qlds + x * QROW + ((((uint32_t)cc >> 3) ^ (uint32_t)(x & (NCQ - 1))) << 4) + (cc & 7) * 2) = (uint16_t)pr;
+        *(uint16_t*)(qlds + x * QROW + ((((uint32_t)cs_ >> 3) ^ (uint32_t)(x & (NCQ - 1))) << 4) + (cs_ & 7) * 2) =
+            (uint16_t)(pr >> 16);
+      }
+      staged = true;
+    }
+  }
+  if (!staged && w == 0) {
     const E* qrow = (const E*)a.q + ((int64_t)(b * a.Hq + h) * a.Sq + qi) * DQK;
     u32x4 qv[NQF];
 #pragma unroll

@@ -112,6 +112,9 @@ int launch_prep(const PrepArgs& a, hipStream_t s);
 // whether launch_prep takes the vectorised PoPE path for `a` and can copy the rows described by
 // its cv / cdst fields in the same launch
 bool prep_vec_copy_ok(const PrepArgs& a);
+// whether `a` (query side) takes the vectorised PoPE path with no content part and no padding, the
+// case whose per-element arithmetic the decode split kernel repeats for its own query rows
+bool prep_vec_query_ok(const PrepArgs& a);
 // cos / sin of the query phases fl(pe_pos(start + s) * freqs[c]) for s < S, c < Dr into tab
 // [S][2][Dr] (cos row then sin row), with the same routine and rounding as the prologue kernels
 int launch_phase_table(const float* freqs, int start, int S, int Dr, int pos_round, float* tab, hipStream_t s);
@@ -135,8 +138,14 @@ struct DecodeArgs {
   float* part_l;    // [B*Hkv][nqt][nunit][32] sum of 2^(score - part_m)
   void* o; int64_t o_sb, o_sh, o_ss; int o_dtype; int dv_real;
   float* lse;       // (B, Hq, Sq)
+  // raw bf16 query rows (B, Hq, Sq, Dr) that the split kernel transforms itself (PoPE, no content
+  // part, 2 Dr = the operand width, at most 8 rows per tile), with phases
+  // fl(pe_pos(start_pos + i) * freqs[d]); null: q holds the rows the prologue transformed
+  const void* qraw; int64_t qr_s[4]; const float* freqs; int Dr, start_pos, pos_round;
 };
 int launch_decode(int dt, int dqk, int dv, const DecodeArgs& a, hipStream_t s);
+// most query rows per tile that the decode split kernel transforms itself
+constexpr int DECODE_FUSED_ROWS = 8;
 
 // Stand-alone RMSNorm over the last dim of a (rows, n) view.
 struct NormArgs {

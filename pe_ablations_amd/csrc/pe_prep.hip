@@ -413,6 +413,10 @@ bool prep_vec_copy_ok(const PrepArgs& a) {
          ((uintptr_t)a.cdst % 16) == 0 && a.cv_cols % 8 == 0 && a.cwidth % 8 == 0 && a.cv_cols <= a.cwidth;
 }
 
+bool prep_vec_query_ok(const PrepArgs& a) {
+  return prep_vec_ok(a) && !a.is_key && a.Dc == 0 && a.width == 2 * a.Dr;
+}
+
 int launch_prep(const PrepArgs& a, hipStream_t s) {
   const int64_t nrows = (int64_t)a.B * a.H * a.S;
   const bool vec = prep_vec_ok(a);

@@ -131,6 +131,29 @@ def test_decode_bitwise_reproducible_and_nonfull_rows(cuda):
 
 
 @torch.no_grad()
+def test_decode_in_kernel_query_transform_matches_prologue(cuda):
+    """A tile of at most 8 query rows (here GQA 2 x 1 token) has its PoPE transform done inside the
+    split kernel; 2 x 5 rows go through the prologue launch.  With no mask and the same query
+    positions, the first token's output and lse agree bit for bit between the two paths, and both
+    match the oracle."""
+    B, Hq, Hkv, L, D = 2, 4, 2, 777, 64
+    k, v = rnd(B, Hkv, L, D, seed=21).bfloat16(), rnd(B, Hkv, L, D, seed=22).bfloat16()
+    q5 = rnd(B, Hq, 5, D, seed=23).bfloat16()
+    freqs = O.pope_freqs(D)
+    delta = -torch.rand(Hkv, D, generator=torch.Generator().manual_seed(24)) * 6
+    kc, vc = fill_cache(cuda, k, v, freqs, delta, 800, torch.bfloat16, [L])
+    kw = dict(d_v=D, freqs=freqs.to(cuda), scale=0.125, causal="none", start_pos_q=L - 5, return_lse=True)
+    o5, l5 = pe_attention_decode(q5.to(cuda), kc, vc, L, **kw)
+    o1, l1 = pe_attention_decode(q5[:, :, :1].contiguous().to(cuda), kc, vc, L, **kw)
+    assert torch.equal(o1, o5[:, :, :1]) and torch.equal(l1, l5[:, :, :1])
+    for b, h in ((0, 0), (1, 3)):
+        ref = O.pope_attention_chunked(q5[b, h, :1].float(), k[b, h // 2].float(), v[b, h // 2].float(), freqs,
+                                       delta[h // 2], scale=0.125, start_q=L - 5, causal=False,
+                                       operand_dtype=torch.bfloat16, chunk=1024)
+        assert err(o1[b, h], ref["out"]) < 2e-2 and err(l1[b, h], ref["lse"]) < 2e-3, (b, h)
+
+
+@torch.no_grad()
 def test_decode_argument_errors(cuda):
     B, H, D = 1, 2, 64
     freqs = O.pope_freqs(D).to(cuda)
