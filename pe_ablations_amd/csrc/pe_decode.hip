@@ -235,12 +235,14 @@ __global__ __launch_bounds__(1024) void decode_merge_kernel(DecodeArgs a) {
   __shared__ float red[G][DV];
   __shared__ float wred[2][NWV];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t rowid = blockIdx.x;  // (bh, qt, row)
-  const int row = (int)(rowid % 32);
-  const int64_t tile = rowid / 32;
+  // (bh, qt, row) over the rpt = min(32, query rows) rows a tile can hold: a tile of a few decoded
+  // rows launches only those
+  const int grp = a.Hq / a.Hkv, nrows = grp * a.Sq, rpt = min(32, nrows);
+  const int64_t rowid = blockIdx.x;
+  const int row = (int)(rowid % rpt);
+  const int64_t tile = rowid / rpt;
   const int qt = (int)(tile % a.nqt);
   const int bh = (int)(tile / a.nqt);
-  const int grp = a.Hq / a.Hkv, nrows = grp * a.Sq;
   const int r = qt * 32 + row;
   if (r >= nrows) return;  // uniform over the workgroup
   const int b = bh / a.Hkv, hk = bh % a.Hkv;
@@ -298,7 +300,7 @@ template <int DT, int DQK, int DV>
 static int run_decode(const DecodeArgs& a, hipStream_t s) {
   const int64_t blocks = (int64_t)a.B * a.Hkv * a.nqt * (a.nunit / 4);
   hipLaunchKernelGGL((decode_split_kernel<DT, DQK, DV>), dim3((unsigned)blocks), dim3(256), 0, s, a);
-  const int64_t rows = (int64_t)a.B * a.Hkv * a.nqt * 32;
+  const int64_t rows = (int64_t)a.B * a.Hkv * a.nqt * std::min(32, (a.Hq / a.Hkv) * a.Sq);
   hipLaunchKernelGGL((decode_merge_kernel<DV>), dim3((unsigned)rows), dim3(1024), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
