@@ -484,8 +484,12 @@ def decoder_cpu_baseline(torch, model, ids, tokens: int):
 
 def run_decoder(args, torch, dev) -> dict:
     from pe_ablations_amd import _lib
+    from pe_ablations_amd.gemm_select import use_tuned_gemms
     from pe_ablations_amd.transformer import Transformer
 
+    # the projection GEMMs take the committed hipBLASLt selections (torch TunableOp, tuning off)
+    gemm_selection = use_tuned_gemms()
+    log(f"bench: decoder GEMMs: {gemm_selection}")
     cfg = _decoder_config(torch)
     S = DECODER["S"]
     torch.manual_seed(0)
@@ -534,7 +538,7 @@ def run_decoder(args, torch, dev) -> dict:
         "config": {"workload": "decoder forward with next-token CE loss", "layers": DECODER["num_layers"],
                    "d_model": DECODER["hidden_dim"], "heads": H, "head_dim": D, "ffn": DECODER["ffn_dim"],
                    "vocab": DECODER["vocab_size"], "tokens": S, "attention": "fused PoPE (all head dims)",
-                   "params": nparam, "parallelism": "single GPU"},
+                   "params": nparam, "parallelism": "single GPU", "gemm_selection": gemm_selection},
         "loss": round(loss, 4),
         "expected_loss_at_init": round(expected, 4),
         "model_tflops": round(Fd["total"] / (ms * 1e-3) / 1e12, 2),
