@@ -222,6 +222,13 @@ int pe_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t x_row_stride, int64_t
                    const void* weight, int32_t weight_dtype, float eps,
                    void* y, int32_t y_dtype, int64_t y_row_stride, void* stream);
 
+/* SwiGLU forward of the feed-forward block (src/model/ffn.py:17-27, SwiGLU.forward(x, gate) =
+ * F.silu(gate) * x): out = bf16(bf16(gate / (1 + exp(-gate))) * x) element by element over n
+ * contiguous bf16 values, bitwise what torch computes for the two bf16 ops.  n % 8 == 0, 16-byte
+ * aligned pointers (out may alias x or gate).  Forward only: the module calls it when no gradient
+ * is needed. */
+int pe_swiglu_fwd(const void* x, const void* gate, void* out, int64_t n, void* stream);
+
 /* Elementwise positional prologue on its own (the HBM-bound half of the forward): writes the
  * transformed rows [content | transform | zero pad] of x into dst (B,H,S,width) contiguous in
  * p->dtype, width = pe_attn_operand_width(p).  is_key selects the key phase bias.  Replaces

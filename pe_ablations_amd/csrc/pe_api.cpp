@@ -621,6 +621,15 @@ int pe_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t x_row_stride, int64_t
   return pe::launch_rmsnorm(a, (hipStream_t)stream);
 }
 
+int pe_swiglu_fwd(const void* x, const void* gate, void* out, int64_t n, void* stream) {
+  if (!x || !gate || !out) return PE_ERR_NULL;
+  if (n < 0 || n % 8 != 0) return PE_ERR_SHAPE;
+  if (((uintptr_t)x | (uintptr_t)gate | (uintptr_t)out) % 16) return PE_ERR_STRIDE;
+  const int rc = device_ok();
+  if (rc) return rc;
+  return pe::launch_swiglu(x, gate, out, n, (hipStream_t)stream);
+}
+
 int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
                 const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
                 const float* freqs, const float* delta, const pe_tensor_t* out, const float* lse,

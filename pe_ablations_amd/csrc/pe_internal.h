@@ -155,6 +155,8 @@ struct NormArgs {
   int64_t rows; int n; float eps;
 };
 int launch_rmsnorm(const NormArgs& a, hipStream_t s);
+// silu(gate) * x over n bf16 elements (n % 8 == 0, 16-byte aligned pointers)
+int launch_swiglu(const void* x, const void* gate, void* out, int64_t n, hipStream_t s);
 
 // dO repack (to compute dtype, width DV, contiguous), Di = rowsum(dO * O) and the log2-scaled
 // lse, both into (B, H, S_pad) arrays whose padding rows hold Di = 0, L2 = +inf.

@@ -194,6 +194,34 @@ int launch_rmsnorm(const NormArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
+// SwiGLU of the feed-forward block, silu(gate) * x over bf16 (src/model/ffn.py:17-27), as torch
+// evaluates F.silu(gate) * x: the silu in fp32 as g / (1 + exp(-g)) rounded to bf16, then the
+// product in fp32 rounded to bf16, so the result is bitwise torch's; one pass over the two inputs
+// instead of two kernels and an intermediate tensor.  Eight elements per thread.
+__global__ __launch_bounds__(256) void swiglu_kernel(const u32x4* __restrict__ x, const u32x4* __restrict__ gate,
+                                                     u32x4* __restrict__ out, int64_t n8) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  float xf[8], gf[8];
+  unpack8(x[i], xf);
+  unpack8(gate[i], gf);
+  float r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = round_bf16(gf[e] / (1.f + expf(-gf[e]))) * xf[e];
+  out[i] = u32x4{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+}
+
+int launch_swiglu(const void* x, const void* gate, void* out, int64_t n, hipStream_t s) {
+  if (n < 0 || n % 8 != 0) return -2;
+  if (((uintptr_t)x | (uintptr_t)gate | (uintptr_t)out) % 16) return -5;
+  const int64_t n8 = n / 8;
+  if (n8 == 0) return 0;
+  if ((n8 + 255) / 256 > 0x7fffffff) return -2;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const u32x4*)x,
+                     (const u32x4*)gate, (u32x4*)out, n8);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
 int launch_prep_norm(const PrepArgs& a, hipStream_t s) {
   if (a.mode != 0 || !a.norm_w || ((a.norm_w_dtype | a.xr_dtype | a.dst_dtype) & ~1)) return -4;
   if (a.dst_rows != 0 || a.dst_row0 != 0) return -2;  // writes contiguous (B, H, S, width) rows only

@@ -2,7 +2,9 @@
 
 Same parameter names (w1, w2, w3) and the same gating as the reference: the activation is called
 as ``activation(w1(x), w3(x))`` and returns ``silu(gate) * x``, so w3 is the gate
-(src/model/ffn.py:17-27,53-68).  The projections are plain hipBLASLt GEMMs through torch.
+(src/model/ffn.py:17-27,53-68).  The projections are plain hipBLASLt GEMMs through torch.  When no
+gradient is needed, bf16 SwiGLU on the GPU runs the library's one-pass kernel (pe_swiglu_fwd),
+bitwise equal to torch's two ops; in training it is the reference's torch expression.
 """
 
 from __future__ import annotations
@@ -13,11 +15,16 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .functional import swiglu as _hip_swiglu
+
 
 class SwiGLU(nn.Module):
     """silu(gate) * x (src/model/ffn.py:8-27)."""
 
     def forward(self, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        if (x.is_cuda and not torch.is_grad_enabled() and x.dtype == torch.bfloat16
+                and gate.dtype == torch.bfloat16 and x.shape == gate.shape):
+            return _hip_swiglu(x, gate)
         return F.silu(gate) * x
 
 

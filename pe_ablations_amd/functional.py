@@ -461,6 +461,27 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
     return y.view(*x.shape[:-1], n)
 
 
+def swiglu(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """F.silu(gate) * x over bf16 through pe_swiglu_fwd (src/model/ffn.py:17-27), bitwise torch's
+    result for the two bf16 ops, in one pass.  Both tensors bf16, same shape, on the GPU.  No
+    autograd: the module uses it when no gradient is needed."""
+    if not (x.is_cuda and gate.is_cuda):
+        raise RuntimeError("swiglu runs on the GPU only")
+    if x.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16 or x.shape != gate.shape:
+        raise TypeError("swiglu takes two bf16 tensors of one shape")
+    if x.device != gate.device:
+        raise ValueError("swiglu: x and gate are on different devices")
+    xc, gc = x.contiguous(), gate.contiguous()
+    out = torch.empty_like(xc)
+    n = xc.numel()
+    if n % 8 or xc.data_ptr() % 16 or gc.data_ptr() % 16:
+        return torch.nn.functional.silu(gate) * x
+    if n:
+        with torch.cuda.device(x.device):
+            _lib.check(_lib.lib().pe_swiglu_fwd(xc.data_ptr(), gc.data_ptr(), out.data_ptr(), n, _stream(x.device)))
+    return out
+
+
 # ------------------------------------------------------------------------------------------------
 # KV cache (src/model/fpope_attention.py:226-327): caches of transformed keys and values, and the
 # split-key decode attention over them.  Inference only.

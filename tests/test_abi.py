@@ -18,7 +18,7 @@ HEADER = os.path.join(ROOT, "include", "pe_attn.h")
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(pe_(?:attn|rmsnorm)_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(pe_(?:attn|rmsnorm|swiglu)_\w+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
