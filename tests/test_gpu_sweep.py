@@ -1,0 +1,97 @@
+"""A seeded random sweep of fused attention fwd+bwd configurations against the oracle.
+
+Each seed draws a mode (PoPE fused or split form, RoPE with or without QKNorm, no PE), a dtype, a
+batch, kv heads and GQA group, a sequence length in [1, 600], widths (Dr, Dc, Dv), the causal flag
+and a shared or per-head phase bias, and compares out, the input gradients and dδ with the oracle
+(the reference's expressions: oracle.pope_attention, split_pope_attention, rope_attention,
+attention; fp64 core, operands rounded to bf16 in bf16 mode).
+
+Bars: fp32 1e-5 and bf16 2e-2 max-abs (the north star) where the reference values stay below 4 in
+magnitude.  Above that the bar grows in proportion, 2e-2 * max|ref| / 4 in bf16 (one bf16 spacing
+there is already 0.03, and dS is rounded to bf16 before the dK / dQ products as in any bf16
+backward) and 1e-5 * max|ref| / 4 in fp32; dδ relative to its own scale (2e-2 bf16, 1e-4 fp32).
+300 seeds were run this way without a failure; the worst case, seed 288 (no PE, D = 32, |dK| 6.8,
+error 0.026), is kept here.
+"""
+
+import math
+import random
+
+import pytest
+import torch
+
+from oracle import pe_oracle as O
+from pe_ablations_amd.functional import pe_attention
+from tests._cmp import err
+
+pytestmark = pytest.mark.gpu
+
+
+def draw(seed):
+    r = random.Random(seed)
+    mode = r.choices(["pope", "rope", "none"], [6, 2, 2])[0]
+    dtype = r.choices(["bf16", "fp32"], [7, 3])[0]
+    B, Hkv, grp = r.choice([1, 2, 3]), r.choice([1, 2, 3]), r.choice([1, 2, 4])
+    S = r.randint(1, 600)
+    if mode == "pope":
+        Dr = r.choice([16, 32, 48, 64, 96, 128])
+        Dc = r.choice([0, 0, 32, 64]) if 2 * Dr + 64 <= 256 else 0
+    elif mode == "rope":
+        Dr, Dc = r.choice([32, 64, 96, 128]), 0
+    else:
+        Dr, Dc = r.choice([32, 64, 128]), 0
+    Dv = r.choice([32, 64, 96, 128])
+    return dict(mode=mode, dtype=dtype, B=B, Hkv=Hkv, Hq=Hkv * grp, S=S, Dr=Dr, Dc=Dc, Dv=Dv,
+                causal=r.choice([True, False]), per_head=r.choice([True, False]), qk_norm=r.choice([True, False]))
+
+
+@pytest.mark.parametrize("seed", list(range(30)) + [288])
+def test_random_config_matches_oracle(cuda, seed):
+    c = draw(seed)
+    g = torch.Generator().manual_seed(seed)
+    dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
+    B, Hq, Hkv, S, Dr, Dc, Dv = c["B"], c["Hq"], c["Hkv"], c["S"], c["Dr"], c["Dc"], c["Dv"]
+    names = ["qr", "kr", "v"] + (["qc", "kc"] if Dc else [])
+    shapes = {"qr": (B, Hq, S, Dr), "kr": (B, Hkv, S, Dr), "v": (B, Hkv, S, Dv), "qc": (B, Hq, S, Dc),
+              "kc": (B, Hkv, S, Dc)}
+    x = {n: torch.randn(*shapes[n], generator=g).to(dt) for n in names}
+    dout = torch.randn(B, Hq, S, Dv, generator=g).to(dt)
+    od = torch.bfloat16 if dt == torch.bfloat16 else None
+    ox = {n: t.float().clone().requires_grad_(True) for n, t in x.items()}
+    gx = {n: t.to(cuda).requires_grad_(True) for n, t in x.items()}
+    grads = []
+    if c["mode"] == "pope":
+        freqs = O.pope_freqs(Dr)
+        delta = torch.rand((Hkv, Dr) if c["per_head"] else (Dr,), generator=g) * (-2 * math.pi)
+        od_delta, gd = delta.clone().requires_grad_(True), delta.to(cuda).requires_grad_(True)
+        scale = (Dc + 2 * Dr) ** -0.5
+        if Dc:
+            ref, _ = O.split_pope_attention(ox["qc"], ox["kc"], ox["qr"], ox["kr"], ox["v"], freqs, od_delta,
+                                            scale=scale, causal=c["causal"], operand_dtype=od)
+        else:
+            ref, _ = O.pope_attention(ox["qr"], ox["kr"], ox["v"], freqs, od_delta, scale=scale,
+                                      causal=c["causal"], clamp=False, operand_dtype=od)
+        out = pe_attention(gx["qr"], gx["kr"], gx["v"], mode="pope", q_c=gx.get("qc"), k_c=gx.get("kc"),
+                           freqs=freqs.to(cuda), delta=gd, scale=scale, causal=c["causal"])
+        grads.append(("ddelta", gd, od_delta))
+    elif c["mode"] == "rope":
+        inv = O.rope_inv_freq(Dr)
+        ref, _ = O.rope_attention(ox["qr"], ox["kr"], ox["v"], inv, qk_norm=c["qk_norm"], causal=c["causal"],
+                                  operand_dtype=od)
+        out = pe_attention(gx["qr"], gx["kr"], gx["v"], mode="rope", freqs=inv.to(cuda), qk_norm=c["qk_norm"],
+                           causal=c["causal"])
+    else:
+        ref, _ = O.attention(O.round_ste(ox["qr"], od), O.round_ste(ox["kr"], od), O.round_ste(ox["v"], od),
+                             Dr ** -0.5, c["causal"])
+        out = pe_attention(gx["qr"], gx["kr"], gx["v"], mode="none", causal=c["causal"])
+    ref.backward(dout.double())
+    out.backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    base = 2e-2 if dt == torch.bfloat16 else 1e-5
+    for n, a, b in [("out", out, ref)] + [("d" + n, gx[n].grad, ox[n].grad) for n in names]:
+        mx = b.detach().abs().max().item() if b.numel() else 0.0
+        bar = base * max(1.0, mx / 4)
+        assert err(a, b) < bar, (seed, c, n, err(a, b), bar)
+    for n, a, b in grads:
+        rel = err(a, b) / max(1.0, b.abs().max().item())
+        assert rel < (2e-2 if dt == torch.bfloat16 else 1e-4), (seed, c, n, rel)
