@@ -11,7 +11,8 @@ magnitude.  Above that the bar grows in proportion, 2e-2 * max|ref| / 4 in bf16 
 there is already 0.03, and dS is rounded to bf16 before the dK / dQ products as in any bf16
 backward) and 1e-5 * max|ref| / 4 in fp32; dδ relative to its own scale (2e-2 bf16, 1e-4 fp32).
 300 seeds were run this way without a failure; the worst case, seed 288 (no PE, D = 32, |dK| 6.8,
-error 0.026), is kept here.
+error 0.026), is kept here.  Long configurations (lengths 1024-6000) passed for 24 seeds; four are
+kept.
 """
 
 import math
@@ -27,12 +28,16 @@ from tests._cmp import err
 pytestmark = pytest.mark.gpu
 
 
-def draw(seed):
+def draw(seed, long=False):
+    """A configuration; ``long`` draws lengths in [1024, 6000] (where the forward takes 96-key tiles
+    from 2048 on) with at most 4 heads, so the dense fp64 oracle stays small."""
     r = random.Random(seed)
     mode = r.choices(["pope", "rope", "none"], [6, 2, 2])[0]
     dtype = r.choices(["bf16", "fp32"], [7, 3])[0]
     B, Hkv, grp = r.choice([1, 2, 3]), r.choice([1, 2, 3]), r.choice([1, 2, 4])
-    S = r.randint(1, 600)
+    S = r.randint(1, 600) if not long else r.randint(1024, 6000)
+    if long:
+        B, Hkv, grp = 1, r.choice([1, 2]), r.choice([1, 2])
     if mode == "pope":
         Dr = r.choice([16, 32, 48, 64, 96, 128])
         Dc = r.choice([0, 0, 32, 64]) if 2 * Dr + 64 <= 256 else 0
@@ -47,7 +52,18 @@ def draw(seed):
 
 @pytest.mark.parametrize("seed", list(range(30)) + [288])
 def test_random_config_matches_oracle(cuda, seed):
-    c = draw(seed)
+    check(cuda, seed)
+
+
+@pytest.mark.parametrize("seed", [1001, 1007, 1014, 1022])
+def test_random_long_config_matches_oracle(cuda, seed):
+    """RoPE bf16 at 4114 (GQA 2), no PE fp32 at 2476, split PoPE bf16 at 2444 (GQA 2, per-head
+    delta) and split PoPE fp32 at 5482 (24 long seeds ran without a failure)."""
+    check(cuda, seed, long=True)
+
+
+def check(cuda, seed, long=False):
+    c = draw(seed, long)
     g = torch.Generator().manual_seed(seed)
     dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
     B, Hq, Hkv, S, Dr, Dc, Dv = c["B"], c["Hq"], c["Hkv"], c["S"], c["Dr"], c["Dc"], c["Dv"]
