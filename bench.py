@@ -312,13 +312,17 @@ def prologue_entry(w: dict, ms: float, headline: bool) -> dict:
         try:
             with open(TRAFFIC_FILE) as f:
                 kern = json.load(f).get("kernels", {})
-            # per step: one prep dispatch per operand (q, k) and one phase-table dispatch
+            # per step: the key transform with the query phase table in one dispatch and the query
+            # transform in another (older summaries: a dispatch per operand and one for the table)
+            parts = ((("prep_vec_and_table_kernel", 1), ("prep_pope_vec_kernel", 1)) if "prep_vec_and_table_kernel" in kern
+                     else (("prep_pope_vec_kernel", 2), ("phase_table_kernel", 1)))
             t = 0.0
-            for name, per in (("prep_pope_vec_kernel", 2), ("phase_table_kernel", 1)):
+            for name, per in parts:
                 v = kern[name]
                 t += per * (v["fetch_bytes"] + v["write_bytes"])
             out["traffic"] = int(t)
-            out["traffic_source"] = f"profiles/{os.path.basename(TRAFFIC_FILE)}: prep_pope_vec_kernel x2 + phase_table_kernel"
+            out["traffic_source"] = (f"profiles/{os.path.basename(TRAFFIC_FILE)}: "
+                                     + " + ".join(f"{n} x{k}" for n, k in parts))
         except (OSError, ValueError, KeyError, TypeError):
             pass
     return out

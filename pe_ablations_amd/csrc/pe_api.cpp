@@ -376,22 +376,26 @@ static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe
   pe::PrepArgs a;
   stage_mark(PE_STAGE_FWD_PREP, 0, s);
   float* qtab = use_qtab(p) ? (float*)(ws + L.tab_off) : nullptr;
-  if (qtab && (rc = pe::launch_phase_table(freqs, p->start_pos_q, p->Sq, p->Dr, p->position_rounding, qtab, s)))
-    return rc;
-  fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
-  a.tab = qtab;
   if (nrm) {
+    if (qtab && (rc = pe::launch_phase_table(freqs, p->start_pos_q, p->Sq, p->Dr, p->position_rounding, qtab, s)))
+      return rc;
+    fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
+    a.tab = qtab;
     a.norm_w = nrm->q_weight; a.norm_w_dtype = nrm->weight_dtype; a.norm_eps = nrm->eps;
     if ((rc = pe::launch_prep_norm(a, s))) return rc;
-  } else if ((rc = pe::launch_prep(a, s))) {
-    return rc;
-  }
-  fill_prep(a, p, 1, kc, kr, freqs, delta, ws + L.k_off, L.dqk);
-  if (nrm) {
+    fill_prep(a, p, 1, kc, kr, freqs, delta, ws + L.k_off, L.dqk);
     a.norm_w = nrm->k_weight; a.norm_w_dtype = nrm->weight_dtype; a.norm_eps = nrm->eps;
     if ((rc = pe::launch_prep_norm(a, s))) return rc;
-  } else if ((rc = pe::launch_prep(a, s))) {
-    return rc;
+  } else {
+    // keys first, with the query phase table in the same launch; the queries, which read the
+    // table, after it
+    fill_prep(a, p, 1, kc, kr, freqs, delta, ws + L.k_off, L.dqk);
+    if (qtab) rc = pe::launch_prep_and_table(a, freqs, p->start_pos_q, p->Sq, p->Dr, p->position_rounding, qtab, s);
+    else rc = pe::launch_prep(a, s);
+    if (rc) return rc;
+    fill_prep(a, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
+    a.tab = qtab;
+    if ((rc = pe::launch_prep(a, s))) return rc;
   }
   if (!v_direct(p, v, L.dv)) {
     pe_attn_params pv = *p;

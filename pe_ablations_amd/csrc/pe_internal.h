@@ -118,6 +118,10 @@ bool prep_vec_query_ok(const PrepArgs& a);
 // cos / sin of the query phases fl(pe_pos(start + s) * freqs[c]) for s < S, c < Dr into tab
 // [S][2][Dr] (cos row then sin row), with the same routine and rounding as the prologue kernels
 int launch_phase_table(const float* freqs, int start, int S, int Dr, int pos_round, float* tab, hipStream_t s);
+// launch_prep(a) (the key side) and launch_phase_table(...) together: one launch on the vectorised
+// path, else the two launches in turn
+int launch_prep_and_table(const PrepArgs& a, const float* freqs, int start, int S, int Dr, int pos_round, float* tab,
+                          hipStream_t s);
 // PoPE prologue with the RMSNorm fused in: one workgroup per token (all heads)
 int launch_prep_norm(const PrepArgs& a, hipStream_t s);
 

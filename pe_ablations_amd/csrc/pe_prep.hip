@@ -302,9 +302,8 @@ __global__ __launch_bounds__(RW * 64) void reduce_kernel(ReduceArgs a) {
 // ---------------------------------------------------------------------------------------------
 // thread t of a row: transform chunk t (cos chunk t, sin chunk t), then content chunks t, t + TPR,
 // ... and zero padding chunks the same way; TPR = Dr / 8
-__global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
+__device__ __forceinline__ void prep_pope_vec_body(const PrepArgs& a, int64_t gid) {
   const int tpr = a.Dr >> 3;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t row = gid / tpr;
   const int t = (int)(gid - row * tpr);
   if (row >= (int64_t)a.B * a.H * a.S) return;
@@ -361,6 +360,10 @@ __global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
     for (int j = t; j < a.cwidth / 8; j += tpr)
       *(u32x4*)(cd + j * 8) = j * 8 < a.cv_cols ? *(const u32x4*)(crow + j * 8) : u32x4{0u, 0u, 0u, 0u};
   }
+}
+
+__global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
+  prep_pope_vec_body(a, (int64_t)blockIdx.x * 256 + threadIdx.x);
 }
 
 // one group of TPR = Dv / 8 lanes per padded row (TPR a power of two, groups never straddle a
@@ -430,15 +433,42 @@ int launch_prep(const PrepArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
-__global__ __launch_bounds__(256) void phase_table_kernel(const float* freqs, int start, int S, int Dr, int pos_round,
-                                                          float* tab) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+__device__ __forceinline__ void phase_table_body(const float* freqs, int start, int S, int Dr, int pos_round,
+                                                 float* tab, int64_t gid) {
   if (gid >= (int64_t)S * Dr) return;
   const int s = (int)(gid / Dr), c = (int)(gid % Dr);
   float sn, cs;
   pe_sincos(mul_nc(pe_pos(start + s, pos_round), freqs[c]), sn, cs);
   tab[(int64_t)s * 2 * Dr + c] = cs;
   tab[(int64_t)s * 2 * Dr + Dr + c] = sn;
+}
+
+__global__ __launch_bounds__(256) void phase_table_kernel(const float* freqs, int start, int S, int Dr, int pos_round,
+                                                          float* tab) {
+  phase_table_body(freqs, start, S, Dr, pos_round, tab, (int64_t)blockIdx.x * 256 + threadIdx.x);
+}
+
+// the key prologue (vectorised path) and the query phase table in one launch: blocks below nblk
+// transform key rows, the rest write the table; the two share no data
+__global__ __launch_bounds__(256) void prep_vec_and_table_kernel(PrepArgs a, unsigned nblk, const float* freqs,
+                                                                 int start, int S, int Dr, int pos_round, float* tab) {
+  if (blockIdx.x < nblk) prep_pope_vec_body(a, (int64_t)blockIdx.x * 256 + threadIdx.x);
+  else phase_table_body(freqs, start, S, Dr, pos_round, tab, (int64_t)(blockIdx.x - nblk) * 256 + threadIdx.x);
+}
+
+int launch_prep_and_table(const PrepArgs& a, const float* freqs, int start, int S, int Dr, int pos_round, float* tab,
+                          hipStream_t s) {
+  const int64_t nrows = (int64_t)a.B * a.H * a.S;
+  const int64_t nt = (int64_t)S * Dr;
+  if (!prep_vec_ok(a) || a.cdst || nt == 0) {
+    int rc = launch_phase_table(freqs, start, S, Dr, pos_round, tab, s);
+    return rc ? rc : launch_prep(a, s);
+  }
+  const int64_t nblk = (nrows * (a.Dr / 8) + 255) / 256, ntab = (nt + 255) / 256;
+  if (nblk + ntab > 0x7fffffff) return -2;
+  hipLaunchKernelGGL(prep_vec_and_table_kernel, dim3((unsigned)(nblk + ntab)), dim3(256), 0, s, a, (unsigned)nblk,
+                     freqs, start, S, Dr, pos_round, tab);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
 int launch_phase_table(const float* freqs, int start, int S, int Dr, int pos_round, float* tab, hipStream_t s) {
