@@ -149,14 +149,24 @@ def prologue_bytes(w: dict) -> int:
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it (what lscpu prints as the model name), with the family
+    and model numbers, which identify the generation where a virtual machine shortens the name."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" in line:
+                    k, v = (x.strip() for x in line.split(":", 1))
+                    if k in ("model name", "cpu family", "model") and k not in info:
+                        info[k] = v
+                if not line.strip() and info:
+                    break
     except OSError:
         pass
-    return "unknown"
+    name = info.get("model name", "unknown")
+    if "cpu family" in info and "model" in info:
+        name += f" (family {info['cpu family']}, model {info['model']}, {os.cpu_count()} logical CPUs)"
+    return name
 
 
 def log(*a):
