@@ -491,8 +491,11 @@ DecodePlan decode_plan(const pe_attn_params* p) {
   d.nqt = (int)(((int64_t)grp * p->Sq + 31) / 32);
   const int64_t tiles = (int64_t)p->B * p->Hkv * d.nqt;
   const int nkb = (p->Sk + 31) / 32;
-  // about 2048 waves over the GPU, at least two 32-key blocks per range, a multiple of 4 ranges
-  int64_t nu = (2048 + tiles - 1) / tiles;
+  // about 1024 waves over the GPU (one 4-wave workgroup per CU of the MI355X: in one A/B at 16384
+  // cached rows 1024 measured 44.8 us per decode step against 53.2 for 512, 45.6 for 768, 46.1 for
+  // 2048 and 49.8 for 4096), at least two 32-key blocks per range, a multiple of 4 ranges.  A fixed
+  // count, not the device's: the workspace query and the call must size the partials alike.
+  int64_t nu = (1024 + tiles - 1) / tiles;
   nu = std::min<int64_t>(nu, (nkb + 1) / 2);
   nu = std::max<int64_t>(4, std::min<int64_t>(512, (nu + 3) / 4 * 4));
   d.nunit = (int)nu;
