@@ -366,6 +366,50 @@ __global__ __launch_bounds__(256) void prep_pope_vec_kernel(PrepArgs a) {
   prep_pope_vec_body(a, (int64_t)blockIdx.x * 256 + threadIdx.x);
 }
 
+// The same key-side work for a few rows (a decoded token's cache append): one thread per
+// transformed element instead of eight, so a launch of a few hundred rows does not serialise
+// eight softplus / sin / cos evaluations per thread; the per-element arithmetic is the vectorised
+// body's, so the rows are bitwise the same.  Threads past the elements copy or clear one 16-byte
+// chunk each: the content part, the operand row's zero padding and the companion value row.
+constexpr int64_t PREP_SMALL_ELEMS = 8192;  // rows x Dr at most, for this path
+__global__ __launch_bounds__(256) void prep_pope_small_kernel(PrepArgs a) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nrows = (int64_t)a.B * a.H * a.S, nel = nrows * a.Dr;
+  const int ncc = a.Dc / 8, npad = (a.width - a.Dc - 2 * a.Dr) / 8, nval = a.cdst ? a.cwidth / 8 : 0;
+  const int nch = ncc + npad + nval;
+  const int64_t row = gid < nel ? gid / a.Dr : (gid - nel) / (nch > 0 ? nch : 1);
+  if (row >= nrows) return;
+  const int s = (int)(row % a.S), bh = (int)(row / a.S);
+  const int h = bh % a.H, b = bh / a.H;
+  const int64_t orow = (int64_t)bh * (a.dst_rows ? a.dst_rows : a.S) + a.dst_row0 + s;
+  uint16_t* drow = (uint16_t*)a.dst + orow * a.width;
+  if (gid < nel) {
+    const int d = (int)(gid - row * a.Dr);
+    const uint16_t raw = ((const uint16_t*)a.xr)[b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + d];
+    const float mu = softplus_f(__builtin_bit_cast(float, (uint32_t)raw << 16));
+    float ph = mul_nc(pe_pos(a.start_pos + s, a.pos_round), a.freqs[d]);
+    if (a.delta) ph = add_nc(ph, a.delta[h * a.delta_hs + d]);
+    float sn, cs;
+    pe_sincos(ph, sn, cs);
+    const uint32_t pr = pack_bf2(mul_nc(mu, cs), mul_nc(mu, sn));
+    drow[a.Dc + d] = (uint16_t)pr;
+    drow[a.Dc + a.Dr + d] = (uint16_t)(pr >> 16);
+    return;
+  }
+  const int j = (int)(gid - nel - row * nch);
+  if (j < ncc) {
+    const uint16_t* xc = (const uint16_t*)a.xc + b * a.xc_s[0] + h * a.xc_s[1] + (int64_t)s * a.xc_s[2];
+    *(u32x4*)(drow + j * 8) = *(const u32x4*)(xc + j * 8);
+  } else if (j < ncc + npad) {
+    *(u32x4*)(drow + a.Dc + 2 * a.Dr + (j - ncc) * 8) = u32x4{0u, 0u, 0u, 0u};
+  } else {
+    const int c = j - ncc - npad;
+    const uint16_t* crow = (const uint16_t*)a.cv + b * a.cv_s[0] + h * a.cv_s[1] + (int64_t)s * a.cv_s[2];
+    uint16_t* cd = (uint16_t*)a.cdst + orow * a.cwidth;
+    *(u32x4*)(cd + c * 8) = c * 8 < a.cv_cols ? *(const u32x4*)(crow + c * 8) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
 // one group of TPR = Dv / 8 lanes per padded row (TPR a power of two, groups never straddle a
 // wave); Di is the group's fixed-order butterfly sum
 __global__ __launch_bounds__(256) void prebwd_vec_kernel(PreBwdArgs a, int lg_tpr) {
@@ -424,7 +468,11 @@ int launch_prep(const PrepArgs& a, hipStream_t s) {
   const int64_t nrows = (int64_t)a.B * a.H * a.S;
   const bool vec = prep_vec_ok(a);
   if (a.cdst && !(vec && prep_vec_copy_ok(a))) return -2;  // the caller checks prep_vec_copy_ok first
-  if (vec) {
+  if (vec && a.is_key && nrows * a.Dr <= PREP_SMALL_ELEMS) {
+    const int64_t nch = a.Dc / 8 + (a.width - a.Dc - 2 * a.Dr) / 8 + (a.cdst ? a.cwidth / 8 : 0);
+    const int64_t nthr = nrows * (a.Dr + nch);
+    hipLaunchKernelGGL(prep_pope_small_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, a);
+  } else if (vec) {
     const int64_t nthr = nrows * (a.Dr / 8);
     hipLaunchKernelGGL(prep_pope_vec_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, a);
   } else {

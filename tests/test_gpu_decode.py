@@ -154,6 +154,24 @@ def test_decode_in_kernel_query_transform_matches_prologue(cuda):
 
 
 @torch.no_grad()
+def test_small_appends_match_bulk_append_bitwise(cuda):
+    """A few rows per call (here one token of 2 kv heads) take the one-thread-per-element append
+    kernel, a long chunk the vectorised one; the caches they fill agree bit for bit, including the
+    content part, the operand rows' zero padding (width 96 -> 128) and value rows narrower than
+    the cache (48 -> 64)."""
+    B, Hkv, L, Dc, Dr, Dv = 1, 2, 300, 32, 32, 48
+    g = torch.Generator().manual_seed(31)
+    kr, kc_ = rnd(B, Hkv, L, Dr, seed=32).bfloat16(), rnd(B, Hkv, L, Dc, seed=33).bfloat16()
+    v = rnd(B, Hkv, L, Dv, seed=34).bfloat16()
+    freqs = O.pope_freqs(Dr)
+    delta = -torch.rand(Hkv, Dr, generator=g) * 6
+    bulk = fill_cache(cuda, kr, v, freqs, delta, 320, torch.bfloat16, [L], k_c=kc_)
+    small = fill_cache(cuda, kr, v, freqs, delta, 320, torch.bfloat16, [1] * L, k_c=kc_)
+    assert torch.equal(bulk[0], small[0]) and torch.equal(bulk[1], small[1])
+    assert bool((bulk[0][:, :, :, Dc + 2 * Dr:] == 0).all()) and bool((bulk[1][:, :, :, Dv:] == 0).all())
+
+
+@torch.no_grad()
 def test_decode_argument_errors(cuda):
     B, H, D = 1, 2, 64
     freqs = O.pope_freqs(D).to(cuda)
