@@ -105,7 +105,16 @@ int pe_attn_check(const pe_attn_params* p);
 
 /* Bytes of caller-provided device workspace each pass needs (0 on invalid params).  The forward
  * workspace holds the transformed operands; pass the SAME, unmodified forward workspace to
- * pe_attn_bwd. */
+ * pe_attn_bwd.
+ *
+ * The bf16 backward stores the score gradient dS of the causal triangle (2 bytes per visible
+ * (query, key) pair, about Sq * Sk bytes per query head) for its dQ pass.  Its share of the backward
+ * workspace is capped at PE_BWD_DS_CAP_BYTES: the backward runs its two gradient kernels over
+ * groups of (batch, kv head) units, each with its query heads, whose dS fits the cap, reusing one
+ * buffer (one group, the whole problem, up to the cap; at H = 16, D = 128 that is S = 16384).  A
+ * single kv head whose query heads' dS alone exceeds the cap (Sq = Sk beyond about 68k with one query
+ * head per kv head) still gets its whole dS; the reported size then exceeds the cap by that much. */
+#define PE_BWD_DS_CAP_BYTES ((size_t)4608 << 20) /* 4.5 GiB */
 size_t pe_attn_fwd_workspace_bytes(const pe_attn_params* p);
 size_t pe_attn_bwd_workspace_bytes(const pe_attn_params* p);
 

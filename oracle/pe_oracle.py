@@ -242,19 +242,85 @@ def round_ste(x: torch.Tensor, dtype) -> torch.Tensor:
     return x + (x.to(dtype).to(x.dtype) - x).detach()
 
 
+def _bf16(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
+class _SdpaBf16Path(torch.autograd.Function):
+    """The attention core with the rounding points of a bf16 fused SDPA (the kernel the reference
+    reaches through F.scaled_dot_product_attention under bf16 autocast,
+    src/model/fpope_attention.py:171-177 and src/model/attention.py:91-96), not its exact value.
+
+    Forward: scores and the row sums in full precision, the probabilities exp(s - max) rounded to
+    bf16 before the PV product, out = (sum bf16(p) v) / sum p rounded to bf16.  Backward (the
+    flash-attention recomputation): Di = rowsum(dO * out) over the bf16 out, P = exp(s - lse),
+    dV = bf16(P)^T dO, dS = P (dP - Di) rounded to bf16 before dQ = dS K and dK = dS^T Q, every
+    gradient rounded to bf16 per query head; GQA sums the per-head dK / dV afterwards (the
+    reference's repeat_interleave backward).  Inputs hold bf16 values; math is float64 between the
+    rounding points.  Used only to measure the reference path's own error beside the kernel's."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, causal):
+        f64 = torch.float64
+        Hq, Hkv = q.shape[1], k.shape[1]
+        g = Hq // Hkv
+        kr, vr = k.to(f64).repeat_interleave(g, 1), v.to(f64).repeat_interleave(g, 1)
+        qd = q.to(f64)
+        s = torch.matmul(qd, kr.transpose(-2, -1)) * scale
+        if causal:
+            s = s.masked_fill(causal_mask(q.shape[2], k.shape[2]), float("-inf"))
+        m = s.amax(-1, keepdim=True).clamp_min(-1e300)
+        pt = torch.exp(s - m)
+        lsum = pt.sum(-1, keepdim=True)
+        out = _bf16(torch.matmul(_bf16(pt), vr) / lsum)
+        lse = (m + torch.log(lsum)).squeeze(-1)
+        ctx.save_for_backward(qd, kr, vr, out, lse)
+        ctx.scale, ctx.causal, ctx.g = scale, causal, g
+        return out.to(q.dtype), lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        qd, kr, vr, out, lse = ctx.saved_tensors
+        scale, g = ctx.scale, ctx.g
+        do = _bf16(dout.to(torch.float64))
+        di = (do * out).sum(-1, keepdim=True)
+        s = torch.matmul(qd, kr.transpose(-2, -1)) * scale
+        if ctx.causal:
+            s = s.masked_fill(causal_mask(qd.shape[2], kr.shape[2]), float("-inf"))
+        p = torch.exp(s - lse.unsqueeze(-1))
+        dv = _bf16(torch.matmul(_bf16(p).transpose(-2, -1), do))
+        ds = _bf16(p * (torch.matmul(do, vr.transpose(-2, -1)) - di))
+        dq = _bf16(torch.matmul(ds, kr) * scale)
+        dk = _bf16(torch.matmul(ds.transpose(-2, -1), qd) * scale)
+
+        def fold(x):  # per-head gradients summed over each kv head's query group
+            B, H, S, D = x.shape
+            return x.view(B, H // g, g, S, D).sum(2)
+
+        return dq, fold(dk), fold(dv), None, None
+
+
+def attention_bf16_path(q, k, v, scale: float, causal: bool = True):
+    """(out, lse) of ``attention`` with a bf16 fused SDPA's rounding points (_SdpaBf16Path);
+    differentiable, so the transforms around it carry the path's gradients to the raw inputs."""
+    return _SdpaBf16Path.apply(q, k, v, scale, bool(causal))
+
+
 # --------------------------------------------------------------------------------------------
 # fused-form PoPE attention (BASELINE configs; legacy fused API)
 # --------------------------------------------------------------------------------------------
 
 def pope_attention(q, k, v, freqs, delta, scale: Optional[float] = None, causal: bool = True,
                    start_q: int = 0, start_k: int = 0, clamp: bool = True,
-                   operand_dtype=None, core_dtype=torch.float64, transform_dtype=torch.float32):
+                   operand_dtype=None, core_dtype=torch.float64, transform_dtype=torch.float32,
+                   core=None):
     """Fused-form PoPE causal attention, factorised (what the reference module computes,
     src/model/pope.py:124-183 + src/model/fpope_attention.py:166-177 with d_content = 0).
 
     q (B,Hq,S,D), k/v (B,Hkv,S,D); freqs (D,); delta (D,) or (Hkv?,D) -- per head uses the key
     head index; ``clamp`` applies the module's [-2pi, 0] clamp.  ``operand_dtype`` rounds the
-    transformed q~/k~ and v (e.g. torch.bfloat16, what SDPA sees under autocast).
+    transformed q~/k~ and v (e.g. torch.bfloat16, what SDPA sees under autocast).  ``core``
+    replaces the attention core (signature of ``attention_bf16_path``).
     Differentiable (autograd) w.r.t. q, k, v, freqs, delta.  Returns (out, lse)."""
     D = q.shape[-1]
     scale = (1.0 / math.sqrt(D)) if scale is None else scale
@@ -264,6 +330,8 @@ def pope_attention(q, k, v, freqs, delta, scale: Optional[float] = None, causal:
     qt = round_ste(qt, operand_dtype)
     kt = round_ste(kt, operand_dtype)
     vv = round_ste(v.to(transform_dtype), operand_dtype)
+    if core is not None:
+        return core(qt, kt, vv, scale, causal)
     return attention(qt, kt, vv, scale, causal, core_dtype)
 
 
@@ -351,7 +419,7 @@ def pope_attention_backward_closed_form(q, k, v, freqs, delta, dout, scale=None,
 # --------------------------------------------------------------------------------------------
 
 def split_pope_attention(qc, kc, qr, kr, v, freqs, delta, scale=None, causal=True, start: int = 0,
-                         operand_dtype=None, core_dtype=torch.float64):
+                         operand_dtype=None, core_dtype=torch.float64, core=None):
     """The reference module's contraction: Q = [q_c | PoPE(q_r)], K = [k_c | PoPE(k_r, delta)]
     (src/model/fpope_attention.py:128-177).  q_c/q_r (B,Hq,S,Dc/Dr), k_c/k_r/v (B,Hkv,S,.).
     delta is the (already clamped) key phase bias.  scale defaults to (Dc + 2 Dr)^-1/2
@@ -362,11 +430,13 @@ def split_pope_attention(qc, kc, qr, kr, v, freqs, delta, scale=None, causal=Tru
     kt = torch.cat([kc.float(), pope_transform(kr, freqs, start, delta)], -1)
     qt, kt = round_ste(qt, operand_dtype), round_ste(kt, operand_dtype)
     vv = round_ste(v.float(), operand_dtype)
+    if core is not None:
+        return core(qt, kt, vv, scale, causal)
     return attention(qt, kt, vv, scale, causal, core_dtype)
 
 
 def rope_attention(q, k, v, inv_freq, mscale: float = 1.0, qk_norm: bool = True, causal=True,
-                   start: int = 0, scale=None, operand_dtype=None):
+                   start: int = 0, scale=None, operand_dtype=None, core=None):
     """RoPE module path: interleaved rotation (x mscale for YaRN), QKNorm, SDPA with scale
     1/sqrt(D) (src/model/attention.py:69-96, src/model/rope.py:209-217).  (B,H,S,D) layout."""
     D = q.shape[-1]
@@ -376,7 +446,7 @@ def rope_attention(q, k, v, inv_freq, mscale: float = 1.0, qk_norm: bool = True,
     if qk_norm:
         qr, kr = qk_l2norm(qr), qk_l2norm(kr)
     qr, kr = round_ste(qr, operand_dtype), round_ste(kr, operand_dtype)
-    return attention(qr, kr, round_ste(v.float(), operand_dtype), scale, causal)
+    return (core or attention)(qr, kr, round_ste(v.float(), operand_dtype), scale, causal)
 
 
 # --------------------------------------------------------------------------------------------
@@ -488,7 +558,7 @@ def pope_attention_chunked(q, k, v, freqs, delta, dout=None, scale=None, causal=
 # --------------------------------------------------------------------------------------------
 
 def decoder_forward(state: dict, cfg, input_ids: torch.Tensor, start: int = 0,
-                    labels: Optional[torch.Tensor] = None) -> dict:
+                    labels: Optional[torch.Tensor] = None, yarn_extended: bool = False) -> dict:
     """Transformer.forward of the reference (src/model/transformer.py:313-364) restated over a
     state dict: token embedding -> per layer x + attn(RMSNorm(x)), x + w2(silu(w3 h) * w1 h)
     (src/model/transformer.py:186-205, src/model/ffn.py:17-27,53-68) -> RMSNorm -> LM head ->
@@ -497,7 +567,9 @@ def decoder_forward(state: dict, cfg, input_ids: torch.Tensor, start: int = 0,
     ``cfg`` has TransformerConfig's attributes.  The attention per pe_mode follows
     src/model/transformer.py:127-178: "pope" / "pope_floor" / "fpope" use the split module
     contraction (or, with ``cfg.pope_fused``, the fused form of the legacy API: every head dim
-    PoPE-encoded, scale 1/sqrt(head_dim)); "rope" / "nope" use the RoPE module path."""
+    PoPE-encoded, scale 1/sqrt(head_dim)); "rope" / "nope" use the RoPE module path.
+    ``yarn_extended``: the YaRN module after extend_seq_len, which rebuilds the plain RoPE table
+    from theta and keeps its mscale (src/model/rope.py:103-119 inherited, :209-217)."""
     w = {k: v.float() for k, v in state.items()}
     B, S = input_ids.shape
     H, Hkv, D, eps = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.norm_eps
@@ -514,6 +586,8 @@ def decoder_forward(state: dict, cfg, input_ids: torch.Tensor, start: int = 0,
     elif mode == "rope":
         if cfg.rope_type == "yarn":
             inv_freq, mscale, _, _ = yarn_inv_freq(D, cfg.rope_theta, cfg.rope_scale, 512)
+            if yarn_extended:
+                inv_freq = rope_inv_freq(D, cfg.rope_theta)
         elif cfg.rope_type == "ntk":
             inv_freq, mscale = rope_inv_freq(D, ntk_theta(D, cfg.rope_theta, cfg.rope_scale)), 1.0
         else:

@@ -40,6 +40,7 @@ struct Layout {
   int sq_pad;
   int ds_nqt, ds_rows, ds_e;
   int64_t ds_head;
+  int ds_group;  // (batch, kv head) units per backward head group (pe_attn_bwd loops over groups)
   int nq_blocks, nk_blocks;
 };
 
@@ -115,8 +116,14 @@ Layout layout(const pe_attn_params* p) {
   const int off = p->causal == PE_CAUSAL_BOTTOM_RIGHT ? p->Sk - p->Sq : 0;
   L.ds_e = causal ? (off + 63) / 64 : 0;
   L.ds_head = pe::ds_row_base(L.ds_rows / 32, L.ds_e, L.ds_nqt, causal);
-  const size_t ds_bytes =
-      p->dtype == PE_DTYPE_BF16 ? (size_t)p->B * p->Hq * L.ds_head * 4096 : 0;
+  // dS of one (batch, kv head) unit: its query heads' regions; as many units per group as the cap
+  // holds (at least one)
+  const int units = p->B * p->Hkv;
+  const size_t unit_bytes = (size_t)(p->Hq / p->Hkv) * L.ds_head * 4096;
+  L.ds_group = units;
+  if (p->dtype == PE_DTYPE_BF16 && unit_bytes > 0 && (size_t)units * unit_bytes > PE_BWD_DS_CAP_BYTES)
+    L.ds_group = std::max<int>(1, (int)(PE_BWD_DS_CAP_BYTES / unit_bytes));
+  const size_t ds_bytes = p->dtype == PE_DTYPE_BF16 ? (size_t)L.ds_group * unit_bytes : 0;
   L.bwd_total = L.ds_off + align_up(ds_bytes);
   return L;
 }
@@ -210,6 +217,8 @@ pe::CoreArgs core_args(const pe_attn_params* p, const Layout& L, const char* ws,
   c.causal = p->causal != PE_CAUSAL_NONE;
   c.causal_off = p->causal == PE_CAUSAL_BOTTOM_RIGHT ? p->Sk - p->Sq : 0;
   c.scale = p->scale;
+  c.bh0 = 0;
+  c.nbh = p->B * p->Hkv;
   return c;
 }
 
@@ -734,10 +743,24 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     c.ek.part_freq = dfreqs ? (float*)(bws + L.pk_off) : nullptr;
     c.ek.part_delta = ddelta ? (float*)(bws + L.pkd_off) : nullptr;
   }
-  if ((rc = pe::launch_bwd_dkdv(dt, L.dqk, L.dv, c, s))) return rc;
-  stage_mark(PE_STAGE_BWD_DKDV, 1, s);
-  stage_mark(PE_STAGE_BWD_DQ, 0, s);
-  if ((rc = pe::launch_bwd_dq(dt, L.dqk, L.dv, c, s))) return rc;
+  // the gradient kernels over head groups whose dS fits the workspace (one group up to the cap);
+  // with several groups the dK/dV stage mark spans every group's kernels and the dQ mark is empty
+  const int units = p->B * p->Hkv;
+  const int group = dt == 0 ? L.ds_group : units;
+  for (int g0 = 0; g0 < units; g0 += group) {
+    c.bh0 = g0;
+    c.nbh = std::min(group, units - g0);
+    if ((rc = pe::launch_bwd_dkdv(dt, L.dqk, L.dv, c, s))) return rc;
+    if (group == units) {
+      stage_mark(PE_STAGE_BWD_DKDV, 1, s);
+      stage_mark(PE_STAGE_BWD_DQ, 0, s);
+    }
+    if ((rc = pe::launch_bwd_dq(dt, L.dqk, L.dv, c, s))) return rc;
+  }
+  if (group != units) {
+    stage_mark(PE_STAGE_BWD_DKDV, 1, s);
+    stage_mark(PE_STAGE_BWD_DQ, 0, s);
+  }
   stage_mark(PE_STAGE_BWD_DQ, 1, s);
   stage_mark(PE_STAGE_BWD_INV, 0, s);
 

@@ -15,6 +15,23 @@
 
 namespace pe {
 
+// The fp32 kernels recompute P in natural units, exp(fma(s, scale, -lse)): the one rounding of the
+// exponent is at the size of s * scale - lse, which is small exactly where P is large, as in the
+// reference's fp32 softmax.  The log2-unit form exp2(s * (scale log2 e) - lse log2 e) rounds at the
+// size of the raw score (tens), and its P carried about three times the reference's error into dV
+// and dK.  The bf16 kernels keep the log2 form (their error is set by the bf16 roundings).
+// lse of query row q of (b, h) in natural units, +inf for rows past Sq and rows without keys (so
+// their P is 0)
+__device__ __forceinline__ float lse_nat(const CoreArgs& a, int bh, int q) {
+  if (q >= a.Sq) return INFINITY;
+  const float x = a.lse_in[(int64_t)bh * a.Sq + q];
+  return x > -INFINITY ? x : INFINITY;
+}
+template <int DT> __device__ __forceinline__ float prob(float s, float scale, float sl2, float l) {
+  if constexpr (DT == 1) return exp2f(__builtin_fmaf(s, scale, -l) * LOG2E);
+  else return exp2f(s * sl2 - l);
+}
+
 template <int DT, int DQK, int DV, int BMQ, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void dkdv_kernel(CoreArgs a) {
   using E = typename Elem<DT>::T;
@@ -34,7 +51,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_kernel(CoreArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int nkb = (a.Sk + BNK - 1) / BNK;
   int kb, bh;
-  map_block(blockIdx.x, nkb, a.B * a.Hkv, false, kb, bh);
+  map_block(blockIdx.x, nkb, a.nbh, false, kb, bh);
+  bh += a.bh0;  // the head group's units
   const int b = bh / a.Hkv, hk = bh % a.Hkv, grp = a.Hq / a.Hkv;
   const int k0 = kb * BNK, kw0 = k0 + w * 32, myk = kw0 + l32;
   const int off = a.causal_off;
@@ -91,7 +109,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_kernel(CoreArgs a) {
     stO.store(sO, tid);
     if (tid < BMQ) {
       const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
-      sL[tid] = a.L2[p0 + tid];
+      if constexpr (DT == 1) sL[tid] = lse_nat(a, b * a.Hq + h, q0 + tid);
+      else sL[tid] = a.L2[p0 + tid];
       sD[tid] = a.Di[p0 + tid];
     }
     __syncthreads();
@@ -119,7 +138,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_kernel(CoreArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int qi = mt * 32 + c_logical<DT>(j, g);
-        float p = exp2f(s[j] * sl2 - sL[qi]);
+        float p = prob<DT>(s[j], a.scale, sl2, sL[qi]);
         if (edge && myk > q0 + qi + off) p = 0.f;
         s[j] = p;
         dp[j] = p * (dp[j] - sD[qi]);
@@ -130,16 +149,24 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_kernel(CoreArgs a) {
         dsf[mt * SPT + si] = M::pack(dp, si * EPL);
       }
     }
+    // two-level sums: each tile's products go into a zeroed accumulator that is then added to the
+    // running one, so the running sums (|dv| reaches ~8 on early keys) are rounded once per tile
+    // rather than once per product; chained over a whole sequence they carried about three times
+    // the error of the reference's blocked fp32 products
 #pragma unroll
-    for (int t = 0; t < NDV; ++t)
+    for (int t = 0; t < NDV; ++t) {
+      f32x16 acc = {};
 #pragma unroll
-      for (int ks = 0; ks < NPF; ++ks)
-        dv[t] = M::mma(pf[ks], lds_col_frag<DT, NCO>(sO, ks * KC, t * 32, lane), dv[t]);
+      for (int ks = 0; ks < NPF; ++ks) acc = M::mma(pf[ks], lds_col_frag<DT, NCO>(sO, ks * KC, t * 32, lane), acc);
+      dv[t] += acc;
+    }
 #pragma unroll
-    for (int t = 0; t < NDK; ++t)
+    for (int t = 0; t < NDK; ++t) {
+      f32x16 acc = {};
 #pragma unroll
-      for (int ks = 0; ks < NPF; ++ks)
-        dk[t] = M::mma(dsf[ks], lds_col_frag<DT, NCQ>(sQ, ks * KC, t * 32, lane), dk[t]);
+      for (int ks = 0; ks < NPF; ++ks) acc = M::mma(dsf[ks], lds_col_frag<DT, NCQ>(sQ, ks * KC, t * 32, lane), acc);
+      dk[t] += acc;
+    }
   }
 
   // epilogue: C rows = keys (kw0 + c_row), cols = feature / value column t*32 + l32
@@ -178,7 +205,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int nqb = (a.Sq + BM - 1) / BM;
   int qb, bh;
-  map_block(blockIdx.x, nqb, a.B * a.Hq, a.causal != 0, qb, bh);
+  map_block(blockIdx.x, nqb, a.nbh * (a.Hq / a.Hkv), a.causal != 0, qb, bh);
+  bh += a.bh0 * (a.Hq / a.Hkv);  // the head group's query heads
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
   const int q0 = qb * BM, qw = q0 + w * 32, myq = qw + l32;
   const int off = a.causal_off;
@@ -195,7 +223,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
     for (int kk = 0; kk < NVF; ++kk) of[kk] = myq < a.Sq ? *(const u32x4*)(orow + kk * KC + g * EPL) : z;
   }
   const int64_t prow = (int64_t)(b * a.Hq + h) * a.sq_pad + myq;
-  const float lse2 = a.L2[prow], Dq = a.Di[prow];
+  const float lse2 = DT == 1 ? lse_nat(a, b * a.Hq + h, myq) : a.L2[prow], Dq = a.Di[prow];
   f32x16 dq[NDQ];
 #pragma unroll
   for (int t = 0; t < NDQ; ++t)
@@ -242,7 +270,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
       for (int kk = 0; kk < NVF; ++kk) dp = M::mma(lds_row_frag<NCV>(sV, row, 2 * kk + g), of[kk], dp);
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float p = exp2f(s[j] * sl2 - lse2);
+        float p = prob<DT>(s[j], a.scale, sl2, lse2);
         if (edge) {
           const int key = k0 + nt * 32 + c_logical<DT>(j, g);
           if (key >= a.Sk || (a.causal && key > myq + off)) p = 0.f;
@@ -253,10 +281,12 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
       for (int si = 0; si < SPT; ++si) dsf[nt * SPT + si] = M::pack(dp, si * EPL);
     }
 #pragma unroll
-    for (int t = 0; t < NDQ; ++t)
+    for (int t = 0; t < NDQ; ++t) {  // two-level sums, as in dkdv_kernel
+      f32x16 acc = {};
 #pragma unroll
-      for (int ks = 0; ks < NPF; ++ks)
-        dq[t] = M::mma(dsf[ks], lds_col_frag<DT, NCK>(sK, ks * KC, t * 32, lane), dq[t]);
+      for (int ks = 0; ks < NPF; ++ks) acc = M::mma(dsf[ks], lds_col_frag<DT, NCK>(sK, ks * KC, t * 32, lane), acc);
+      dq[t] += acc;
+    }
   }
 
   float* dqb = a.dq_t + (int64_t)(b * a.Hq + h) * a.Sq * DQK;
@@ -302,7 +332,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int nkb = (a.Sk + BNK - 1) / BNK;
   int kb, bh;
-  map_block(blockIdx.x, nkb, a.B * a.Hkv, false, kb, bh);
+  map_block(blockIdx.x, nkb, a.nbh, false, kb, bh);
+  bh += a.bh0;  // the head group's units
   const int b = bh / a.Hkv, hk = bh % a.Hkv, grp = a.Hq / a.Hkv;
   const int k0 = kb * BNK, kw0 = k0 + w * 32, myk = kw0 + l32;
   const int off = a.causal_off;
@@ -500,7 +531,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     // contiguous (block (key/32, q0/64), chunks (mt*2 + h2)*64 + lane); rows past Sk are padding
     {
       const int h = hk * grp + t / nper;
-      char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * a.ds_head + ds_row_base(kw0 >> 5, a.ds_e, a.ds_nqt, a.causal) +
+      char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h - a.bh0 * grp) * a.ds_head + ds_row_base(kw0 >> 5, a.ds_e, a.ds_nqt, a.causal) +
                                  (q0 >> 6) - ds_first(kb, a.ds_e, a.causal)) * 4096;
       __builtin_nontemporal_store(cdsf[0], (u32x4*)(blk + ((mt * 2 + 0) * 64 + lane) * 16));  // read once
       __builtin_nontemporal_store(cdsf[1], (u32x4*)(blk + ((mt * 2 + 1) * 64 + lane) * 16));
@@ -770,7 +801,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const bool roleB = __builtin_amdgcn_readfirstlane(w >> 2) != 0;
   const int nkb = (a.Sk + BNK - 1) / BNK;
   int kb, bh;
-  map_block(blockIdx.x, nkb, a.B * a.Hkv, false, kb, bh);
+  map_block(blockIdx.x, nkb, a.nbh, false, kb, bh);
+  bh += a.bh0;  // the head group's units
   const int b = bh / a.Hkv, hk = bh % a.Hkv, grp = a.Hq / a.Hkv;
   const int k0 = kb * BNK, kw0 = k0 + pw * 32, myk = kw0 + l32;
   const int off = a.causal_off;
@@ -1028,7 +1060,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           prev_qt = qb0;
           ++prev_h;
         }
-        char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h) * a.ds_head + ds_row + (q0 >> 6)) * 4096;
+        char* blk = (char*)a.dS + ((int64_t)(b * a.Hq + h - a.bh0 * grp) * a.ds_head + ds_row + (q0 >> 6)) * 4096;
         const int mt = (q0 >> 5) & 1;  // 0 for 64-query tiles, which fill their block
         // dS is read once, by the dQ GEMM after this kernel: non-temporal stores keep it from
         // displacing the q~ / dO tiles that the other key blocks re-read (4 % of this kernel's
@@ -1213,7 +1245,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int nqb = (a.Sq + BQ - 1) / BQ;
   int qb, bh;
-  map_block(blockIdx.x, nqb, a.B * a.Hq, a.causal != 0, qb, bh);
+  map_block(blockIdx.x, nqb, a.nbh * (a.Hq / a.Hkv), a.causal != 0, qb, bh);
+  bh += a.bh0 * (a.Hq / a.Hkv);  // the head group's query heads
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
   const int q0 = qb * BQ;
   const int qp = w % NQG, dh = w / NQG;
@@ -1242,7 +1275,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   // the packed dS of this (b, h) (pe_internal.h): key row r of the block's 64-query blocks
   // j0 .. j0 + 3 (j0 = q0 / 64) starts at block ds_row_base(r) + j0 - ds_first(r / 4)
   const int j0 = q0 >> 6;
-  const char* sbase = (const char*)a.dS + ((int64_t)(b * a.Hq + h) * a.ds_head + j0) * 4096;
+  const char* sbase = (const char*)a.dS + ((int64_t)(b * a.Hq + h - a.bh0 * (a.Hq / a.Hkv)) * a.ds_head + j0) * 4096;
   const int64_t krs = (int64_t)DQK * 2;
   // dS window for keys k0 .. k0+BK-1 and this block's 256 queries: LDS slot (row kl, physical chunk
   // pc) holds query chunk lc = pc ^ swz(kl) of key k0 + kl; its source is key row r = (k0 + kl) / 32
@@ -1496,9 +1529,9 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
         // 64-query tiles where they fit the LDS (QK width 128, V width 64: the ~125M GPT shape and the
         // split training form), which halves the per-step barriers and waits per product
         constexpr int QT = DQK == 128 && DV == 64 ? 2 : 1;
-        hipLaunchKernelGGL((dkdv_pair_kernel<DQK, DV, QT>), dim3(nkb * a.B * a.Hkv), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((dkdv_pair_kernel<DQK, DV, QT>), dim3(nkb * a.nbh), dim3(512), 0, s, a);
       } else {
-        hipLaunchKernelGGL((dkdv_bf16_kernel<DQK, DV, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
+        hipLaunchKernelGGL((dkdv_bf16_kernel<DQK, DV, NW>), dim3(nkb * a.nbh), dim3(NW * 64), 0, s, a);
       }
     } else {
       const int nqb = (a.Sq + 255) / 256;
@@ -1507,17 +1540,17 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       // 64-wide k~ (a 32-key tile of it is less than one DMA instruction per wave) keeps 64-key
       // steps double-buffered
       constexpr bool TW = DQK == 256 || DQK == 128;
-      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8, (TW ? 32 : 64), (TW ? 4 : 2)>), dim3(nqb * a.B * a.Hq), dim3(8 * 64), 0, s, a);
+      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8, (TW ? 32 : 64), (TW ? 4 : 2)>), dim3(nqb * a.nbh * (a.Hq / a.Hkv)), dim3(8 * 64), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {
     constexpr int BMQ = 32, BN = 32;
     if (which == 0) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
-      hipLaunchKernelGGL((dkdv_kernel<DT, DQK, DV, BMQ, NW>), dim3(nkb * a.B * a.Hkv), dim3(NW * 64), 0, s, a);
+      hipLaunchKernelGGL((dkdv_kernel<DT, DQK, DV, BMQ, NW>), dim3(nkb * a.nbh), dim3(NW * 64), 0, s, a);
     } else {
       const int nqb = (a.Sq + NW * 32 - 1) / (NW * 32);
-      hipLaunchKernelGGL((dq_kernel<DT, DQK, DV, BN, NW>), dim3(nqb * a.B * a.Hq), dim3(NW * 64), 0, s, a);
+      hipLaunchKernelGGL((dq_kernel<DT, DQK, DV, BN, NW>), dim3(nqb * a.nbh * (a.Hq / a.Hkv)), dim3(NW * 64), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   }

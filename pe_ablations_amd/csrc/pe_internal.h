@@ -77,6 +77,10 @@ struct CoreArgs {
   const float* freqs; const float* delta; int64_t delta_hs;
   EpiPoPE eq, ek;
   int n_cu;  // compute units of the device: launchers pick smaller blocks when a grid would not fill them
+  // backward head group: the gradient kernels cover the (batch, kv head) units bh0 .. bh0 + nbh - 1
+  // (flattened b * Hkv + hk) and their query heads; dS holds that group only, indexed from its first
+  // query head (b * Hq + h - bh0 * Hq / Hkv), so one capped buffer serves every group in turn
+  int bh0, nbh;
 };
 
 int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);

@@ -153,3 +153,36 @@ def test_stage_hook_toggles(lib):
     arr = (ctypes.c_void_p * (2 * len(_lib.STAGES)))()
     assert lib.pe_attn_set_stage_events(ctypes.cast(arr, ctypes.c_void_p)) == 0
     assert lib.pe_attn_set_stage_events(None) == 0
+
+
+def ds_unit_bytes(Sq, grp, causal=True):
+    """dS bytes of one (batch, kv head) unit at Sq = Sk: grp query heads of ds_row_base(rows / 32)
+    4 KiB blocks (pe_internal.h), from the row lengths summed directly (causal top-left: row r
+    holds the 64-query blocks from 2 * (r / 4) on; no mask: all of them)."""
+    nqt = (Sq + 255) // 256 * 4
+    rows = (Sq + 127) // 128 * 128
+    blocks = sum(nqt - (max(0, 2 * (r // 4)) if causal else 0) for r in range(rows // 32))
+    return grp * blocks * 4096
+
+
+@pytest.mark.parametrize("S, H, Hkv, groups", [(16384, 16, 16, 1), (32768, 16, 16, 4), (32768, 16, 4, 4),
+                                               (65536, 4, 4, 4), (8192, 64, 8, 1), (4096, 1, 1, 1)])
+def test_bwd_workspace_caps_the_score_gradient(lib, S, H, Hkv, groups):
+    """The bf16 backward's dS share of the workspace holds as many (batch, kv head) units as
+    PE_BWD_DS_CAP_BYTES (4.5 GiB) allows: the whole problem at the headline shape (16 heads at
+    S = 16384, 4.33 GB), one unit group in `groups` at longer lengths.  Only dS depends on the mask,
+    so the causal and unmasked workspaces differ by exactly the two capped dS shares."""
+    cap = 4608 << 20
+    lib.pe_attn_bwd_workspace_bytes.restype = ctypes.c_size_t
+    kw = dict(B=1, Hq=H, Hkv=Hkv, Sq=S, Sk=S, Dr=128, Dv=128, scale=1 / 16.0, delta_head_stride=128)
+    share = {}
+    for causal in (True, False):
+        unit = ds_unit_bytes(S, H // Hkv, causal)
+        per_group = min(Hkv, max(1, cap // unit))
+        share[causal] = per_group * unit
+        if causal:
+            assert -(-Hkv // per_group) == groups
+            assert share[causal] <= cap or per_group == 1
+    tc = lib.pe_attn_bwd_workspace_bytes(ctypes.byref(params(**kw, causal=_lib.PE_CAUSAL_TOP_LEFT)))
+    tn = lib.pe_attn_bwd_workspace_bytes(ctypes.byref(params(**kw, causal=_lib.PE_CAUSAL_NONE)))
+    assert abs((tc - tn) - (share[True] - share[False])) < 512, (tc, tn, share)

@@ -11,7 +11,9 @@ and checks that
 * no two written blocks share an address and every written block lies inside its (b, h) region;
 * every dS element the reader uses unmasked was written (by block and 32-query half);
 * every address the reader loads, masked ones included, lies inside the B * Hq regions that
-  pe_attn_bwd_workspace_bytes sizes (the reads before a row's first block fall in earlier rows).
+  pe_attn_bwd_workspace_bytes sizes (the reads before a row's first block fall in earlier rows),
+  and never past its own head's region, so that a head group indexed from its first head (the
+  capped backward, PE_BWD_DS_CAP_BYTES) reads only its own regions.
 
 The closed form of ds_row_base is also compiled from pe_internal.h on the host and compared with
 the running sum of the row lengths it must equal."""
@@ -112,6 +114,10 @@ def test_packed_ds_layout_covers_every_read(Sq, Sk, causal, br, pair):
                         for j in range(j0, j0 + 4):
                             a = hh * head + addr(row, j, e, nqt64, causal)
                             assert 0 <= a < nheads * head, (hh, qb, kb, row, j, a, head)
+                            # never past the head's own region: with head 0 never before the
+                            # buffer, a group of n heads (the capped backward runs the kernels over
+                            # groups, indexing dS from the group's first head) reads [0, n * head)
+                            assert a < (hh + 1) * head, (hh, qb, kb, row, j, a, head)
                             for half in (0, 1):
                                 qlo = 64 * j + 32 * half
                                 if qlo >= Sq:

@@ -120,3 +120,33 @@ def test_headline_fwd_bwd_bf16_full_head(cuda):
     freqs = O.pope_freqs(D)
     res = run_kernel(cuda, q, k, v, do, freqs, delta, 1 / math.sqrt(D))
     check_slices(res, q, k, v, do, freqs, delta, 1 / math.sqrt(D), heads=[3], batches=[0], tol=2e-2)
+
+
+def test_long_fwd_bwd_runs_over_capped_head_groups(cuda):
+    """S = 32768, H = 16, D = 128 bf16 fwd+bwd.  The whole dS would be 17.2 GB; the backward holds
+    at most PE_BWD_DS_CAP_BYTES (4.5 GiB) of it and runs its gradient kernels over 4 groups of 4
+    heads.  Heads 0 and 13 (first and last group) are checked end to end against the chunked
+    oracle, and the workspace the call asks for is measured."""
+    from pe_ablations_amd import _lib
+    import ctypes
+    B, H, S, D = 1, 16, 32768, 128
+    q, k, v, do, delta = make(B, H, S, D, seed=7)
+    freqs = O.pope_freqs(D)
+    p = _lib.PeParams()
+    for name, val in dict(B=B, Hq=H, Hkv=H, Sq=S, Sk=S, Dc=0, Dr=D, Dv=D, mode=_lib.PE_MODE_POPE,
+                          dtype=_lib.PE_DTYPE_BF16, causal=_lib.PE_CAUSAL_TOP_LEFT, scale=1 / math.sqrt(D),
+                          rope_mscale=1.0, delta_head_stride=D).items():
+        setattr(p, name, val)
+    fn = _lib.lib().pe_attn_bwd_workspace_bytes
+    fn.restype = ctypes.c_size_t
+    ws = fn(ctypes.byref(p))
+    cap = 4608 << 20
+    assert cap - 2 ** 30 < ws < cap + 2 ** 28, ws   # 4 heads of dS (4.29 GB) plus the small buffers
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    res = run_kernel(cuda, q, k, v, do, freqs, delta, 1 / math.sqrt(D))
+    peak = torch.cuda.max_memory_allocated() - base
+    print(f"bwd workspace {ws / 2**30:.2f} GiB, peak allocated {peak / 2**30:.2f} GiB", flush=True)
+    assert peak < 6 * 2 ** 30, peak
+    check_slices(res, q, k, v, do, freqs, delta, 1 / math.sqrt(D), heads=[0, 13], batches=[0], tol=2e-2)

@@ -15,7 +15,8 @@ import pytest
 import torch
 
 from oracle import pe_oracle as O
-from tests._cmp import argmax_err, err, err_both
+from tests._cmp import argmax_err, err
+from tests.test_gpu_sweep import bar_for, fp32_core
 from pe_ablations_amd.functional import pe_attention
 
 pytestmark = pytest.mark.gpu
@@ -52,11 +53,12 @@ def oracle_operands(mode, qc, kc, qr, kr, freqs, delta, start_q, start_k, mscale
 def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=64, Dc=0,
              dtype=torch.bfloat16, causal=True, freqs=None, delta=None, scale=None, mscale=1.0,
              qk_norm=False, start_q=0, start_k=0, seed=0, grad_freqs=False, grad_delta=True,
-             net_names=(), pos_dtype=None):
-    """One case through pe_attention against the oracle.  Every listed error is the raw max-abs;
-    ``net_names`` lists results whose magnitude puts the raw bf16 bar out of reach of any bf16
-    number (the test names the magnitude): those are asserted net of their own rounding and their
-    raw figure and largest-error element are reported in the message."""
+             path_names=(), pos_dtype=None):
+    """One case through pe_attention against the oracle.  Every listed error is the raw max-abs.
+    Each result is held to the raw bar (1e-5 fp32, 2e-2 bf16) wherever the reference path meets it
+    at the same elements, else to PATH_FACTOR times the reference path's own error (bar_for);
+    ``path_names`` lists the results for which the test expects the latter (it asserts that the
+    reference path does miss the raw bar there)."""
     Sk = Sq if Sk is None else Sk
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
     qr, kr = rnd(B, Hq, Sq, Dr, seed=seed), rnd(B, Hkv, Sk, Dr, seed=seed + 1)
@@ -70,16 +72,27 @@ def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=
         scale = (Dc + (2 * Dr if mode == "pope" else Dr)) ** -0.5
     causal_flag = ("bottom_right" if Sq != Sk else True) if causal else False
 
-    # oracle: fp32 transforms, fp64 core, bf16 operand rounding in bf16 mode
-    o_in = [None if t is None else t.float().clone().requires_grad_(True) for t in ins]
-    of = None if freqs is None else freqs.clone().requires_grad_(grad_freqs)
-    od = None if delta is None else delta.clone().requires_grad_(grad_delta)
-    tq, tk = oracle_operands(mode, o_in[3], o_in[4], o_in[0], o_in[1], of, od, start_q, start_k, mscale, qk_norm,
-                             pos_dtype)
+    # oracle: fp32 transforms, fp64 core, bf16 operand rounding in bf16 mode; the same graph with
+    # the reference path's core (bf16: a bf16 fused SDPA's rounding points; fp32: float32 math)
+    # gives the reference path's own error at every element
     rd = torch.bfloat16 if dtype == torch.bfloat16 else None
-    tq, tk, vv = O.round_ste(tq, rd), O.round_ste(tk, rd), O.round_ste(o_in[2].float(), rd)
-    ref, ref_lse = O.attention(tq, tk, vv, scale, causal=bool(causal))
-    ref.backward(dout.double())
+
+    def oracle_graph(core=None):
+        o_in = [None if t is None else t.float().clone().requires_grad_(True) for t in ins]
+        of = None if freqs is None else freqs.clone().requires_grad_(grad_freqs)
+        od = None if delta is None else delta.clone().requires_grad_(grad_delta)
+        tq, tk = oracle_operands(mode, o_in[3], o_in[4], o_in[0], o_in[1], of, od, start_q, start_k, mscale,
+                                 qk_norm, pos_dtype)
+        tq, tk, vv = O.round_ste(tq, rd), O.round_ste(tk, rd), O.round_ste(o_in[2].float(), rd)
+        if core is None:
+            ref, ref_lse = O.attention(tq, tk, vv, scale, causal=bool(causal))
+        else:
+            ref, ref_lse = core(tq, tk, vv, scale, bool(causal))
+        ref.backward(dout.to(ref.dtype))
+        return o_in, of, od, ref, ref_lse, vv
+
+    o_in, of, od, ref, ref_lse, vv = oracle_graph()
+    p_in, _, _, pref, _, _ = oracle_graph(O.attention_bf16_path if rd is not None else fp32_core)
 
     g_in = [None if t is None else t.to(cuda).requires_grad_(True) for t in ins]
     gf = None if freqs is None else freqs.to(cuda).requires_grad_(grad_freqs)
@@ -90,18 +103,19 @@ def run_case(cuda, *, mode="pope", B=1, Hq=2, Hkv=2, Sq=128, Sk=None, Dr=64, Dv=
     out.backward(dout.to(cuda))
     torch.cuda.synchronize()
     errs = {"out": md(out, ref), "lse": md(lse, ref_lse)}
+    path = {"out": err(pref.to(dtype), ref, "path out")}
     pairs = {"out": (out, ref)}
-    for name, a, b in zip(("dq", "dk", "dv", "dqc", "dkc"), g_in, o_in):
+    for name, a, b, p in zip(("dq", "dk", "dv", "dqc", "dkc"), g_in, o_in, p_in):
         if a is not None:
             errs[name] = md(a.grad, b.grad)
+            path[name] = err(p.grad.to(dtype), b.grad, "path " + name)
             pairs[name] = (a.grad, b.grad)
     for name, e in errs.items():
-        if name in net_names:
-            a, b = pairs[name]
-            raw, net = err_both(a, b)
-            assert net < tol, (name, "net", net, "raw", raw, "at (index, |ref|, err)", argmax_err(a, b), errs)
-        else:
-            assert e < tol, (name, errs)
+        bar = bar_for(path[name], tol) if name in path else tol
+        if name in path_names:  # the reference path itself misses the raw bar here (named by the test)
+            assert path[name] >= tol, (name, "reference path meets the raw bar", path[name], errs)
+        assert e < bar, (name, e, "bar", bar, "reference path", path.get(name),
+                         "at (index, |ref|, err)", argmax_err(*pairs[name]) if name in pairs else None, errs)
     for name, a, b in (("dfreqs", gf, of), ("ddelta", gd, od)):
         if a is not None and a.requires_grad:
             rel = md(a.grad, b.grad) / max(1.0, b.grad.abs().max().item())
@@ -149,10 +163,10 @@ def test_split_form_reference_module_shape(cuda):
     scale (64 + 64)^-1/2 (src/model/fpope_attention.py:107,166-177).
 
     dv sums two query heads' gradients per key and reaches |dv| = 7.2 here, where the bf16
-    spacing is 2^-5: any bf16 dv is up to 0.0156 from the exact value there, so dv is held to
-    2e-2 net of its own rounding (raw measured 0.023 at an element of |dv| in [4, 8))."""
+    spacing is 2^-5.  The reference path (bf16 SDPA rounding points) misses the raw 2e-2 bar on dv
+    itself, so dv is held to 1.25 times that path's own error (raw kernel error measured 0.023)."""
     run_case(cuda, Dc=64, Dr=32, Dv=64, Hq=8, Hkv=4, Sq=256, B=2, freqs=O.pope_freqs(32),
-             delta=-torch.rand(32) * 6, seed=50, net_names=("dv",))
+             delta=-torch.rand(32) * 6, seed=50, path_names=("dv",))
 
 
 def test_split_form_fp32(cuda):

@@ -6,13 +6,18 @@ and a shared or per-head phase bias, and compares out, the input gradients and d
 (the reference's expressions: oracle.pope_attention, split_pope_attention, rope_attention,
 attention; fp64 core, operands rounded to bf16 in bf16 mode).
 
-Bars: fp32 1e-5 and bf16 2e-2 max-abs (the north star) where the reference values stay below 4 in
-magnitude.  Above that the bar grows in proportion, 2e-2 * max|ref| / 4 in bf16 (one bf16 spacing
-there is already 0.03, and dS is rounded to bf16 before the dK / dQ products as in any bf16
-backward) and 1e-5 * max|ref| / 4 in fp32; dδ relative to its own scale (2e-2 bf16, 1e-4 fp32).
-300 seeds were run this way without a failure; the worst case, seed 288 (no PE, D = 32, |dK| 6.8,
-error 0.026), is kept here.  Long configurations (lengths 1024-6000) passed for 24 seeds; four are
-kept.
+Bars.  The same graph is also evaluated with the reference path's own attention core: in bf16 mode
+the rounding points of the bf16 fused SDPA the reference calls under autocast
+(oracle.attention_bf16_path: P rounded to bf16 before PV and dV, dS rounded to bf16 before dQ and
+dK, every result rounded to bf16), in fp32 mode the core in float32.  Each result is held to the
+north-star bar (2e-2 bf16, 1e-5 fp32, raw max-abs) wherever the reference path meets it, and to
+1.25 times the reference path's own error where the path itself misses it (bf16 results of
+magnitude above about 4, where one bf16 spacing is already 0.03); dδ relative to its own scale
+(2e-2 bf16, 1e-4 fp32).  Over seeds 0-299 and the long seeds 1000-1023: the reference path missed
+2e-2 in 66 bf16 results; there the kernel's error was at most 1.19 times the path's (seed 257 dv
+0.034 against 0.029) and equal to it in most.  Elsewhere the tightest bf16 result was seed 56's dK
+(kernel 0.0199, path 0.0188), and fp32 stayed within 4.8e-6 (path 3.6e-6).  Seed 288 (no PE, D =
+32, |dK| 6.8: kernel and path both 0.026) is kept; four long configurations are kept.
 """
 
 import math
@@ -62,7 +67,53 @@ def test_random_long_config_matches_oracle(cuda, seed):
     check(cuda, seed, long=True)
 
 
-def check(cuda, seed, long=False):
+def oracle_run(c, x, dout, delta, core=None):
+    """The oracle's graph for configuration ``c`` on fresh float leaves of the inputs ``x`` (and the
+    phase bias ``delta`` in PoPE mode), with the attention core replaced by ``core`` when given;
+    returns {name: result} for out, the input gradients and ddelta."""
+    dt = x["qr"].dtype
+    B, Hq, Hkv, S, Dr, Dc, Dv = c["B"], c["Hq"], c["Hkv"], c["S"], c["Dr"], c["Dc"], c["Dv"]
+    od = torch.bfloat16 if dt == torch.bfloat16 else None
+    ox = {n: t.float().clone().requires_grad_(True) for n, t in x.items()}
+    res = {}
+    if c["mode"] == "pope":
+        freqs = O.pope_freqs(Dr)
+        od_delta = delta.clone().requires_grad_(True)
+        scale = (Dc + 2 * Dr) ** -0.5
+        if Dc:
+            ref, _ = O.split_pope_attention(ox["qc"], ox["kc"], ox["qr"], ox["kr"], ox["v"], freqs, od_delta,
+                                            scale=scale, causal=c["causal"], operand_dtype=od, core=core)
+        else:
+            ref, _ = O.pope_attention(ox["qr"], ox["kr"], ox["v"], freqs, od_delta, scale=scale,
+                                      causal=c["causal"], clamp=False, operand_dtype=od, core=core)
+        res["_pope"] = (freqs, delta, scale)
+    elif c["mode"] == "rope":
+        inv = O.rope_inv_freq(Dr)
+        ref, _ = O.rope_attention(ox["qr"], ox["kr"], ox["v"], inv, qk_norm=c["qk_norm"], causal=c["causal"],
+                                  operand_dtype=od, core=core)
+        res["_rope"] = inv
+    else:
+        ref, _ = (core or O.attention)(O.round_ste(ox["qr"], od), O.round_ste(ox["kr"], od),
+                                       O.round_ste(ox["v"], od), Dr ** -0.5, c["causal"])
+    ref.backward(dout.double() if core is None else dout.to(ref.dtype))
+    res["out"] = ref.detach()
+    for n in x:
+        res["d" + n] = ox[n].grad
+    if c["mode"] == "pope":
+        res["ddelta"] = od_delta.grad
+    return res
+
+
+def fp32_core(q, k, v, scale, causal):
+    """The reference's fp32 attention core: the same expression evaluated in float32."""
+    return O.attention(q, k, v, scale, causal, dtype=torch.float32)
+
+
+def measure(cuda, seed, long=False):
+    """Kernel results, the oracle (fp64 core) and the reference path (bf16 mode: the core with a bf16
+    fused SDPA's rounding points, oracle.attention_bf16_path, and every result rounded to bf16 as the
+    reference returns it for bf16 inputs; fp32 mode: the core in float32) for one seed.  Returns
+    (config, [(name, kernel error, reference-path error, bar)])."""
     c = draw(seed, long)
     g = torch.Generator().manual_seed(seed)
     dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
@@ -72,42 +123,49 @@ def check(cuda, seed, long=False):
               "kc": (B, Hkv, S, Dc)}
     x = {n: torch.randn(*shapes[n], generator=g).to(dt) for n in names}
     dout = torch.randn(B, Hq, S, Dv, generator=g).to(dt)
-    od = torch.bfloat16 if dt == torch.bfloat16 else None
-    ox = {n: t.float().clone().requires_grad_(True) for n, t in x.items()}
-    gx = {n: t.to(cuda).requires_grad_(True) for n, t in x.items()}
-    grads = []
+    delta = None
     if c["mode"] == "pope":
-        freqs = O.pope_freqs(Dr)
         delta = torch.rand((Hkv, Dr) if c["per_head"] else (Dr,), generator=g) * (-2 * math.pi)
-        od_delta, gd = delta.clone().requires_grad_(True), delta.to(cuda).requires_grad_(True)
-        scale = (Dc + 2 * Dr) ** -0.5
-        if Dc:
-            ref, _ = O.split_pope_attention(ox["qc"], ox["kc"], ox["qr"], ox["kr"], ox["v"], freqs, od_delta,
-                                            scale=scale, causal=c["causal"], operand_dtype=od)
-        else:
-            ref, _ = O.pope_attention(ox["qr"], ox["kr"], ox["v"], freqs, od_delta, scale=scale,
-                                      causal=c["causal"], clamp=False, operand_dtype=od)
+    exact = oracle_run(c, x, dout, delta)
+    path = oracle_run(c, x, dout, delta, core=O.attention_bf16_path if dt == torch.bfloat16 else fp32_core)
+    gx = {n: t.to(cuda).requires_grad_(True) for n, t in x.items()}
+    if c["mode"] == "pope":
+        freqs, delta, scale = exact["_pope"]
+        gd = delta.to(cuda).requires_grad_(True)
         out = pe_attention(gx["qr"], gx["kr"], gx["v"], mode="pope", q_c=gx.get("qc"), k_c=gx.get("kc"),
                            freqs=freqs.to(cuda), delta=gd, scale=scale, causal=c["causal"])
-        grads.append(("ddelta", gd, od_delta))
     elif c["mode"] == "rope":
-        inv = O.rope_inv_freq(Dr)
-        ref, _ = O.rope_attention(ox["qr"], ox["kr"], ox["v"], inv, qk_norm=c["qk_norm"], causal=c["causal"],
-                                  operand_dtype=od)
-        out = pe_attention(gx["qr"], gx["kr"], gx["v"], mode="rope", freqs=inv.to(cuda), qk_norm=c["qk_norm"],
-                           causal=c["causal"])
+        out = pe_attention(gx["qr"], gx["kr"], gx["v"], mode="rope", freqs=exact["_rope"].to(cuda),
+                           qk_norm=c["qk_norm"], causal=c["causal"])
     else:
-        ref, _ = O.attention(O.round_ste(ox["qr"], od), O.round_ste(ox["kr"], od), O.round_ste(ox["v"], od),
-                             Dr ** -0.5, c["causal"])
         out = pe_attention(gx["qr"], gx["kr"], gx["v"], mode="none", causal=c["causal"])
-    ref.backward(dout.double())
     out.backward(dout.to(cuda))
     torch.cuda.synchronize()
+    kern = {"out": out} | {"d" + n: gx[n].grad for n in names}
     base = 2e-2 if dt == torch.bfloat16 else 1e-5
-    for n, a, b in [("out", out, ref)] + [("d" + n, gx[n].grad, ox[n].grad) for n in names]:
-        mx = b.detach().abs().max().item() if b.numel() else 0.0
-        bar = base * max(1.0, mx / 4)
-        assert err(a, b) < bar, (seed, c, n, err(a, b), bar)
-    for n, a, b in grads:
-        rel = err(a, b) / max(1.0, b.abs().max().item())
-        assert rel < (2e-2 if dt == torch.bfloat16 else 1e-4), (seed, c, n, rel)
+    rows = []
+    for n, a in kern.items():
+        p = path[n].to(dt) if dt == torch.bfloat16 else path[n]
+        pe = err(p, exact[n], f"path {n}")
+        rows.append((n, err(a, exact[n], n), pe, bar_for(pe, base)))
+    if c["mode"] == "pope":
+        b = exact["ddelta"]
+        rel = err(gd.grad, b) / max(1.0, b.abs().max().item())
+        rows.append(("ddelta", rel, None, 2e-2 if dt == torch.bfloat16 else 1e-4))
+    return c, rows
+
+
+# Where the reference path meets the north-star bar the kernel is held to it.  Where the reference
+# path itself misses it (bf16 results of magnitude above about 4, where one bf16 spacing is 0.03),
+# the kernel is held to 1.25 times the reference path's own error at the same elements.
+PATH_FACTOR = 1.25
+
+
+def bar_for(path_err, base):
+    return base if path_err < base else PATH_FACTOR * path_err
+
+
+def check(cuda, seed, long=False):
+    c, rows = measure(cuda, seed, long)
+    for n, ke, pe, bar in rows:
+        assert ke < bar, (seed, c, n, "kernel", ke, "reference path", pe, "bar", bar)

@@ -360,3 +360,80 @@ def test_positions_in_input_dtype(dtype, bits, top):
     f = O.pope_freqs(8)
     assert torch.equal(O.pope_phases(20, f, 300, pos_dtype=torch.bfloat16),
                        torch.outer(O.positions(20, 300, torch.bfloat16), f))
+
+
+# ------------------------------------------------------------------ reference path (bf16 SDPA)
+
+def _qkv(seed, B, Hq, Hkv, S, D, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(*s, generator=g).to(dtype) for s in
+            ((B, Hq, S, D), (B, Hkv, S, D), (B, Hkv, S, D), (B, Hq, S, D))]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_bf16_path_without_rounding_is_the_exact_core(monkeypatch, causal):
+    """With its rounding points switched off, attention_bf16_path is the fp64 core: the forward,
+    lse and the hand-written backward (Di, dS, dQ, dK, dV and the GQA fold) equal autograd through
+    oracle.attention.  A dropped term, a wrong sign or a transposed operand in the backward fails."""
+    monkeypatch.setattr(O, "_bf16", lambda x: x)
+    q, k, v, do = (t.double() for t in _qkv(3, 2, 4, 2, 37, 16, torch.float64))
+    a = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    b = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    oa, la = O.attention(*a, 0.3, causal)
+    ob, lb = O.attention_bf16_path(*b, 0.3, causal)
+    oa.backward(do)
+    ob.backward(do)
+    assert torch.allclose(oa, ob, atol=1e-12) and torch.allclose(la, lb, atol=1e-12)
+    for x, y in zip(a, b):
+        assert torch.allclose(x.grad, y.grad, atol=1e-12)
+
+
+def test_bf16_path_tracks_torch_bf16_sdpa():
+    """The rounding points are those of a bf16 fused SDPA: against torch's own bf16
+    F.scaled_dot_product_attention (CPU flash kernel), out and dQ agree to one bf16 spacing at their
+    largest magnitude and
+    have the same largest error to the exact core (within 25 %); dK / dV, which the fused GPU kernels accumulate
+    in fp32 over every query block, carry at most torch's CPU error.  Both miss the 2e-2 bar on dv
+    at |dv| ~ 5, which is why the GPU parity tests measure the path beside the kernel."""
+    q, k, v, do = _qkv(0, 1, 2, 2, 300, 64)
+    ts = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    o = F.scaled_dot_product_attention(*ts, is_causal=True)
+    o.backward(do)
+    ex = [t.double().requires_grad_(True) for t in (q, k, v)]
+    oe, _ = O.attention(*ex, 64 ** -0.5, True)
+    oe.backward(do.double())
+    pa = [t.double().requires_grad_(True) for t in (q, k, v)]
+    op, _ = O.attention_bf16_path(*pa, 64 ** -0.5, True)
+    op.backward(do.double())
+    ulp = lambda x: 2.0 ** (math.floor(math.log2(x)) - 7)  # bf16 spacing at magnitude x
+    e_torch = {"out": o, "dq": ts[0].grad, "dk": ts[1].grad, "dv": ts[2].grad}
+    e_path = {"out": op, "dq": pa[0].grad, "dk": pa[1].grad, "dv": pa[2].grad}
+    e_ex = {"out": oe, "dq": ex[0].grad, "dk": ex[1].grad, "dv": ex[2].grad}
+    for n in ("out", "dq"):
+        d = (e_torch[n].double() - e_path[n].double()).abs().max().item()
+        assert d <= ulp(e_ex[n].abs().max().item()), (n, d)
+        et = (e_torch[n].double() - e_ex[n]).abs().max().item()
+        ep = (e_path[n].double() - e_ex[n]).abs().max().item()
+        assert 0.75 * et <= ep <= 1.25 * et, (n, et, ep)
+    for n in ("dk", "dv"):
+        et = (e_torch[n].double() - e_ex[n]).abs().max().item()
+        ep = (e_path[n].double() - e_ex[n]).abs().max().item()
+        assert 0 < ep <= et, (n, et, ep)
+    assert (e_path["dv"].double() - e_ex["dv"]).abs().max().item() > 0.005
+    assert (e_torch["dv"].double() - e_ex["dv"]).abs().max().item() > 2e-2
+
+
+def test_bf16_path_gqa_fold():
+    """GQA: per-head gradients are rounded to bf16 by the core, then summed over the kv head's query
+    group (repeat_interleave backward), equal to running the expanded heads and summing."""
+    q, k, v, do = (t.double() for t in _qkv(5, 1, 4, 2, 40, 16))
+    a = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    o, _ = O.attention_bf16_path(*a, 0.25, True)
+    o.backward(do)
+    b = [q.clone().requires_grad_(True), k.repeat_interleave(2, 1).requires_grad_(True),
+         v.repeat_interleave(2, 1).requires_grad_(True)]
+    o2, _ = O.attention_bf16_path(*b, 0.25, True)
+    o2.backward(do)
+    assert torch.equal(o, o2) and torch.equal(a[0].grad, b[0].grad)
+    assert torch.equal(a[1].grad, b[1].grad.view(1, 2, 2, 40, 16).sum(2))
+    assert torch.equal(a[2].grad, b[2].grad.view(1, 2, 2, 40, 16).sum(2))
