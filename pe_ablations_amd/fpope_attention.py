@@ -135,12 +135,25 @@ class KVCache:
         self.v = None
         self.length = 0
 
-    def ensure(self, B: int, Hkv: int, capacity: int, wk: int, wv: int, dtype, device) -> None:
+    def ensure(self, B: int, Hkv: int, capacity: int, wk: int, wv: int, dtype, device, keep: int = 0) -> None:
+        """Buffers of this shape, dtype and device.  When they have to be replaced, the first ``keep``
+        rows (those a chunk at start_pos = keep still attends to) are carried over into the new ones;
+        a change of batch, heads or row widths cannot keep them and raises."""
         shape_k, shape_v = (B, Hkv, capacity, wk), (B, Hkv, capacity, wv)
-        if (self.k is None or tuple(self.k.shape) != shape_k or tuple(self.v.shape) != shape_v
-                or self.k.dtype != dtype or self.k.device != device):
-            self.k = torch.zeros(shape_k, dtype=dtype, device=device)
-            self.v = torch.zeros(shape_v, dtype=dtype, device=device)
+        if (self.k is not None and tuple(self.k.shape) == shape_k and tuple(self.v.shape) == shape_v
+                and self.k.dtype == dtype and self.k.device == device):
+            return
+        old_k, old_v = self.k, self.v
+        keep = min(keep, self.length)
+        if keep > 0 and (old_k is None or old_k.shape[:2] != (B, Hkv) or old_k.shape[3] != wk
+                         or old_v.shape[3] != wv or keep > capacity):
+            raise ValueError(f"the cache holds {self.length} rows for another batch / head / width layout; "
+                             "start over at start_pos = 0")
+        self.k = torch.zeros(shape_k, dtype=dtype, device=device)
+        self.v = torch.zeros(shape_v, dtype=dtype, device=device)
+        if keep > 0:
+            self.k[:, :, :keep] = old_k[:, :, :keep].to(device=device, dtype=dtype)
+            self.v[:, :, :keep] = old_v[:, :, :keep].to(device=device, dtype=dtype)
 
     def reset(self) -> None:
         self.k = None
@@ -178,11 +191,13 @@ def cached_attention(cache: KVCache, capacity: int, start_pos: int, *, q, k, v, 
         raise ValueError(f"cache rows {start_pos}..{start_pos + S - 1} exceed max_cache_len {capacity}")
     cdt = cache_compute_dtype(k)
     wk, wv = cache_widths(mode=mode, d_content=0 if k_c is None else k_c.shape[-1], d_pe=k.shape[-1], d_v=d_v)
-    cache.ensure(B, Hkv, capacity, wk, wv, cdt, k.device)
-    if start_pos == 0:
-        cache.length = 0
-    elif start_pos != cache.length:
-        raise ValueError(f"the cache holds {cache.length} rows; the next chunk must start there, not at {start_pos}")
+    if start_pos > cache.length:
+        raise ValueError(f"the cache holds {cache.length} rows; a chunk at {start_pos} would leave a gap "
+                         "(start at or before the cached length)")
+    cache.ensure(B, Hkv, capacity, wk, wv, cdt, k.device, keep=start_pos)
+    # a chunk at start_pos <= length overwrites rows start_pos.. and ends the cache after itself, as
+    # the reference's cache update does (src/model/fpope_attention.py:296-302)
+    cache.length = start_pos
     pe_cache_append(k, v, cache.k, cache.v, start_pos=start_pos, mode=mode, k_c=k_c, freqs=freqs, delta=delta,
                     rope_mscale=rope_mscale, qk_norm=qk_norm, position_dtype=position_dtype)
     cache.length = start_pos + S
@@ -200,8 +215,9 @@ class FPoPEGroupedQueryAttentionWithCache(FPoPEGroupedQueryAttention):
     ``v_cache`` / ``cache_len`` / ``reset_cache`` and ``forward(x, mask, start_pos, use_cache)``.
     With ``use_cache`` the new keys are transformed once into the cache (pe_attn_cache_append) and
     the new queries attend to all ``cache_len`` cached rows under the bottom-right mask
-    (pe_attn_decode); chunks must arrive in order (start_pos = the current cache length, or 0 to
-    start over)."""
+    (pe_attn_decode).  A chunk may start at any start_pos up to the current cache length (the
+    length after it is start_pos + S, so an earlier start_pos rewinds); a later one would leave a
+    gap of rows never written and raises."""
 
     def __init__(self, hidden_dim: int, num_heads: int, num_kv_heads: int, head_dim: int = 64,
                  d_rope: int = 32, use_qk_norm: bool = True, fpope: Optional[nn.Module] = None,

@@ -251,26 +251,52 @@ class Transformer(nn.Module):
         Unlike the reference, which re-runs the whole sequence for every new token, the prompt is
         run once (prefill) and every layer keeps a cache of transformed keys and values sized for
         P + max_new_tokens; each further step feeds one token through the caches (the split-key
-        decode kernel).  The caches are freed on return."""
+        decode kernel).  As in the reference, the PE tables are extended only when the running
+        length passes max_seq_len, to that length.  An extension that changes the kernel
+        frequencies (YaRN reverts to the plain RoPE table) invalidates the cached rows, so the
+        whole sequence is then run again through fresh caches, which is what the reference's
+        full re-run computes.  The caches are freed on return."""
         self.eval()
         B, P = input_ids.shape
         total = P + max_new_tokens
-        if total > self.config.max_seq_len:
-            self.extend_context_length(total)
         for layer in self.layers:
             layer.attention.max_cache_len = max(layer.attention.max_cache_len, total)
-        self.reset_caches()
-        tokens = [input_ids]
+
+        def prefill(ids):
+            self.reset_caches()
+            return self.forward(ids, start_pos=0, use_cache=True)["logits"][:, -1, :]
+
+        seq = input_ids
         try:
-            logits = self.forward(input_ids, start_pos=0, use_cache=True)["logits"][:, -1, :]
+            if P > self.config.max_seq_len:
+                self.extend_context_length(P)
+            logits = prefill(seq)
             for step in range(max_new_tokens):
                 nxt = _next_token(logits, temperature, top_k, top_p)
-                tokens.append(nxt)
-                if step + 1 < max_new_tokens:
-                    logits = self.forward(nxt, start_pos=P + step, use_cache=True)["logits"][:, -1, :]
+                seq = torch.cat([seq, nxt], dim=1)
+                if step + 1 == max_new_tokens:
+                    break
+                n = seq.shape[1]
+                if n > self.config.max_seq_len:
+                    before = self._kernel_tables()
+                    self.extend_context_length(n)
+                    after = self._kernel_tables()
+                    if any(not torch.equal(a, b) for a, b in zip(before, after)):
+                        logits = prefill(seq)
+                        continue
+                logits = self.forward(nxt, start_pos=n - 1, use_cache=True)["logits"][:, -1, :]
         finally:
             self.reset_caches()
-        return torch.cat(tokens, dim=1)
+        return seq
+
+    def _kernel_tables(self) -> list:
+        """Copies of what the kernels read from the RoPE module (frequencies, mscale): rows cached
+        under one set are invalid under another.  The PoPE / FoPE extensions only lengthen their
+        position tables (src/model/pope.py:106-122, src/model/fpope.py:246-264); their frequencies
+        and phase bias stay, so cached rows stay valid."""
+        if self.rope is None:
+            return []
+        return [self.rope.kernel_inv_freq().detach().clone(), torch.tensor(self.rope.kernel_mscale())]
 
 
 def _next_token(logits: torch.Tensor, temperature: float, top_k: Optional[int], top_p: Optional[float]) -> torch.Tensor:

@@ -30,9 +30,20 @@ def test_tuned_file_validators_name_this_gpu():
 
 
 def test_use_tuned_gemms_reports_what_it_did():
-    msg = gemm_select.use_tuned_gemms()
-    if not torch.cuda.is_available():
-        assert msg == "hipBLASLt default heuristic (no GPU)"
-    else:
-        assert "TunableOp" in msg or "default heuristic" in msg
-    assert not any(n.startswith("pe_tunableop_") for n in os.listdir(os.path.dirname(gemm_select.TUNED_FILE)))
+    """use_tuned_gemms switches TunableOp on for the whole process; the test puts torch's TunableOp
+    state back afterwards so that later tests' GEMMs do not depend on whether this one ran."""
+    from torch.cuda import tunable
+    gpu = torch.cuda.is_available()  # the TunableOp calls need a device
+    state = (tunable.is_enabled(), tunable.tuning_is_enabled(), tunable.get_filename()) if gpu else None
+    try:
+        msg = gemm_select.use_tuned_gemms()
+        if not torch.cuda.is_available():
+            assert msg == "hipBLASLt default heuristic (no GPU)"
+        else:
+            assert "TunableOp" in msg or "default heuristic" in msg
+        assert not any(n.startswith("pe_tunableop_") for n in os.listdir(os.path.dirname(gemm_select.TUNED_FILE)))
+    finally:
+        if gpu:
+            tunable.enable(state[0])
+            tunable.tuning_enable(state[1])
+            tunable.set_filename(state[2])

@@ -149,21 +149,58 @@ def test_generate_greedy_follows_oracle_argmax(cuda, case):
             assert logits[b, out[b, t]].item() >= logits[b].max().item() - 1e-4, (case, t, b)
 
 
-def test_fused_form_module_matches_oracle(cuda):
-    """d_content = 0: the legacy fused form, q = PoPE(RMSNorm(wq_r x)) with scale 1/sqrt(head_dim)."""
-    torch.manual_seed(14)
-    pe = PoPEEmbedding(64, 512, delta_init="uniform")
-    m = FPoPEGroupedQueryAttention(128, 4, 2, 64, 64, fpope=pe, d_content=0)
-    x = torch.randn(2, 70, 128)
-    B, S = 2, 70
-    qr = O.rms_norm(x @ m.wq_r.weight.T, m.qr_norm.weight).view(B, S, 4, 64).transpose(1, 2)
-    kr = O.rms_norm(x @ m.wk_r.weight.T, m.kr_norm.weight).view(B, S, 2, 64).transpose(1, 2)
-    v = (x @ m.wv.weight.T).view(B, S, 2, 64).transpose(1, 2)
-    ref, _ = O.pope_attention(qr, kr, v, pe.effective_freqs, pe.phase_bias, scale=64 ** -0.5, start_q=3,
-                              start_k=3)
-    ref = ref.float().transpose(1, 2).reshape(B, S, -1) @ m.wo.weight.T
-    out = m.to(cuda)(x.to(cuda), start_pos=3)
-    assert md(out, ref) < 1e-4
+def test_generate_yarn_crossing_max_seq_len_follows_oracle(cuda, monkeypatch):
+    """YaRN generation that runs past max_seq_len.  The reference extends the tables when the
+    running length passes max_seq_len (src/model/transformer.py:412-414), and YaRN's extension
+    rebuilds the plain RoPE table with mscale kept (src/model/rope.py:103-119), under which the
+    whole sequence is re-run.  With a 100-token prompt and max_seq_len 103, the logits behind tokens
+    100..103 follow the YaRN table and those behind 104 and 105 the plain one: every step's logits
+    (captured on their way to the sampler) equal the oracle's under the right table, and differ
+    from the oracle's under the other table after the crossing."""
+    from pe_ablations_amd import transformer as TR
+    seen = []
+    real = TR._next_token
+    monkeypatch.setattr(TR, "_next_token", lambda lg, *a: (seen.append(lg.detach().cpu()), real(lg, *a))[1])
+    cfg, m = make("rope_yarn", seed=16)
+    for c in (cfg, m.config):
+        c.max_seq_len = 103
+    m.rope.max_seq_len = 103
+    prompt = ids_for(cfg, 2, 100, seed=17)
+    out = m.to(cuda).eval().generate(prompt.to(cuda), max_new_tokens=6, temperature=0.0).cpu()
+    assert out.shape == (2, 106) and m.config.max_seq_len == 105 and len(seen) == 6
+    sd = {k: v.cpu() for k, v in m.state_dict().items()}
+    for i, t in enumerate(range(100, 106)):
+        right = O.decoder_forward(sd, cfg, out[:, :t], yarn_extended=t > 103)["logits"][:, -1]
+        assert md(seen[i], right) < 1e-4, (t, md(seen[i], right))
+        assert torch.equal(out[:, t], seen[i].argmax(-1))
+        if t > 103:
+            wrong = O.decoder_forward(sd, cfg, out[:, :t])["logits"][:, -1]
+            assert md(seen[i], wrong) > 3e-4, (t, md(seen[i], wrong))
+
+
+def test_kv_cache_rewind_growth_and_gap(cuda):
+    """The cache path accepts any start_pos up to the cached length, as the reference's does
+    (src/model/fpope_attention.py:296-302): a chunk at an earlier start_pos overwrites the rows from
+    there and the length becomes start_pos + S.  Growing max_cache_len mid-sequence keeps the rows
+    cached so far; a start_pos past the cached length (rows never written) raises."""
+    torch.manual_seed(18)
+    pe = PoPEEmbedding(32, 512, delta_init="uniform")
+    m = FPoPEGroupedQueryAttentionWithCache(128, 4, 2, 32, 32, fpope=pe, max_cache_len=48).to(cuda)
+    x = torch.randn(1, 40, 128, device=cuda)
+    other = torch.randn(1, 6, 128, device=cuda)
+    with torch.no_grad():
+        full = m(x)
+        m(x[:, :30], use_cache=True)
+        m(other, start_pos=30, use_cache=True)          # rows 30..35 hold other tokens
+        assert m.cache_len == 36
+        outs = [m(x[:, 30:33], start_pos=30, use_cache=True)]   # rewind: overwrite from 30
+        assert m.cache_len == 33
+        m.max_cache_len = 64                               # larger buffers, rows 0..32 carried over
+        outs += [m(x[:, t:t + 1], start_pos=t, use_cache=True) for t in range(33, 40)]
+        assert tuple(m.k_cache.shape[:3]) == (1, 2, 64) and m.cache_len == 40
+        with pytest.raises(ValueError, match="gap"):
+            m(x[:, :1], start_pos=41, use_cache=True)
+    assert md(torch.cat(outs, 1), full[:, 30:40]) < 1e-5
 
 
 def test_fused_form_kv_cache_decode(cuda):
