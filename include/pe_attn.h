@@ -231,6 +231,19 @@ int pe_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t x_row_stride, int64_t
                    const void* weight, int32_t weight_dtype, float eps,
                    void* y, int32_t y_dtype, int64_t y_row_stride, void* stream);
 
+/* RMSNorm backward for pe_rmsnorm_fwd's expression, as autograd differentiates it in fp32
+ * (src/model/normalization.py:22-27): from dy (y's dtype: bf16 exactly when x and weight are both
+ * bf16) writes dx (x's dtype) and the weight gradient dw (weight's dtype, summed over the rows in a
+ * fixed order, bitwise reproducible).  Same shape and alignment rules as pe_rmsnorm_fwd; the
+ * workspace (pe_rmsnorm_bwd_workspace_bytes) holds per-workgroup partial sums of dw.  The training
+ * path of the fused position-projection norm (pe_attn_fwd_normed) runs it after pe_attn_bwd, which
+ * no reference interface exposes as one call: it replaces the autograd of RMSNorm.forward. */
+size_t pe_rmsnorm_bwd_workspace_bytes(int64_t rows, int32_t n);
+int pe_rmsnorm_bwd(const void* x, int32_t x_dtype, int64_t x_row_stride, int64_t rows, int32_t n,
+                   const void* weight, int32_t weight_dtype, float eps,
+                   const void* dy, int64_t dy_row_stride, void* dx, int64_t dx_row_stride, void* dw,
+                   void* workspace, size_t ws_bytes, void* stream);
+
 /* SwiGLU forward of the feed-forward block (src/model/ffn.py:17-27, SwiGLU.forward(x, gate) =
  * F.silu(gate) * x): out = bf16(bf16(gate / (1 + exp(-gate))) * x) element by element over n
  * contiguous bf16 values, bitwise what torch computes for the two bf16 ops.  n % 8 == 0, 16-byte

@@ -199,8 +199,11 @@ def qk_l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """x * rsqrt(mean(x^2) + eps) in fp32, cast back, then * weight (src/model/normalization.py:22-27)."""
-    out = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps)).type_as(x)
+    """x * rsqrt(mean(x^2) + eps) in fp32, cast back, then * weight (src/model/normalization.py:22-27).
+    One cast to fp32 feeds both uses of x, as in the reference's self._norm(x.float()), so that under
+    autograd the two gradient parts are summed in fp32 and rounded to x's dtype once."""
+    xf = x.float()
+    out = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).type_as(x)
     return out * weight
 
 

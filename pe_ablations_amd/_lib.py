@@ -31,7 +31,7 @@ EXPORTED = [
     "pe_attn_set_stage_events", "pe_attn_transform_bwd_workspace_bytes", "pe_attn_transform_bwd",
     "pe_attn_fwd_normed", "pe_rmsnorm_fwd", "pe_attn_fwd_noalloc", "pe_attn_noalloc_scratch_bytes",
     "pe_attn_value_width", "pe_attn_cache_append", "pe_attn_decode_workspace_bytes", "pe_attn_decode",
-    "pe_swiglu_fwd",
+    "pe_swiglu_fwd", "pe_rmsnorm_bwd_workspace_bytes", "pe_rmsnorm_bwd",
 ]
 
 # kernel stages bracketed by pe_attn_set_stage_events
@@ -117,6 +117,11 @@ def lib():
             i32, i64 = ctypes.c_int32, ctypes.c_int64
             L.pe_rmsnorm_fwd.argtypes = [vp, i32, i64, i64, i32, vp, i32, ctypes.c_float, vp, i32, i64, vp]
             L.pe_rmsnorm_fwd.restype = ctypes.c_int
+            L.pe_rmsnorm_bwd_workspace_bytes.argtypes = [i64, i32]
+            L.pe_rmsnorm_bwd_workspace_bytes.restype = sz
+            L.pe_rmsnorm_bwd.argtypes = [vp, i32, i64, i64, i32, vp, i32, ctypes.c_float, vp, i64, vp, i64, vp,
+                                         vp, sz, vp]
+            L.pe_rmsnorm_bwd.restype = ctypes.c_int
             L.pe_swiglu_fwd.argtypes = [vp, vp, vp, i64, vp]
             L.pe_swiglu_fwd.restype = ctypes.c_int
             L.pe_attn_fwd_noalloc.argtypes = [P, T, T, T, T, T, vp, vp, T, vp, vp]

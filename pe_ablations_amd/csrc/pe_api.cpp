@@ -637,6 +637,35 @@ int pe_rmsnorm_fwd(const void* x, int32_t x_dtype, int64_t x_row_stride, int64_t
   return pe::launch_rmsnorm(a, (hipStream_t)stream);
 }
 
+// the backward's row partition assumes MI355X's 256 compute units in both the workspace size and
+// the launch, so the size a caller allocated always matches the launch
+constexpr int kNormBwdCus = 256;
+
+size_t pe_rmsnorm_bwd_workspace_bytes(int64_t rows, int32_t n) {
+  if (rows <= 0 || n <= 0) return 0;
+  return align_up((size_t)pe::rmsnorm_bwd_part_floats(rows, n, kNormBwdCus) * 4);
+}
+
+int pe_rmsnorm_bwd(const void* x, int32_t x_dtype, int64_t x_row_stride, int64_t rows, int32_t n,
+                   const void* weight, int32_t weight_dtype, float eps, const void* dy, int64_t dy_row_stride,
+                   void* dx, int64_t dx_row_stride, void* dw, void* workspace, size_t ws_bytes, void* stream) {
+  if (!x || !weight || !dy || !dx || !dw || !workspace) return PE_ERR_NULL;
+  if (rows <= 0 || n <= 0) return PE_ERR_SHAPE;
+  if (ws_bytes < pe_rmsnorm_bwd_workspace_bytes(rows, n)) return PE_ERR_WORKSPACE;
+  int rc = device_ok();
+  if (rc) return rc;
+  pe::NormBwdArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = x; a.x_dtype = x_dtype; a.x_rs = x_row_stride;
+  a.w = weight; a.w_dtype = weight_dtype;
+  a.dy = dy; a.dy_rs = dy_row_stride;
+  a.dx = dx; a.dx_rs = dx_row_stride;
+  a.dw = dw; a.dw_dtype = weight_dtype;
+  a.part = (float*)workspace;
+  a.rows = rows; a.n = n; a.eps = eps;
+  return pe::launch_rmsnorm_bwd(a, kNormBwdCus, (hipStream_t)stream);
+}
+
 int pe_swiglu_fwd(const void* x, const void* gate, void* out, int64_t n, void* stream) {
   if (!x || !gate || !out) return PE_ERR_NULL;
   if (n < 0 || n % 8 != 0) return PE_ERR_SHAPE;

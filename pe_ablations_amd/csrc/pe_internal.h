@@ -163,6 +163,22 @@ struct NormArgs {
   int64_t rows; int n; float eps;
 };
 int launch_rmsnorm(const NormArgs& a, hipStream_t s);
+// RMSNorm backward: dx (x's dtype) and the weight gradient dw (the weight's dtype) from
+// dy (y's dtype, bf16 exactly when x and w are both bf16); per-workgroup partial sums of dw go to
+// `part` ([groups][n] fp32) and are summed in workgroup order by a second launch
+struct NormBwdArgs {
+  const void* x; int x_dtype; int64_t x_rs;
+  const void* w; int w_dtype;
+  const void* dy; int64_t dy_rs;
+  void* dx; int64_t dx_rs;
+  void* dw; int dw_dtype;
+  float* part;
+  int64_t rows; int n; float eps;
+  int rpw;  // rows per wave (a workgroup of WPB waves covers WPB * rpw consecutive rows)
+};
+// fp32 floats of partial-sum workspace launch_rmsnorm_bwd needs for rows x n
+int64_t rmsnorm_bwd_part_floats(int64_t rows, int n, int n_cu);
+int launch_rmsnorm_bwd(NormBwdArgs a, int n_cu, hipStream_t s);
 // silu(gate) * x over n bf16 elements (n % 8 == 0, 16-byte aligned pointers)
 int launch_swiglu(const void* x, const void* gate, void* out, int64_t n, hipStream_t s);
 

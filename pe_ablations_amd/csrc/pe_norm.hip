@@ -194,6 +194,146 @@ int launch_rmsnorm(const NormArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
+// RMSNorm backward (the autograd of rmsnorm_kernel's expression, src/model/normalization.py:22-27,
+// in fp32): with r = rsqrt(mean(x^2) + eps) (the forward's sum, in the forward's order) and
+// nc = (x r) rounded to x's dtype,
+//   gc = (dy w) rounded to x's dtype   (the product in y's dtype, the gradient of the cast value)
+//   c  = sum_j gc_j x_j                 (the gradient reaching r through x * r)
+//   dx = gc r + x (2/n) (-r^3 c / 2)    (rsqrt's and mean's gradients), rounded to x's dtype
+//   dw = sum over rows of (dy nc)       (each product rounded to y's dtype when y is bf16; the sum
+//                                         in fp32, rounded to the weight's dtype)
+// One wave per row, rpw consecutive rows per wave.  Each lane accumulates dw for its own chunks
+// over its rows; the WPB waves of a workgroup add theirs through LDS in wave order, one 512-feature
+// slab at a time, into the workgroup's partial row, which rmsnorm_dw_reduce_kernel sums in
+// workgroup order.  Fixed order throughout: the result is bitwise reproducible.
+template <int CPL>
+__global__ __launch_bounds__(WPB * 64) void rmsnorm_bwd_kernel(NormBwdArgs a) {
+  __shared__ __attribute__((aligned(16))) float slab[WPB][64 * 8];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nch = a.n >> 3;
+  const bool x_bf = a.x_dtype == 0, y_bf = a.x_dtype == 0 && a.w_dtype == 0;
+  const int ydt = y_bf ? 0 : 1;
+  float dwa[CPL][8];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dwa[k][e] = 0.f;
+  const int64_t row0 = ((int64_t)blockIdx.x * WPB + w) * a.rpw;
+  for (int i = 0; i < a.rpw; ++i) {
+    const int64_t row = row0 + i;
+    if (row >= a.rows) break;
+    float x[CPL][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = lane + k * 64;
+      if (c < nch) {
+        load8(a.x, row * a.x_rs + c * 8, a.x_dtype, x[k]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[k][e] * x[k][e];
+      }
+    }
+    const float r = rsqrtf(wave_sum(ss) * (1.0f / (float)a.n) + a.eps);
+    float gc[CPL][8];
+    float cs = 0.f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = lane + k * 64;
+      if (c < nch) {
+        float dy[8], wv[8];
+        load8(a.dy, row * a.dy_rs + c * 8, ydt, dy);
+        load8(a.w, c * 8, a.w_dtype, wv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float g = dy[e] * wv[e];
+          if (y_bf) g = round_bf16(g);
+          if (x_bf) g = round_bf16(g);
+          gc[k][e] = g;
+          cs += g * x[k][e];
+          float nc = x[k][e] * r;
+          if (x_bf) nc = round_bf16(nc);
+          float p = dy[e] * nc;
+          if (y_bf) p = round_bf16(p);
+          dwa[k][e] += p;
+        }
+      }
+    }
+    const float cr = wave_sum(cs) * (-0.5f * r * r * r) * (2.0f / (float)a.n);
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+      const int c = lane + k * 64;
+      if (c < nch) {
+        float dx[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dx[e] = gc[k][e] * r + x[k][e] * cr;
+        store8(a.dx, row * a.dx_rs + c * 8, a.x_dtype, dx);
+      }
+    }
+  }
+  // the workgroup's partial dw row: waves add in order, 512 features (one chunk per lane) a slab
+  float* prow = a.part + (int64_t)blockIdx.x * a.n;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    if (64 * k >= nch) break;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) slab[w][lane * 8 + e] = dwa[k][e];
+    __syncthreads();
+    for (int f = threadIdx.x; f < 64 * 8; f += WPB * 64) {
+      const int c = k * 64 + f / 8;
+      if (c < nch) {
+        float acc = slab[0][f];
+#pragma unroll
+        for (int ww = 1; ww < WPB; ++ww) acc += slab[ww][f];
+        prow[k * 512 + f] = acc;
+      }
+    }
+  }
+}
+
+// dw[f] = sum of the groups' partial rows in group order, rounded to dw's dtype
+__global__ __launch_bounds__(256) void rmsnorm_dw_reduce_kernel(const float* __restrict__ part, int groups, int n,
+                                                                void* dw, int dw_dtype) {
+  const int f = blockIdx.x * 256 + threadIdx.x;
+  if (f >= n) return;
+  float acc = 0.f;
+  for (int g = 0; g < groups; ++g) acc += part[(int64_t)g * n + f];
+  store_from_float(dw, f, dw_dtype, acc);
+}
+
+// rows per wave: about two workgroups per compute unit, at most 32 rows per wave
+static int bwd_rows_per_wave(int64_t rows, int n_cu) {
+  const int64_t waves = (int64_t)WPB * 2 * (n_cu > 0 ? n_cu : 256);
+  int64_t r = (rows + waves - 1) / waves;
+  return (int)(r < 1 ? 1 : (r > 32 ? 32 : r));
+}
+
+int64_t rmsnorm_bwd_part_floats(int64_t rows, int n, int n_cu) {
+  const int64_t per = (int64_t)WPB * bwd_rows_per_wave(rows, n_cu);
+  return ((rows + per - 1) / per) * (int64_t)n;
+}
+
+int launch_rmsnorm_bwd(NormBwdArgs a, int n_cu, hipStream_t s) {
+  if (a.rows <= 0 || a.rows > 0x7fffffff || a.n <= 0) return -2;
+  if (a.n % 8 != 0 || a.n > 64 * MAXCPL * 8) return -3;
+  if ((a.x_dtype | a.w_dtype) & ~1) return -4;
+  if (a.dw_dtype != a.w_dtype) return -4;
+  const int ydt = (a.x_dtype == 0 && a.w_dtype == 0) ? 0 : 1;
+  if (!rows_aligned(a.x, a.x_dtype, a.x_rs, 0, 0) || !rows_aligned(a.dy, ydt, a.dy_rs, 0, 0) ||
+      !rows_aligned(a.dx, a.x_dtype, a.dx_rs, 0, 0) || ((uintptr_t)a.w % 16) != 0 || ((uintptr_t)a.part % 16) != 0)
+    return -5;
+  a.rpw = bwd_rows_per_wave(a.rows, n_cu);
+  const int64_t per = (int64_t)WPB * a.rpw;
+  const int groups = (int)((a.rows + per - 1) / per);
+  with_cpl(chunks_per_lane(a.n >> 3), [&](auto c) {
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<decltype(c)::value>), dim3(groups), dim3(WPB * 64), 0, s, a);
+  });
+  if (hipGetLastError() != hipSuccess) return -7;
+  hipLaunchKernelGGL(rmsnorm_dw_reduce_kernel, dim3((a.n + 255) / 256), dim3(256), 0, s, (const float*)a.part, groups,
+                     a.n, a.dw, a.dw_dtype);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
 // SwiGLU of the feed-forward block, silu(gate) * x over bf16 (src/model/ffn.py:17-27), as torch
 // evaluates F.silu(gate) * x: the silu in fp32 as g / (1 + exp(-g)) rounded to bf16, then the
 // product in fp32 rounded to bf16, so the result is bitwise torch's; one pass over the two inputs

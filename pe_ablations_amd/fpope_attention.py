@@ -67,10 +67,12 @@ class FPoPEGroupedQueryAttention(nn.Module):
         self.scale = (self.d_content + d_rope * 2) ** -0.5 if self.d_content else head_dim ** -0.5
 
     def _fuse_norm(self, x: torch.Tensor) -> bool:
-        """Inference with PoPE / FoPE and QK RMSNorm on the GPU: the norm runs inside the
-        transform kernel (pe_attn_fwd_normed) instead of as a separate op."""
+        """PoPE / FoPE with QK RMSNorm on the GPU: the norm runs inside the transform kernel
+        (pe_attn_fwd_normed) instead of as a separate op; in training its backward follows the
+        attention backward (pe_rmsnorm_bwd), with the same gradients for the projections and the
+        norm weights as the module's RMSNorm under autograd."""
         return (x.is_cuda and self.qr_norm is not None and self.fpope is not None
-                and not torch.is_grad_enabled() and self.qr_norm.eps == self.kr_norm.eps
+                and self.qr_norm.eps == self.kr_norm.eps
                 and self.qr_norm.weight.dtype == self.kr_norm.weight.dtype)
 
     def _project(self, x: torch.Tensor, fuse_norm: bool = False):

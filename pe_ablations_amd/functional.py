@@ -272,45 +272,51 @@ class PEAttentionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, _dlse):
-        L = _lib.lib()
         qr, kr, v, qc, kc, freqs, delta, out, lse, fws = ctx.saved_tensors
-        cfg = ctx.cfg
-        dev = qr.device
-        plans = _plans()
-        fp = plans.get(ctx.key)
-        if fp is None:
-            fp = plans[ctx.key] = _FwdPlan(cfg, qr, kr, v, qc, kc, delta)
-        if dout is None:  # out was not used by the loss either
-            dout = torch.zeros_like(out)
-        if dout.stride(-1) != 1:
-            dout = dout.contiguous()
-        if dout.dtype not in (torch.bfloat16, torch.float32):
-            dout = dout.float()
-        dqr, dkr = torch.empty_like(qr), torch.empty_like(kr)
-        dqc = None if qc is None else torch.empty_like(qc)
-        dkc = None if kc is None else torch.empty_like(kc)
-        cdt = fp.cdt
-        dv = torch.empty_like(v, dtype=cdt) if v.dtype != cdt else torch.empty_like(v)
-        need_f = freqs is not None and ctx.needs_input_grad[5]
-        need_d = delta is not None and ctx.needs_input_grad[6]
-        dfreqs = torch.empty(freqs.shape, dtype=torch.float32, device=dev) if need_f else None
-        ddelta = torch.empty(delta.shape, dtype=torch.float32, device=dev) if need_d else None
-        bkey = (_sig(dout), _sig(dqr), _sig(dkr), _sig(dqc), _sig(dkc), _sig(dv))
-        bp = fp.bwd.get(bkey)
-        if bp is None:
-            bp = fp.bwd[bkey] = _BwdPlan(fp, (qc, qr, kc, kr, v, out, dout, dqc, dqr, dkc, dkr, dv))
-        bws = torch.empty(bp.bws, dtype=torch.uint8, device=dev)
-        d = bp.d
-        with _on(dev):
-            rc = L.pe_attn_bwd(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr), d[4].bind(v),
-                               _ptr(freqs), _ptr(delta), d[5].bind(out), lse.data_ptr(), d[6].bind(dout),
-                               d[7].bind(dqc), d[8].bind(dqr), d[9].bind(dkc), d[10].bind(dkr), d[11].bind(dv),
-                               _ptr(dfreqs), _ptr(ddelta), fws.data_ptr(), fp.ws, bws.data_ptr(), bp.bws,
-                               _stream(dev))
-        _lib.check(rc)
-        if dv.dtype != v.dtype:
-            dv = dv.to(v.dtype)
-        return dqr, dkr, dv, dqc, dkc, dfreqs, ddelta, None
+        grads = _attn_backward(ctx.key, ctx.cfg, qr, kr, v, qc, kc, freqs, delta, out, lse, fws, dout,
+                               freqs is not None and ctx.needs_input_grad[5],
+                               delta is not None and ctx.needs_input_grad[6])
+        return grads + (None,)
+
+
+def _attn_backward(key, cfg, qr, kr, v, qc, kc, freqs, delta, out, lse, fws, dout, need_f, need_d):
+    """pe_attn_bwd for a forward saved as (qr, kr, v, qc, kc, freqs, delta, out, lse, workspace):
+    returns (dqr, dkr, dv, dqc, dkc, dfreqs, ddelta), each gradient in its input's dtype."""
+    L = _lib.lib()
+    dev = qr.device
+    plans = _plans()
+    fp = plans.get(key)
+    if fp is None:
+        fp = plans[key] = _FwdPlan(cfg, qr, kr, v, qc, kc, delta)
+    if dout is None:  # out was not used by the loss either
+        dout = torch.zeros_like(out)
+    if dout.stride(-1) != 1:
+        dout = dout.contiguous()
+    if dout.dtype not in (torch.bfloat16, torch.float32):
+        dout = dout.float()
+    dqr, dkr = torch.empty_like(qr), torch.empty_like(kr)
+    dqc = None if qc is None else torch.empty_like(qc)
+    dkc = None if kc is None else torch.empty_like(kc)
+    cdt = fp.cdt
+    dv = torch.empty_like(v, dtype=cdt) if v.dtype != cdt else torch.empty_like(v)
+    dfreqs = torch.empty(freqs.shape, dtype=torch.float32, device=dev) if need_f else None
+    ddelta = torch.empty(delta.shape, dtype=torch.float32, device=dev) if need_d else None
+    bkey = (_sig(dout), _sig(dqr), _sig(dkr), _sig(dqc), _sig(dkc), _sig(dv))
+    bp = fp.bwd.get(bkey)
+    if bp is None:
+        bp = fp.bwd[bkey] = _BwdPlan(fp, (qc, qr, kc, kr, v, out, dout, dqc, dqr, dkc, dkr, dv))
+    bws = torch.empty(bp.bws, dtype=torch.uint8, device=dev)
+    d = bp.d
+    with _on(dev):
+        rc = L.pe_attn_bwd(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr), d[4].bind(v),
+                           _ptr(freqs), _ptr(delta), d[5].bind(out), lse.data_ptr(), d[6].bind(dout),
+                           d[7].bind(dqc), d[8].bind(dqr), d[9].bind(dkc), d[10].bind(dkr), d[11].bind(dv),
+                           _ptr(dfreqs), _ptr(ddelta), fws.data_ptr(), fp.ws, bws.data_ptr(), bp.bws,
+                           _stream(dev))
+    _lib.check(rc)
+    if dv.dtype != v.dtype:
+        dv = dv.to(v.dtype)
+    return dqr, dkr, dv, dqc, dkc, dfreqs, ddelta
 
 
 def ref(x):
@@ -347,9 +353,10 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
     mode "rope": freqs (Dr/2,) inverse frequencies, rope_mscale (YaRN), qk_norm (QKNorm).
     scale defaults to (Dc + Dqk)^-1/2 with Dqk = 2 Dr (PoPE) or Dr.
     causal: True / "top_left" (SDPA is_causal), "bottom_right" (KV-cache mask) or False.
-    qr_norm_weight / kr_norm_weight (PoPE only, forward only): q / k are the raw position
-    projections and the library applies the modules' RMSNorm over each token's H*Dr features in
-    the transform kernel (pe_attn_fwd_normed); raises when a gradient would be needed.
+    qr_norm_weight / kr_norm_weight (PoPE only): q / k are the raw position projections and the
+    library applies the modules' RMSNorm over each token's H*Dr features in the transform kernel
+    (pe_attn_fwd_normed); with a gradient needed the backward also runs the norm's backward
+    (PENormedAttentionFn), giving the gradients of the raw projections and of the norm weights.
     position_dtype (PoPE / FoPE): None or torch.float32 keeps positions exact; torch.bfloat16 /
     torch.float16 rounds each position to that type before the phase product (and in the phase
     gradient), reproducing FoPE's positions in x.dtype (src/model/fpope.py:285,322).
@@ -402,17 +409,23 @@ def default_pope_scale(d: int) -> float:
 
 def _fwd_normed(qr, kr, v, qc, kc, freqs, delta, cfg, wq, wk, eps):
     """Forward through pe_attn_fwd_normed: RMSNorm of the raw position projections fused into the
-    PoPE prologue.  Inference only (no autograd graph is recorded)."""
+    PoPE prologue.  With a gradient needed it runs as PENormedAttentionFn, whose backward applies
+    the attention backward to the normalised projections and then the norm's backward
+    (pe_rmsnorm_bwd); otherwise no graph is recorded."""
     if cfg["mode"] != _lib.PE_MODE_POPE:
         raise ValueError("the fused position-projection RMSNorm applies to PoPE / FoPE only")
     if wq is None or wk is None:
         raise ValueError("pass both qr_norm_weight and kr_norm_weight")
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
-                                       for t in (qr, kr, v, qc, kc, freqs, delta, wq, wk)):
-        raise RuntimeError("pe_attention with fused RMSNorm is forward-only; apply the norm with the "
-                           "module (RMSNorm) for training")
     if wq.dtype != wk.dtype or wq.dtype not in (torch.bfloat16, torch.float32):
         raise TypeError("qr/kr norm weights must share one dtype, bf16 or fp32")
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (qr, kr, v, qc, kc, freqs, delta, wq, wk)):
+        return PENormedAttentionFn.apply(qr, kr, v, qc, kc, freqs, delta, wq, wk, cfg, float(eps))
+    out, lse, _ = _launch_normed(qr, kr, v, qc, kc, freqs, delta, cfg, wq, wk, eps)
+    return out, lse
+
+
+def _launch_normed(qr, kr, v, qc, kc, freqs, delta, cfg, wq, wk, eps):
     L = _lib.lib()
     dev = qr.device
     wq, wk = wq.contiguous(), wk.contiguous()
@@ -432,7 +445,83 @@ def _fwd_normed(qr, kr, v, qc, kc, freqs, delta, cfg, wq, wk, eps):
                                   ref(_tensor(kc)), ref(_tensor(kr)), ref(_tensor(v)), _ptr(freqs), _ptr(delta),
                                   ref(_tensor(out)), lse.data_ptr(), fws.data_ptr(), ws_bytes, _stream(dev))
     _lib.check(rc)
-    return out, lse
+    return out, lse, fws
+
+
+def _token_rows(x: torch.Tensor) -> torch.Tensor:
+    """(B, H, S, D) view of a projection -> its (B * S, H * D) token rows (a view when x is the
+    (B, S, H, D) transpose the modules pass, else a copy)."""
+    B, H, S, D = x.shape
+    return x.transpose(1, 2).reshape(B * S, H * D)
+
+
+class PENormedAttentionFn(torch.autograd.Function):
+    """forward(qr, kr, v, qc, kc, freqs, delta, wq, wk, cfg, eps) -> (out, lse): the modules'
+    RMSNorm of the raw position projections qr / kr over each token's H*Dr features
+    (src/model/fpope_attention.py:132-137, src/model/normalization.py:22-27) fused into the PoPE
+    prologue (pe_attn_fwd_normed).  The backward recomputes the normalised projections y with
+    pe_rmsnorm_fwd (the prologue's arithmetic and summation order, so bitwise the y it used), runs
+    pe_attn_bwd on y, and turns the gradient of y into those of the raw projections and the norm
+    weights with pe_rmsnorm_bwd.  Gradients: qr, kr, v, qc, kc, freqs, delta, wq, wk."""
+
+    @staticmethod
+    def forward(ctx, qr, kr, v, qc, kc, freqs, delta, wq, wk, cfg, eps):
+        out, lse, fws = _launch_normed(qr, kr, v, qc, kc, freqs, delta, cfg, wq, wk, eps)
+        ctx.cfg, ctx.eps = cfg, eps
+        ctx.save_for_backward(qr, kr, v, qc, kc, freqs, delta, wq, wk, out, lse, fws)
+        ctx.mark_non_differentiable(lse)
+        ctx.set_materialize_grads(False)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        qr, kr, v, qc, kc, freqs, delta, wq, wk, out, lse, fws = ctx.saved_tensors
+        B, Hq, Sq, Dr = qr.shape
+        Hkv, Sk = kr.shape[1], kr.shape[2]
+        xq, xk = _token_rows(qr), _token_rows(kr)
+        yq = rms_norm(xq, wq, ctx.eps).view(B, Sq, Hq, Dr).transpose(1, 2)
+        yk = rms_norm(xk, wk, ctx.eps).view(B, Sk, Hkv, Dr).transpose(1, 2)
+        key = ("normed-bwd", ctx.cfg["key"], _sig(yq), _sig(yk), _sig(v), _sig(qc), _sig(kc),
+               None if delta is None else delta.dim())
+        dyq, dyk, dv, dqc, dkc, dfreqs, ddelta = _attn_backward(
+            key, ctx.cfg, yq, yk, v, qc, kc, freqs, delta, out, lse, fws, dout,
+            freqs is not None and ctx.needs_input_grad[5], delta is not None and ctx.needs_input_grad[6])
+        dxq, dwq = rms_norm_backward(xq, wq, _token_rows(dyq), ctx.eps)
+        dxk, dwk = rms_norm_backward(xk, wk, _token_rows(dyk), ctx.eps)
+        dqr = dxq.view(B, Sq, Hq, Dr).transpose(1, 2)
+        dkr = dxk.view(B, Sk, Hkv, Dr).transpose(1, 2)
+        return dqr, dkr, dv, dqc, dkc, dfreqs, ddelta, dwq, dwk, None, None
+
+
+def rms_norm_backward(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, eps: float = 1e-6):
+    """Gradients (dx, dweight) of rms_norm(x, weight, eps) for the output gradient dy, as autograd
+    computes them through the reference module (src/model/normalization.py:22-27), through
+    pe_rmsnorm_bwd: (rows, n) views with unit element stride; dy in rms_norm's output dtype; dx in
+    x's dtype, dweight in weight's dtype (summed over the rows in a fixed order)."""
+    if not x.is_cuda:
+        raise RuntimeError("rms_norm_backward runs on the GPU only (got a CPU tensor)")
+    n = x.shape[-1]
+    ydt = torch.bfloat16 if (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16) else torch.float32
+    x2 = x.reshape(-1, n)
+    dy2 = dy.reshape(-1, n).to(ydt)
+    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % (8 if x.dtype == torch.bfloat16 else 4):
+        x2 = x2.contiguous()
+    if dy2.stride(-1) != 1 or dy2.data_ptr() % 16 or dy2.stride(0) % (8 if ydt == torch.bfloat16 else 4):
+        dy2 = dy2.contiguous()
+    w = weight.contiguous()
+    dx = torch.empty((x2.shape[0], n), dtype=x.dtype, device=x.device)
+    dw = torch.empty(n, dtype=weight.dtype, device=x.device)
+    if x2.shape[0] == 0:
+        return dx.view(x.shape), dw.zero_()
+    L = _lib.lib()
+    ws = L.pe_rmsnorm_bwd_workspace_bytes(x2.shape[0], n)
+    part = torch.empty(ws, dtype=torch.uint8, device=x.device)
+    with _on(x.device):
+        rc = L.pe_rmsnorm_bwd(x2.data_ptr(), _dtype_code(x2.dtype), x2.stride(0), x2.shape[0], n, w.data_ptr(),
+                              _dtype_code(w.dtype), float(eps), dy2.data_ptr(), dy2.stride(0), dx.data_ptr(),
+                              dx.stride(0), dw.data_ptr(), part.data_ptr(), ws, _stream(x.device))
+    _lib.check(rc)
+    return dx.view(x.shape), dw
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

@@ -437,3 +437,24 @@ def test_bf16_path_gqa_fold():
     assert torch.equal(o, o2) and torch.equal(a[0].grad, b[0].grad)
     assert torch.equal(a[1].grad, b[1].grad.view(1, 2, 2, 40, 16).sum(2))
     assert torch.equal(a[2].grad, b[2].grad.view(1, 2, 2, 40, 16).sum(2))
+
+
+def test_rms_norm_gradient_rounds_once():
+    """The reference casts x to fp32 once (self._norm(x.float()), src/model/normalization.py:25), so
+    autograd sums the two paths of the gradient through x (x * r and r's dependence on x) in fp32
+    and rounds to bf16 once.  Two separate casts would round each path before adding them, which
+    for these inputs moves dx by a bf16 spacing (checked against that variant below)."""
+    g = torch.Generator().manual_seed(1 * 3 + 64)
+    x = (torch.randn(1, 64, generator=g) * 3).to(torch.bfloat16)
+    w = (0.5 + torch.rand(64, generator=g)).to(torch.bfloat16)
+    dy = torch.randn(1, 64, generator=g).to(torch.bfloat16)
+    xr = x.clone().requires_grad_(True)
+    O.rms_norm(xr, w).backward(dy)
+    gc = (dy * w).float()                      # the gradient of the cast value, a bf16 product
+    xf = x.float().requires_grad_(True)
+    n = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    once = torch.autograd.grad(n, xf, gc)[0].to(torch.bfloat16)
+    assert torch.equal(xr.grad, once)
+    xt = x.clone().requires_grad_(True)
+    ((xt.float() * torch.rsqrt(xt.float().pow(2).mean(-1, keepdim=True) + 1e-6)).type_as(xt) * w).backward(dy)
+    assert not torch.equal(xt.grad, once)     # the two-cast form differs here
