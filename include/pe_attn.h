@@ -42,8 +42,10 @@ enum {
   PE_MODE_NONE = 2  /* no positional transform (reference pe_mode "nope", or fpope=None modules) */
 };
 
-/* element types of tensors crossing the boundary */
-enum { PE_DTYPE_BF16 = 0, PE_DTYPE_FP32 = 1 };
+/* element types of tensors crossing the boundary.  A compute dtype (pe_attn_params.dtype) of bf16
+ * or fp16 runs the matrix products on 16-bit operands with fp32 accumulation (fp16: the reference
+ * trainer's mixed_precision fp16, src/training/trainer.py:343-347); fp32 runs them in fp32. */
+enum { PE_DTYPE_BF16 = 0, PE_DTYPE_FP32 = 1, PE_DTYPE_FP16 = 2 };
 
 /* how the PoPE / FoPE phase product sees a position p (pe_attn_params.position_rounding) */
 enum {
@@ -134,7 +136,9 @@ int pe_attn_fwd(const pe_attn_params* p,
 /* Backward.  Inputs as for pe_attn_fwd plus out/lse from it and dout (B,Hq,Sq,Dv).  Gradients are
  * written through the tensor views dqc/dqr/dkc/dkr (same shapes and dtypes as the inputs;
  * dqc/dkc data may be NULL when Dc == 0) and dv (dtype p->dtype).  dfreqs (Dr,) and ddelta
- * (Dr,) or (Hkv, Dr) are fp32 and overwritten; either may be NULL to skip it. */
+ * (Dr,) or (Hkv, Dr) are fp32 and overwritten; either may be NULL to skip it.  With a 16-bit
+ * p->dtype, qc/qr/kc/kr/v and the gradients are each fp32 or p->dtype (the other 16-bit type:
+ * PE_ERR_MODE). */
 int pe_attn_bwd(const pe_attn_params* p,
                 const pe_tensor_t* qc, const pe_tensor_t* qr,
                 const pe_tensor_t* kc, const pe_tensor_t* kr,

@@ -245,26 +245,31 @@ def round_ste(x: torch.Tensor, dtype) -> torch.Tensor:
     return x + (x.to(dtype).to(x.dtype) - x).detach()
 
 
+def _round16(x: torch.Tensor, dtype) -> torch.Tensor:
+    return x.to(dtype).to(x.dtype)
+
+
 def _bf16(x: torch.Tensor) -> torch.Tensor:
-    return x.to(torch.bfloat16).to(x.dtype)
+    return _round16(x, torch.bfloat16)
 
 
-class _SdpaBf16Path(torch.autograd.Function):
-    """The attention core with the rounding points of a bf16 fused SDPA (the kernel the reference
-    reaches through F.scaled_dot_product_attention under bf16 autocast,
+class _SdpaHalfPath(torch.autograd.Function):
+    """The attention core with the rounding points of a 16-bit fused SDPA (the kernel the reference
+    reaches through F.scaled_dot_product_attention under bf16 or fp16 autocast,
     src/model/fpope_attention.py:171-177 and src/model/attention.py:91-96), not its exact value.
 
     Forward: scores and the row sums in full precision, the probabilities exp(s - max) rounded to
-    bf16 before the PV product, out = (sum bf16(p) v) / sum p rounded to bf16.  Backward (the
-    flash-attention recomputation): Di = rowsum(dO * out) over the bf16 out, P = exp(s - lse),
-    dV = bf16(P)^T dO, dS = P (dP - Di) rounded to bf16 before dQ = dS K and dK = dS^T Q, every
-    gradient rounded to bf16 per query head; GQA sums the per-head dK / dV afterwards (the
-    reference's repeat_interleave backward).  Inputs hold bf16 values; math is float64 between the
-    rounding points.  Used only to measure the reference path's own error beside the kernel's."""
+    the 16-bit type before the PV product, out = (sum p v) / sum p rounded to it.  Backward (the
+    flash-attention recomputation): Di = rowsum(dO * out) over the rounded out, P = exp(s - lse),
+    dV = P^T dO with P rounded, dS = P (dP - Di) rounded before dQ = dS K and dK = dS^T Q, every
+    gradient rounded per query head; GQA sums the per-head dK / dV afterwards (the reference's
+    repeat_interleave backward).  Inputs hold values of the 16-bit type; math is float64 between
+    the rounding points.  Used only to measure the reference path's own error beside the kernel's."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, causal):
+    def forward(ctx, q, k, v, scale, causal, dtype):
         f64 = torch.float64
+        r = (lambda x: _bf16(x)) if dtype == torch.bfloat16 else (lambda x: _round16(x, dtype))
         Hq, Hkv = q.shape[1], k.shape[1]
         g = Hq // Hkv
         kr, vr = k.to(f64).repeat_interleave(g, 1), v.to(f64).repeat_interleave(g, 1)
@@ -275,38 +280,43 @@ class _SdpaBf16Path(torch.autograd.Function):
         m = s.amax(-1, keepdim=True).clamp_min(-1e300)
         pt = torch.exp(s - m)
         lsum = pt.sum(-1, keepdim=True)
-        out = _bf16(torch.matmul(_bf16(pt), vr) / lsum)
+        out = r(torch.matmul(r(pt), vr) / lsum)
         lse = (m + torch.log(lsum)).squeeze(-1)
         ctx.save_for_backward(qd, kr, vr, out, lse)
-        ctx.scale, ctx.causal, ctx.g = scale, causal, g
+        ctx.scale, ctx.causal, ctx.g, ctx.r = scale, causal, g, r
         return out.to(q.dtype), lse
 
     @staticmethod
     def backward(ctx, dout, dlse):
         qd, kr, vr, out, lse = ctx.saved_tensors
-        scale, g = ctx.scale, ctx.g
-        do = _bf16(dout.to(torch.float64))
+        scale, g, r = ctx.scale, ctx.g, ctx.r
+        do = r(dout.to(torch.float64))
         di = (do * out).sum(-1, keepdim=True)
         s = torch.matmul(qd, kr.transpose(-2, -1)) * scale
         if ctx.causal:
             s = s.masked_fill(causal_mask(qd.shape[2], kr.shape[2]), float("-inf"))
         p = torch.exp(s - lse.unsqueeze(-1))
-        dv = _bf16(torch.matmul(_bf16(p).transpose(-2, -1), do))
-        ds = _bf16(p * (torch.matmul(do, vr.transpose(-2, -1)) - di))
-        dq = _bf16(torch.matmul(ds, kr) * scale)
-        dk = _bf16(torch.matmul(ds.transpose(-2, -1), qd) * scale)
+        dv = r(torch.matmul(r(p).transpose(-2, -1), do))
+        ds = r(p * (torch.matmul(do, vr.transpose(-2, -1)) - di))
+        dq = r(torch.matmul(ds, kr) * scale)
+        dk = r(torch.matmul(ds.transpose(-2, -1), qd) * scale)
 
         def fold(x):  # per-head gradients summed over each kv head's query group
             B, H, S, D = x.shape
             return x.view(B, H // g, g, S, D).sum(2)
 
-        return dq, fold(dk), fold(dv), None, None
+        return dq, fold(dk), fold(dv), None, None, None
 
 
 def attention_bf16_path(q, k, v, scale: float, causal: bool = True):
-    """(out, lse) of ``attention`` with a bf16 fused SDPA's rounding points (_SdpaBf16Path);
+    """(out, lse) of ``attention`` with a bf16 fused SDPA's rounding points (_SdpaHalfPath);
     differentiable, so the transforms around it carry the path's gradients to the raw inputs."""
-    return _SdpaBf16Path.apply(q, k, v, scale, bool(causal))
+    return _SdpaHalfPath.apply(q, k, v, scale, bool(causal), torch.bfloat16)
+
+
+def attention_fp16_path(q, k, v, scale: float, causal: bool = True):
+    """The same with an fp16 fused SDPA's rounding points (fp16 autocast)."""
+    return _SdpaHalfPath.apply(q, k, v, scale, bool(causal), torch.float16)
 
 
 # --------------------------------------------------------------------------------------------

@@ -14,7 +14,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libpe_attn.so")
 
 PE_MODE_POPE, PE_MODE_ROPE, PE_MODE_NONE = 0, 1, 2
-PE_DTYPE_BF16, PE_DTYPE_FP32 = 0, 1
+PE_DTYPE_BF16, PE_DTYPE_FP32, PE_DTYPE_FP16 = 0, 1, 2
 PE_CAUSAL_NONE, PE_CAUSAL_TOP_LEFT, PE_CAUSAL_BOTTOM_RIGHT = 0, 1, 2
 PE_POS_EXACT, PE_POS_BF16, PE_POS_FP16 = 0, 1, 2
 

@@ -31,7 +31,10 @@ int qk_width(const pe_attn_params* p) {
 }
 int pad_qk(int w) { return w <= 64 ? 64 : w <= 128 ? 128 : w <= 256 ? 256 : -1; }
 int pad_v(int d) { return d <= 64 ? 64 : d <= 128 ? 128 : -1; }
-size_t esz(const pe_attn_params* p) { return p->dtype == PE_DTYPE_BF16 ? 2 : 4; }
+size_t esz(const pe_attn_params* p) { return p->dtype == PE_DTYPE_FP32 ? 4 : 2; }
+// a 16-bit compute dtype (bf16 or fp16): the matrix-core kernels of the 16-bit path
+bool half_dt(int dtype) { return dtype == PE_DTYPE_BF16 || dtype == PE_DTYPE_FP16; }
+bool valid_dt(int dtype) { return dtype == PE_DTYPE_BF16 || dtype == PE_DTYPE_FP32 || dtype == PE_DTYPE_FP16; }
 
 struct Layout {
   int dqk, dv;
@@ -51,7 +54,7 @@ bool use_qtab(const pe_attn_params* p) { return p->mode == PE_MODE_POPE && p->Dr
 // apply the inverse transform in their epilogues and write dq / dk directly, so the backward needs
 // no fp32 dq~ / dk~ buffers (pe_attn_bwd's input checks require the q / k views whenever Dr > 0)
 bool fused_bwd(const pe_attn_params* p) {
-  return p->dtype == PE_DTYPE_BF16 && p->mode == PE_MODE_POPE && p->Dc == 0 && (p->Dr == 64 || p->Dr == 128) &&
+  return half_dt(p->dtype) && p->mode == PE_MODE_POPE && p->Dc == 0 && (p->Dr == 64 || p->Dr == 128) &&
          pad_qk(qk_width(p)) == 2 * p->Dr;
 }
 
@@ -59,7 +62,7 @@ bool fused_bwd(const pe_attn_params* p) {
 // every row 16-byte aligned
 bool vec16(const pe_tensor_t* t) {
   if (!t || !t->data) return false;
-  const int64_t e = t->dtype == PE_DTYPE_BF16 ? 2 : 4;
+  const int64_t e = t->dtype == PE_DTYPE_FP32 ? 4 : 2;
   return t->stride[3] == 1 && (uintptr_t)t->data % 16 == 0 && (t->stride[0] * e) % 16 == 0 &&
          (t->stride[1] * e) % 16 == 0 && (t->stride[2] * e) % 16 == 0;
 }
@@ -70,7 +73,7 @@ bool vec16(const pe_tensor_t* t) {
 bool fused_split_bwd(const pe_attn_params* p, const pe_tensor_t* qr, const pe_tensor_t* kr,
                      const pe_tensor_t* dqc, const pe_tensor_t* dqr, const pe_tensor_t* dkc,
                      const pe_tensor_t* dkr) {
-  return p->dtype == PE_DTYPE_BF16 && p->mode == PE_MODE_POPE && p->Dc == 64 && p->Dr == 32 &&
+  return half_dt(p->dtype) && p->mode == PE_MODE_POPE && p->Dc == 64 && p->Dr == 32 &&
          (p->Dv == 64 || p->Dv == 128) && vec16(qr) && vec16(kr) && vec16(dqc) && vec16(dqr) && vec16(dkc) &&
          vec16(dkr);
 }
@@ -121,9 +124,9 @@ Layout layout(const pe_attn_params* p) {
   const int units = p->B * p->Hkv;
   const size_t unit_bytes = (size_t)(p->Hq / p->Hkv) * L.ds_head * 4096;
   L.ds_group = units;
-  if (p->dtype == PE_DTYPE_BF16 && unit_bytes > 0 && (size_t)units * unit_bytes > PE_BWD_DS_CAP_BYTES)
+  if (half_dt(p->dtype) && unit_bytes > 0 && (size_t)units * unit_bytes > PE_BWD_DS_CAP_BYTES)
     L.ds_group = std::max<int>(1, (int)(PE_BWD_DS_CAP_BYTES / unit_bytes));
-  const size_t ds_bytes = p->dtype == PE_DTYPE_BF16 ? (size_t)L.ds_group * unit_bytes : 0;
+  const size_t ds_bytes = half_dt(p->dtype) ? (size_t)L.ds_group * unit_bytes : 0;
   L.bwd_total = L.ds_off + align_up(ds_bytes);
   return L;
 }
@@ -143,7 +146,7 @@ inline void stage_mark(int stage, int end, hipStream_t s) {
 int check_tensor(const pe_tensor_t* t, bool required) {
   if (!t) return required ? PE_ERR_NULL : PE_OK;
   if (!t->data) return required ? PE_ERR_NULL : PE_OK;
-  if (t->dtype != PE_DTYPE_BF16 && t->dtype != PE_DTYPE_FP32) return PE_ERR_MODE;
+  if (!valid_dt(t->dtype)) return PE_ERR_MODE;
   if (t->stride[3] != 1) return PE_ERR_STRIDE;
   return PE_OK;
 }
@@ -254,7 +257,7 @@ int pe_attn_check(const pe_attn_params* p) {
   if (p->B <= 0 || p->Hq <= 0 || p->Hkv <= 0 || p->Sq <= 0 || p->Sk <= 0 || p->Dv <= 0 || p->Dr < 0 || p->Dc < 0)
     return PE_ERR_SHAPE;
   if (p->Hq % p->Hkv != 0) return PE_ERR_SHAPE;
-  if (p->mode < 0 || p->mode > 2 || (p->dtype != PE_DTYPE_BF16 && p->dtype != PE_DTYPE_FP32) || p->causal < 0 || p->causal > 2)
+  if (p->mode < 0 || p->mode > 2 || !valid_dt(p->dtype) || p->causal < 0 || p->causal > 2)
     return PE_ERR_MODE;
   if (p->mode != PE_MODE_POPE && (p->Dr % 2) != 0) return PE_ERR_MODE;
   if (p->position_rounding < PE_POS_EXACT || p->position_rounding > PE_POS_FP16 ||
@@ -368,7 +371,7 @@ static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe
   if (nrm) {
     if (p->mode != PE_MODE_POPE || p->Dr <= 0) return PE_ERR_MODE;
     if (!nrm->q_weight || !nrm->k_weight) return PE_ERR_NULL;
-    if (nrm->weight_dtype != PE_DTYPE_BF16 && nrm->weight_dtype != PE_DTYPE_FP32) return PE_ERR_MODE;
+    if (!valid_dt(nrm->weight_dtype)) return PE_ERR_MODE;
   }
   if ((rc = check_tensor(qr, p->Dr > 0)) || (rc = check_tensor(kr, p->Dr > 0)) ||
       (rc = check_tensor(qc, p->Dc > 0)) || (rc = check_tensor(kc, p->Dc > 0)) ||
@@ -418,7 +421,7 @@ static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe
   c.o_dtype = out->dtype;
   c.lse = lse;
   stage_mark(PE_STAGE_FWD_CORE, 0, s);
-  rc = pe::launch_fwd(p->dtype == PE_DTYPE_BF16 ? 0 : 1, L.dqk, L.dv, c, s);
+  rc = pe::launch_fwd(p->dtype, L.dqk, L.dv, c, s);
   stage_mark(PE_STAGE_FWD_CORE, 1, s);
   return rc;
 }
@@ -611,7 +614,7 @@ int pe_attn_decode(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tens
   da.o = (void*)out->data; da.o_sb = out->stride[0]; da.o_sh = out->stride[1]; da.o_ss = out->stride[2];
   da.o_dtype = out->dtype; da.dv_real = p->Dv;
   da.lse = lse;
-  return pe::launch_decode(p->dtype == PE_DTYPE_BF16 ? 0 : 1, dqk, dv, da, s);
+  return pe::launch_decode(p->dtype, dqk, dv, da, s);
 }
 
 int pe_attn_fwd_normed(const pe_attn_params* p, const pe_norm_params* n, const pe_tensor_t* qc,
@@ -692,6 +695,12 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
       (rc = check_tensor(dv, true)))
     return rc;
   if (!lse || (p->mode != PE_MODE_NONE && p->Dr > 0 && !freqs)) return PE_ERR_NULL;
+  // 16-bit compute: the gradient kernels' epilogues read the operands and write the gradients in
+  // fp32 or in the compute's own 16-bit type, not in the other one
+  if (half_dt(p->dtype)) {
+    for (const pe_tensor_t* t : {qc, qr, kc, kr, v, dqc, dqr, dkc, dkr, dv})
+      if (t && t->data && t->dtype != p->dtype && t->dtype != PE_DTYPE_FP32) return PE_ERR_MODE;
+  }
   const Layout L = layout(p);
   if (!fwd_workspace || fwd_ws_bytes < L.fwd_total || !bwd_workspace || bwd_ws_bytes < L.bwd_total)
     return PE_ERR_WORKSPACE;
@@ -699,7 +708,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   hipStream_t s = (hipStream_t)stream;
   const char* fws = (const char*)fwd_workspace;
   char* bws = (char*)bwd_workspace;
-  const int dt = p->dtype == PE_DTYPE_BF16 ? 0 : 1;
+  const int dt = p->dtype;  // the kernels' dtype codes are the ABI's
 
   pe::PreBwdArgs pb;
   memset(&pb, 0, sizeof(pb));
@@ -707,7 +716,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   pb.out = out->data; pb.out_dtype = out->dtype;
   for (int i = 0; i < 4; ++i) { pb.do_s[i] = dout->stride[i]; pb.o_s[i] = out->stride[i]; }
   // the bf16 dK/dV kernel reads dO in place when its rows are 16-byte aligned and exactly Dv wide
-  const bool do_direct = dt == 0 && v_direct(p, dout, L.dv);
+  const bool do_direct = half_dt(dt) && v_direct(p, dout, L.dv);
   pb.dO_op = do_direct ? nullptr : bws + L.do_off; pb.op_dtype = p->dtype; pb.width = L.dv;
   pb.Di = (float*)(bws + L.di_off);
   pb.L2 = (float*)(bws + L.l2_off);
@@ -775,7 +784,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   // the gradient kernels over head groups whose dS fits the workspace (one group up to the cap);
   // with several groups the dK/dV stage mark spans every group's kernels and the dQ mark is empty
   const int units = p->B * p->Hkv;
-  const int group = dt == 0 ? L.ds_group : units;
+  const int group = half_dt(dt) ? L.ds_group : units;
   for (int g0 = 0; g0 < units; g0 += group) {
     c.bh0 = g0;
     c.nbh = std::min(group, units - g0);

@@ -318,9 +318,9 @@ __device__ __forceinline__ bool masked_row(int kd, int j) { return kd > ((j >> 3
 // group.  LDS ring of 3 stages (q~ 64 x DQK, dO 64 x DV, the rows' log2 lse and Di): the tile being
 // loaded, the tile being consumed and the previous tile, whose last half's dV / dK products run
 // during the first half of the current one.
-template <int DQK, int DV, int NW>
+template <int HT, int DQK, int DV, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
-  using M = MT<0>;
+  using M = MT<HT>;  // HT: the 16-bit operand type, bf16 (0) or fp16 (2)
   constexpr int BMQ = 64, BNK = NW * 32;
   constexpr int NCQ = DQK / 8, NCO = DV / 8;
   constexpr int NKF = DQK / 16, NVF = DV / 16, NDK = DQK / 32, NDV = DV / 32;
@@ -517,8 +517,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
         const float p = fast_exp2(s[i] * sl2 - lv);
         const float ds = p * (dp[i] - dd);
         if (i & 1) {  // element pairs are packed as soon as they are complete
-          cpf[i / 8][(i % 8) / 2] = pack_bf2(pprev, p);
-          cdsf[i / 8][(i % 8) / 2] = pack_bf2(dprev, ds);
+          cpf[i / 8][(i % 8) / 2] = pack2<HT>(pprev, p);
+          cdsf[i / 8][(i % 8) / 2] = pack2<HT>(dprev, ds);
         } else {
           pprev = p;
           dprev = ds;
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
 #pragma unroll
       for (int u = 0; u < EU; ++u) {
         const int r = r0 + u * rstep, key = k0 + r;
-        xv[u] = (r < BNK && key < a.Sk) ? load_as_float(e.x, xb + (int64_t)key * e.x_s[2], e.x_dtype) : 0.f;
+        xv[u] = (r < BNK && key < a.Sk) ? load_as_float_t<HT>(e.x, xb + (int64_t)key * e.x_s[2], e.x_dtype) : 0.f;
       }
     };
     float xv[EU], xn[EU];
@@ -615,7 +615,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
           float dx;
           const float dph = inv_pope_elem(xv[u], pos, fr, dl, a.delta != nullptr, st[r * DQK + c],
                                           st[r * DQK + Dr + c], dx);
-          store_from_float(e.dx, b * e.dx_s[0] + hk * e.dx_s[1] + (int64_t)key * e.dx_s[2] + c * e.dx_s[3],
+          store_from_float_t<HT>(e.dx, b * e.dx_s[0] + hk * e.dx_s[1] + (int64_t)key * e.dx_s[2] + c * e.dx_s[3],
                            e.dx_dtype, dx);
           sd += dph;
           sf += pos * dph;
@@ -658,7 +658,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     for (int j = 0; j < 16; ++j) {
       const int key = kw0 + c_row(j, g), col = t * 32 + l32;
       if (key < a.Sk && col < a.dv_real)
-        store_from_float(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + col, a.dv_dtype, dv[t][j]);
+        store_from_float_t<HT>(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + col, a.dv_dtype, dv[t][j]);
     }
 }
 
@@ -666,7 +666,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
 // dxc) with a unit dim stride and every row 16-byte aligned (true of the projections'
 // (B, S, H, D) views).
 __device__ __forceinline__ bool epi_vec_ok(const EpiPoPE& e, int dc) {
-  const int64_t xe = e.x_dtype == 0 ? 2 : 4, de = e.dx_dtype == 0 ? 2 : 4, ce = e.dxc_dtype == 0 ? 2 : 4;
+  const int64_t xe = e.x_dtype == 1 ? 4 : 2, de = e.dx_dtype == 1 ? 4 : 2, ce = e.dxc_dtype == 1 ? 4 : 2;
   const bool c_ok = dc == 0 || (e.dxc_s[3] == 1 && (uintptr_t)e.dxc % 16 == 0 && (e.dxc_s[0] * ce) % 16 == 0 &&
                                 (e.dxc_s[1] * ce) % 16 == 0 && (e.dxc_s[2] * ce) % 16 == 0);
   return c_ok && e.x_s[3] == 1 && e.dx_s[3] == 1 && (uintptr_t)e.x % 16 == 0 && (uintptr_t)e.dx % 16 == 0 &&
@@ -682,7 +682,7 @@ __device__ __forceinline__ bool epi_vec_ok(const EpiPoPE& e, int dc) {
 // bias; sdl / sf accumulate sum(dphi) and sum(pos * dphi) per dim over the thread's rows.  With TAB
 // (query side) the sin / cos of each row's phases come from launch_phase_table's [S][2][DR] table,
 // indexed by the row's sequence index, instead of being evaluated.
-template <int DQK, int DC, int NT, int NR, bool TAB>
+template <int HT, int DQK, int DC, int NT, int NR, bool TAB>
 __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st, int tid, int64_t xb,
                                               int64_t dxb, int base, int nidx, const float (&fr)[8],
                                               const float (&dl)[8], bool key, const float* tab,
@@ -695,7 +695,7 @@ __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st,
   for (int i = 0; i < NI; ++i) {
     const int idx = base + rr + RPP * i;
     if (idx < nidx) {
-      load8(e.x, xb + (int64_t)idx * e.x_s[2] + c0, e.x_dtype, xv[i]);
+      load8t<HT>(e.x, xb + (int64_t)idx * e.x_s[2] + c0, e.x_dtype, xv[i]);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) xv[i][j] = 0.f;
@@ -731,13 +731,13 @@ __device__ __forceinline__ void inv_pope_rows(const EpiPoPE& e, const float* st,
           sf[j] += pos * dph;
         }
       }
-      store8(e.dx, dxb + (int64_t)idx * e.dx_s[2] + c0, e.dx_dtype, dx);
+      store8t<HT>(e.dx, dxb + (int64_t)idx * e.dx_s[2] + c0, e.dx_dtype, dx);
     }
   }
 }
 // The content part [0, DC) of NR staged rows, copied to dxc 8 dims at a time (no transform: the
 // content dims enter the scores unchanged, so their gradient is the staged one).
-template <int DQK, int DC, int NT, int NR>
+template <int HT, int DQK, int DC, int NT, int NR>
 __device__ __forceinline__ void content_rows(const EpiPoPE& e, const float* st, int tid, int64_t dxcb, int base,
                                              int nidx) {
   constexpr int CG = DC / 8, RPP = NT / CG;
@@ -749,7 +749,7 @@ __device__ __forceinline__ void content_rows(const EpiPoPE& e, const float* st, 
     if (idx < nidx) {
       const f32x4 lo = *(const f32x4*)(st + r * DQK + c0), hi = *(const f32x4*)(st + r * DQK + c0 + 4);
       const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      store8(e.dxc, dxcb + (int64_t)idx * e.dxc_s[2] + c0, e.dxc_dtype, v);
+      store8t<HT>(e.dxc, dxcb + (int64_t)idx * e.dxc_s[2] + c0, e.dxc_dtype, v);
     }
   }
 }
@@ -765,19 +765,10 @@ __device__ __forceinline__ void content_rows(const EpiPoPE& e, const float* st, 
 // tile t-1 (so A starts the step on products while B forms dS), and B's dS / dK~ of tile t-1 and
 // dP of tile t, then one barrier; the 32-query tiles stream through a ring of
 // 4 LDS stages (q~ 32 x DQK, dO 32 x DV, the rows' log2 lse and Di) loaded two steps ahead.
-// two floats <-> one dword of fp16 (lo in bits 0-15), round-to-nearest-even (v_cvt_pk_f16_f32)
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, h2_t));
-}
-__device__ __forceinline__ void unpack_h2(uint32_t v, float& lo, float& hi) {
-  const f32x2_t f = __builtin_convertvector(__builtin_bit_cast(h2_t, v), f32x2_t);
-  lo = f[0];
-  hi = f[1];
-}
-template <int DQK, int DV, int QT>
+// (pack_h2 / unpack_h2, pe_common.h: two floats <-> one dword of fp16, round-to-nearest-even)
+template <int HT, int DQK, int DV, int QT>
 __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
-  using M = MT<0>;
+  using M = MT<HT>;  // HT: the 16-bit operand type, bf16 (0) or fp16 (2)
   constexpr int NW = 8, BMQ = 32 * QT, BNK = 128, NSTG = 4;
   constexpr int NCQ = DQK / 8, NCO = DV / 8;
   constexpr int NKF = DQK / 16, NVF = DV / 16, NDK = DQK / 32, NDV = DV / 32;
@@ -985,8 +976,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
             for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[m][4 * G + e] * sl2 - lv[e]);
             ph[G >> 1][(G & 1) * 2] = pack_h2(p[0], p[1]);
             ph[G >> 1][(G & 1) * 2 + 1] = pack_h2(p[2], p[3]);
-            pn[2 * m + (G >> 1)][(G & 1) * 2] = pack_bf2(p[0], p[1]);
-            pn[2 * m + (G >> 1)][(G & 1) * 2 + 1] = pack_bf2(p[2], p[3]);
+            pn[2 * m + (G >> 1)][(G & 1) * 2] = pack2<HT>(p[0], p[1]);
+            pn[2 * m + (G >> 1)][(G & 1) * 2 + 1] = pack2<HT>(p[2], p[3]);
           }
           *(u32x4*)(xb + ((2 * m + 0) * 64 + lane) * 16) = ph[0];
           *(u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16) = ph[1];
@@ -1010,7 +1001,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       for (int j = 0; j < 16; ++j) {
         const int key = kw0 + c_row(j, g), col = t * 32 + l32;
         if (key < a.Sk && col < a.dv_real)
-          store_from_float(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + col, a.dv_dtype, dv[t][j]);
+          store_from_float_t<HT>(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + col, a.dv_dtype, dv[t][j]);
       }
   } else {
     u32x4 vf[NVF];
@@ -1051,8 +1042,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
             float ds[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) ds[e] = p[e] * (dp[m][4 * G + e] - dd[e]);
-            dsf[2 * m + (G >> 1)][(G & 1) * 2] = pack_bf2(ds[0], ds[1]);
-            dsf[2 * m + (G >> 1)][(G & 1) * 2 + 1] = pack_bf2(ds[2], ds[3]);
+            dsf[2 * m + (G >> 1)][(G & 1) * 2] = pack2<HT>(ds[0], ds[1]);
+            dsf[2 * m + (G >> 1)][(G & 1) * 2 + 1] = pack2<HT>(ds[2], ds[3]);
           }
         }
         const int h = prev_h, q0 = prev_qt * BMQ;
@@ -1106,8 +1097,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     }
     __syncthreads();  // every dk~ row staged
     if constexpr (DC > 0)
-      content_rows<DQK, DC, NW * 64, BNK>(e, st_epi, tid, b * e.dxc_s[0] + hk * e.dxc_s[1], k0, a.Sk);
-    inv_pope_rows<DQK, DC, NW * 64, BNK, false>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1],
+      content_rows<HT, DQK, DC, NW * 64, BNK>(e, st_epi, tid, b * e.dxc_s[0] + hk * e.dxc_s[1], k0, a.Sk);
+    inv_pope_rows<HT, DQK, DC, NW * 64, BNK, false>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1],
                                                 b * e.dx_s[0] + hk * e.dx_s[1], k0, a.Sk, fr, dl,
                                                 a.delta != nullptr, nullptr, sdl, sf);
     if (e.part_delta || e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
@@ -1147,7 +1138,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 #pragma unroll
       for (int u = 0; u < EU; ++u) {
         const int r = r0 + u * rstep, key = k0 + r;
-        xv[u] = (r < BNK && key < a.Sk) ? load_as_float(e.x, xb + (int64_t)key * e.x_s[2], e.x_dtype) : 0.f;
+        xv[u] = (r < BNK && key < a.Sk) ? load_as_float_t<HT>(e.x, xb + (int64_t)key * e.x_s[2], e.x_dtype) : 0.f;
       }
     };
     float xv[EU], xn[EU];
@@ -1167,7 +1158,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           float dx;
           const float dph = inv_pope_elem(xv[u], pos, fr, dl, a.delta != nullptr, st[r * DQK + c],
                                           st[r * DQK + Dr + c], dx);
-          store_from_float(e.dx, b * e.dx_s[0] + hk * e.dx_s[1] + (int64_t)key * e.dx_s[2] + c * e.dx_s[3],
+          store_from_float_t<HT>(e.dx, b * e.dx_s[0] + hk * e.dx_s[1] + (int64_t)key * e.dx_s[2] + c * e.dx_s[3],
                            e.dx_dtype, dx);
           sdl += dph;
           sf += pos * dph;
@@ -1213,9 +1204,9 @@ __device__ __forceinline__ uint32_t keep_bf2(uint32_t v, bool lo, bool hi) {
   return (lo ? (v & 0xffffu) : 0u) | (hi ? (v & 0xffff0000u) : 0u);
 }
 
-template <int DQK, int NW, int BK, int NSTAGE>
+template <int HT, int DQK, int NW, int BK, int NSTAGE>
 __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
-  using M = MT<0>;
+  using M = MT<HT>;  // HT: the 16-bit operand type, bf16 (0) or fp16 (2)
   static_assert(NW == 8, "4 query groups x 2 column halves");
   constexpr int SZ = 1;  // tile swizzle kind (both tiles are only read with the transpose load)
   constexpr int NQG = NW / 2, QT = 8 / NQG;  // query groups; 32-query tiles per wave
@@ -1403,7 +1394,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
 #pragma unroll
         for (int u = 0; u < EU; ++u) {
           const int q = q0 + R0 + u * rstep;
-          xv[u] = q < a.Sq ? load_as_float(e.x, xb + (int64_t)q * e.x_s[2], e.x_dtype) : 0.f;
+          xv[u] = q < a.Sq ? load_as_float_t<HT>(e.x, xb + (int64_t)q * e.x_s[2], e.x_dtype) : 0.f;
         }
       };
       auto stage = [&](int half) {
@@ -1434,8 +1425,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
         for (int half = 0; half < 2; ++half) {
           stage(half);
           if constexpr (DC > 0)
-            content_rows<DQK, DC, NW * 64, 128>(e, st, tid, b * e.dxc_s[0] + h * e.dxc_s[1], q0 + half * 128, a.Sq);
-          inv_pope_rows<DQK, DC, NW * 64, 128, true>(e, st, tid, b * e.x_s[0] + h * e.x_s[1],
+            content_rows<HT, DQK, DC, NW * 64, 128>(e, st, tid, b * e.dxc_s[0] + h * e.dxc_s[1], q0 + half * 128, a.Sq);
+          inv_pope_rows<HT, DQK, DC, NW * 64, 128, true>(e, st, tid, b * e.x_s[0] + h * e.x_s[1],
                                                      b * e.dx_s[0] + h * e.dx_s[1], q0 + half * 128, a.Sq, fr8,
                                                      dl8, false, a.qtab, sdl8, sf8);
         }
@@ -1482,7 +1473,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
             const float pos = pe_pos(e.start_pos + q, e.pos_round);
             float dx;
             const float dph = inv_pope_elem(xv[u], pos, fr, 0.f, false, st[r * DQK + c], st[r * DQK + Dr + c], dx);
-            store_from_float(e.dx, b * e.dx_s[0] + h * e.dx_s[1] + (int64_t)q * e.dx_s[2] + c * e.dx_s[3],
+            store_from_float_t<HT>(e.dx, b * e.dx_s[0] + h * e.dx_s[1] + (int64_t)q * e.dx_s[2] + c * e.dx_s[3],
                              e.dx_dtype, dx);
             sf += pos * dph;
           }
@@ -1521,7 +1512,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
 template <int DT, int DQK, int DV>
 static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 4;
-  if constexpr (DT == 0) {
+  if constexpr (DT != 1) {
     if (which == 0) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
       if constexpr ((DQK == 128 || DQK == 256) && (DV == 128 || DV == 64)) {
@@ -1529,9 +1520,9 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
         // 64-query tiles where they fit the LDS (QK width 128, V width 64: the ~125M GPT shape and the
         // split training form), which halves the per-step barriers and waits per product
         constexpr int QT = DQK == 128 && DV == 64 ? 2 : 1;
-        hipLaunchKernelGGL((dkdv_pair_kernel<DQK, DV, QT>), dim3(nkb * a.nbh), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((dkdv_pair_kernel<DT, DQK, DV, QT>), dim3(nkb * a.nbh), dim3(512), 0, s, a);
       } else {
-        hipLaunchKernelGGL((dkdv_bf16_kernel<DQK, DV, NW>), dim3(nkb * a.nbh), dim3(NW * 64), 0, s, a);
+        hipLaunchKernelGGL((dkdv_bf16_kernel<DT, DQK, DV, NW>), dim3(nkb * a.nbh), dim3(NW * 64), 0, s, a);
       }
     } else {
       const int nqb = (a.Sq + 255) / 256;
@@ -1540,7 +1531,7 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       // 64-wide k~ (a 32-key tile of it is less than one DMA instruction per wave) keeps 64-key
       // steps double-buffered
       constexpr bool TW = DQK == 256 || DQK == 128;
-      hipLaunchKernelGGL((dq_gemm_kernel<DQK, 8, (TW ? 32 : 64), (TW ? 4 : 2)>), dim3(nqb * a.nbh * (a.Hq / a.Hkv)), dim3(8 * 64), 0, s, a);
+      hipLaunchKernelGGL((dq_gemm_kernel<DT, DQK, 8, (TW ? 32 : 64), (TW ? 4 : 2)>), dim3(nqb * a.nbh * (a.Hq / a.Hkv)), dim3(8 * 64), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {
@@ -1567,12 +1558,17 @@ static int bwd_dt(int which, int dqk, int dv, const CoreArgs& a, hipStream_t s) 
   return -3;
 }
 
+// dt: 0 bf16, 1 fp32, 2 fp16 operands
 int launch_bwd_dkdv(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s) {
-  return dt == 0 ? bwd_dt<0>(0, dqk, dv, a, s) : bwd_dt<1>(0, dqk, dv, a, s);
+  if (dt == 0) return bwd_dt<0>(0, dqk, dv, a, s);
+  if (dt == 2) return bwd_dt<2>(0, dqk, dv, a, s);
+  return bwd_dt<1>(0, dqk, dv, a, s);
 }
 
 int launch_bwd_dq(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s) {
-  return dt == 0 ? bwd_dt<0>(1, dqk, dv, a, s) : bwd_dt<1>(1, dqk, dv, a, s);
+  if (dt == 0) return bwd_dt<0>(1, dqk, dv, a, s);
+  if (dt == 2) return bwd_dt<2>(1, dqk, dv, a, s);
+  return bwd_dt<1>(1, dqk, dv, a, s);
 }
 
 }  // namespace pe

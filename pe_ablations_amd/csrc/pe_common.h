@@ -1,6 +1,6 @@
 // Device-side building blocks shared by the gfx950 PE-attention kernels.
 //
-// Matrix core layout (v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x2_f32, wave64), lane l, l32 = l%32,
+// Matrix core layout (v_mfma_f32_32x32x16_bf16 / _f16 / v_mfma_f32_32x32x2_f32, wave64), lane l, l32 = l%32,
 // g = l/32:
 //   A operand : row l32, contraction elements g*EPL .. g*EPL+EPL-1 of the current KC-wide step
 //   B operand : col l32, same contraction elements
@@ -53,6 +53,33 @@ __device__ __forceinline__ float bf2f(uint16_t h) {
 
 __device__ __forceinline__ float round_bf16(float x) { return bf2f(f2bf(x)); }
 
+// fp16 the same way (v_cvt_pk_f16_f32 / v_cvt_f32_f16, round-to-nearest-even)
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, h2_t));
+}
+__device__ __forceinline__ void unpack_h2(uint32_t v, float& lo, float& hi) {
+  const f32x2_t f = __builtin_convertvector(__builtin_bit_cast(h2_t, v), f32x2_t);
+  lo = f[0];
+  hi = f[1];
+}
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f2h(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+__device__ __forceinline__ float round_f16(float x) { return (float)(_Float16)x; }
+
+// Element types by the C ABI's dtype codes: 0 bf16, 1 fp32, 2 fp16.  The matrix-core kernels take
+// the 16-bit ones (HT 0 or 2) as a template parameter; these pack two floats into the operand dword
+// and round one float to the type.
+template <int HT> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  static_assert(HT == 0 || HT == 2, "16-bit type");
+  if constexpr (HT == 0) return pack_bf2(lo, hi);
+  else return pack_h2(lo, hi);
+}
+// round to the element type of dtype code `dt` (identity for fp32)
+__device__ __forceinline__ float round_to(float x, int dt) {
+  return dt == 0 ? round_bf16(x) : (dt == 2 ? round_f16(x) : x);
+}
+
 // A position as the phase product sees it (PE_POS_*): exact (0), or first rounded to the nearest
 // bf16 (1) or fp16 (2), ties to even, which is what torch.arange(..., dtype=x.dtype) holds for a
 // bf16 / fp16 x (fp16 overflows to inf past 65519)
@@ -70,12 +97,18 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float (&x)[8]) {
     x[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
   }
 }
+__device__ __forceinline__ void unpack8_h(const u32x4& v, float (&x)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) unpack_h2(v[i], x[2 * i], x[2 * i + 1]);
+}
 
 // 8 consecutive elements starting at element i (16-byte aligned) as floats / from floats;
-// dtype 0 = bf16 (one 16-byte access), 1 = fp32 (two)
+// dtype 0 = bf16 (one 16-byte access), 1 = fp32 (two), 2 = fp16 (one)
 __device__ __forceinline__ void load8(const void* p, int64_t i, int dtype, float (&x)[8]) {
   if (dtype == 0) {
     unpack8(*(const u32x4*)((const uint16_t*)p + i), x);
+  } else if (dtype == 2) {
+    unpack8_h(*(const u32x4*)((const uint16_t*)p + i), x);
   } else {
     const f32x4 a = *(const f32x4*)((const float*)p + i), b = *(const f32x4*)((const float*)p + i + 4);
 #pragma unroll
@@ -86,22 +119,62 @@ __device__ __forceinline__ void store8(void* p, int64_t i, int dtype, const floa
   if (dtype == 0) {
     *(u32x4*)((uint16_t*)p + i) =
         u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])};
+  } else if (dtype == 2) {
+    *(u32x4*)((uint16_t*)p + i) =
+        u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])};
   } else {
     *(f32x4*)((float*)p + i) = f32x4{x[0], x[1], x[2], x[3]};
     *(f32x4*)((float*)p + i + 4) = f32x4{x[4], x[5], x[6], x[7]};
   }
 }
 
-// storage element per compute dtype: DT 0 = bf16 (raw uint16), DT 1 = fp32
+// The same accesses inside the 16-bit kernels' epilogues, whose views hold either fp32 (dtype 1) or
+// the kernel's own 16-bit type HT (the host passes nothing else): two cases, chosen at compile time,
+// so the other 16-bit type adds no code to the kernels.
+template <int HT> __device__ __forceinline__ void load8t(const void* p, int64_t i, int dtype, float (&x)[8]) {
+  if (dtype != 1) {
+    if constexpr (HT == 0) unpack8(*(const u32x4*)((const uint16_t*)p + i), x);
+    else unpack8_h(*(const u32x4*)((const uint16_t*)p + i), x);
+  } else {
+    const f32x4 a = *(const f32x4*)((const float*)p + i), b = *(const f32x4*)((const float*)p + i + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
+  }
+}
+template <int HT> __device__ __forceinline__ void store8t(void* p, int64_t i, int dtype, const float (&x)[8]) {
+  if (dtype != 1) {
+    *(u32x4*)((uint16_t*)p + i) = u32x4{pack2<HT>(x[0], x[1]), pack2<HT>(x[2], x[3]), pack2<HT>(x[4], x[5]),
+                                        pack2<HT>(x[6], x[7])};
+  } else {
+    *(f32x4*)((float*)p + i) = f32x4{x[0], x[1], x[2], x[3]};
+    *(f32x4*)((float*)p + i + 4) = f32x4{x[4], x[5], x[6], x[7]};
+  }
+}
+template <int HT> __device__ __forceinline__ float load_as_float_t(const void* p, int64_t i, int dtype) {
+  if (dtype == 1) return ((const float*)p)[i];
+  if constexpr (HT == 0) return bf2f(((const uint16_t*)p)[i]);
+  else return h2f(((const uint16_t*)p)[i]);
+}
+template <int HT> __device__ __forceinline__ void store_from_float_t(void* p, int64_t i, int dtype, float x) {
+  if (dtype == 1) ((float*)p)[i] = x;
+  else if constexpr (HT == 0) ((uint16_t*)p)[i] = f2bf(x);
+  else ((uint16_t*)p)[i] = f2h(x);
+}
+
+// storage element per compute dtype: DT 0 = bf16 (raw uint16), DT 1 = fp32, DT 2 = fp16 (raw uint16)
 template <int DT> struct Elem;
 template <> struct Elem<0> { using T = uint16_t; };
 template <> struct Elem<1> { using T = float; };
+template <> struct Elem<2> { using T = uint16_t; };
 
 __device__ __forceinline__ float load_as_float(const void* p, int64_t i, int dtype) {
-  return dtype == 0 ? bf2f(((const uint16_t*)p)[i]) : ((const float*)p)[i];
+  if (dtype == 0) return bf2f(((const uint16_t*)p)[i]);
+  if (dtype == 2) return h2f(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
 }
 __device__ __forceinline__ void store_from_float(void* p, int64_t i, int dtype, float x) {
   if (dtype == 0) ((uint16_t*)p)[i] = f2bf(x);
+  else if (dtype == 2) ((uint16_t*)p)[i] = f2h(x);
   else ((float*)p)[i] = x;
 }
 
@@ -120,6 +193,22 @@ template <> struct MT<0> {
     r[1] = pack_bf2(c[j0 + 2], c[j0 + 3]);
     r[2] = pack_bf2(c[j0 + 4], c[j0 + 5]);
     r[3] = pack_bf2(c[j0 + 6], c[j0 + 7]);
+    return r;
+  }
+};
+template <> struct MT<2> {  // fp16 operands, the same fragment layout as bf16
+  static constexpr int KC = 16, EPL = 8, ESZ = 2;
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+  __device__ __forceinline__ static u32x4 pack(const f32x16& c, int j0) {
+    u32x4 r;
+    r[0] = pack_h2(c[j0 + 0], c[j0 + 1]);
+    r[1] = pack_h2(c[j0 + 2], c[j0 + 3]);
+    r[2] = pack_h2(c[j0 + 4], c[j0 + 5]);
+    r[3] = pack_h2(c[j0 + 6], c[j0 + 7]);
     return r;
   }
 };
@@ -150,12 +239,12 @@ template <> struct MT<1> {
 __device__ __forceinline__ int c_row(int j, int g) { return ((j >> 2) << 3) + (g << 2) + (j & 3); }
 
 template <int DT> __device__ __forceinline__ int perm_row(int r) {
-  if constexpr (DT == 0) return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+  if constexpr (DT != 1) return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
   else return r;
 }
 // logical row (contraction index) of C value j in lane group g after perm_row loading
 template <int DT> __device__ __forceinline__ int c_logical(int j, int g) {
-  if constexpr (DT == 0) return ((j >> 3) << 4) + (g << 3) + (j & 7);
+  if constexpr (DT != 1) return ((j >> 3) << 4) + (g << 3) + (j & 7);
   else return ((j >> 2) << 3) + (g << 2) + (j & 3);
 }
 
@@ -193,7 +282,7 @@ template <int NCH> __device__ __forceinline__ u32x4 lds_row_frag(const char* til
 // Operand fragment whose contraction runs down the tile rows: rows k0 + g*EPL .. +EPL-1,
 // column n0 + l32 (element units).
 template <int DT, int NCH> __device__ __forceinline__ u32x4 lds_col_frag(const char* tile, int k0, int n0, int lane) {
-  if constexpr (DT == 0) {
+  if constexpr (DT != 1) {
     const int i = lane & 15, G4 = (lane >> 4) & 3;
     const int col = n0 + ((G4 & 1) << 4) + ((i & 3) << 2);
     const int row = k0 + ((lane >> 5) << 3) + (i >> 2);

@@ -322,7 +322,9 @@ static int decode_dt(int dqk, int dv, const DecodeArgs& a, hipStream_t s) {
 
 int launch_decode(int dt, int dqk, int dv, const DecodeArgs& a, hipStream_t s) {
   if (a.nunit % 4 != 0 || a.nunit <= 0 || a.nunit > 512 || a.nqt <= 0) return -2;
-  return dt == 0 ? decode_dt<0>(dqk, dv, a, s) : decode_dt<1>(dqk, dv, a, s);
+  if (dt == 0) return decode_dt<0>(dqk, dv, a, s);  // bf16
+  if (dt == 2) return decode_dt<2>(dqk, dv, a, s);  // fp16
+  return decode_dt<1>(dqk, dv, a, s);
 }
 
 }  // namespace pe

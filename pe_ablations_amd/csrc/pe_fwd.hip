@@ -171,9 +171,9 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) 
 // waves share each SIMD (<= 256 registers per wave), so one wave's softmax overlaps the other's
 // MFMAs.  The running max is raised lazily: O and l are rescaled only when some query's block
 // max exceeds the current one by more than TAU (in log2 units), which bounds p by 2^TAU.
-template <int DQK, int DV, int BN, int NW, int NDW, int NSTG>
+template <int HT, int DQK, int DV, int BN, int NW, int NDW, int NSTG>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(CoreArgs a, int o_vec) {
-  using M = MT<0>;
+  using M = MT<HT>;  // HT: the 16-bit operand type, bf16 (0) or fp16 (2)
   constexpr int BM = NW * 32;
   constexpr int NCK = DQK / 8, NCV = DV / 8;
   constexpr int NQF = DQK / 16, NKT = BN / 32, NPF = BN / 16, NOT = DV / 32;
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int dv = t * 32 + c_row(j, g);
-      *(uint16_t*)(smem + (w * 32 + l32) * SO_STRIDE + dv * 2) = f2bf(o[t][j] * inv);
+      *(uint16_t*)(smem + (w * 32 + l32) * SO_STRIDE + dv * 2) = HT == 0 ? f2bf(o[t][j] * inv) : f2h(o[t][j] * inv);
     }
   if (g == 0 && myq < a.Sq)
     a.lse[(int64_t)(b * a.Hq + h) * a.Sq + myq] = lt > 0.f ? (m + __log2f(lt)) * LN2 : -INFINITY;
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
   }
 }
 
-template <int DQK, int DV>
+template <int HT, int DQK, int DV>
 static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 8;
   // four DMA waves, a double-buffered ring (a 3-tile ring measured 1.44 against 1.41 ms)
@@ -402,11 +402,11 @@ static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
   // 1.37 vs 1.40 ms at S = 16384, 3 % faster at S = 2048); on short sequences the wider diagonal
   // tiles waste more than that saves (S = 512: 0.023 vs 0.021 ms), so they keep 64-key tiles
   if (small)
-    hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, 64, 4, 4, NSTG>), dim3(grid4), dim3(4 * 64), 0, s, a, o_vec);
+    hipLaunchKernelGGL((fwd_bf16_kernel<HT, DQK, DV, 64, 4, 4, NSTG>), dim3(grid4), dim3(4 * 64), 0, s, a, o_vec);
   else if (a.Sk >= 2048)
-    hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, 96, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
+    hipLaunchKernelGGL((fwd_bf16_kernel<HT, DQK, DV, 96, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
   else
-    hipLaunchKernelGGL((fwd_bf16_kernel<DQK, DV, 64, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
+    hipLaunchKernelGGL((fwd_bf16_kernel<HT, DQK, DV, 64, NW, NDW, NSTG>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
@@ -431,13 +431,13 @@ bool core_supported(int dqk, int dv) {
 
 template <int DT>
 static int fwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
-  if constexpr (DT == 0) {
-    if (dqk == 64 && dv == 64) return run_fwd_bf16<64, 64>(a, s);
-    if (dqk == 64 && dv == 128) return run_fwd_bf16<64, 128>(a, s);
-    if (dqk == 128 && dv == 64) return run_fwd_bf16<128, 64>(a, s);
-    if (dqk == 128 && dv == 128) return run_fwd_bf16<128, 128>(a, s);
-    if (dqk == 256 && dv == 64) return run_fwd_bf16<256, 64>(a, s);
-    if (dqk == 256 && dv == 128) return run_fwd_bf16<256, 128>(a, s);
+  if constexpr (DT != 1) {
+    if (dqk == 64 && dv == 64) return run_fwd_bf16<DT, 64, 64>(a, s);
+    if (dqk == 64 && dv == 128) return run_fwd_bf16<DT, 64, 128>(a, s);
+    if (dqk == 128 && dv == 64) return run_fwd_bf16<DT, 128, 64>(a, s);
+    if (dqk == 128 && dv == 128) return run_fwd_bf16<DT, 128, 128>(a, s);
+    if (dqk == 256 && dv == 64) return run_fwd_bf16<DT, 256, 64>(a, s);
+    if (dqk == 256 && dv == 128) return run_fwd_bf16<DT, 256, 128>(a, s);
     return -3;
   } else {
     if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64>(a, s);
@@ -450,8 +450,11 @@ static int fwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
   }
 }
 
+// dt: 0 bf16, 1 fp32, 2 fp16 operands
 int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s) {
-  return dt == 0 ? fwd_dt<0>(dqk, dv, a, s) : fwd_dt<1>(dqk, dv, a, s);
+  if (dt == 0) return fwd_dt<0>(dqk, dv, a, s);
+  if (dt == 2) return fwd_dt<2>(dqk, dv, a, s);
+  return fwd_dt<1>(dqk, dv, a, s);
 }
 
 }  // namespace pe

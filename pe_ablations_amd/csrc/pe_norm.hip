@@ -29,18 +29,22 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// normalise one chunk in place: n = fl(x * r) rounded to x's dtype, y = fl(n * w) (bf16 if both are)
-__device__ __forceinline__ void norm_chunk(float (&x)[8], float r, bool x_bf, const void* w, int w_dtype,
+// y's dtype code under torch's type promotion of (normalised value in x's dtype) * weight: the
+// 16-bit type when x and w share it, else fp32 (bf16 * fp16 promotes to fp32 as well)
+__host__ __device__ inline int norm_y_dtype(int x_dtype, int w_dtype) {
+  return (x_dtype == w_dtype && x_dtype != 1) ? x_dtype : 1;
+}
+
+// normalise one chunk in place: n = fl(x * r) rounded to x's dtype, y = fl(n * w) rounded to y's
+__device__ __forceinline__ void norm_chunk(float (&x)[8], float r, int x_dtype, const void* w, int w_dtype,
                                            int64_t wi) {
   float wv[8];
   load8(w, wi, w_dtype, wv);
-  const bool y_bf = x_bf && w_dtype == 0;
+  const int ydt = norm_y_dtype(x_dtype, w_dtype);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float n = x[e] * r;
-    if (x_bf) n = round_bf16(n);
-    const float y = n * wv[e];
-    x[e] = y_bf ? round_bf16(y) : y;
+    const float n = round_to(x[e] * r, x_dtype);
+    x[e] = round_to(n * wv[e], ydt);
   }
 }
 
@@ -67,7 +71,7 @@ __global__ __launch_bounds__(WPB * 64) void rmsnorm_kernel(NormArgs a) {
   for (int k = 0; k < CPL; ++k) {
     const int c = lane + k * 64;
     if (c < nch) {
-      norm_chunk(x[k], r, a.x_dtype == 0, a.w, a.w_dtype, c * 8);
+      norm_chunk(x[k], r, a.x_dtype, a.w, a.w_dtype, c * 8);
       store8(a.y, row * a.y_rs + c * 8, a.y_dtype, x[k]);
     }
   }
@@ -101,7 +105,7 @@ __global__ __launch_bounds__(WPB * 64) void prep_pope_norm_kernel(PrepArgs a) {
     const int c = lane + k * 64;
     if (c < nch) {
       const int h = c / tpr, t = c - h * tpr;
-      norm_chunk(x[k], r, a.xr_dtype == 0, a.norm_w, a.norm_w_dtype, c * 8);
+      norm_chunk(x[k], r, a.xr_dtype, a.norm_w, a.norm_w_dtype, c * 8);
       const f32x4 f0 = *(const f32x4*)(a.freqs + t * 8), f1 = *(const f32x4*)(a.freqs + t * 8 + 4);
       f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
       if (add) {
@@ -175,15 +179,15 @@ static void with_cpl(int cpl, F&& f) {
 
 // 16-byte aligned base and 8-element chunks that stay 16-byte aligned along every stride
 static bool rows_aligned(const void* p, int dtype, int64_t s0, int64_t s1, int64_t s2) {
-  const int64_t q = dtype == 0 ? 8 : 4;
+  const int64_t q = dtype == 1 ? 4 : 8;
   return ((uintptr_t)p % 16) == 0 && s0 % q == 0 && s1 % q == 0 && s2 % q == 0;
 }
 
 int launch_rmsnorm(const NormArgs& a, hipStream_t s) {
   if (a.rows <= 0 || a.rows > 0x7fffffff || a.n <= 0) return -2;
   if (a.n % 8 != 0 || a.n > 64 * MAXCPL * 8) return -3;
-  if ((a.x_dtype | a.w_dtype | a.y_dtype) & ~1) return -4;
-  if (a.y_dtype != ((a.x_dtype == 0 && a.w_dtype == 0) ? 0 : 1)) return -4;
+  if (a.x_dtype < 0 || a.x_dtype > 2 || a.w_dtype < 0 || a.w_dtype > 2) return -4;
+  if (a.y_dtype != norm_y_dtype(a.x_dtype, a.w_dtype)) return -4;
   if (!rows_aligned(a.x, a.x_dtype, a.x_rs, 0, 0) || !rows_aligned(a.y, a.y_dtype, a.y_rs, 0, 0) ||
       ((uintptr_t)a.w % 16) != 0)
     return -5;
@@ -198,6 +202,7 @@ int launch_rmsnorm(const NormArgs& a, hipStream_t s) {
 // in fp32): with r = rsqrt(mean(x^2) + eps) (the forward's sum, in the forward's order) and
 // nc = (x r) rounded to x's dtype,
 //   gc = (dy w) rounded to x's dtype   (the product in y's dtype, the gradient of the cast value)
+//   (y's dtype: the 16-bit type when x and w share it, else fp32)
 //   c  = sum_j gc_j x_j                 (the gradient reaching r through x * r)
 //   dx = gc r + x (2/n) (-r^3 c / 2)    (rsqrt's and mean's gradients), rounded to x's dtype
 //   dw = sum over rows of (dy nc)       (each product rounded to y's dtype when y is bf16; the sum
@@ -211,8 +216,7 @@ __global__ __launch_bounds__(WPB * 64) void rmsnorm_bwd_kernel(NormBwdArgs a) {
   __shared__ __attribute__((aligned(16))) float slab[WPB][64 * 8];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nch = a.n >> 3;
-  const bool x_bf = a.x_dtype == 0, y_bf = a.x_dtype == 0 && a.w_dtype == 0;
-  const int ydt = y_bf ? 0 : 1;
+  const int ydt = norm_y_dtype(a.x_dtype, a.w_dtype);
   float dwa[CPL][8];
 #pragma unroll
   for (int k = 0; k < CPL; ++k)
@@ -245,16 +249,11 @@ __global__ __launch_bounds__(WPB * 64) void rmsnorm_bwd_kernel(NormBwdArgs a) {
         load8(a.w, c * 8, a.w_dtype, wv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          float g = dy[e] * wv[e];
-          if (y_bf) g = round_bf16(g);
-          if (x_bf) g = round_bf16(g);
+          const float g = round_to(round_to(dy[e] * wv[e], ydt), a.x_dtype);
           gc[k][e] = g;
           cs += g * x[k][e];
-          float nc = x[k][e] * r;
-          if (x_bf) nc = round_bf16(nc);
-          float p = dy[e] * nc;
-          if (y_bf) p = round_bf16(p);
-          dwa[k][e] += p;
+          const float nc = round_to(x[k][e] * r, a.x_dtype);
+          dwa[k][e] += round_to(dy[e] * nc, ydt);
         }
       }
     }
@@ -316,9 +315,9 @@ int64_t rmsnorm_bwd_part_floats(int64_t rows, int n, int n_cu) {
 int launch_rmsnorm_bwd(NormBwdArgs a, int n_cu, hipStream_t s) {
   if (a.rows <= 0 || a.rows > 0x7fffffff || a.n <= 0) return -2;
   if (a.n % 8 != 0 || a.n > 64 * MAXCPL * 8) return -3;
-  if ((a.x_dtype | a.w_dtype) & ~1) return -4;
+  if (a.x_dtype < 0 || a.x_dtype > 2 || a.w_dtype < 0 || a.w_dtype > 2) return -4;
   if (a.dw_dtype != a.w_dtype) return -4;
-  const int ydt = (a.x_dtype == 0 && a.w_dtype == 0) ? 0 : 1;
+  const int ydt = norm_y_dtype(a.x_dtype, a.w_dtype);
   if (!rows_aligned(a.x, a.x_dtype, a.x_rs, 0, 0) || !rows_aligned(a.dy, ydt, a.dy_rs, 0, 0) ||
       !rows_aligned(a.dx, a.x_dtype, a.dx_rs, 0, 0) || ((uintptr_t)a.w % 16) != 0 || ((uintptr_t)a.part % 16) != 0)
     return -5;
@@ -363,7 +362,9 @@ int launch_swiglu(const void* x, const void* gate, void* out, int64_t n, hipStre
 }
 
 int launch_prep_norm(const PrepArgs& a, hipStream_t s) {
-  if (a.mode != 0 || !a.norm_w || ((a.norm_w_dtype | a.xr_dtype | a.dst_dtype) & ~1)) return -4;
+  if (a.mode != 0 || !a.norm_w || a.norm_w_dtype < 0 || a.norm_w_dtype > 2 || a.xr_dtype < 0 || a.xr_dtype > 2 ||
+      a.dst_dtype < 0 || a.dst_dtype > 2)
+    return -4;
   if (a.dst_rows != 0 || a.dst_row0 != 0) return -2;  // writes contiguous (B, H, S, width) rows only
   if (a.Dr <= 0 || a.Dr % 8 != 0 || a.Dc % 8 != 0 || a.width % 8 != 0 || a.H * (a.Dr / 8) > 64 * MAXCPL) return -3;
   if ((int64_t)a.B * a.S > 0x7fffffff) return -2;
@@ -376,6 +377,7 @@ int launch_prep_norm(const PrepArgs& a, hipStream_t s) {
   with_cpl(chunks_per_lane(a.H * (a.Dr / 8)), [&](auto c) {
     constexpr int C = decltype(c)::value;
     if (a.dst_dtype == 0) hipLaunchKernelGGL((prep_pope_norm_kernel<0, C>), grid, dim3(WPB * 64), 0, s, a);
+    else if (a.dst_dtype == 2) hipLaunchKernelGGL((prep_pope_norm_kernel<2, C>), grid, dim3(WPB * 64), 0, s, a);
     else hipLaunchKernelGGL((prep_pope_norm_kernel<1, C>), grid, dim3(WPB * 64), 0, s, a);
   });
   return hipGetLastError() == hipSuccess ? 0 : -7;

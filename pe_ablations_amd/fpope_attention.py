@@ -17,7 +17,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .functional import cache_widths, pe_attention, pe_attention_decode, pe_cache_append
+from .functional import cache_widths, norm_out_dtype, pe_attention, pe_attention_decode, pe_cache_append
 from .normalization import RMSNorm
 
 
@@ -106,9 +106,8 @@ class FPoPEGroupedQueryAttention(nn.Module):
         if fuse_norm:
             norm = dict(qr_norm_weight=self.qr_norm.weight, kr_norm_weight=self.kr_norm.weight,
                         norm_eps=self.qr_norm.eps)
-            # RMSNorm's output: bf16 only when the projection and the weight are both bf16
-            both_bf16 = q_r.dtype == torch.bfloat16 and self.qr_norm.weight.dtype == torch.bfloat16
-            x_dtype = torch.bfloat16 if both_bf16 else torch.float32
+            # RMSNorm's output dtype: the 16-bit type when the projection and the weight share it
+            x_dtype = norm_out_dtype(q_r.dtype, self.qr_norm.weight.dtype)
         return pe_attention(q_r, k_r, v, mode="pope", q_c=q_c, k_c=k_c, freqs=self.fpope.kernel_freqs(),
                             delta=self.fpope.kernel_delta(), scale=self.scale, causal=causal,
                             start_pos_q=start_q, start_pos_k=start_k,
@@ -164,9 +163,12 @@ class KVCache:
 
 
 def cache_compute_dtype(x: torch.Tensor) -> torch.dtype:
-    """bf16 under autocast or for bf16 / fp16 activations, else fp32 (as pe_attention decides)."""
-    if torch.is_autocast_enabled() or x.dtype in (torch.bfloat16, torch.float16):
-        return torch.bfloat16
+    """Autocast's dtype under autocast, the activations' 16-bit type, else fp32 (as pe_attention
+    decides)."""
+    if torch.is_autocast_enabled():
+        return torch.get_autocast_dtype("cuda")
+    if x.dtype in (torch.bfloat16, torch.float16):
+        return x.dtype
     return torch.float32
 
 

@@ -35,7 +35,20 @@ def _dtype_code(t: torch.dtype) -> int:
         return _lib.PE_DTYPE_BF16
     if t == torch.float32:
         return _lib.PE_DTYPE_FP32
+    if t == torch.float16:
+        return _lib.PE_DTYPE_FP16
     raise TypeError(f"pe_attention: unsupported tensor dtype {t}")
+
+
+_TORCH_DTYPE = {_lib.PE_DTYPE_BF16: torch.bfloat16, _lib.PE_DTYPE_FP32: torch.float32,
+                _lib.PE_DTYPE_FP16: torch.float16}
+_HALF = (torch.bfloat16, torch.float16)
+
+
+def norm_out_dtype(x_dtype: torch.dtype, w_dtype: torch.dtype) -> torch.dtype:
+    """RMSNorm's output dtype, torch's promotion of (normalised value in x's dtype) * weight: the
+    16-bit type when x and the weight share it, else fp32 (bf16 * fp16 promotes to fp32 too)."""
+    return x_dtype if (x_dtype == w_dtype and x_dtype in _HALF) else torch.float32
 
 
 def _tensor(t: Optional[torch.Tensor]) -> _lib.PeTensor:
@@ -56,8 +69,8 @@ def _tensor(t: Optional[torch.Tensor]) -> _lib.PeTensor:
 def _prep_in(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     if t is None:
         return None
-    if t.dtype not in (torch.bfloat16, torch.float32):
-        t = t.to(torch.bfloat16 if t.dtype == torch.float16 else torch.float32)
+    if t.dtype not in (torch.bfloat16, torch.float32, torch.float16):
+        t = t.to(torch.float32)
     if t.stride(-1) != 1 and t.shape[-1] != 1:
         t = t.contiguous()
     return t
@@ -206,7 +219,7 @@ class _FwdPlan:
         self.pref = ctypes.byref(self.p)
         _lib.check(L.pe_attn_check(self.pref))
         self.ws = L.pe_attn_fwd_workspace_bytes(self.pref)
-        self.cdt = torch.bfloat16 if cfg["dtype"] == _lib.PE_DTYPE_BF16 else torch.float32
+        self.cdt = _TORCH_DTYPE[cfg["dtype"]]
         B, Hq, Sq, Dv = qr.shape[0], qr.shape[1], qr.shape[2], v.shape[3]
         self.out_shape = (B, Sq, Hq, Dv)
         out = torch.empty(self.out_shape, dtype=self.cdt, device=qr.device).transpose(1, 2)
@@ -292,7 +305,7 @@ def _attn_backward(key, cfg, qr, kr, v, qc, kc, freqs, delta, out, lse, fws, dou
         dout = torch.zeros_like(out)
     if dout.stride(-1) != 1:
         dout = dout.contiguous()
-    if dout.dtype not in (torch.bfloat16, torch.float32):
+    if dout.dtype not in (torch.bfloat16, torch.float32, torch.float16):
         dout = dout.float()
     dqr, dkr = torch.empty_like(qr), torch.empty_like(kr)
     dqc = None if qc is None else torch.empty_like(qc)
@@ -328,11 +341,15 @@ ctypes_ref = ref
 
 
 def _compute_dtype(tensors) -> int:
+    """The dtype SDPA would compute in: autocast's (fp16 or bf16) when autocast is on, else the
+    inputs' 16-bit type (bf16 when both occur), else fp32."""
     if torch.is_autocast_enabled():
+        return _lib.PE_DTYPE_FP16 if torch.get_autocast_dtype("cuda") == torch.float16 else _lib.PE_DTYPE_BF16
+    dts = {t.dtype for t in tensors if t is not None}
+    if torch.bfloat16 in dts:
         return _lib.PE_DTYPE_BF16
-    for t in tensors:
-        if t is not None and t.dtype in (torch.bfloat16, torch.float16):
-            return _lib.PE_DTYPE_BF16
+    if torch.float16 in dts:
+        return _lib.PE_DTYPE_FP16
     return _lib.PE_DTYPE_FP32
 
 
@@ -369,7 +386,6 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
     m = _MODES[mode]
     check_operands(q, k, v, q_c, k_c, freqs if m != _lib.PE_MODE_NONE else None, delta, mode=m,
                    q_norm_weight=qr_norm_weight, k_norm_weight=kr_norm_weight)
-    half_in = q.dtype == torch.float16
     q, k, v, q_c, k_c = (_prep_in(t) for t in (q, k, v, q_c, k_c))
     if m != _lib.PE_MODE_NONE:
         if freqs is None:
@@ -389,6 +405,10 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
         dt = _compute_dtype((q, k, v, q_c, k_c))
     else:
         dt = _dtype_code(compute_dtype)
+    if dt != _lib.PE_DTYPE_FP32:
+        # the other 16-bit type goes in as fp32 (exact); the kernels round it to the compute's
+        q, k, v, q_c, k_c = (t.float() if t is not None and t.dtype in _HALF and t.dtype != _TORCH_DTYPE[dt]
+                             else t for t in (q, k, v, q_c, k_c))
     cfg = dict(mode=m, dtype=dt, causal=_CAUSAL[causal], start_pos_q=int(start_pos_q),
                start_pos_k=int(start_pos_k), qk_norm=bool(qk_norm), scale=float(scale),
                mscale=float(rope_mscale), pos_round=position_rounding(position_dtype, m))
@@ -397,8 +417,6 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
         out, lse = _fwd_normed(q, k, v, q_c, k_c, freqs, delta, cfg, qr_norm_weight, kr_norm_weight, norm_eps)
     else:
         out, lse = PEAttentionFn.apply(q, k, v, q_c, k_c, freqs, delta, cfg)
-    if half_in:
-        out = out.to(torch.float16)
     return (out, lse) if return_lse else out
 
 
@@ -416,8 +434,8 @@ def _fwd_normed(qr, kr, v, qc, kc, freqs, delta, cfg, wq, wk, eps):
         raise ValueError("the fused position-projection RMSNorm applies to PoPE / FoPE only")
     if wq is None or wk is None:
         raise ValueError("pass both qr_norm_weight and kr_norm_weight")
-    if wq.dtype != wk.dtype or wq.dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError("qr/kr norm weights must share one dtype, bf16 or fp32")
+    if wq.dtype != wk.dtype or wq.dtype not in (torch.bfloat16, torch.float32, torch.float16):
+        raise TypeError("qr/kr norm weights must share one dtype, bf16, fp16 or fp32")
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad
                                        for t in (qr, kr, v, qc, kc, freqs, delta, wq, wk)):
         return PENormedAttentionFn.apply(qr, kr, v, qc, kc, freqs, delta, wq, wk, cfg, float(eps))
@@ -434,7 +452,7 @@ def _launch_normed(qr, kr, v, qc, kc, freqs, delta, cfg, wq, wk, eps):
     n = _lib.PeNormParams()
     n.q_weight, n.k_weight = wq.data_ptr(), wk.data_ptr()
     n.weight_dtype, n.eps = _dtype_code(wq.dtype), float(eps)
-    cdt = torch.bfloat16 if cfg["dtype"] == _lib.PE_DTYPE_BF16 else torch.float32
+    cdt = _TORCH_DTYPE[cfg["dtype"]]
     B, Hq, Sq, Dv = qr.shape[0], qr.shape[1], qr.shape[2], v.shape[3]
     ws_bytes = L.pe_attn_fwd_workspace_bytes(ctypes_ref(p))
     fws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -501,12 +519,12 @@ def rms_norm_backward(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, e
     if not x.is_cuda:
         raise RuntimeError("rms_norm_backward runs on the GPU only (got a CPU tensor)")
     n = x.shape[-1]
-    ydt = torch.bfloat16 if (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16) else torch.float32
+    ydt = norm_out_dtype(x.dtype, weight.dtype)
     x2 = x.reshape(-1, n)
     dy2 = dy.reshape(-1, n).to(ydt)
-    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % (8 if x.dtype == torch.bfloat16 else 4):
+    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % (8 if x.dtype in _HALF else 4):
         x2 = x2.contiguous()
-    if dy2.stride(-1) != 1 or dy2.data_ptr() % 16 or dy2.stride(0) % (8 if ydt == torch.bfloat16 else 4):
+    if dy2.stride(-1) != 1 or dy2.data_ptr() % 16 or dy2.stride(0) % (8 if ydt in _HALF else 4):
         dy2 = dy2.contiguous()
     w = weight.contiguous()
     dx = torch.empty((x2.shape[0], n), dtype=x.dtype, device=x.device)
@@ -530,14 +548,15 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
     bf16, else fp32.  No autograd: the module uses it when no gradient is needed."""
     if not x.is_cuda:
         raise RuntimeError("rms_norm runs on the GPU only (got a CPU tensor)")
-    if x.dtype not in (torch.bfloat16, torch.float32) or weight.dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError("rms_norm supports bf16 / fp32 tensors")
+    if x.dtype not in (torch.bfloat16, torch.float32, torch.float16) or \
+            weight.dtype not in (torch.bfloat16, torch.float32, torch.float16):
+        raise TypeError("rms_norm supports bf16 / fp16 / fp32 tensors")
     n = x.shape[-1]
     x2 = x.reshape(-1, n)
-    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % (8 if x.dtype == torch.bfloat16 else 4):
+    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % (8 if x.dtype in _HALF else 4):
         x2 = x2.contiguous()
     w = weight.contiguous()
-    ydt = torch.bfloat16 if (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16) else torch.float32
+    ydt = norm_out_dtype(x.dtype, w.dtype)
     y = torch.empty((x2.shape[0], n), dtype=ydt, device=x.device)
     if x2.shape[0] == 0:
         return y.view(*x.shape[:-1], n)

@@ -458,3 +458,30 @@ def test_rms_norm_gradient_rounds_once():
     xt = x.clone().requires_grad_(True)
     ((xt.float() * torch.rsqrt(xt.float().pow(2).mean(-1, keepdim=True) + 1e-6)).type_as(xt) * w).backward(dy)
     assert not torch.equal(xt.grad, once)     # the two-cast form differs here
+
+
+def test_fp16_path_tracks_torch_fp16_sdpa():
+    """The fp16 variant of the reference path against torch's own fp16
+    F.scaled_dot_product_attention on the CPU: out and dQ agree to one fp16 spacing at their largest
+    magnitude, with largest errors to the exact core within a factor 1.5 of torch's; dK / dV errors
+    at most 1.5 times torch's."""
+    q, k, v, do = _qkv(0, 1, 2, 2, 300, 64, torch.float16)
+    ts = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    o = F.scaled_dot_product_attention(*ts, is_causal=True)
+    o.backward(do)
+    ex = [t.double().requires_grad_(True) for t in (q, k, v)]
+    oe, _ = O.attention(*ex, 64 ** -0.5, True)
+    oe.backward(do.double())
+    pa = [t.double().requires_grad_(True) for t in (q, k, v)]
+    op, _ = O.attention_fp16_path(*pa, 64 ** -0.5, True)
+    op.backward(do.double())
+    ulp = lambda x: 2.0 ** (math.floor(math.log2(x)) - 10)  # fp16 spacing at magnitude x
+    res = {"out": (o, op, oe), "dq": (ts[0].grad, pa[0].grad, ex[0].grad),
+           "dk": (ts[1].grad, pa[1].grad, ex[1].grad), "dv": (ts[2].grad, pa[2].grad, ex[2].grad)}
+    for n, (t, pth, e) in res.items():
+        et = (t.double() - e).abs().max().item()
+        ep = (pth.double() - e).abs().max().item()
+        assert 0 < ep <= 1.5 * et, (n, et, ep)
+        if n in ("out", "dq"):
+            assert (t.double() - pth.double()).abs().max().item() <= ulp(e.abs().max().item()), n
+            assert ep >= et / 1.5, (n, et, ep)
