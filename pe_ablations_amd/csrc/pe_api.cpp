@@ -39,7 +39,8 @@ bool valid_dt(int dtype) { return dtype == PE_DTYPE_BF16 || dtype == PE_DTYPE_FP
 struct Layout {
   int dqk, dv;
   size_t q_off, k_off, v_off, tab_off, fwd_total;
-  size_t do_off, di_off, l2_off, dq_off, dk_off, pq_off, pk_off, pkd_off, ds_off, bwd_total;
+  size_t do_off, di_off, l2_off, dq_off, dk_off, pq_off, pk_off, pkd_off, dvp_off, ds_off, bwd_total;
+  int ksplit;    // query-head split of the dK/dV pair kernel (pe::CoreArgs::qsplit)
   int sq_pad;
   int ds_nqt, ds_rows, ds_e;
   int64_t ds_head;
@@ -56,6 +57,22 @@ bool use_qtab(const pe_attn_params* p) { return p->mode == PE_MODE_POPE && p->Dr
 bool fused_bwd(const pe_attn_params* p) {
   return half_dt(p->dtype) && p->mode == PE_MODE_POPE && p->Dc == 0 && (p->Dr == 64 || p->Dr == 128) &&
          pad_qk(qk_width(p)) == 2 * p->Dr;
+}
+
+// Compute units of an MI355X.  The query-head split of dK/dV below depends on the shape only (not
+// on the device queried), so a workspace size taken before any device call stays valid.
+constexpr int kSplitCus = 256;
+
+// dK/dV pair kernel (16-bit, transformed width 128 / 256, value width 64 / 128) on a grid of fewer
+// key blocks than compute units: each key block's GQA group of query heads is shared out over up
+// to Hq / Hkv workgroups (a power of two dividing it) until the grid reaches the compute units
+int key_split(const pe_attn_params* p, int dqk, int dv) {
+  if (!half_dt(p->dtype) || !((dqk == 128 || dqk == 256) && (dv == 64 || dv == 128))) return 1;
+  const int grp = p->Hq / p->Hkv;
+  const int64_t blocks = (int64_t)p->B * p->Hkv * ((p->Sk + 127) / 128);
+  int ks = 1;
+  while (grp % (2 * ks) == 0 && blocks * ks < kSplitCus) ks *= 2;
+  return ks;
 }
 
 // a view the vectorised epilogues can read or write 8 elements at a time: unit dim stride and
@@ -104,11 +121,14 @@ Layout layout(const pe_attn_params* p) {
   L.l2_off = L.di_off + align_up(nq_pad * 4);
   L.dq_off = L.l2_off + align_up(nq_pad * 4);
   const bool fb = fused_bwd(p);
+  L.ksplit = key_split(p, L.dqk, L.dv);
   L.dk_off = L.dq_off + (fb ? 0 : align_up(nq * L.dqk * 4));
-  L.pq_off = L.dk_off + (fb ? 0 : align_up(nk * L.dqk * 4));
+  // dk~ (unfused) or the split's partial dk~ slices
+  L.pq_off = L.dk_off + (fb && L.ksplit == 1 ? 0 : align_up(nk * L.dqk * 4 * L.ksplit));
   L.pk_off = L.pq_off + align_up((size_t)L.nq_blocks * p->Dr * 4);
   L.pkd_off = L.pk_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
-  L.ds_off = L.pkd_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
+  L.dvp_off = L.pkd_off + align_up((size_t)L.nk_blocks * p->Dr * 4);
+  L.ds_off = L.dvp_off + (L.ksplit > 1 ? align_up(nk * L.dv * 4 * L.ksplit) : 0);
   // bf16 path: dS in fragment order, 4 KiB blocks packed per (b, h) to the blocks the causal
   // dK/dV kernel stores (pe::ds_row_base), written by it for the dQ GEMM.  The dQ GEMM's masked
   // edge steps also load up to four blocks before a key row's first stored one; those lie in the
@@ -222,6 +242,7 @@ pe::CoreArgs core_args(const pe_attn_params* p, const Layout& L, const char* ws,
   c.scale = p->scale;
   c.bh0 = 0;
   c.nbh = p->B * p->Hkv;
+  c.qsplit = 1;
   return c;
 }
 
@@ -745,6 +766,8 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   c.dq_t = (float*)(bws + L.dq_off);
   c.qtab = use_qtab(p) ? (const float*)(fws + L.tab_off) : nullptr;
   c.dk_t = (float*)(bws + L.dk_off);
+  c.qsplit = L.ksplit;
+  c.dv_part = L.ksplit > 1 ? (float*)(bws + L.dvp_off) : nullptr;
   c.dv = (void*)dv->data; c.dv_sb = dv->stride[0]; c.dv_sh = dv->stride[1]; c.dv_ss = dv->stride[2];
   c.dv_dtype = dv->dtype;
   stage_mark(PE_STAGE_BWD_DKDV, 0, s);

@@ -754,6 +754,121 @@ __device__ __forceinline__ void content_rows(const EpiPoPE& e, const float* st, 
   }
 }
 
+// The dK~ epilogue of the pair kernel and of dkdv_combine, 512 threads: the inverse PoPE
+// transform of the staged rows st_epi[128 keys][DQK] (fp32, scaled) of key block kb of (b, hk)
+// into dk (and the content part's copy into dk_c), plus the block's phase-gradient partials at
+// index bh * nkb + kb.  Only with a.fuse_inv set.
+template <int HT, int DQK>
+__device__ __forceinline__ void dk_epilogue(const CoreArgs& a, float* st_epi, int tid, int b, int hk, int kb,
+                                            int bh, int nkb) {
+  constexpr int NW = 8, BNK = 128;
+  const int k0 = kb * BNK;
+  // DC is the content width, 0, or DQK / 2 at DQK = 128 (the host fuses no other split)
+  auto epi_vec = [&](auto dc_tag) {
+    constexpr int DC = decltype(dc_tag)::value;
+    const EpiPoPE& e = a.ek;
+    constexpr int Dr = (DQK - DC) / 2, CG = Dr / 8, RPP = NW * 64 / CG;
+    const int c0 = (tid % CG) * 8, rr = tid / CG;
+    float fr[8], dl[8], sdl[8], sf[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      fr[j] = a.freqs[c0 + j];
+      dl[j] = a.delta ? a.delta[hk * a.delta_hs + c0 + j] : 0.f;
+      sdl[j] = sf[j] = 0.f;
+    }
+    __syncthreads();  // every dk~ row staged
+    if constexpr (DC > 0)
+      content_rows<HT, DQK, DC, NW * 64, BNK>(e, st_epi, tid, b * e.dxc_s[0] + hk * e.dxc_s[1], k0, a.Sk);
+    inv_pope_rows<HT, DQK, DC, NW * 64, BNK, false>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1],
+                                                b * e.dx_s[0] + hk * e.dx_s[1], k0, a.Sk, fr, dl,
+                                                a.delta != nullptr, nullptr, sdl, sf);
+    if (e.part_delta || e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
+      __syncthreads();
+      float* red = st_epi;  // [2][RPP][Dr]
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        red[(0 * RPP + rr) * Dr + c0 + j] = sdl[j];
+        red[(1 * RPP + rr) * Dr + c0 + j] = sf[j];
+      }
+      __syncthreads();
+      const int64_t blk = (int64_t)bh * nkb + kb;
+      if (tid < Dr) {
+        float d0 = 0.f, f0 = 0.f;
+        for (int i = 0; i < RPP; ++i) {
+          d0 += red[(0 * RPP + i) * Dr + tid];
+          f0 += red[(1 * RPP + i) * Dr + tid];
+        }
+        if (e.part_delta) e.part_delta[blk * Dr + tid] = d0;
+        if (e.part_freq) e.part_freq[blk * Dr + tid] = f0;
+      }
+    }
+  };
+  if (DQK == 128 && a.fuse_inv && a.Dc == DQK / 2) {  // split form: fused only at width 128, vector views
+    if constexpr (DQK == 128) epi_vec(std::integral_constant<int, DQK / 2>{});
+  } else if (a.fuse_inv && epi_vec_ok(a.ek, 0)) {
+    epi_vec(std::integral_constant<int, 0>{});
+  } else if (a.fuse_inv) {  // the same, element by element, for strided x / dx
+    const EpiPoPE& e = a.ek;
+    const int Dr = DQK / 2;
+    float* st = st_epi;
+    const int c = tid % Dr;
+    constexpr int EU = 4;
+    const int rstep = NW * 64 / Dr;
+    const int64_t xb = b * e.x_s[0] + hk * e.x_s[1] + c * e.x_s[3];
+    auto load_trip = [&](int r0, float (&xv)[EU]) {
+#pragma unroll
+      for (int u = 0; u < EU; ++u) {
+        const int r = r0 + u * rstep, key = k0 + r;
+        xv[u] = (r < BNK && key < a.Sk) ? load_as_float_t<HT>(e.x, xb + (int64_t)key * e.x_s[2], e.x_dtype) : 0.f;
+      }
+    };
+    float xv[EU], xn[EU];
+    load_trip(tid / Dr, xv);
+    __syncthreads();
+    const float fr = a.freqs[c];
+    const float dl = a.delta ? a.delta[hk * a.delta_hs + c] : 0.f;
+    float sdl = 0.f, sf = 0.f;
+#pragma unroll 1
+    for (int r0 = tid / Dr; r0 < BNK; r0 += EU * rstep) {
+      load_trip(r0 + EU * rstep, xn);
+#pragma unroll
+      for (int u = 0; u < EU; ++u) {
+        const int r = r0 + u * rstep, key = k0 + r;
+        if (r < BNK && key < a.Sk) {
+          const float pos = pe_pos(e.start_pos + key, e.pos_round);
+          float dx;
+          const float dph = inv_pope_elem(xv[u], pos, fr, dl, a.delta != nullptr, st[r * DQK + c],
+                                          st[r * DQK + Dr + c], dx);
+          store_from_float_t<HT>(e.dx, b * e.dx_s[0] + hk * e.dx_s[1] + (int64_t)key * e.dx_s[2] + c * e.dx_s[3],
+                           e.dx_dtype, dx);
+          sdl += dph;
+          sf += pos * dph;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < EU; ++u) xv[u] = xn[u];
+    }
+    if (e.part_delta || e.part_freq) {
+      __syncthreads();
+      float* red = st;  // [2][NW*64/Dr][Dr]
+      const int nt = NW * 64 / Dr;
+      red[(0 * nt + tid / Dr) * Dr + c] = sdl;
+      red[(1 * nt + tid / Dr) * Dr + c] = sf;
+      __syncthreads();
+      const int64_t blk = (int64_t)bh * nkb + kb;
+      if (tid < Dr) {
+        float d0 = 0.f, f0 = 0.f;
+        for (int i = 0; i < nt; ++i) {
+          d0 += red[(0 * nt + i) * Dr + tid];
+          f0 += red[(1 * nt + i) * Dr + tid];
+        }
+        if (e.part_delta) e.part_delta[blk * Dr + tid] = d0;
+        if (e.part_freq) e.part_freq[blk * Dr + tid] = f0;
+      }
+    }
+  }
+}
+
 // dK~/dV with two waves per SIMD.  A workgroup of 8 waves owns 128 keys of one kv head; the 32
 // keys of pair p are shared by wave p (role A: scores S, P = softmax numerator, dV += P^T dO) and
 // wave p + 4 (role B: dP = dO v^T, dS = P (dP - Di), the dS store, dK~ += dS^T q~), which land on
@@ -766,7 +881,7 @@ __device__ __forceinline__ void content_rows(const EpiPoPE& e, const float* st, 
 // dP of tile t, then one barrier; the 32-query tiles stream through a ring of
 // 4 LDS stages (q~ 32 x DQK, dO 32 x DV, the rows' log2 lse and Di) loaded two steps ahead.
 // (pack_h2 / unpack_h2, pe_common.h: two floats <-> one dword of fp16, round-to-nearest-even)
-template <int HT, int DQK, int DV, int QT>
+template <int HT, int DQK, int DV, int QT, bool QS>
 __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   using M = MT<HT>;  // HT: the 16-bit operand type, bf16 (0) or fp16 (2)
   constexpr int NW = 8, BMQ = 32 * QT, BNK = 128, NSTG = 4;
@@ -792,9 +907,14 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const bool roleB = __builtin_amdgcn_readfirstlane(w >> 2) != 0;
   const int nkb = (a.Sk + BNK - 1) / BNK;
   int kb, bh;
-  map_block(blockIdx.x, nkb, a.nbh, false, kb, bh);
+  // QS (launched with a.qsplit > 1): workgroup jq of a key block takes query heads jq * hpw .. of
+  // its group and leaves fp32 partial dK~ / dV for dkdv_combine (run by the dQ launch).  A separate
+  // instantiation, so the unsplit kernel carries none of its registers.
+  const int nblk = nkb * a.nbh, jq = QS ? (int)blockIdx.x / nblk : 0;
+  map_block(blockIdx.x - jq * nblk, nkb, a.nbh, false, kb, bh);
   bh += a.bh0;  // the head group's units
   const int b = bh / a.Hkv, hk = bh % a.Hkv, grp = a.Hq / a.Hkv;
+  const int hpw = QS ? grp / a.qsplit : grp, h_first = hk * grp + jq * hpw;
   const int k0 = kb * BNK, kw0 = k0 + pw * 32, myk = kw0 + l32;
   const int off = a.causal_off;
 
@@ -803,7 +923,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   if (a.causal) qb0 = max(0, k0 - off) / BMQ;
   if (qb0 > nqt) qb0 = nqt;
   const int nper = nqt - qb0;
-  const int niter = nper * grp;
+  const int niter = nper * hpw;
   const float sl2 = a.scale * LOG2E;
   const int64_t qrs = (int64_t)DQK * 2;
 
@@ -812,7 +932,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const DmaPlan<BMQ, NCQ, NA, SZ> plan_q(pw, lane, (uint32_t)qrs);
   const DmaPlan<BMQ, NCO, NA, SZ> plan_o(pw, lane, (uint32_t)(a.do_ss * 2));
   const uint32_t smem_l = lds_addr(smem);
-  int iss_h = hk * grp, iss_qt = qb0;
+  int iss_h = h_first, iss_qt = qb0;
   auto issue = [&](int it) {
     char* st = smem + (it % NSTG) * STAGE;
     const uint32_t stl = smem_l + (uint32_t)((it % NSTG) * STAGE);
@@ -995,14 +1115,26 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       astep(t, pa0, pa1);
       if (t + 1 <= niter) astep(t + 1, pa1, pa0);
     }
+    if constexpr (QS) {
+      float* dvp = a.dv_part + ((int64_t)jq * a.B * a.Hkv + bh) * a.Sk * DV;
 #pragma unroll
-    for (int t = 0; t < NDV; ++t)
+      for (int t = 0; t < NDV; ++t)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = kw0 + c_row(j, g), col = t * 32 + l32;
-        if (key < a.Sk && col < a.dv_real)
-          store_from_float_t<HT>(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + col, a.dv_dtype, dv[t][j]);
-      }
+        for (int j = 0; j < 16; ++j) {
+          const int key = kw0 + c_row(j, g);
+          if (key < a.Sk) dvp[(int64_t)key * DV + t * 32 + l32] = dv[t][j];
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NDV; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = kw0 + c_row(j, g), col = t * 32 + l32;
+          if (key < a.Sk && col < a.dv_real)
+            store_from_float_t<HT>(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + col, a.dv_dtype,
+                                   dv[t][j]);
+        }
+    }
   } else {
     u32x4 vf[NVF];
     {
@@ -1016,7 +1148,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) dk[t][j] = 0.f;
     f32x16 dp[QT];
-    int prev_h = hk * grp, prev_qt = qb0;  // head and query tile of step t - 1
+    int prev_h = h_first, prev_qt = qb0;  // head and query tile of step t - 1
     // the wave's key row in the packed dS (pe_internal.h), less its first stored 64-query block
     const int64_t ds_row = ds_row_base(kw0 >> 5, a.ds_e, a.ds_nqt, a.causal) - ds_first(kb, a.ds_e, a.causal);
     // role B is the critical path of every step: its instructions go first when both waves of a
@@ -1064,13 +1196,13 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       if (t < niter) scores_dp(smem + (t % NSTG) * STAGE + SQ_BYTES + rro, vf, dp);
       __syncthreads();  // role A waited for tile t + 1's loads before this barrier
     }
-    if (a.fuse_inv) {
+    if (a.fuse_inv && !QS) {
 #pragma unroll
       for (int t = 0; t < NDK; ++t)
 #pragma unroll
         for (int j = 0; j < 16; ++j) st_epi[(pw * 32 + c_row(j, g)) * DQK + t * 32 + l32] = dk[t][j] * a.scale;
-    } else {
-      float* dkb = a.dk_t + (int64_t)(b * a.Hkv + hk) * a.Sk * DQK;
+    } else {  // dk_t, or partial jq of it
+      float* dkb = a.dk_t + ((int64_t)jq * a.B * a.Hkv + bh) * a.Sk * DQK;
 #pragma unroll
       for (int t = 0; t < NDK; ++t)
 #pragma unroll
@@ -1081,111 +1213,48 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     }
   }
 
-  // inverse PoPE transform of the staged dk~ rows (and the content part's copy), all 8 waves; DC is
-  // the content width, 0, or DQK / 2 at DQK = 128 (the host fuses no other split)
-  auto epi_vec = [&](auto dc_tag) {
-    constexpr int DC = decltype(dc_tag)::value;
-    const EpiPoPE& e = a.ek;
-    constexpr int Dr = (DQK - DC) / 2, CG = Dr / 8, RPP = NW * 64 / CG;
-    const int c0 = (tid % CG) * 8, rr = tid / CG;
-    float fr[8], dl[8], sdl[8], sf[8];
+  if constexpr (!QS) dk_epilogue<HT, DQK>(a, st_epi, tid, b, hk, kb, bh, nkb);
+}
+
+// The query-head split of the pair kernel (a.qsplit > 1, grids with fewer key blocks than compute
+// units): one workgroup of 512 threads per key block of (b, hk) adds the qsplit fp32 partials of
+// dV and dK~ in slice order, stores dV in dv's dtype, and either runs the dK~ epilogue
+// (a.fuse_inv) or leaves the sum in slice 0 of dk_t for the stand-alone inverse-transform kernels.
+// Both paths see the same sums, so the fused and unfused gradients stay bitwise equal.  It runs as
+// extra workgroups of the dQ GEMM's launch (the two are independent), on the compute units that a
+// small dQ grid leaves idle.  st_epi: 128 x DQK floats of LDS.
+template <int HT, int DQK, int DV>
+__device__ __forceinline__ void dkdv_combine(const CoreArgs& a, int blk_id, float* st_epi) {
+  constexpr int BNK = 128, NT = 512;
+  const int tid = threadIdx.x;
+  const int nkb = (a.Sk + BNK - 1) / BNK;
+  int kb, bh;
+  map_block(blk_id, nkb, a.nbh, false, kb, bh);
+  bh += a.bh0;
+  const int b = bh / a.Hkv, hk = bh % a.Hkv, k0 = kb * BNK;
+  const int64_t units = (int64_t)a.B * a.Hkv;
+  for (int i = tid; i < BNK * (DV / 4); i += NT) {
+    const int r = i / (DV / 4), c = (i % (DV / 4)) * 4, key = k0 + r;
+    if (key >= a.Sk) continue;
+    f32x4 sum = *(const f32x4*)(a.dv_part + ((int64_t)bh * a.Sk + key) * DV + c);
+    for (int j = 1; j < a.qsplit; ++j) sum += *(const f32x4*)(a.dv_part + ((j * units + bh) * a.Sk + key) * DV + c);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      fr[j] = a.freqs[c0 + j];
-      dl[j] = a.delta ? a.delta[hk * a.delta_hs + c0 + j] : 0.f;
-      sdl[j] = sf[j] = 0.f;
-    }
-    __syncthreads();  // every dk~ row staged
-    if constexpr (DC > 0)
-      content_rows<HT, DQK, DC, NW * 64, BNK>(e, st_epi, tid, b * e.dxc_s[0] + hk * e.dxc_s[1], k0, a.Sk);
-    inv_pope_rows<HT, DQK, DC, NW * 64, BNK, false>(e, st_epi, tid, b * e.x_s[0] + hk * e.x_s[1],
-                                                b * e.dx_s[0] + hk * e.dx_s[1], k0, a.Sk, fr, dl,
-                                                a.delta != nullptr, nullptr, sdl, sf);
-    if (e.part_delta || e.part_freq) {  // fixed-order sums over the RPP row groups of each dim
-      __syncthreads();
-      float* red = st_epi;  // [2][RPP][Dr]
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        red[(0 * RPP + rr) * Dr + c0 + j] = sdl[j];
-        red[(1 * RPP + rr) * Dr + c0 + j] = sf[j];
-      }
-      __syncthreads();
-      const int64_t blk = (int64_t)bh * nkb + kb;
-      if (tid < Dr) {
-        float d0 = 0.f, f0 = 0.f;
-        for (int i = 0; i < RPP; ++i) {
-          d0 += red[(0 * RPP + i) * Dr + tid];
-          f0 += red[(1 * RPP + i) * Dr + tid];
-        }
-        if (e.part_delta) e.part_delta[blk * Dr + tid] = d0;
-        if (e.part_freq) e.part_freq[blk * Dr + tid] = f0;
-      }
-    }
-  };
-  if (DQK == 128 && a.fuse_inv && a.Dc == DQK / 2) {  // split form: fused only at width 128, vector views
-    if constexpr (DQK == 128) epi_vec(std::integral_constant<int, DQK / 2>{});
-  } else if (a.fuse_inv && epi_vec_ok(a.ek, 0)) {
-    epi_vec(std::integral_constant<int, 0>{});
-  } else if (a.fuse_inv) {  // the same, element by element, for strided x / dx
-    const EpiPoPE& e = a.ek;
-    const int Dr = DQK / 2;
-    float* st = st_epi;
-    const int c = tid % Dr;
-    constexpr int EU = 4;
-    const int rstep = NW * 64 / Dr;
-    const int64_t xb = b * e.x_s[0] + hk * e.x_s[1] + c * e.x_s[3];
-    auto load_trip = [&](int r0, float (&xv)[EU]) {
-#pragma unroll
-      for (int u = 0; u < EU; ++u) {
-        const int r = r0 + u * rstep, key = k0 + r;
-        xv[u] = (r < BNK && key < a.Sk) ? load_as_float_t<HT>(e.x, xb + (int64_t)key * e.x_s[2], e.x_dtype) : 0.f;
-      }
-    };
-    float xv[EU], xn[EU];
-    load_trip(tid / Dr, xv);
-    __syncthreads();
-    const float fr = a.freqs[c];
-    const float dl = a.delta ? a.delta[hk * a.delta_hs + c] : 0.f;
-    float sdl = 0.f, sf = 0.f;
-#pragma unroll 1
-    for (int r0 = tid / Dr; r0 < BNK; r0 += EU * rstep) {
-      load_trip(r0 + EU * rstep, xn);
-#pragma unroll
-      for (int u = 0; u < EU; ++u) {
-        const int r = r0 + u * rstep, key = k0 + r;
-        if (r < BNK && key < a.Sk) {
-          const float pos = pe_pos(e.start_pos + key, e.pos_round);
-          float dx;
-          const float dph = inv_pope_elem(xv[u], pos, fr, dl, a.delta != nullptr, st[r * DQK + c],
-                                          st[r * DQK + Dr + c], dx);
-          store_from_float_t<HT>(e.dx, b * e.dx_s[0] + hk * e.dx_s[1] + (int64_t)key * e.dx_s[2] + c * e.dx_s[3],
-                           e.dx_dtype, dx);
-          sdl += dph;
-          sf += pos * dph;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < EU; ++u) xv[u] = xn[u];
-    }
-    if (e.part_delta || e.part_freq) {
-      __syncthreads();
-      float* red = st;  // [2][NW*64/Dr][Dr]
-      const int nt = NW * 64 / Dr;
-      red[(0 * nt + tid / Dr) * Dr + c] = sdl;
-      red[(1 * nt + tid / Dr) * Dr + c] = sf;
-      __syncthreads();
-      const int64_t blk = (int64_t)bh * nkb + kb;
-      if (tid < Dr) {
-        float d0 = 0.f, f0 = 0.f;
-        for (int i = 0; i < nt; ++i) {
-          d0 += red[(0 * nt + i) * Dr + tid];
-          f0 += red[(1 * nt + i) * Dr + tid];
-        }
-        if (e.part_delta) e.part_delta[blk * Dr + tid] = d0;
-        if (e.part_freq) e.part_freq[blk * Dr + tid] = f0;
-      }
-    }
+    for (int e = 0; e < 4; ++e)
+      if (c + e < a.dv_real)
+        store_from_float_t<HT>(a.dv, b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss + c + e, a.dv_dtype, sum[e]);
   }
+  for (int i = tid; i < BNK * (DQK / 4); i += NT) {
+    const int r = i / (DQK / 4), c = (i % (DQK / 4)) * 4, key = k0 + r;
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+    if (key < a.Sk) {
+      float* d0 = a.dk_t + ((int64_t)bh * a.Sk + key) * DQK + c;
+      sum = *(const f32x4*)d0;
+      for (int j = 1; j < a.qsplit; ++j) sum += *(const f32x4*)(a.dk_t + ((j * units + bh) * a.Sk + key) * DQK + c);
+      if (!a.fuse_inv) *(f32x4*)d0 = sum;
+    }
+    if (a.fuse_inv) *(f32x4*)(st_epi + r * DQK + c) = sum;
+  }
+  if (a.fuse_inv) dk_epilogue<HT, DQK>(a, st_epi, tid, b, hk, kb, bh, nkb);
 }
 
 // dQ~ = dS k~ as a GEMM over the dS^T rows the dK/dV kernel stored (no score recompute).  A
@@ -1204,7 +1273,9 @@ __device__ __forceinline__ uint32_t keep_bf2(uint32_t v, bool lo, bool hi) {
   return (lo ? (v & 0xffffu) : 0u) | (hi ? (v & 0xffff0000u) : 0u);
 }
 
-template <int HT, int DQK, int NW, int BK, int NSTAGE>
+// CDV > 0: the launch also carries the key blocks' dkdv_combine (value width CDV) as workgroups
+// past the dQ grid
+template <int HT, int DQK, int NW, int BK, int NSTAGE, int CDV>
 __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
   using M = MT<HT>;  // HT: the 16-bit operand type, bf16 (0) or fp16 (2)
   static_assert(NW == 8, "4 query groups x 2 column halves");
@@ -1235,6 +1306,14 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int nqb = (a.Sq + BQ - 1) / BQ;
+  if constexpr (CDV > 0) {
+    static_assert(NW == 8 && SMEM >= 128 * DQK * 4, "the combine takes 512 threads and 128 x DQK floats");
+    const int ndq = nqb * a.nbh * (a.Hq / a.Hkv);
+    if ((int)blockIdx.x >= ndq) {
+      dkdv_combine<HT, DQK, CDV>(a, (int)blockIdx.x - ndq, (float*)smem);
+      return;
+    }
+  }
   int qb, bh;
   map_block(blockIdx.x, nqb, a.nbh * (a.Hq / a.Hkv), a.causal != 0, qb, bh);
   bh += a.bh0 * (a.Hq / a.Hkv);  // the head group's query heads
@@ -1527,7 +1606,10 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
         // 64-query tiles where they fit the LDS (QK width 128, V width 64: the ~125M GPT shape and the
         // split training form), which halves the per-step barriers and waits per product
         constexpr int QT = DQK == 128 && DV == 64 ? 2 : 1;
-        hipLaunchKernelGGL((dkdv_pair_kernel<DT, DQK, DV, QT>), dim3(nkb * a.nbh), dim3(512), 0, s, a);
+        if (a.qsplit > 1)
+          hipLaunchKernelGGL((dkdv_pair_kernel<DT, DQK, DV, QT, true>), dim3(nkb * a.nbh * a.qsplit), dim3(512), 0, s, a);
+        else
+          hipLaunchKernelGGL((dkdv_pair_kernel<DT, DQK, DV, QT, false>), dim3(nkb * a.nbh), dim3(512), 0, s, a);
       } else {
         hipLaunchKernelGGL((dkdv_bf16_kernel<DT, DQK, DV, NW>), dim3(nkb * a.nbh), dim3(NW * 64), 0, s, a);
       }
@@ -1538,7 +1620,15 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       // 64-wide k~ (a 32-key tile of it is less than one DMA instruction per wave) keeps 64-key
       // steps double-buffered
       constexpr bool TW = DQK == 256 || DQK == 128;
-      hipLaunchKernelGGL((dq_gemm_kernel<DT, DQK, 8, (TW ? 32 : 64), (TW ? 4 : 2)>), dim3(nqb * a.nbh * (a.Hq / a.Hkv)), dim3(8 * 64), 0, s, a);
+      const int ndq = nqb * a.nbh * (a.Hq / a.Hkv);
+      if constexpr ((DQK == 128 || DQK == 256) && (DV == 128 || DV == 64)) {
+        if (a.qsplit > 1) {  // with the pair kernel's partials to combine, one workgroup per key block
+          const int nkb = (a.Sk + 127) / 128;
+          hipLaunchKernelGGL((dq_gemm_kernel<DT, DQK, 8, 32, 4, DV>), dim3(ndq + nkb * a.nbh), dim3(8 * 64), 0, s, a);
+          return hipGetLastError() == hipSuccess ? 0 : -7;
+        }
+      }
+      hipLaunchKernelGGL((dq_gemm_kernel<DT, DQK, 8, (TW ? 32 : 64), (TW ? 4 : 2), 0>), dim3(ndq), dim3(8 * 64), 0, s, a);
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {

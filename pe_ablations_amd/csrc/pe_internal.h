@@ -81,6 +81,12 @@ struct CoreArgs {
   // (flattened b * Hkv + hk) and their query heads; dS holds that group only, indexed from its first
   // query head (b * Hq + h - bh0 * Hq / Hkv), so one capped buffer serves every group in turn
   int bh0, nbh;
+  // query-head split of the bf16 / fp16 dK/dV pair kernel: qsplit (a divisor of Hq / Hkv) workgroups
+  // per key block share out the group's query heads; workgroup j writes fp32 partials to dk_t slice
+  // j ((B, Hkv, Sk, DQK) each, already multiplied by scale) and dv_part slice j ((B, Hkv, Sk, DV)
+  // each), summed in slice order by dkdv_combine in the dQ launch.  1: off (dv and dk written directly)
+  int qsplit;
+  float* dv_part;
 };
 
 int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
