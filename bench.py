@@ -44,7 +44,10 @@ stage (read raw rows, write transformed rows), its time from the stage events, G
   query attends to every cached row (split-key decode kernel).  Reported as cache GB/s against
   the 8 TB/s HBM peak, the bound of decode.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+``--graph`` (attention workloads) also captures the step once in a HIP graph and times its
+replays: the small shapes, such as ``split``, are bound by host time per launch when run eagerly.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--graph]
                        [--workload fwdbwd|fwd|fwd32|c2|c3|split|decoder|decode]
 """
 
@@ -292,6 +295,30 @@ def timed_loop(torch, L, step, arrays, steps):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def graph_loop(torch, step, warmup: int, steps: int) -> float:
+    """ms per step of `step` captured in a HIP graph (torch's recipe: side-stream warm-up, one
+    captured step) and replayed `steps` times after `warmup` untimed replays.  Every replay runs
+    every kernel of the step on the same static inputs; the library records no stage events inside
+    the graph (stage times come from the eager steps)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
 def roofline(stage: str, flop: float, ms: float, peak: float = PEAK_BF16_TFLOPS, headline: bool = True) -> dict:
     """Roofline entry of a kernel stage.  The measured HBM traffic comes from the committed PMC
     summary of the headline workload, so other workloads report it as null."""
@@ -392,6 +419,10 @@ def run_attention(args, torch, dev, wname: str) -> dict:
     log(f"bench: timing {args.steps} steps")
     ms = timed_loop(torch, L, step, arrays, args.steps)
     log(f"bench: {ms:.3f} ms/step")
+    eager_ms = ms
+    if getattr(args, "graph", False):
+        ms = graph_loop(torch, step, args.warmup, args.steps)
+        log(f"bench: {ms:.3f} ms/step as graph replays")
 
     core = ["fwd_core", "bwd_dkdv", "bwd_dq"] if backward else ["fwd_core"]
     names = _lib.STAGES if backward else ["fwd_prep", "fwd_core"]
@@ -411,7 +442,9 @@ def run_attention(args, torch, dev, wname: str) -> dict:
                   if backward else "none", parallelism="single GPU")
     if fm is not None:
         config["fope"] = {"M": w["fope"][0], "coeff_sigma": w["fope"][1], "training_length": w["fope"][2]}
-    return {
+    if getattr(args, "graph", False):
+        config["graph"] = "the step captured once in a HIP graph (torch.cuda.CUDAGraph) and replayed"
+    res = {
         "metric": w["metric"],
         "value": round(value, 2),
         "unit": "TFLOP/s",
@@ -432,6 +465,9 @@ def run_attention(args, torch, dev, wname: str) -> dict:
         "roofline": roofline(dom, F[dom], stage_ms[dom], peak, headline),
         "prologue": prologue_entry(w, stage_ms["fwd_prep"], headline),
     }
+    if getattr(args, "graph", False):
+        res["eager_ms_per_step"] = round(eager_ms, 4)
+    return res
 
 
 DECODER = dict(vocab_size=32000, hidden_dim=2048, num_layers=24, num_heads=16, num_kv_heads=16, head_dim=128,
@@ -677,6 +713,9 @@ def main() -> int:
     ap.add_argument("--cpu-heads", type=int, default=None, help="CPU baseline sample: query heads at full S")
     ap.add_argument("--cpu-reps", type=int, default=None, help="CPU baseline: timed passes (default per workload)")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="decoder CPU baseline: tokens of the sample")
+    ap.add_argument("--graph", action="store_true",
+                    help="attention workloads: also time the step captured in a HIP graph and replayed "
+                         "(ms_per_step then reports the replays; the eager figure stays in eager_ms_per_step)")
     args = ap.parse_args()
     dec = args.workload == "decoder"
     # Defaults: about half a second of untimed work before the timed steps.  Under this load the
