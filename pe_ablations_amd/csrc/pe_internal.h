@@ -132,6 +132,11 @@ int launch_phase_table(const float* freqs, int start, int S, int Dr, int pos_rou
 // path, else the two launches in turn
 int launch_prep_and_table(const PrepArgs& a, const float* freqs, int start, int S, int Dr, int pos_round, float* tab,
                           hipStream_t s);
+// both sides of a small vectorised PoPE prologue (ak: keys, aq: queries with aq.tab null) in one
+// launch, the queries evaluating their own phases and the rows of (0, 0) writing tab; returns 1
+// without launching when the shape or layout does not qualify (the caller then takes the two-launch
+// path)
+int launch_prep_qk(const PrepArgs& ak, const PrepArgs& aq, float* tab, hipStream_t s);
 // PoPE prologue with the RMSNorm fused in: one workgroup per token (all heads)
 int launch_prep_norm(const PrepArgs& a, hipStream_t s);
 

@@ -302,7 +302,9 @@ __global__ __launch_bounds__(RW * 64) void reduce_kernel(ReduceArgs a) {
 // ---------------------------------------------------------------------------------------------
 // thread t of a row: transform chunk t (cos chunk t, sin chunk t), then content chunks t, t + TPR,
 // ... and zero padding chunks the same way; TPR = Dr / 8
-__device__ __forceinline__ void prep_pope_vec_body(const PrepArgs& a, int64_t gid) {
+// tab_out (query side, phases evaluated here): the rows of (b, h) = (0, 0) also write their cos /
+// sin to the [S][2][Dr] phase table, the values launch_phase_table would write
+__device__ __forceinline__ void prep_pope_vec_body(const PrepArgs& a, int64_t gid, float* tab_out = nullptr) {
   const int tpr = a.Dr >> 3;
   const int64_t row = gid / tpr;
   const int t = (int)(gid - row * tpr);
@@ -343,6 +345,10 @@ __device__ __forceinline__ void prep_pope_vec_body(const PrepArgs& a, int64_t gi
       pe_sincos(ph, sn, cs);
       cv[e] = mul_nc(mu, cs);
       sv[e] = mul_nc(mu, sn);
+      if (tab_out && bh == 0) {
+        tab_out[(int64_t)s * 2 * a.Dr + t * 8 + e] = cs;
+        tab_out[(int64_t)s * 2 * a.Dr + a.Dr + t * 8 + e] = sn;
+      }
     }
   }
   *(u32x4*)(drow + a.Dc + t * 8) =
@@ -502,6 +508,31 @@ __global__ __launch_bounds__(256) void prep_vec_and_table_kernel(PrepArgs a, uns
                                                                  int start, int S, int Dr, int pos_round, float* tab) {
   if (blockIdx.x < nblk) prep_pope_vec_body(a, (int64_t)blockIdx.x * 256 + threadIdx.x);
   else phase_table_body(freqs, start, S, Dr, pos_round, tab, (int64_t)(blockIdx.x - nblk) * 256 + threadIdx.x);
+}
+
+// Both sides of a small prologue in one launch: blocks below nkblk transform key rows, the rest
+// query rows, which evaluate their own phases (no table to wait for) and, in the rows of (0, 0),
+// write the phase table.  The per-element arithmetic is the two-launch path's, so every value is
+// bitwise the same.
+__global__ __launch_bounds__(256) void prep_qk_vec_kernel(PrepArgs ak, PrepArgs aq, unsigned nkblk, float* tab) {
+  if (blockIdx.x < nkblk) prep_pope_vec_body(ak, (int64_t)blockIdx.x * 256 + threadIdx.x);
+  else prep_pope_vec_body(aq, (int64_t)(blockIdx.x - nkblk) * 256 + threadIdx.x, tab);
+}
+
+// prologues of at most this many 256-thread blocks (keys and queries together) take one launch:
+// they are bound by launch latency, not by the queries' extra sin / cos
+constexpr int64_t PREP_QK_MAX_BLOCKS = 1024;
+
+int launch_prep_qk(const PrepArgs& ak, const PrepArgs& aq, float* tab, hipStream_t s) {
+  if (!prep_vec_ok(ak) || !prep_vec_ok(aq) || ak.cdst || aq.cdst || aq.tab || !ak.is_key || aq.is_key ||
+      aq.Dr != ak.Dr)
+    return 1;
+  const int64_t nk = (int64_t)ak.B * ak.H * ak.S * (ak.Dr / 8), nq = (int64_t)aq.B * aq.H * aq.S * (aq.Dr / 8);
+  const int64_t nkblk = (nk + 255) / 256, nqblk = (nq + 255) / 256;
+  if (nkblk + nqblk > PREP_QK_MAX_BLOCKS || nk * 8 <= PREP_SMALL_ELEMS || nk == 0 || nq == 0) return 1;
+  hipLaunchKernelGGL(prep_qk_vec_kernel, dim3((unsigned)(nkblk + nqblk)), dim3(256), 0, s, ak, aq, (unsigned)nkblk,
+                     tab);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
 int launch_prep_and_table(const PrepArgs& a, const float* freqs, int start, int S, int Dr, int pos_round, float* tab,
