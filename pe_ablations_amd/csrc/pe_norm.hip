@@ -209,8 +209,8 @@ int launch_rmsnorm(const NormArgs& a, hipStream_t s) {
 //                                         in fp32, rounded to the weight's dtype)
 // One wave per row, rpw consecutive rows per wave.  Each lane accumulates dw for its own chunks
 // over its rows; the WPB waves of a workgroup add theirs through LDS in wave order, one 512-feature
-// slab at a time, into the workgroup's partial row, which rmsnorm_dw_reduce_kernel sums in
-// workgroup order.  Fixed order throughout: the result is bitwise reproducible.
+// slab at a time, into the workgroup's partial row, which rmsnorm_dw_reduce_kernel sums in a
+// fixed order.  Fixed order throughout: the result is bitwise reproducible.
 template <int CPL>
 __global__ __launch_bounds__(WPB * 64) void rmsnorm_bwd_kernel(NormBwdArgs a) {
   __shared__ __attribute__((aligned(16))) float slab[WPB][64 * 8];
@@ -290,14 +290,35 @@ __global__ __launch_bounds__(WPB * 64) void rmsnorm_bwd_kernel(NormBwdArgs a) {
   }
 }
 
-// dw[f] = sum of the groups' partial rows in group order, rounded to dw's dtype
-__global__ __launch_bounds__(256) void rmsnorm_dw_reduce_kernel(const float* __restrict__ part, int groups, int n,
-                                                                void* dw, int dw_dtype) {
-  const int f = blockIdx.x * 256 + threadIdx.x;
-  if (f >= n) return;
+// dw[f] = the groups' partial rows summed in a fixed order, rounded to dw's dtype: a workgroup of
+// 1024 threads takes 32 features, its 32 waves' half-rows (slice j = thread / 32) sum the groups
+// j, j + 32, j + 64, ... in increasing order with eight loads in flight, and one wave adds the 32
+// slice sums in slice order.  (One thread per feature walking every group in turn waited on each
+// load: 118 us per call for 512 groups.)
+__global__ __launch_bounds__(1024) void rmsnorm_dw_reduce_kernel(const float* __restrict__ part, int groups, int n,
+                                                                 void* dw, int dw_dtype) {
+  __shared__ float red[32][33];
+  const int lc = threadIdx.x & 31, j = threadIdx.x >> 5;
+  const int f = blockIdx.x * 32 + lc;
   float acc = 0.f;
-  for (int g = 0; g < groups; ++g) acc += part[(int64_t)g * n + f];
-  store_from_float(dw, f, dw_dtype, acc);
+  if (f < n) {
+    int g = j;
+    for (; g + 7 * 32 < groups; g += 8 * 32) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(g + u * 32) * n + f];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; g < groups; g += 32) acc += part[(int64_t)g * n + f];
+  }
+  red[j][lc] = acc;
+  __syncthreads();
+  if (j == 0 && f < n) {
+    float t = red[0][lc];
+    for (int i = 1; i < 32; ++i) t += red[i][lc];
+    store_from_float(dw, f, dw_dtype, t);
+  }
 }
 
 // rows per wave: about two workgroups per compute unit, at most 32 rows per wave
@@ -328,7 +349,7 @@ int launch_rmsnorm_bwd(NormBwdArgs a, int n_cu, hipStream_t s) {
     hipLaunchKernelGGL((rmsnorm_bwd_kernel<decltype(c)::value>), dim3(groups), dim3(WPB * 64), 0, s, a);
   });
   if (hipGetLastError() != hipSuccess) return -7;
-  hipLaunchKernelGGL(rmsnorm_dw_reduce_kernel, dim3((a.n + 255) / 256), dim3(256), 0, s, (const float*)a.part, groups,
+  hipLaunchKernelGGL(rmsnorm_dw_reduce_kernel, dim3((a.n + 31) / 32), dim3(1024), 0, s, (const float*)a.part, groups,
                      a.n, a.dw, a.dw_dtype);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
