@@ -49,6 +49,7 @@ def test_enums_match_header():
     assert val("PE_MODE_NONE") == _lib.PE_MODE_NONE
     assert val("PE_DTYPE_BF16") == _lib.PE_DTYPE_BF16
     assert val("PE_DTYPE_FP32") == _lib.PE_DTYPE_FP32
+    assert val("PE_DTYPE_FP16") == _lib.PE_DTYPE_FP16
     assert val("PE_CAUSAL_BOTTOM_RIGHT") == _lib.PE_CAUSAL_BOTTOM_RIGHT
     assert (val("PE_POS_EXACT"), val("PE_POS_BF16"), val("PE_POS_FP16")) == \
         (_lib.PE_POS_EXACT, _lib.PE_POS_BF16, _lib.PE_POS_FP16)
@@ -186,3 +187,25 @@ def test_bwd_workspace_caps_the_score_gradient(lib, S, H, Hkv, groups):
     tc = lib.pe_attn_bwd_workspace_bytes(ctypes.byref(params(**kw, causal=_lib.PE_CAUSAL_TOP_LEFT)))
     tn = lib.pe_attn_bwd_workspace_bytes(ctypes.byref(params(**kw, causal=_lib.PE_CAUSAL_NONE)))
     assert abs((tc - tn) - (share[True] - share[False])) < 512, (tc, tn, share)
+
+
+def test_bwd_workspace_reserves_the_query_head_split_partials(lib):
+    """A 16-bit GQA backward whose dK/dV grid has fewer key blocks than the MI355X's 256 CUs shares
+    each key block's query heads over workgroups that leave fp32 partials: at the reference training
+    shape (B=8, 8 -> 4 heads, S=512, QK width 128, V width 64, 128 key blocks) two slices of dK~ and
+    dV, one more dK~ slice and two dV slices than the unsplit layout (16 MiB).  At B=64 (1024 key
+    blocks) and without GQA there is no split, so the workspace per batch entry is the same up to the
+    small per-block partial sums."""
+    lib.pe_attn_bwd_workspace_bytes.restype = ctypes.c_size_t
+
+    def per_batch(B, Hq, dtype=_lib.PE_DTYPE_BF16):
+        p = params(B=B, Hq=Hq, Hkv=4, Sq=512, Sk=512, Dc=64, Dr=32, Dv=64, dtype=dtype)
+        return lib.pe_attn_bwd_workspace_bytes(ctypes.byref(p)) / B
+
+    rows = 4 * 512  # kv rows per batch entry
+    split_extra = rows * (128 + 2 * 64) * 4
+    for dt in (_lib.PE_DTYPE_BF16, _lib.PE_DTYPE_FP16):
+        extra = 8 * (per_batch(8, 8, dt) - per_batch(64, 8, dt))
+        assert split_extra * 8 <= extra < split_extra * 8 + (1 << 20), (dt, extra)
+    assert abs(8 * (per_batch(8, 4) - per_batch(64, 4))) < 1 << 20  # no GQA: no split
+    assert abs(8 * (per_batch(8, 8, _lib.PE_DTYPE_FP32) - per_batch(64, 8, _lib.PE_DTYPE_FP32))) < 1 << 20
