@@ -276,6 +276,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
     for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) s[nt][j] = 0.f;
+    // the score products at raised priority, the rest at the lowest: a wave whose S is ready goes
+    // ahead of the other wave's softmax and PV (the forward 0.5-1 % faster at every shape measured)
+    __builtin_amdgcn_s_setprio(2);
     {
       // S = k~ q~^T: NKT*NQF products, each with its own k~ row fragment, through a fenced ring
       // of depth FD (reads FD products ahead; left to itself the scheduler waits on every read
@@ -294,6 +297,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
     // the running max is kept in log2 units; as sl2 > 0 it is the max of the raw scores times
     // sl2, and each probability is one fma and one exp2 of a raw score
     const bool edge = (a.causal && k0 + BN - 1 > qw + off) || (k0 + BN > a.Sk);
