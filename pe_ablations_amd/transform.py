@@ -32,12 +32,15 @@ def _params(B, H, S, D, mode, dtype, start_pos, delta, mscale, pos_round) -> _li
     return p
 
 
+_CODE = {torch.bfloat16: _lib.PE_DTYPE_BF16, torch.float16: _lib.PE_DTYPE_FP16, torch.float32: _lib.PE_DTYPE_FP32}
+
+
 def _view(t: Optional[torch.Tensor]) -> _lib.PeTensor:
     d = _lib.PeTensor()
     if t is None:
         return d
     d.data = t.data_ptr()
-    d.dtype = _lib.PE_DTYPE_BF16 if t.dtype == torch.bfloat16 else _lib.PE_DTYPE_FP32
+    d.dtype = _CODE.get(t.dtype, _lib.PE_DTYPE_FP32)
     for i, s in enumerate(t.stride()):
         d.stride[i] = s
     if t.shape[3] == 1:
@@ -49,19 +52,18 @@ class PETransformFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, freqs, delta, mode, start_pos, is_key, mscale, pos_round):
         L = _lib.lib()
-        if x.dtype not in (torch.float32, torch.bfloat16):
+        if x.dtype not in _CODE:
             x = x.float()
         xv = x.transpose(1, 2)                       # (B, H, S, D) view
         if xv.stride(-1) != 1:
             xv = xv.contiguous()
         B, H, S, D = xv.shape
-        cdt = _lib.PE_DTYPE_FP32 if x.dtype == torch.float32 else _lib.PE_DTYPE_BF16
+        cdt = _CODE[x.dtype]
         p = _params(B, H, S, D, mode, cdt, start_pos, delta if is_key else None, mscale, pos_round)
         _lib.check(L.pe_attn_check(ctypes.byref(p)))
         width = L.pe_attn_operand_width(ctypes.byref(p))
         out_w = 2 * D if mode == _lib.PE_MODE_POPE else D
-        dst = torch.empty((B, H, S, width), dtype=torch.float32 if cdt == _lib.PE_DTYPE_FP32 else torch.bfloat16,
-                          device=x.device)
+        dst = torch.empty((B, H, S, width), dtype=x.dtype, device=x.device)
         fptr = None if freqs is None else freqs.data_ptr()
         dptr = None if (delta is None or not is_key) else delta.data_ptr()
         with torch.cuda.device(x.device):
@@ -130,7 +132,8 @@ def pe_transform(x: torch.Tensor, freqs: torch.Tensor, delta: Optional[torch.Ten
                  position_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """x (B, S, H, D) -> PoPE [mu cos, mu sin] (B, S, H, 2D) or RoPE-rotated (B, S, H, D) on the GPU.
 
-    fp32 inputs are transformed in fp32; bf16 / fp16 inputs produce bf16.  position_dtype (PoPE):
+    fp32 inputs are transformed in fp32; bf16 and fp16 inputs produce their own type (the reference
+    returns fp32 there, which SDPA under autocast rounds to the autocast type).  position_dtype (PoPE):
     None / torch.float32 exact positions, torch.bfloat16 / torch.float16 positions rounded to that
     type (FoPE's torch.arange(..., dtype=x.dtype), src/model/fpope.py:285,322)."""
     if not x.is_cuda:
@@ -143,7 +146,5 @@ def pe_transform(x: torch.Tensor, freqs: torch.Tensor, delta: Optional[torch.Ten
     freqs = freqs.float().contiguous()
     if delta is not None:
         delta = delta.float().contiguous()
-    if x.dtype == torch.float16:
-        x = x.to(torch.bfloat16)
     pr = position_rounding(position_dtype, m)
     return PETransformFn.apply(x, freqs, delta, m, int(start_pos), bool(is_key), float(mscale), pr)

@@ -19,6 +19,7 @@ from oracle import pe_oracle as O
 from pe_ablations_amd.fpope_attention import FPoPEGroupedQueryAttention, FPoPEGroupedQueryAttentionWithCache
 from pe_ablations_amd.functional import pe_attention, rms_norm, rms_norm_backward
 from pe_ablations_amd.pope import PoPEEmbedding
+from pe_ablations_amd.transform import pe_transform
 from tests._cmp import err
 
 pytestmark = pytest.mark.gpu
@@ -178,3 +179,38 @@ def test_fp16_rmsnorm_forward_and_backward(cuda, xd, wd):
     assert ((dx.double().cpu() - xr.grad.double()).abs() <= 2 * spacing(xr.grad, x.dtype) +
             1e-5 * xr.grad.double().abs().max()).all()
     assert ((dw.double().cpu() - wr.grad.double()).abs() <= 1e-3 * wr.grad.double().abs().max()).all()
+
+
+@pytest.mark.parametrize("mode", ["pope", "rope"])
+def test_fp16_standalone_transform_keeps_fp16(cuda, mode):
+    """forward_query / forward_key (src/model/pope.py:124-183, src/model/rope.py:35-57) as the
+    standalone transform on fp16 input: the output stays fp16 (not narrowed to bf16) and equals the
+    oracle's fp32 transform to fp16 rounding; the input gradient likewise."""
+    g = torch.Generator().manual_seed(24)
+    x = (torch.randn(2, 40, 3, 64, generator=g) * 2).half()
+    if mode == "pope":
+        freqs, delta = O.pope_freqs(64), O.clamp_delta(-torch.rand(3, 64, generator=g) * 6)
+    else:
+        freqs, delta = O.rope_inv_freq(64), None
+    xo = x.float().requires_grad_(True)
+    if mode == "pope":
+        ref = O.pope_transform(xo.transpose(1, 2), freqs, 5, delta).transpose(1, 2)
+    else:
+        ref = O.rope_rotate(xo.transpose(1, 2), freqs, 5).transpose(1, 2)
+    gout = torch.randn(ref.shape, generator=g)
+    ref.backward(gout)
+    xg = x.to(cuda).requires_grad_(True)
+    out = pe_transform(xg, freqs.to(cuda), None if delta is None else delta.to(cuda), start_pos=5,
+                       is_key=delta is not None, mode=mode)
+    assert out.dtype == torch.float16
+    out.backward(gout.to(cuda).half())
+    torch.cuda.synchronize()
+    assert xg.grad.dtype == torch.float16
+
+    def spacing(t):  # fp16 spacing at each element's magnitude
+        return torch.pow(2.0, torch.floor(torch.log2(t.double().abs().clamp_min(2.0 ** -14))) - 10)
+
+    assert ((out.double().cpu() - ref.double()).abs() <= spacing(ref) + 1e-6).all()
+    # the gradient of the fp16-rounded output: gout is rounded to fp16 first
+    dref = xo.grad.double()
+    assert ((xg.grad.double().cpu() - dref).abs() <= 2 * spacing(dref) + 2e-3 * gout.abs().max()).all()
