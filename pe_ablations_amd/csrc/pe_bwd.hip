@@ -895,10 +895,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   constexpr int RING = NSTG * STAGE + XB_BYTES;
   constexpr int EPI = BNK * DQK * 4;
   constexpr int SMEM = RING > EPI ? RING : EPI;
-  // the four role-A waves issue all tile loads (role B is the critical path): DMA instructions
-  // per A wave per tile for q~, dO and one for the 64 floats of L2 / Di
+  // the four role-A waves issue all tile loads (issued by role B too, in place of its idle time at
+  // the barrier, the kernel measured 1-2 % slower): DMA instructions per A wave per tile for q~,
+  // dO and, from wave 0 only, one for the floats of L2 / Di
   constexpr int NA = 4;
-  constexpr int PER = BMQ * NCQ / (64 * NA) + BMQ * NCO / (64 * NA) + 1;
+  constexpr int PER = BMQ * NCQ / (64 * NA) + BMQ * NCO / (64 * NA) + 1;  // with the L2 / Di load
   static_assert(BMQ * NCQ % (64 * NA) == 0 && BMQ * NCO % (64 * NA) == 0, "whole wave instructions");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
   char* xbuf = smem + NSTG * STAGE;
@@ -906,6 +907,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int pw = w & 3;
   const bool roleB = __builtin_amdgcn_readfirstlane(w >> 2) != 0;
+  const bool l2w = __builtin_amdgcn_readfirstlane(w) == 0;  // the wave that loads each tile's L2 / Di
   const int nkb = (a.Sk + BNK - 1) / BNK;
   int kb, bh;
   // QS (launched with a.qsplit > 1): workgroup jq of a key block takes query heads jq * hpw .. of
@@ -947,11 +949,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       dma_tile<BMQ, NCQ, NA, SZ>(st, qsrc, qrs, a.Sq - q0, pw, lane);
       dma_tile<BMQ, NCO, NA, SZ>(st + SQ_BYTES, osrc, a.do_ss * 2, a.Sq - q0, pw, lane);
     }
-    // every A wave issues the same load of the tile's L2 (lanes 0 .. NL-1) and Di (lanes NL ..
-    // 2 NL-1), NL = BMQ / 4 lanes of 4 floats each
+    // the first A wave alone loads the tile's L2 (lanes 0 .. NL-1) and Di (lanes NL .. 2 NL-1),
+    // NL = BMQ / 4 lanes of 4 floats each (when every A wave issued it, dK/dV was 0.5 % slower)
     constexpr int NL = BMQ / 4;
     const int64_t p0 = (int64_t)(b * a.Hq + h) * a.sq_pad + q0;
-    if (lane < 2 * NL) dma16((lane < NL ? a.L2 : a.Di) + p0 + (lane % NL) * 4, stl + SQ_BYTES + SO_BYTES);
+    if (l2w && lane < 2 * NL) dma16((lane < NL ? a.L2 : a.Di) + p0 + (lane % NL) * 4, stl + SQ_BYTES + SO_BYTES);
     if (++iss_qt == nqt) {
       iss_qt = qb0;
       ++iss_h;
@@ -1037,8 +1039,12 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   if (!roleB) {
     if (niter > 0) issue(0);
     if (niter > 1) issue(1);
-    if (niter > 1) wait_vmcnt<PER>();
-    else wait_vmcnt<0>();
+    if (niter > 1) {
+      if (l2w) wait_vmcnt<PER>();
+      else wait_vmcnt<PER - 1>();
+    } else {
+      wait_vmcnt<0>();
+    }
   }
   __syncthreads();
   float* st_epi = (float*)smem;  // [BNK keys][DQK] fp32 dk~ for the fused inverse transform
@@ -1115,8 +1121,12 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
       }
       if (t >= 1) products(dv, pp, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);
       if (t + 1 < niter) {  // tile t + 1 has landed: only tile t + 2's loads may be outstanding
-        if (t + 2 < niter) wait_vmcnt<PER>();
-        else wait_vmcnt<0>();
+        if (t + 2 < niter) {
+          if (l2w) wait_vmcnt<PER>();
+          else wait_vmcnt<PER - 1>();
+        } else {
+          wait_vmcnt<0>();
+        }
       }
       __syncthreads();
     };
