@@ -876,7 +876,10 @@ __device__ __forceinline__ void dk_epilogue(const CoreArgs& a, float* st_epi, in
 // and neither wave's exponentials, loads or waits leave the matrix core idle.  B gets the P it
 // needs through an LDS exchange buffer in fp16 (11 significant bits, 2 KiB per wave per tile): dS
 // = P (dP - Di) is rounded to bf16 (8 bits) right after, so the hand-off adds about an eighth of
-// dS's own rounding error, where a bf16 hand-off would double it.  Each loop step t runs A's S of
+// dS's own rounding error, where a bf16 hand-off would double it.  On fp16 operands dS itself keeps
+// 11 bits, so there P goes over in fp32 (4 KiB per wave per 32-query sub-tile), as the fused SDPA
+// backward forms dS from fp32 P; an fp16 hand-off made dQ's and dK's mean error 1.25 times that
+// path's.  Each loop step t runs A's S of
 // tile t, the loads of tile t+2, P of tile t and dV of tile t-1 (so A starts the step on products
 // while B forms dS), and B's dS / dK~ of tile t-1 and dP of tile t, then one barrier; the 32-query
 // tiles stream through a ring of 4 LDS stages (q~ 32 x DQK, dO 32 x DV, the rows' log2 lse and Di)
@@ -890,7 +893,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   constexpr int NKF = DQK / 16, NVF = DV / 16, NDK = DQK / 32, NDV = DV / 32;
   constexpr int SQ_BYTES = BMQ * NCQ * 16, SO_BYTES = BMQ * NCO * 16;
   constexpr int STAGE = SQ_BYTES + SO_BYTES + 2 * BMQ * 4;
-  constexpr int XBP = 2048 * QT;          // one pair's fp16 P of a step: [sub-tile][half][lane] 8 fp16
+  constexpr bool P32 = HT == 2;           // fp32 hand-off on fp16 operands
+  // one pair's P of a step: fp16 [sub-tile][half][lane] 8 values, fp32 [sub-tile][quarter][lane] 4
+  constexpr int XBP = (P32 ? 4096 : 2048) * QT;
   constexpr int XB_BYTES = 2 * 4 * XBP;   // P exchange: [step parity][pair]
   constexpr int RING = NSTG * STAGE + XB_BYTES;
   constexpr int EPI = BNK * DQK * 4;
@@ -1116,13 +1121,19 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
             f32x4 p;
 #pragma unroll
             for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[m][4 * G + e] * sl2 - lv[e]);
-            ph[G >> 1][(G & 1) * 2] = pack_h2(p[0], p[1]);
-            ph[G >> 1][(G & 1) * 2 + 1] = pack_h2(p[2], p[3]);
+            if constexpr (P32) {
+              *(f32x4*)(xb + ((4 * m + G) * 64 + lane) * 16) = p;
+            } else {
+              ph[G >> 1][(G & 1) * 2] = pack_h2(p[0], p[1]);
+              ph[G >> 1][(G & 1) * 2 + 1] = pack_h2(p[2], p[3]);
+            }
             pn[2 * m + (G >> 1)][(G & 1) * 2] = pack2<HT>(p[0], p[1]);
             pn[2 * m + (G >> 1)][(G & 1) * 2 + 1] = pack2<HT>(p[2], p[3]);
           }
-          *(u32x4*)(xb + ((2 * m + 0) * 64 + lane) * 16) = ph[0];
-          *(u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16) = ph[1];
+          if constexpr (!P32) {
+            *(u32x4*)(xb + ((2 * m + 0) * 64 + lane) * 16) = ph[0];
+            *(u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16) = ph[1];
+          }
         }
         __builtin_amdgcn_s_setprio(0);
       }
@@ -1181,21 +1192,29 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
     // role A forms S and P (priority 3 there, 0 elsewhere)
     __builtin_amdgcn_s_setprio(2);
     for (int t = 0; t <= niter; ++t) {
-      if (t >= 1) {  // dS of tile t - 1 from A's fp32 P; store it; dK~ += dS^T q~
+      if (t >= 1) {  // dS of tile t - 1 from A's P; store it; dK~ += dS^T q~
         const char* st = smem + ((t - 1) % NSTG) * STAGE;
         const float* sD = (const float*)(st + SQ_BYTES + SO_BYTES) + BMQ;
         const char* xb = xbuf + (((t - 1) & 1) * 4 + pw) * XBP;
         u32x4 dsf[2 * QT];
 #pragma unroll
         for (int m = 0; m < QT; ++m) {
-          const u32x4 ph[2] = {*(const u32x4*)(xb + ((2 * m + 0) * 64 + lane) * 16),
-                               *(const u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16)};
+          u32x4 ph[2];
+          if constexpr (!P32) {
+            ph[0] = *(const u32x4*)(xb + ((2 * m + 0) * 64 + lane) * 16);
+            ph[1] = *(const u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16);
+          }
 #pragma unroll
           for (int G = 0; G < 4; ++G) {
-            float p0, p1, p2, p3;
-            unpack_h2(ph[G >> 1][(G & 1) * 2], p0, p1);
-            unpack_h2(ph[G >> 1][(G & 1) * 2 + 1], p2, p3);
-            const f32x4 p = {p0, p1, p2, p3};
+            f32x4 p;
+            if constexpr (P32) {
+              p = *(const f32x4*)(xb + ((4 * m + G) * 64 + lane) * 16);
+            } else {
+              float p0, p1, p2, p3;
+              unpack_h2(ph[G >> 1][(G & 1) * 2], p0, p1);
+              unpack_h2(ph[G >> 1][(G & 1) * 2 + 1], p2, p3);
+              p = f32x4{p0, p1, p2, p3};
+            }
             const f32x4 dd = *(const f32x4*)(sD + m * 32 + (G >> 1) * 16 + g * 8 + (G & 1) * 4);
             float ds[4];
 #pragma unroll
@@ -1633,8 +1652,9 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
       if constexpr ((DQK == 128 || DQK == 256) && (DV == 128 || DV == 64)) {
         // two waves per SIMD (role-split pairs); the one-wave kernel serves the other widths
         // 64-query tiles where they fit the LDS (QK width 128, V width 64: the ~125M GPT shape and the
-        // split training form), which halves the per-step barriers and waits per product
-        constexpr int QT = DQK == 128 && DV == 64 ? 2 : 1;
+        // split training form), which halves the per-step barriers and waits per product; on fp16
+        // operands the fp32 P exchange of 64-query tiles would not fit (162 KiB), so 32-query tiles
+        constexpr int QT = DQK == 128 && DV == 64 && DT != 2 ? 2 : 1;
         if (a.qsplit > 1)
           hipLaunchKernelGGL((dkdv_pair_kernel<DT, DQK, DV, QT, true>), dim3(nkb * a.nbh * a.qsplit), dim3(512), 0, s, a);
         else
