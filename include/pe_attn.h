@@ -46,6 +46,9 @@ enum {
  * or fp16 runs the matrix products on 16-bit operands with fp32 accumulation (fp16: the reference
  * trainer's mixed_precision fp16, src/training/trainer.py:343-347); fp32 runs them in fp32. */
 enum { PE_DTYPE_BF16 = 0, PE_DTYPE_FP32 = 1, PE_DTYPE_FP16 = 2 };
+/* element type of an explicit attention mask only: one byte per element, nonzero = the key takes
+ * part (torch.bool, SDPA's boolean attn_mask) */
+enum { PE_DTYPE_BOOL = 3 };
 
 /* how the PoPE / FoPE phase product sees a position p (pe_attn_params.position_rounding) */
 enum {
@@ -151,6 +154,41 @@ int pe_attn_bwd(const pe_attn_params* p,
                 float* dfreqs, float* ddelta,
                 const void* fwd_workspace, size_t fwd_ws_bytes,
                 void* bwd_workspace, size_t bwd_ws_bytes, void* stream);
+
+/* Explicit attention masks: F.scaled_dot_product_attention(q, k, v, attn_mask=mask) of
+ * GroupedQueryAttention.forward (src/model/attention.py:91-96), which the reference module calls with
+ * is_causal=False when a mask is given (pass PE_CAUSAL_NONE to match; a causal value applies both).
+ * mask is a (B, Hq, Sq, Sk) view, indexed by the query head: PE_DTYPE_BOOL (nonzero = attend) or a
+ * float type whose value is added to the scaled score; element strides may be 0 where it broadcasts
+ * (torch's expand) and must not be negative.  A row whose every key is masked gives out = 0, lse =
+ * -inf and zero gradients, as torch's SDPA does.  Float values below -FLT_MAX / log2(e) count as
+ * -inf.  These calls run the generic kernels with the mask read per score (the tuned causal kernels
+ * do not take one) and store no dS: the masked backward needs
+ * pe_attn_bwd_masked_workspace_bytes, which grows with S, not S^2.  The forward workspace is
+ * pe_attn_fwd_workspace_bytes.  Arguments otherwise as pe_attn_fwd / pe_attn_bwd; the mask has no
+ * gradient. */
+size_t pe_attn_bwd_masked_workspace_bytes(const pe_attn_params* p);
+int pe_attn_fwd_masked(const pe_attn_params* p,
+                       const pe_tensor_t* qc, const pe_tensor_t* qr,
+                       const pe_tensor_t* kc, const pe_tensor_t* kr,
+                       const pe_tensor_t* v,
+                       const float* freqs, const float* delta,
+                       const pe_tensor_t* mask,
+                       const pe_tensor_t* out, float* lse,
+                       void* fwd_workspace, size_t fwd_ws_bytes, void* stream);
+int pe_attn_bwd_masked(const pe_attn_params* p,
+                       const pe_tensor_t* qc, const pe_tensor_t* qr,
+                       const pe_tensor_t* kc, const pe_tensor_t* kr,
+                       const pe_tensor_t* v,
+                       const float* freqs, const float* delta,
+                       const pe_tensor_t* mask,
+                       const pe_tensor_t* out, const float* lse, const pe_tensor_t* dout,
+                       const pe_tensor_t* dqc, const pe_tensor_t* dqr,
+                       const pe_tensor_t* dkc, const pe_tensor_t* dkr,
+                       const pe_tensor_t* dv,
+                       float* dfreqs, float* ddelta,
+                       const void* fwd_workspace, size_t fwd_ws_bytes,
+                       void* bwd_workspace, size_t bwd_ws_bytes, void* stream);
 
 /* RMSNorm weights of the position projections (qr_norm / kr_norm of FPoPEGroupedQueryAttention,
  * src/model/fpope_attention.py:88-90,132-137; RMSNorm, src/model/normalization.py:7-27). */

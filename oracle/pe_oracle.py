@@ -27,6 +27,9 @@ far below every tolerance it is used with.
 Parity pins (each checked in ``tests/test_oracle.py``):
 * attention core ............ brute-force Python loops on tiny inputs; torch SDPA special case
                                (freqs = 0, delta = 0 reduces PoPE to plain attention on softplus)
+* explicit masks ............ torch's SDPA with attn_mask (bool, float with -inf, per head, fully
+                               masked rows) in fp64, out and gradients; brute force on tiny inputs;
+                               the 16-bit path core with its roundings off equals the exact core
 * factorised PE transform ... equals the independent difference form (s-t)*theta + delta in fp64
 * backward .................. closed form == fp64 autograd == fp64 finite differences (gradcheck)
 * known answers ............. V = 0 -> O = 0, S = 1 -> O = V, diagonal phase = delta,
@@ -218,10 +221,34 @@ def causal_mask(sq: int, sk: int) -> torch.Tensor:
     return torch.triu(torch.ones(sq, sk, dtype=torch.bool), diagonal=sk - sq + 1)
 
 
+def mask_bias(mask: torch.Tensor, shape) -> torch.Tensor:
+    """SDPA's attn_mask (src/model/attention.py:91-96) as an additive float64 bias broadcast to
+    ``shape`` (B, Hq, Sq, Sk): a bool mask gives 0 where True (the key takes part) and -inf where
+    False; a float mask is added as given."""
+    if mask.dtype == torch.bool:
+        b = torch.zeros(mask.shape, dtype=torch.float64).masked_fill(~mask, float("-inf"))
+    else:
+        b = mask.to(torch.float64)
+    return b.expand(shape)
+
+
+def softmax_rows(s: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(p, lse) over the last axis.  A row whose every score is -inf gives p = 0 and lse = -inf, as
+    torch's SDPA returns zeros for it, with no NaN in the forward or in autograd's backward (the
+    row's scores are replaced by a constant before the logsumexp)."""
+    dead = torch.isneginf(s).all(-1, keepdim=True)
+    s = s.masked_fill(dead, 0.0)
+    lse = torch.logsumexp(s, dim=-1, keepdim=True)
+    p = torch.exp(s - lse).masked_fill(dead, 0.0)
+    return p, lse.masked_fill(dead, float("-inf")).squeeze(-1)
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
-              causal: bool = True, dtype=torch.float64) -> Tuple[torch.Tensor, torch.Tensor]:
-    """softmax(q k^T * scale, causal) v.  q (B,Hq,Sq,Dqk), k (B,Hkv,Sk,Dqk), v (B,Hkv,Sk,Dv).
+              causal: bool = True, dtype=torch.float64, mask: Optional[torch.Tensor] = None
+              ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """softmax(q k^T * scale + mask, causal) v.  q (B,Hq,Sq,Dqk), k (B,Hkv,Sk,Dqk), v (B,Hkv,Sk,Dv).
     GQA: kv head = h // (Hq/Hkv) (repeat_interleave, src/model/fpope_attention.py:160-163).
+    ``mask``: SDPA's attn_mask broadcastable to (B, Hq, Sq, Sk) (mask_bias).
     Returns (out (B,Hq,Sq,Dv), lse (B,Hq,Sq)) in ``dtype``."""
     B, Hq, Sq, _ = q.shape
     Hkv = k.shape[1]
@@ -231,10 +258,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
         v = v.repeat_interleave(g, dim=1)
     qd, kd, vd = q.to(dtype), k.to(dtype), v.to(dtype)
     s = torch.matmul(qd, kd.transpose(-2, -1)) * scale
+    if mask is not None:
+        s = s + mask_bias(mask, s.shape).to(dtype)
     if causal:
         s = s.masked_fill(causal_mask(Sq, k.shape[2]), float("-inf"))
-    lse = torch.logsumexp(s, dim=-1)
-    p = torch.exp(s - lse.unsqueeze(-1))
+    p, lse = softmax_rows(s)
     return torch.matmul(p, vd), lse
 
 
@@ -267,7 +295,7 @@ class _SdpaHalfPath(torch.autograd.Function):
     the rounding points.  Used only to measure the reference path's own error beside the kernel's."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, causal, dtype):
+    def forward(ctx, q, k, v, scale, causal, dtype, mask=None):
         f64 = torch.float64
         r = (lambda x: _bf16(x)) if dtype == torch.bfloat16 else (lambda x: _round16(x, dtype))
         Hq, Hkv = q.shape[1], k.shape[1]
@@ -275,15 +303,19 @@ class _SdpaHalfPath(torch.autograd.Function):
         kr, vr = k.to(f64).repeat_interleave(g, 1), v.to(f64).repeat_interleave(g, 1)
         qd = q.to(f64)
         s = torch.matmul(qd, kr.transpose(-2, -1)) * scale
+        bias = None if mask is None else mask_bias(mask, s.shape)
+        if bias is not None:
+            s = s + bias
         if causal:
             s = s.masked_fill(causal_mask(q.shape[2], k.shape[2]), float("-inf"))
         m = s.amax(-1, keepdim=True).clamp_min(-1e300)
         pt = torch.exp(s - m)
         lsum = pt.sum(-1, keepdim=True)
-        out = r(torch.matmul(r(pt), vr) / lsum)
+        # a row with every key masked: out 0 and lse -inf (torch's SDPA returns zeros)
+        out = r(torch.matmul(r(pt), vr) / lsum.masked_fill(lsum == 0, 1.0))
         lse = (m + torch.log(lsum)).squeeze(-1)
         ctx.save_for_backward(qd, kr, vr, out, lse)
-        ctx.scale, ctx.causal, ctx.g, ctx.r = scale, causal, g, r
+        ctx.scale, ctx.causal, ctx.g, ctx.r, ctx.bias = scale, causal, g, r, bias
         return out.to(q.dtype), lse
 
     @staticmethod
@@ -293,9 +325,11 @@ class _SdpaHalfPath(torch.autograd.Function):
         do = r(dout.to(torch.float64))
         di = (do * out).sum(-1, keepdim=True)
         s = torch.matmul(qd, kr.transpose(-2, -1)) * scale
+        if ctx.bias is not None:
+            s = s + ctx.bias
         if ctx.causal:
             s = s.masked_fill(causal_mask(qd.shape[2], kr.shape[2]), float("-inf"))
-        p = torch.exp(s - lse.unsqueeze(-1))
+        p = torch.exp(s - lse.masked_fill(torch.isneginf(lse), 0.0).unsqueeze(-1))
         dv = r(torch.matmul(r(p).transpose(-2, -1), do))
         ds = r(p * (torch.matmul(do, vr.transpose(-2, -1)) - di))
         dq = r(torch.matmul(ds, kr) * scale)
@@ -305,18 +339,18 @@ class _SdpaHalfPath(torch.autograd.Function):
             B, H, S, D = x.shape
             return x.view(B, H // g, g, S, D).sum(2)
 
-        return dq, fold(dk), fold(dv), None, None, None
+        return dq, fold(dk), fold(dv), None, None, None, None
 
 
-def attention_bf16_path(q, k, v, scale: float, causal: bool = True):
+def attention_bf16_path(q, k, v, scale: float, causal: bool = True, mask: Optional[torch.Tensor] = None):
     """(out, lse) of ``attention`` with a bf16 fused SDPA's rounding points (_SdpaHalfPath);
     differentiable, so the transforms around it carry the path's gradients to the raw inputs."""
-    return _SdpaHalfPath.apply(q, k, v, scale, bool(causal), torch.bfloat16)
+    return _SdpaHalfPath.apply(q, k, v, scale, bool(causal), torch.bfloat16, mask)
 
 
-def attention_fp16_path(q, k, v, scale: float, causal: bool = True):
+def attention_fp16_path(q, k, v, scale: float, causal: bool = True, mask: Optional[torch.Tensor] = None):
     """The same with an fp16 fused SDPA's rounding points (fp16 autocast)."""
-    return _SdpaHalfPath.apply(q, k, v, scale, bool(causal), torch.float16)
+    return _SdpaHalfPath.apply(q, k, v, scale, bool(causal), torch.float16, mask)
 
 
 # --------------------------------------------------------------------------------------------

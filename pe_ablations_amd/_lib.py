@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(PKG_DIR, "libpe_attn.so")
 
 PE_MODE_POPE, PE_MODE_ROPE, PE_MODE_NONE = 0, 1, 2
 PE_DTYPE_BF16, PE_DTYPE_FP32, PE_DTYPE_FP16 = 0, 1, 2
+PE_DTYPE_BOOL = 3  # explicit attention masks only
 PE_CAUSAL_NONE, PE_CAUSAL_TOP_LEFT, PE_CAUSAL_BOTTOM_RIGHT = 0, 1, 2
 PE_POS_EXACT, PE_POS_BF16, PE_POS_FP16 = 0, 1, 2
 
@@ -31,7 +32,8 @@ EXPORTED = [
     "pe_attn_set_stage_events", "pe_attn_transform_bwd_workspace_bytes", "pe_attn_transform_bwd",
     "pe_attn_fwd_normed", "pe_rmsnorm_fwd", "pe_attn_fwd_noalloc", "pe_attn_noalloc_scratch_bytes",
     "pe_attn_value_width", "pe_attn_cache_append", "pe_attn_decode_workspace_bytes", "pe_attn_decode",
-    "pe_swiglu_fwd", "pe_rmsnorm_bwd_workspace_bytes", "pe_rmsnorm_bwd",
+    "pe_swiglu_fwd", "pe_rmsnorm_bwd_workspace_bytes", "pe_rmsnorm_bwd", "pe_attn_fwd_masked",
+    "pe_attn_bwd_masked", "pe_attn_bwd_masked_workspace_bytes",
 ]
 
 # kernel stages bracketed by pe_attn_set_stage_events
@@ -101,6 +103,13 @@ def lib():
             L.pe_attn_bwd.argtypes = [P, T, T, T, T, T, vp, vp, T, vp, T, T, T, T, T, T, vp, vp,
                                       vp, sz, vp, sz, vp]
             L.pe_attn_bwd.restype = ctypes.c_int
+            L.pe_attn_fwd_masked.argtypes = [P, T, T, T, T, T, vp, vp, T, T, vp, vp, sz, vp]
+            L.pe_attn_fwd_masked.restype = ctypes.c_int
+            L.pe_attn_bwd_masked.argtypes = [P, T, T, T, T, T, vp, vp, T, T, vp, T, T, T, T, T, T, vp, vp,
+                                             vp, sz, vp, sz, vp]
+            L.pe_attn_bwd_masked.restype = ctypes.c_int
+            L.pe_attn_bwd_masked_workspace_bytes.argtypes = [P]
+            L.pe_attn_bwd_masked_workspace_bytes.restype = sz
             L.pe_attn_transform.argtypes = [P, ctypes.c_int, T, T, vp, vp, vp, vp]
             L.pe_attn_transform.restype = ctypes.c_int
             L.pe_attn_strerror.argtypes = [ctypes.c_int]

@@ -45,12 +45,14 @@ class GroupedQueryAttention(nn.Module):
 
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0,
                 use_cache: bool = False) -> torch.Tensor:
-        """``mask`` must be None (the reference's TransformerBlock passes None; an explicit dense
-        mask would need a masked kernel variant that this build does not provide).  ``use_cache``
-        (inference only) keeps the rotated, normalised keys of earlier calls and attends the new
-        queries to all of them under the bottom-right causal mask."""
-        if mask is not None:
-            raise NotImplementedError("GroupedQueryAttention: only the causal (mask=None) path is fused")
+        """``mask``: None for the causal path; else SDPA's attn_mask, bool (True = attend) or float
+        (added to the scaled scores), broadcastable to (B, num_heads, S, S), applied without the
+        causal mask as the reference does (is_causal=(mask is None), src/model/attention.py:91-96).
+        ``use_cache`` (inference only) keeps the rotated, normalised keys of earlier calls and
+        attends the new queries to all of them under the bottom-right causal mask; it takes no
+        explicit mask."""
+        if mask is not None and use_cache:
+            raise NotImplementedError("GroupedQueryAttention: use_cache takes no explicit mask")
         B, S, _ = x.shape
         q = self.wq(x).view(B, S, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.wk(x).view(B, S, self.num_kv_heads, self.head_dim).transpose(1, 2)
@@ -64,12 +66,13 @@ class GroupedQueryAttention(nn.Module):
                                    scale=1.0 / (self.head_dim ** 0.5), d_v=self.head_dim, **rope)
             out = out.transpose(1, 2).reshape(B, S, -1)
             return self.wo(out if torch.is_autocast_enabled() else out.to(x.dtype))
+        causal = mask is None
         if self.rope is not None:
             out = pe_attention(q, k, v, mode="rope", freqs=self.rope.kernel_inv_freq(),
                                rope_mscale=self.rope.kernel_mscale(), qk_norm=norm,
-                               scale=1.0 / (self.head_dim ** 0.5), causal=True,
-                               start_pos_q=start_pos, start_pos_k=start_pos)
+                               scale=1.0 / (self.head_dim ** 0.5), causal=causal,
+                               start_pos_q=start_pos, start_pos_k=start_pos, mask=mask)
         else:
             out = pe_attention(q, k, v, mode="none", qk_norm=norm, scale=1.0 / (self.head_dim ** 0.5),
-                               causal=True, start_pos_q=start_pos, start_pos_k=start_pos)
+                               causal=causal, start_pos_q=start_pos, start_pos_k=start_pos, mask=mask)
         return self.wo(out.transpose(1, 2).reshape(B, S, -1))

@@ -95,7 +95,9 @@ bool fused_split_bwd(const pe_attn_params* p, const pe_tensor_t* qr, const pe_te
          vec16(dkr);
 }
 
-Layout layout(const pe_attn_params* p) {
+// masked: the explicit-mask backward (pe_attn_bwd_masked), whose generic gradient kernels write
+// fp32 dq~ / dk~ for the stand-alone inverse transform and store no dS
+Layout layout(const pe_attn_params* p, bool masked = false) {
   Layout L{};
   L.dqk = pad_qk(qk_width(p));
   L.dv = pad_v(p->Dv);
@@ -120,8 +122,8 @@ Layout layout(const pe_attn_params* p) {
   L.di_off = L.do_off + align_up(nq * L.dv * e);
   L.l2_off = L.di_off + align_up(nq_pad * 4);
   L.dq_off = L.l2_off + align_up(nq_pad * 4);
-  const bool fb = fused_bwd(p);
-  L.ksplit = key_split(p, L.dqk, L.dv);
+  const bool fb = !masked && fused_bwd(p);
+  L.ksplit = masked ? 1 : key_split(p, L.dqk, L.dv);
   L.dk_off = L.dq_off + (fb ? 0 : align_up(nq * L.dqk * 4));
   // dk~ (unfused) or the split's partial dk~ slices
   L.pq_off = L.dk_off + (fb && L.ksplit == 1 ? 0 : align_up(nk * L.dqk * 4 * L.ksplit));
@@ -142,11 +144,12 @@ Layout layout(const pe_attn_params* p) {
   // dS of one (batch, kv head) unit: its query heads' regions; as many units per group as the cap
   // holds (at least one)
   const int units = p->B * p->Hkv;
+  const bool store_ds = half_dt(p->dtype) && !masked;
   const size_t unit_bytes = (size_t)(p->Hq / p->Hkv) * L.ds_head * 4096;
   L.ds_group = units;
-  if (half_dt(p->dtype) && unit_bytes > 0 && (size_t)units * unit_bytes > PE_BWD_DS_CAP_BYTES)
+  if (store_ds && unit_bytes > 0 && (size_t)units * unit_bytes > PE_BWD_DS_CAP_BYTES)
     L.ds_group = std::max<int>(1, (int)(PE_BWD_DS_CAP_BYTES / unit_bytes));
-  const size_t ds_bytes = half_dt(p->dtype) ? (size_t)L.ds_group * unit_bytes : 0;
+  const size_t ds_bytes = store_ds ? (size_t)L.ds_group * unit_bytes : 0;
   L.bwd_total = L.ds_off + align_up(ds_bytes);
   return L;
 }
@@ -169,6 +172,25 @@ int check_tensor(const pe_tensor_t* t, bool required) {
   if (!valid_dt(t->dtype)) return PE_ERR_MODE;
   if (t->stride[3] != 1) return PE_ERR_STRIDE;
   return PE_OK;
+}
+
+// an explicit mask view (B, Hq, Sq, Sk): bool bytes or a float type, element strides >= 0 (0 where
+// it broadcasts), the base aligned to its element
+int check_mask(const pe_tensor_t* m) {
+  if (!m || !m->data) return PE_ERR_NULL;
+  if (m->dtype != PE_DTYPE_BOOL && !valid_dt(m->dtype)) return PE_ERR_MODE;
+  for (int i = 0; i < 4; ++i)
+    if (m->stride[i] < 0) return PE_ERR_STRIDE;
+  const uintptr_t e = m->dtype == PE_DTYPE_BOOL ? 1 : m->dtype == PE_DTYPE_FP32 ? 4 : 2;
+  if ((uintptr_t)m->data % e) return PE_ERR_STRIDE;
+  return PE_OK;
+}
+
+void set_mask(pe::CoreArgs& c, const pe_tensor_t* m) {
+  if (!m) return;
+  c.mask = m->data;
+  c.m_sb = m->stride[0]; c.m_sh = m->stride[1]; c.m_sq = m->stride[2]; c.m_sk = m->stride[3];
+  c.mask_dtype = m->dtype;
 }
 
 int dev_flags[64];  // 0 unknown, 1 gfx950, 2 other
@@ -307,6 +329,11 @@ size_t pe_attn_bwd_workspace_bytes(const pe_attn_params* p) {
   return layout(p).bwd_total;
 }
 
+size_t pe_attn_bwd_masked_workspace_bytes(const pe_attn_params* p) {
+  if (pe_attn_check(p) != PE_OK) return 0;
+  return layout(p, true).bwd_total;
+}
+
 int pe_attn_transform(const pe_attn_params* p, int is_key, const pe_tensor_t* xc, const pe_tensor_t* xr,
                       const float* freqs, const float* delta, void* dst, void* stream) {
   int rc = pe_attn_check(p);
@@ -386,9 +413,10 @@ int pe_attn_transform_bwd(const pe_attn_params* p, int is_key, const float* g, c
 static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe_tensor_t* qc,
                     const pe_tensor_t* qr, const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
                     const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,
-                    void* fwd_workspace, size_t fwd_ws_bytes, void* stream) {
+                    void* fwd_workspace, size_t fwd_ws_bytes, void* stream, const pe_tensor_t* mask = nullptr) {
   int rc = pe_attn_check(p);
   if (rc) return rc;
+  if (mask && (rc = check_mask(mask))) return rc;
   if (nrm) {
     if (p->mode != PE_MODE_POPE || p->Dr <= 0) return PE_ERR_MODE;
     if (!nrm->q_weight || !nrm->k_weight) return PE_ERR_NULL;
@@ -446,6 +474,7 @@ static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe
   c.o = (void*)out->data; c.o_sb = out->stride[0]; c.o_sh = out->stride[1]; c.o_ss = out->stride[2];
   c.o_dtype = out->dtype;
   c.lse = lse;
+  set_mask(c, mask);
   stage_mark(PE_STAGE_FWD_CORE, 0, s);
   rc = pe::launch_fwd(p->dtype, L.dqk, L.dv, c, s);
   stage_mark(PE_STAGE_FWD_CORE, 1, s);
@@ -457,6 +486,14 @@ int pe_attn_fwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
                 const float* freqs, const float* delta, const pe_tensor_t* out, float* lse,
                 void* fwd_workspace, size_t fwd_ws_bytes, void* stream) {
   return fwd_impl(p, nullptr, qc, qr, kc, kr, v, freqs, delta, out, lse, fwd_workspace, fwd_ws_bytes, stream);
+}
+
+int pe_attn_fwd_masked(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                       const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                       const float* freqs, const float* delta, const pe_tensor_t* mask, const pe_tensor_t* out,
+                       float* lse, void* fwd_workspace, size_t fwd_ws_bytes, void* stream) {
+  if (!mask) return PE_ERR_NULL;
+  return fwd_impl(p, nullptr, qc, qr, kc, kr, v, freqs, delta, out, lse, fwd_workspace, fwd_ws_bytes, stream, mask);
 }
 
 }  // extern "C"
@@ -704,15 +741,19 @@ int pe_swiglu_fwd(const void* x, const void* gate, void* out, int64_t n, void* s
   return pe::launch_swiglu(x, gate, out, n, (hipStream_t)stream);
 }
 
-int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
-                const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
-                const float* freqs, const float* delta, const pe_tensor_t* out, const float* lse,
-                const pe_tensor_t* dout, const pe_tensor_t* dqc, const pe_tensor_t* dqr,
-                const pe_tensor_t* dkc, const pe_tensor_t* dkr, const pe_tensor_t* dv,
-                float* dfreqs, float* ddelta, const void* fwd_workspace, size_t fwd_ws_bytes,
-                void* bwd_workspace, size_t bwd_ws_bytes, void* stream) {
+}  // extern "C"
+
+static int bwd_impl(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                    const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                    const float* freqs, const float* delta, const pe_tensor_t* mask, const pe_tensor_t* out,
+                    const float* lse, const pe_tensor_t* dout, const pe_tensor_t* dqc, const pe_tensor_t* dqr,
+                    const pe_tensor_t* dkc, const pe_tensor_t* dkr, const pe_tensor_t* dv,
+                    float* dfreqs, float* ddelta, const void* fwd_workspace, size_t fwd_ws_bytes,
+                    void* bwd_workspace, size_t bwd_ws_bytes, void* stream) {
   int rc = pe_attn_check(p);
   if (rc) return rc;
+  const bool masked = mask != nullptr;
+  if (masked && (rc = check_mask(mask))) return rc;
   if ((rc = check_tensor(qr, p->Dr > 0)) || (rc = check_tensor(kr, p->Dr > 0)) ||
       (rc = check_tensor(qc, p->Dc > 0)) || (rc = check_tensor(kc, p->Dc > 0)) ||
       (rc = check_tensor(v, true)) || (rc = check_tensor(out, true)) || (rc = check_tensor(dout, true)) ||
@@ -727,7 +768,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
     for (const pe_tensor_t* t : {qc, qr, kc, kr, v, dqc, dqr, dkc, dkr, dv})
       if (t && t->data && t->dtype != p->dtype && t->dtype != PE_DTYPE_FP32) return PE_ERR_MODE;
   }
-  const Layout L = layout(p);
+  const Layout L = layout(p, masked);
   if (!fwd_workspace || fwd_ws_bytes < L.fwd_total || !bwd_workspace || bwd_ws_bytes < L.bwd_total)
     return PE_ERR_WORKSPACE;
   if ((rc = device_ok())) return rc;
@@ -742,7 +783,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   pb.out = out->data; pb.out_dtype = out->dtype;
   for (int i = 0; i < 4; ++i) { pb.do_s[i] = dout->stride[i]; pb.o_s[i] = out->stride[i]; }
   // the bf16 dK/dV kernel reads dO in place when its rows are 16-byte aligned and exactly Dv wide
-  const bool do_direct = half_dt(dt) && v_direct(p, dout, L.dv);
+  const bool do_direct = half_dt(dt) && !masked && v_direct(p, dout, L.dv);
   pb.dO_op = do_direct ? nullptr : bws + L.do_off; pb.op_dtype = p->dtype; pb.width = L.dv;
   pb.Di = (float*)(bws + L.di_off);
   pb.L2 = (float*)(bws + L.l2_off);
@@ -775,11 +816,12 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   c.dv_part = L.ksplit > 1 ? (float*)(bws + L.dvp_off) : nullptr;
   c.dv = (void*)dv->data; c.dv_sb = dv->stride[0]; c.dv_sh = dv->stride[1]; c.dv_ss = dv->stride[2];
   c.dv_dtype = dv->dtype;
+  set_mask(c, mask);
   stage_mark(PE_STAGE_BWD_DKDV, 0, s);
   // fused form in bf16 with both halves of a column in one wave: the gradient kernels apply the
   // inverse PoPE transform in their epilogues
-  const bool split = fused_split_bwd(p, qr, kr, dqc, dqr, dkc, dkr);
-  const bool fuse = fused_bwd(p) || split;
+  const bool split = !masked && fused_split_bwd(p, qr, kr, dqc, dqr, dkc, dkr);
+  const bool fuse = (!masked && fused_bwd(p)) || split;
   const int nqg = (p->Sq + 255) / 256, nkg = (p->Sk + 127) / 128;
   if (fuse) {
     c.fuse_inv = 1;
@@ -812,7 +854,7 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   // the gradient kernels over head groups whose dS fits the workspace (one group up to the cap);
   // with several groups the dK/dV stage mark spans every group's kernels and the dQ mark is empty
   const int units = p->B * p->Hkv;
-  const int group = half_dt(dt) ? L.ds_group : units;
+  const int group = L.ds_group;
   for (int g0 = 0; g0 < units; g0 += group) {
     c.bh0 = g0;
     c.nbh = std::min(group, units - g0);
@@ -879,6 +921,31 @@ int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_
   }
   stage_mark(PE_STAGE_BWD_INV, 1, s);
   return PE_OK;
+}
+
+extern "C" {
+
+int pe_attn_bwd(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                const float* freqs, const float* delta, const pe_tensor_t* out, const float* lse,
+                const pe_tensor_t* dout, const pe_tensor_t* dqc, const pe_tensor_t* dqr,
+                const pe_tensor_t* dkc, const pe_tensor_t* dkr, const pe_tensor_t* dv,
+                float* dfreqs, float* ddelta, const void* fwd_workspace, size_t fwd_ws_bytes,
+                void* bwd_workspace, size_t bwd_ws_bytes, void* stream) {
+  return bwd_impl(p, qc, qr, kc, kr, v, freqs, delta, nullptr, out, lse, dout, dqc, dqr, dkc, dkr, dv, dfreqs,
+                  ddelta, fwd_workspace, fwd_ws_bytes, bwd_workspace, bwd_ws_bytes, stream);
+}
+
+int pe_attn_bwd_masked(const pe_attn_params* p, const pe_tensor_t* qc, const pe_tensor_t* qr,
+                       const pe_tensor_t* kc, const pe_tensor_t* kr, const pe_tensor_t* v,
+                       const float* freqs, const float* delta, const pe_tensor_t* mask, const pe_tensor_t* out,
+                       const float* lse, const pe_tensor_t* dout, const pe_tensor_t* dqc, const pe_tensor_t* dqr,
+                       const pe_tensor_t* dkc, const pe_tensor_t* dkr, const pe_tensor_t* dv,
+                       float* dfreqs, float* ddelta, const void* fwd_workspace, size_t fwd_ws_bytes,
+                       void* bwd_workspace, size_t bwd_ws_bytes, void* stream) {
+  if (!mask) return PE_ERR_NULL;
+  return bwd_impl(p, qc, qr, kc, kr, v, freqs, delta, mask, out, lse, dout, dqc, dqr, dkc, dkr, dv, dfreqs,
+                  ddelta, fwd_workspace, fwd_ws_bytes, bwd_workspace, bwd_ws_bytes, stream);
 }
 
 }  // extern "C"

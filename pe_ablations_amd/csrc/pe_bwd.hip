@@ -32,7 +32,14 @@ template <int DT> __device__ __forceinline__ float prob(float s, float scale, fl
   else return exp2f(s * sl2 - l);
 }
 
-template <int DT, int DQK, int DV, int BMQ, int NW>
+// P with the explicit mask's log2-unit term ml2 (mask_l2) added to the score
+template <int DT> __device__ __forceinline__ float prob_m(float s, float scale, float sl2, float l, float ml2) {
+  if constexpr (DT == 1) return exp2f(__builtin_fmaf(s, scale, -l) * LOG2E + ml2);
+  else return exp2f(s * sl2 + ml2 - l);
+}
+
+// MB (here and in dq_kernel): the explicit-mask instantiation, for any operand type.
+template <int DT, int DQK, int DV, int BMQ, int NW, bool MB>
 __global__ __launch_bounds__(NW * 64, 1) void dkdv_kernel(CoreArgs a) {
   using E = typename Elem<DT>::T;
   using M = MT<DT>;
@@ -138,7 +145,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_kernel(CoreArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int qi = mt * 32 + c_logical<DT>(j, g);
-        float p = prob<DT>(s[j], a.scale, sl2, sL[qi]);
+        float p;
+        if constexpr (MB) p = prob_m<DT>(s[j], a.scale, sl2, sL[qi], mask_l2(a, b, h, q0 + qi, myk));
+        else p = prob<DT>(s[j], a.scale, sl2, sL[qi]);
         if (edge && myk > q0 + qi + off) p = 0.f;
         s[j] = p;
         dp[j] = p * (dp[j] - sD[qi]);
@@ -188,7 +197,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_kernel(CoreArgs a) {
     }
 }
 
-template <int DT, int DQK, int DV, int BN, int NW>
+template <int DT, int DQK, int DV, int BN, int NW, bool MB>
 __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
   using E = typename Elem<DT>::T;
   using M = MT<DT>;
@@ -270,7 +279,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
       for (int kk = 0; kk < NVF; ++kk) dp = M::mma(lds_row_frag<NCV>(sV, row, 2 * kk + g), of[kk], dp);
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float p = prob<DT>(s[j], a.scale, sl2, lse2);
+        float p;
+        if constexpr (MB) p = prob_m<DT>(s[j], a.scale, sl2, lse2, mask_l2(a, b, h, myq, k0 + nt * 32 + c_logical<DT>(j, g)));
+        else p = prob<DT>(s[j], a.scale, sl2, lse2);
         if (edge) {
           const int key = k0 + nt * 32 + c_logical<DT>(j, g);
           if (key >= a.Sk || (a.causal && key > myq + off)) p = 0.f;
@@ -1643,9 +1654,24 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
       }
 }
 
+// the generic kernels: fp32 operands, and the explicit-mask instantiations (MB) on any type
+template <int DT, int DQK, int DV, bool MB>
+static int run_bwd_generic(int which, const CoreArgs& a, hipStream_t s) {
+  constexpr int NW = 4, BMQ = 32, BN = 32;
+  if (which == 0) {
+    const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
+    hipLaunchKernelGGL((dkdv_kernel<DT, DQK, DV, BMQ, NW, MB>), dim3(nkb * a.nbh), dim3(NW * 64), 0, s, a);
+  } else {
+    const int nqb = (a.Sq + NW * 32 - 1) / (NW * 32);
+    hipLaunchKernelGGL((dq_kernel<DT, DQK, DV, BN, NW, MB>), dim3(nqb * a.nbh * (a.Hq / a.Hkv)), dim3(NW * 64), 0, s, a);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
+
 template <int DT, int DQK, int DV>
 static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 4;
+  if (a.mask) return run_bwd_generic<DT, DQK, DV, true>(which, a, s);
   if constexpr (DT != 1) {
     if (which == 0) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
@@ -1681,15 +1707,7 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
     }
     return hipGetLastError() == hipSuccess ? 0 : -7;
   } else {
-    constexpr int BMQ = 32, BN = 32;
-    if (which == 0) {
-      const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
-      hipLaunchKernelGGL((dkdv_kernel<DT, DQK, DV, BMQ, NW>), dim3(nkb * a.nbh), dim3(NW * 64), 0, s, a);
-    } else {
-      const int nqb = (a.Sq + NW * 32 - 1) / (NW * 32);
-      hipLaunchKernelGGL((dq_kernel<DT, DQK, DV, BN, NW>), dim3(nqb * a.nbh * (a.Hq / a.Hkv)), dim3(NW * 64), 0, s, a);
-    }
-    return hipGetLastError() == hipSuccess ? 0 : -7;
+    return run_bwd_generic<DT, DQK, DV, false>(which, a, s);
   }
 }
 

@@ -179,6 +179,18 @@ __device__ __forceinline__ void store_from_float(void* p, int64_t i, int dtype, 
 }
 
 // ------------------------------------------------------------------ matrix-core traits
+// The explicit mask of (b, h, q, k) in log2 units (pe_internal.h, CoreArgs::mask): 0 or -inf for a
+// bool mask, the float's value times log2(e) otherwise (values below -FLT_MAX / log2(e) overflow to
+// -inf, i.e. masked).  q and k are clamped into the view, so padding rows and keys past the end read
+// an element of the view and are masked by the caller.
+template <class A> __device__ __forceinline__ float mask_l2(const A& a, int b, int h, int q, int k) {
+  q = q < a.Sq ? q : a.Sq - 1;
+  k = k < a.Sk ? k : a.Sk - 1;
+  const int64_t i = b * a.m_sb + h * a.m_sh + (int64_t)q * a.m_sq + (int64_t)k * a.m_sk;
+  if (a.mask_dtype == 3) return ((const uint8_t*)a.mask)[i] ? 0.f : -INFINITY;
+  return load_as_float(a.mask, i, a.mask_dtype) * LOG2E;
+}
+
 template <int DT> struct MT;
 template <> struct MT<0> {
   static constexpr int KC = 16, EPL = 8, ESZ = 2;

@@ -12,7 +12,8 @@
 
 namespace pe {
 
-template <int DT, int DQK, int DV, int BN, int NW>
+// MB: the explicit-mask instantiation (any operand type), which adds mask_l2 to every score.
+template <int DT, int DQK, int DV, int BN, int NW, bool MB>
 __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) {
   using E = typename Elem<DT>::T;
   using M = MT<DT>;
@@ -98,6 +99,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) 
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         float x = s[nt][j] * sl2;
+        if constexpr (MB) x += mask_l2(a, b, h, myq, k0 + nt * 32 + c_logical<DT>(j, g));
         if (edge) {
           const int key = k0 + nt * 32 + c_logical<DT>(j, g);
           if (key >= a.Sk || (a.causal && key > myq + off)) x = -INFINITY;
@@ -142,6 +144,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) 
       const int dv = t * 32 + c_row(j, g);
       char* dst = smem + (w * 32 + l32) * SO_STRIDE + dv * ESZ;
       if constexpr (DT == 0) *(uint16_t*)dst = f2bf(o[t][j] * inv);
+      else if constexpr (DT == 2) *(uint16_t*)dst = f2h(o[t][j] * inv);
       else *(float*)dst = o[t][j] * inv;
     }
   if (g == 0 && myq < a.Sq)
@@ -414,17 +417,17 @@ static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
-template <int DT, int DQK, int DV>
+template <int DT, int DQK, int DV, bool MB>
 static int run_fwd(const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 4;
-  constexpr int BN = DT == 0 ? 64 : 32;
+  constexpr int BN = DT != 1 ? 64 : 32;
   const int BM = NW * 32;
   const int nqb = (a.Sq + BM - 1) / BM;
   const int grid = nqb * a.B * a.Hq;
   const int o_vec = (a.dv_real == DV) && ((uintptr_t)a.o % 16 == 0) &&
                     ((a.o_ss * MT<DT>::ESZ) % 16 == 0) && ((a.o_sh * MT<DT>::ESZ) % 16 == 0) &&
                     ((a.o_sb * MT<DT>::ESZ) % 16 == 0);
-  hipLaunchKernelGGL((fwd_kernel<DT, DQK, DV, BN, NW>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
+  hipLaunchKernelGGL((fwd_kernel<DT, DQK, DV, BN, NW, MB>), dim3(grid), dim3(NW * 64), 0, s, a, o_vec);
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }
 
@@ -435,6 +438,15 @@ bool core_supported(int dqk, int dv) {
 
 template <int DT>
 static int fwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
+  if (a.mask) {  // explicit mask: the generic kernel on any operand type
+    if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64, true>(a, s);
+    if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128, true>(a, s);
+    if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64, true>(a, s);
+    if (dqk == 128 && dv == 128) return run_fwd<DT, 128, 128, true>(a, s);
+    if (dqk == 256 && dv == 64) return run_fwd<DT, 256, 64, true>(a, s);
+    if (dqk == 256 && dv == 128) return run_fwd<DT, 256, 128, true>(a, s);
+    return -3;
+  }
   if constexpr (DT != 1) {
     if (dqk == 64 && dv == 64) return run_fwd_bf16<DT, 64, 64>(a, s);
     if (dqk == 64 && dv == 128) return run_fwd_bf16<DT, 64, 128>(a, s);
@@ -444,12 +456,12 @@ static int fwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
     if (dqk == 256 && dv == 128) return run_fwd_bf16<DT, 256, 128>(a, s);
     return -3;
   } else {
-    if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64>(a, s);
-    if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128>(a, s);
-    if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64>(a, s);
-    if (dqk == 128 && dv == 128) return run_fwd<DT, 128, 128>(a, s);
-    if (dqk == 256 && dv == 64) return run_fwd<DT, 256, 64>(a, s);
-    if (dqk == 256 && dv == 128) return run_fwd<DT, 256, 128>(a, s);
+    if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64, false>(a, s);
+    if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128, false>(a, s);
+    if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64, false>(a, s);
+    if (dqk == 128 && dv == 128) return run_fwd<DT, 128, 128, false>(a, s);
+    if (dqk == 256 && dv == 64) return run_fwd<DT, 256, 64, false>(a, s);
+    if (dqk == 256 && dv == 128) return run_fwd<DT, 256, 128, false>(a, s);
     return -3;
   }
 }

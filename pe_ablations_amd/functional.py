@@ -230,9 +230,43 @@ class _FwdPlan:
 class _BwdPlan:
     __slots__ = ("bws", "d")
 
-    def __init__(self, fp: _FwdPlan, tensors):
-        self.bws = _lib.lib().pe_attn_bwd_workspace_bytes(fp.pref)
+    def __init__(self, fp: _FwdPlan, tensors, masked: bool = False):
+        L = _lib.lib()
+        self.bws = (L.pe_attn_bwd_masked_workspace_bytes if masked else L.pe_attn_bwd_workspace_bytes)(fp.pref)
         self.d = [_Desc(t) for t in tensors]
+
+
+def _mask_view(mask, B, Hq, Sq, Sk, dev, dt) -> torch.Tensor:
+    """SDPA's attn_mask (src/model/attention.py:91-96) as the (B, Hq, Sq, Sk) view the library reads:
+    bool (True = the key takes part) or a float added to the scaled score, broadcast by stride 0
+    (torch's expand, no copy).  Under autocast a float mask is rounded to the autocast dtype, as
+    autocast rounds SDPA's floating-point inputs."""
+    if not isinstance(mask, torch.Tensor):
+        raise TypeError(f"mask must be a tensor, got {type(mask).__name__}")
+    if mask.device != dev:
+        raise ValueError(f"mask is on {mask.device}, the operands on {dev}")
+    if mask.requires_grad and torch.is_grad_enabled():
+        raise NotImplementedError("pe_attention: no gradient flows to an explicit mask; pass mask.detach()")
+    if mask.dtype != torch.bool:
+        if not mask.is_floating_point():
+            raise TypeError(f"mask must be bool or floating point (SDPA's attn_mask), got {mask.dtype}")
+        if torch.is_autocast_enabled() and dt != _lib.PE_DTYPE_FP32:
+            mask = mask.to(_TORCH_DTYPE[dt])
+        elif mask.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            mask = mask.float()
+    try:
+        return mask.expand(B, Hq, Sq, Sk)
+    except RuntimeError as e:
+        raise ValueError(f"mask of shape {tuple(mask.shape)} does not broadcast to {(B, Hq, Sq, Sk)}") from e
+
+
+def _mask_desc(m: torch.Tensor) -> _lib.PeTensor:
+    d = _lib.PeTensor()
+    d.data = m.data_ptr()
+    d.dtype = _lib.PE_DTYPE_BOOL if m.dtype == torch.bool else _dtype_code(m.dtype)
+    for i, st in enumerate(m.stride()):
+        d.stride[i] = st
+    return d
 
 
 # Launch plans per thread (torch runs backward passes on its own device thread), keyed by the
@@ -257,31 +291,7 @@ class PEAttentionFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, qr, kr, v, qc, kc, freqs, delta, cfg):
-        L = _lib.lib()
-        dev = qr.device
-        key = (cfg["key"], _sig(qr), _sig(kr), _sig(v), _sig(qc), _sig(kc),
-               None if delta is None else delta.dim())
-        plans = _plans()
-        fp = plans.get(key)
-        if fp is None:
-            fp = plans[key] = _FwdPlan(cfg, qr, kr, v, qc, kc, delta)
-        fws = torch.empty(fp.ws, dtype=torch.uint8, device=dev)
-        out = torch.empty(fp.out_shape, dtype=fp.cdt, device=dev).transpose(1, 2)
-        lse = torch.empty((fp.out_shape[0], fp.out_shape[2], fp.out_shape[1]), dtype=torch.float32, device=dev)
-        d = fp.d
-        with _on(dev):
-            rc = L.pe_attn_fwd(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr), d[4].bind(v),
-                               _ptr(freqs), _ptr(delta), d[5].bind(out), lse.data_ptr(), fws.data_ptr(), fp.ws,
-                               _stream(dev))
-        _lib.check(rc)
-        ctx.cfg = cfg
-        ctx.key = key
-        ctx.save_for_backward(qr, kr, v, qc, kc, freqs, delta, out, lse, fws)
-        ctx.mark_non_differentiable(lse)
-        # lse carries no gradient: without this, autograd fills a zero (B, Hq, Sq) tensor for it in
-        # every backward
-        ctx.set_materialize_grads(False)
-        return out, lse
+        return _attn_forward(ctx, qr, kr, v, qc, kc, freqs, delta, cfg)
 
     @staticmethod
     def backward(ctx, dout, _dlse):
@@ -292,9 +302,65 @@ class PEAttentionFn(torch.autograd.Function):
         return grads + (None,)
 
 
-def _attn_backward(key, cfg, qr, kr, v, qc, kc, freqs, delta, out, lse, fws, dout, need_f, need_d):
-    """pe_attn_bwd for a forward saved as (qr, kr, v, qc, kc, freqs, delta, out, lse, workspace):
-    returns (dqr, dkr, dv, dqc, dkc, dfreqs, ddelta), each gradient in its input's dtype."""
+class PEMaskedAttentionFn(torch.autograd.Function):
+    """PEAttentionFn with an explicit mask: forward(qr, kr, v, qc, kc, freqs, delta, mask, cfg), mask
+    the (B, Hq, Sq, Sk) view of _mask_view, through pe_attn_fwd_masked / pe_attn_bwd_masked.  The
+    mask gets no gradient."""
+
+    @staticmethod
+    def forward(ctx, qr, kr, v, qc, kc, freqs, delta, mask, cfg):
+        return _attn_forward(ctx, qr, kr, v, qc, kc, freqs, delta, cfg, mask)
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        qr, kr, v, qc, kc, freqs, delta, out, lse, fws, mask = ctx.saved_tensors
+        grads = _attn_backward(ctx.key, ctx.cfg, qr, kr, v, qc, kc, freqs, delta, out, lse, fws, dout,
+                               freqs is not None and ctx.needs_input_grad[5],
+                               delta is not None and ctx.needs_input_grad[6], mask=mask)
+        return grads + (None, None)
+
+
+def _attn_forward(ctx, qr, kr, v, qc, kc, freqs, delta, cfg, mask=None):
+    """pe_attn_fwd (pe_attn_fwd_masked with a mask) for the autograd functions above; saves what
+    _attn_backward needs and returns (out, lse)."""
+    L = _lib.lib()
+    dev = qr.device
+    key = (cfg["key"], _sig(qr), _sig(kr), _sig(v), _sig(qc), _sig(kc),
+           None if delta is None else delta.dim())
+    plans = _plans()
+    fp = plans.get(key)
+    if fp is None:
+        fp = plans[key] = _FwdPlan(cfg, qr, kr, v, qc, kc, delta)
+    fws = torch.empty(fp.ws, dtype=torch.uint8, device=dev)
+    out = torch.empty(fp.out_shape, dtype=fp.cdt, device=dev).transpose(1, 2)
+    lse = torch.empty((fp.out_shape[0], fp.out_shape[2], fp.out_shape[1]), dtype=torch.float32, device=dev)
+    d = fp.d
+    with _on(dev):
+        if mask is None:
+            rc = L.pe_attn_fwd(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr), d[4].bind(v),
+                               _ptr(freqs), _ptr(delta), d[5].bind(out), lse.data_ptr(), fws.data_ptr(), fp.ws,
+                               _stream(dev))
+        else:
+            md = _mask_desc(mask)
+            rc = L.pe_attn_fwd_masked(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr),
+                                      d[4].bind(v), _ptr(freqs), _ptr(delta), ctypes.byref(md), d[5].bind(out),
+                                      lse.data_ptr(), fws.data_ptr(), fp.ws, _stream(dev))
+    _lib.check(rc)
+    ctx.cfg = cfg
+    ctx.key = key
+    saved = (qr, kr, v, qc, kc, freqs, delta, out, lse, fws)
+    ctx.save_for_backward(*(saved if mask is None else saved + (mask,)))
+    ctx.mark_non_differentiable(lse)
+    # lse carries no gradient: without this, autograd fills a zero (B, Hq, Sq) tensor for it in
+    # every backward
+    ctx.set_materialize_grads(False)
+    return out, lse
+
+
+def _attn_backward(key, cfg, qr, kr, v, qc, kc, freqs, delta, out, lse, fws, dout, need_f, need_d, mask=None):
+    """pe_attn_bwd (pe_attn_bwd_masked with a mask) for a forward saved as (qr, kr, v, qc, kc, freqs,
+    delta, out, lse, workspace): returns (dqr, dkr, dv, dqc, dkc, dfreqs, ddelta), each gradient in
+    its input's dtype."""
     L = _lib.lib()
     dev = qr.device
     plans = _plans()
@@ -314,18 +380,26 @@ def _attn_backward(key, cfg, qr, kr, v, qc, kc, freqs, delta, out, lse, fws, dou
     dv = torch.empty_like(v, dtype=cdt) if v.dtype != cdt else torch.empty_like(v)
     dfreqs = torch.empty(freqs.shape, dtype=torch.float32, device=dev) if need_f else None
     ddelta = torch.empty(delta.shape, dtype=torch.float32, device=dev) if need_d else None
-    bkey = (_sig(dout), _sig(dqr), _sig(dkr), _sig(dqc), _sig(dkc), _sig(dv))
+    bkey = (_sig(dout), _sig(dqr), _sig(dkr), _sig(dqc), _sig(dkc), _sig(dv), mask is not None)
     bp = fp.bwd.get(bkey)
     if bp is None:
-        bp = fp.bwd[bkey] = _BwdPlan(fp, (qc, qr, kc, kr, v, out, dout, dqc, dqr, dkc, dkr, dv))
+        bp = fp.bwd[bkey] = _BwdPlan(fp, (qc, qr, kc, kr, v, out, dout, dqc, dqr, dkc, dkr, dv), mask is not None)
     bws = torch.empty(bp.bws, dtype=torch.uint8, device=dev)
     d = bp.d
     with _on(dev):
-        rc = L.pe_attn_bwd(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr), d[4].bind(v),
-                           _ptr(freqs), _ptr(delta), d[5].bind(out), lse.data_ptr(), d[6].bind(dout),
-                           d[7].bind(dqc), d[8].bind(dqr), d[9].bind(dkc), d[10].bind(dkr), d[11].bind(dv),
-                           _ptr(dfreqs), _ptr(ddelta), fws.data_ptr(), fp.ws, bws.data_ptr(), bp.bws,
-                           _stream(dev))
+        if mask is None:
+            rc = L.pe_attn_bwd(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr), d[4].bind(v),
+                               _ptr(freqs), _ptr(delta), d[5].bind(out), lse.data_ptr(), d[6].bind(dout),
+                               d[7].bind(dqc), d[8].bind(dqr), d[9].bind(dkc), d[10].bind(dkr), d[11].bind(dv),
+                               _ptr(dfreqs), _ptr(ddelta), fws.data_ptr(), fp.ws, bws.data_ptr(), bp.bws,
+                               _stream(dev))
+        else:
+            md = _mask_desc(mask)
+            rc = L.pe_attn_bwd_masked(fp.pref, d[0].bind(qc), d[1].bind(qr), d[2].bind(kc), d[3].bind(kr),
+                                      d[4].bind(v), _ptr(freqs), _ptr(delta), ctypes.byref(md), d[5].bind(out),
+                                      lse.data_ptr(), d[6].bind(dout), d[7].bind(dqc), d[8].bind(dqr),
+                                      d[9].bind(dkc), d[10].bind(dkr), d[11].bind(dv), _ptr(dfreqs),
+                                      _ptr(ddelta), fws.data_ptr(), fp.ws, bws.data_ptr(), bp.bws, _stream(dev))
     _lib.check(rc)
     if dv.dtype != v.dtype:
         dv = dv.to(v.dtype)
@@ -360,7 +434,8 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
                  start_pos_k: int = 0, rope_mscale: float = 1.0, qk_norm: bool = False,
                  return_lse: bool = False, compute_dtype: Optional[torch.dtype] = None,
                  qr_norm_weight: Optional[torch.Tensor] = None, kr_norm_weight: Optional[torch.Tensor] = None,
-                 norm_eps: float = 1e-6, position_dtype: Optional[torch.dtype] = None):
+                 norm_eps: float = 1e-6, position_dtype: Optional[torch.dtype] = None,
+                 mask: Optional[torch.Tensor] = None):
     """Fused PE attention on one GPU.
 
     q (B,Hq,Sq,Dr), k (B,Hkv,Sk,Dr): positional parts, transformed inside the kernel library;
@@ -377,6 +452,11 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
     position_dtype (PoPE / FoPE): None or torch.float32 keeps positions exact; torch.bfloat16 /
     torch.float16 rounds each position to that type before the phase product (and in the phase
     gradient), reproducing FoPE's positions in x.dtype (src/model/fpope.py:285,322).
+    mask: SDPA's attn_mask (src/model/attention.py:91-96), broadcastable to (B, Hq, Sq, Sk): bool
+    (True = the key takes part) or a float added to the scaled score; applied together with
+    ``causal`` (the reference module passes is_causal=False with a mask, so pass causal=False to
+    match).  A row with every key masked gives zeros, as torch's SDPA does.  The mask gets no
+    gradient; it does not combine with the fused norm.
     Returns out (B,Hq,Sq,Dv) [and lse (B,Hq,Sq) fp32]."""
     if mode not in _MODES:
         raise ValueError(f"unknown PE mode {mode!r}")
@@ -413,7 +493,12 @@ def pe_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, mode: str
                start_pos_k=int(start_pos_k), qk_norm=bool(qk_norm), scale=float(scale),
                mscale=float(rope_mscale), pos_round=position_rounding(position_dtype, m))
     cfg["key"] = tuple(cfg.values())
-    if qr_norm_weight is not None or kr_norm_weight is not None:
+    if mask is not None:
+        if qr_norm_weight is not None or kr_norm_weight is not None:
+            raise ValueError("pe_attention: an explicit mask does not combine with the fused norm")
+        mview = _mask_view(mask, q.shape[0], q.shape[1], q.shape[2], k.shape[2], q.device, dt)
+        out, lse = PEMaskedAttentionFn.apply(q, k, v, q_c, k_c, freqs, delta, mview, cfg)
+    elif qr_norm_weight is not None or kr_norm_weight is not None:
         out, lse = _fwd_normed(q, k, v, q_c, k_c, freqs, delta, cfg, qr_norm_weight, kr_norm_weight, norm_eps)
     else:
         out, lse = PEAttentionFn.apply(q, k, v, q_c, k_c, freqs, delta, cfg)

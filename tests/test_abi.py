@@ -50,6 +50,7 @@ def test_enums_match_header():
     assert val("PE_DTYPE_BF16") == _lib.PE_DTYPE_BF16
     assert val("PE_DTYPE_FP32") == _lib.PE_DTYPE_FP32
     assert val("PE_DTYPE_FP16") == _lib.PE_DTYPE_FP16
+    assert val("PE_DTYPE_BOOL") == _lib.PE_DTYPE_BOOL
     assert val("PE_CAUSAL_BOTTOM_RIGHT") == _lib.PE_CAUSAL_BOTTOM_RIGHT
     assert (val("PE_POS_EXACT"), val("PE_POS_BF16"), val("PE_POS_FP16")) == \
         (_lib.PE_POS_EXACT, _lib.PE_POS_BF16, _lib.PE_POS_FP16)
@@ -209,3 +210,60 @@ def test_bwd_workspace_reserves_the_query_head_split_partials(lib):
         assert split_extra * 8 <= extra < split_extra * 8 + (1 << 20), (dt, extra)
     assert abs(8 * (per_batch(8, 4) - per_batch(64, 4))) < 1 << 20  # no GQA: no split
     assert abs(8 * (per_batch(8, 8, _lib.PE_DTYPE_FP32) - per_batch(64, 8, _lib.PE_DTYPE_FP32))) < 1 << 20
+
+
+def test_masked_bwd_workspace_grows_with_s_not_s2(lib):
+    """The explicit-mask backward stores no dS: its workspace holds dO, Di / L2 and the fp32 dq~ /
+    dk~ of the generic kernels, linear in S (at the headline widths, 16 heads: 0.61 GB at S = 16384
+    where the causal backward takes 4.40 GB, nearly all of it dS), and it does not depend on the
+    causal flag."""
+    lib.pe_attn_bwd_masked_workspace_bytes.restype = ctypes.c_size_t
+    lib.pe_attn_bwd_workspace_bytes.restype = ctypes.c_size_t
+
+    def ws(S, **kw):
+        return lib.pe_attn_bwd_masked_workspace_bytes(ctypes.byref(params(Hq=16, Hkv=16, Sq=S, Sk=S, Dr=128, Dv=128, **kw)))
+
+    for S in (1024, 16384):
+        rows = 16 * S
+        assert ws(S) >= rows * 128 * 2 + 2 * rows * 4 + 2 * rows * 256 * 4
+        # plus the phase gradient's per-block partial sums (three buffers of at most 2048 blocks x Dr)
+        assert ws(S) < rows * 128 * 2 + 2 * rows * 4 + 2 * rows * 256 * 4 + (4 << 20)
+        assert ws(S) == ws(S, causal=_lib.PE_CAUSAL_NONE)
+    assert abs(ws(32768) / ws(16384) - 2) < 0.01
+    assert ws(16384) < lib.pe_attn_bwd_workspace_bytes(ctypes.byref(params(Hq=16, Hkv=16, Sq=16384, Sk=16384, Dr=128, Dv=128)))
+    assert lib.pe_attn_bwd_masked_workspace_bytes(ctypes.byref(params(B=0))) == 0
+
+
+def test_masked_entry_points_validate_the_mask(lib):
+    """Host-side checks of the mask view, made before any device call: a missing mask, an element
+    type that is neither bool nor a float type, a negative stride and a base that is not aligned to
+    its element each return their code."""
+    p = params(causal=_lib.PE_CAUSAL_NONE)
+    buf = (ctypes.c_float * 16)()
+    base = ctypes.addressof(buf)
+
+    def mask(dtype=_lib.PE_DTYPE_BOOL, stride=(0, 0, 512, 1), offset=0):
+        m = _lib.PeTensor()
+        m.data = base + offset
+        m.dtype = dtype
+        for i, st in enumerate(stride):
+            m.stride[i] = st
+        return m
+
+    def fwd(m):
+        return lib.pe_attn_fwd_masked(ctypes.byref(p), None, None, None, None, None, None, None,
+                                      None if m is None else ctypes.byref(m), None, None, None, 0, None)
+
+    def bwd(m):
+        return lib.pe_attn_bwd_masked(ctypes.byref(p), None, None, None, None, None, None, None,
+                                      None if m is None else ctypes.byref(m), None, None, None, None, None, None,
+                                      None, None, None, None, None, 0, None, 0, None)
+
+    for call in (fwd, bwd):
+        assert call(None) == _lib.ERRORS["PE_ERR_NULL"]
+        assert call(mask(dtype=7)) == _lib.ERRORS["PE_ERR_MODE"]
+        assert call(mask(stride=(0, 0, -512, 1))) == _lib.ERRORS["PE_ERR_STRIDE"]
+        assert call(mask(dtype=_lib.PE_DTYPE_FP32, offset=2)) == _lib.ERRORS["PE_ERR_STRIDE"]
+        assert call(mask(dtype=_lib.PE_DTYPE_BF16, offset=1)) == _lib.ERRORS["PE_ERR_STRIDE"]
+        # a valid mask passes on to the operand checks (qr missing: PE_ERR_NULL from them)
+        assert call(mask()) == _lib.ERRORS["PE_ERR_NULL"]

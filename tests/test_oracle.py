@@ -485,3 +485,88 @@ def test_fp16_path_tracks_torch_fp16_sdpa():
         if n in ("out", "dq"):
             assert (t.double() - pth.double()).abs().max().item() <= ulp(e.abs().max().item()), n
             assert ep >= et / 1.5, (n, et, ep)
+
+
+# ---------------------------------------------------------------------------------------------
+# explicit masks (SDPA's attn_mask, src/model/attention.py:91-96)
+# ---------------------------------------------------------------------------------------------
+
+def _masks(B, Hq, Sq, Sk, seed):
+    """A bool (Sq, Sk) mask with one fully masked row, a float (B, 1, Sq, Sk) mask of finite values
+    and -inf with one fully -inf row, and a per-head bool (B, Hq, Sq, Sk) mask."""
+    g = torch.Generator().manual_seed(seed)
+    mb = torch.rand(Sq, Sk, generator=g) > 0.4
+    mb[1] = False
+    mf = torch.randn(B, 1, Sq, Sk, generator=g, dtype=f64) * 2
+    mf = mf.masked_fill(torch.rand(B, 1, Sq, Sk, generator=g) > 0.7, float("-inf"))
+    mf[0, 0, 2] = float("-inf")
+    mh = torch.rand(B, Hq, Sq, Sk, generator=g) > 0.5
+    return [mb, mf, mh]
+
+
+@pytest.mark.parametrize("which", [0, 1, 2])
+def test_attention_mask_matches_torch_sdpa(which):
+    """oracle.attention(mask=...) against torch's F.scaled_dot_product_attention(attn_mask=...) in
+    fp64 after the reference's repeat_interleave (src/model/attention.py:86-96): out and the q / k / v
+    gradients, GQA 4 -> 2, Sq != Sk, a fully masked row (zeros in both)."""
+    B, Hq, Hkv, Sq, Sk, D = 2, 4, 2, 7, 11, 8
+    mask = _masks(B, Hq, Sq, Sk, which)[which]
+    q, k, v = rnd(B, Hq, Sq, D, seed=1, dtype=f64), rnd(B, Hkv, Sk, D, seed=2, dtype=f64), rnd(B, Hkv, Sk, D, seed=3, dtype=f64)
+    do = rnd(B, Hq, Sq, D, seed=4, dtype=f64)
+    a = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    b = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    oa, _ = O.attention(*a, 0.37, causal=False, mask=mask)
+    ob = F.scaled_dot_product_attention(b[0], b[1].repeat_interleave(2, 1), b[2].repeat_interleave(2, 1),
+                                        attn_mask=mask, scale=0.37)
+    oa.backward(do)
+    ob.backward(do)
+    assert torch.allclose(oa, ob, atol=1e-12, rtol=0)
+    for x, y in zip(a, b):
+        assert torch.isfinite(x.grad).all()
+        assert torch.allclose(x.grad, y.grad, atol=1e-12, rtol=0)
+    if which in (0, 1):  # the fully masked row: zero output and zero query gradient
+        r = 1 if which == 0 else 2
+        assert (oa[0, :, r] == 0).all() and (a[0].grad[0, :, r] == 0).all()
+
+
+def test_attention_mask_brute_force():
+    """Plain Python loops on a tiny input: softmax over the keys of exp(q.k * scale + bias), bias 0
+    / -inf from a bool mask or the float's value; a row with no key left gives 0."""
+    B, Hq, Hkv, Sq, Sk, D = 1, 2, 1, 3, 4, 3
+    q, k, v = rnd(B, Hq, Sq, D, seed=5, dtype=f64), rnd(B, Hkv, Sk, D, seed=6, dtype=f64), rnd(B, Hkv, Sk, D, seed=7, dtype=f64)
+    mf = torch.tensor([[0.5, -1.0, float("-inf"), 2.0],
+                       [float("-inf")] * 4,
+                       [0.0, 0.0, 0.0, -3.0]], dtype=f64)
+    for mask in (mf, ~torch.isneginf(mf)):
+        out, _ = O.attention(q, k, v, 0.5, causal=False, mask=mask)
+        for h in range(Hq):
+            for i in range(Sq):
+                bias = [(0.0 if mask[i][j] else -math.inf) if mask.dtype == torch.bool else mask[i][j].item()
+                        for j in range(Sk)]
+                e = [math.exp(0.5 * sum(q[0, h, i, d].item() * k[0, 0, j, d].item() for d in range(D)) + bias[j])
+                     for j in range(Sk)]
+                z = sum(e)
+                for d in range(D):
+                    want = 0.0 if z == 0 else sum(e[j] * v[0, 0, j, d].item() for j in range(Sk)) / z
+                    assert abs(out[0, h, i, d].item() - want) < 1e-12
+
+
+@pytest.mark.parametrize("which", [0, 1, 2])
+def test_half_path_mask_without_rounding_is_the_exact_core(monkeypatch, which):
+    """The 16-bit path core with a mask and its rounding points switched off equals the exact core
+    with the same mask: forward, lse (-inf on the fully masked row) and the hand-written backward."""
+    monkeypatch.setattr(O, "_bf16", lambda x: x)
+    B, Hq, Hkv, Sq, Sk, D = 2, 4, 2, 7, 11, 8
+    mask = _masks(B, Hq, Sq, Sk, 10 + which)[which]
+    q, k, v = rnd(B, Hq, Sq, D, seed=8, dtype=f64), rnd(B, Hkv, Sk, D, seed=9, dtype=f64), rnd(B, Hkv, Sk, D, seed=10, dtype=f64)
+    do = rnd(B, Hq, Sq, D, seed=11, dtype=f64)
+    a = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    b = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    oa, la = O.attention(*a, 0.37, causal=False, mask=mask)
+    ob, lb = O.attention_bf16_path(*b, 0.37, causal=False, mask=mask)
+    oa.backward(do)
+    ob.backward(do)
+    assert torch.allclose(oa, ob, atol=1e-12) and torch.equal(torch.isneginf(la), torch.isneginf(lb))
+    assert torch.allclose(la[torch.isfinite(la)], lb[torch.isfinite(lb)], atol=1e-12)
+    for x, y in zip(a, b):
+        assert torch.allclose(x.grad, y.grad, atol=1e-12)
