@@ -48,9 +48,9 @@ class GroupedQueryAttention(nn.Module):
         """``mask``: None for the causal path; else SDPA's attn_mask, bool (True = attend) or float
         (added to the scaled scores), broadcastable to (B, num_heads, S, S), applied without the
         causal mask as the reference does (is_causal=(mask is None), src/model/attention.py:91-96).
-        ``use_cache`` (inference only) keeps the rotated, normalised keys of earlier calls and
-        attends the new queries to all of them under the bottom-right causal mask; it takes no
-        explicit mask."""
+        ``use_cache`` keeps the rotated, normalised keys of earlier calls (with gradients, their
+        autograd history too) and attends the new queries to all of them under the bottom-right
+        causal mask; it takes no explicit mask."""
         if mask is not None and use_cache:
             raise NotImplementedError("GroupedQueryAttention: use_cache takes no explicit mask")
         B, S, _ = x.shape

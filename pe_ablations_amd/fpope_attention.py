@@ -135,6 +135,9 @@ class KVCache:
         self.k = None
         self.v = None
         self.length = 0
+        # (k rows, v rows) carrying the autograd history of the calls that wrote them with gradients
+        # on, or None; set by _cached_attention_autograd, cleared by any write without gradients
+        self.hist = None
 
     def ensure(self, B: int, Hkv: int, capacity: int, wk: int, wv: int, dtype, device, keep: int = 0) -> None:
         """Buffers of this shape, dtype and device.  When they have to be replaced, the first ``keep``
@@ -160,6 +163,7 @@ class KVCache:
         self.k = None
         self.v = None
         self.length = 0
+        self.hist = None
 
 
 def cache_compute_dtype(x: torch.Tensor) -> torch.dtype:
@@ -185,11 +189,11 @@ def cached_attention(cache: KVCache, capacity: int, start_pos: int, *, q, k, v, 
                      freqs=None, delta=None, scale: float, rope_mscale: float = 1.0, qk_norm: bool = False,
                      d_v: int, position_dtype=None) -> torch.Tensor:
     """Append the new key / value rows at ``start_pos`` and attend the new queries to every cached
-    row with the bottom-right causal mask (src/model/fpope_attention.py:294-324).  The first chunk
-    (start_pos 0) runs the regular causal forward on the same operands; later chunks run the
-    split-key decode kernel over the cache.  Inference only.  Returns (B, Hq, S, d_v)."""
-    if torch.is_grad_enabled():
-        raise RuntimeError("use_cache=True is an inference path: run it under torch.no_grad() / inference_mode")
+    row with the bottom-right causal mask (src/model/fpope_attention.py:294-324).  Without
+    gradients the first chunk (start_pos 0) runs the regular causal forward on the same operands
+    and later chunks the split-key decode kernel over the cache.  With gradients (grad mode on and
+    an operand that requires one) the chunk runs _cached_attention_autograd.  Returns
+    (B, Hq, S, d_v)."""
     B, Hkv, S = k.shape[0], k.shape[1], k.shape[2]
     if start_pos < 0 or start_pos + S > capacity:
         raise ValueError(f"cache rows {start_pos}..{start_pos + S - 1} exceed max_cache_len {capacity}")
@@ -199,6 +203,11 @@ def cached_attention(cache: KVCache, capacity: int, start_pos: int, *, q, k, v, 
         raise ValueError(f"the cache holds {cache.length} rows; a chunk at {start_pos} would leave a gap "
                          "(start at or before the cached length)")
     cache.ensure(B, Hkv, capacity, wk, wv, cdt, k.device, keep=start_pos)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, q_c, k_c, freqs, delta)):
+        return _cached_attention_autograd(cache, start_pos, q=q, k=k, v=v, q_c=q_c, k_c=k_c, mode=mode, freqs=freqs,
+                                          delta=delta, scale=scale, rope_mscale=rope_mscale, qk_norm=qk_norm,
+                                          position_dtype=position_dtype, cdt=cdt)
+    cache.hist = None
     # a chunk at start_pos <= length overwrites rows start_pos.. and ends the cache after itself, as
     # the reference's cache update does (src/model/fpope_attention.py:296-302)
     cache.length = start_pos
@@ -214,14 +223,68 @@ def cached_attention(cache: KVCache, capacity: int, start_pos: int, *, q, k, v, 
                                qk_norm=qk_norm, position_dtype=position_dtype)
 
 
+def _l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """QKNorm's x / (||x|| + eps) over the head dim (src/model/normalization.py:54-55)."""
+    return x / (x.norm(dim=-1, keepdim=True) + eps)
+
+
+def _cached_attention_autograd(cache: KVCache, start_pos: int, *, q, k, v, q_c, k_c, mode: str, freqs, delta,
+                               scale: float, rope_mscale: float, qk_norm: bool, position_dtype, cdt) -> torch.Tensor:
+    """The cache path with gradients.  The reference writes the new rows into its cache buffers by
+    slice assignment, which carries their autograd history into the buffer, and runs SDPA over
+    cache[:, :, :start_pos + S] (src/model/fpope_attention.py:294-324); gradients reach the
+    queries, the new keys and values and, through the buffer's history, the rows that earlier calls
+    wrote with gradients on.  Here the same graph is built without writing in place: the new rows
+    are transformed by the differentiable transform (pe_transform), rounded to the cache's dtype and
+    appended to the earlier rows, those of earlier calls made with gradients keeping their history
+    (KVCache.hist), and the queries attend to them through the fused attention kernels on the
+    transformed operands (no-PE mode, bottom-right causal mask).  The cache buffers also receive
+    the new rows' values for later decode steps.  Unlike the reference, whose later writes into the
+    buffer invalidate the saved tensors of earlier calls, the outputs of several chunks can be
+    differentiated together."""
+    from .transform import pe_transform
+
+    S = k.shape[2]
+
+    def rows(x, is_key):  # (B, H, S, D) -> the operand rows [content | transform] of the chunk
+        if mode in ("pope", "rope"):
+            x = pe_transform(x.transpose(1, 2), freqs, delta if is_key else None, start_pos=start_pos, is_key=is_key,
+                             mode=mode, mscale=rope_mscale, position_dtype=position_dtype).transpose(1, 2)
+        if qk_norm:
+            x = _l2norm(x.float())
+        c = k_c if is_key else q_c
+        if c is not None:
+            dt = torch.promote_types(c.dtype, x.dtype)
+            x = torch.cat([c.to(dt), x.to(dt)], dim=-1)
+        return x
+
+    kt, vt = rows(k, True).to(cdt), v.to(cdt)
+    qt = rows(q, False)
+    w, dv = kt.shape[-1], vt.shape[-1]
+    hist = cache.hist
+    if hist is not None and hist[0].shape[2] >= start_pos and hist[0].shape[-1] == w and hist[0].dtype == cdt:
+        k_prev, v_prev = hist[0][:, :, :start_pos], hist[1][:, :, :start_pos]
+    else:  # rows written without gradients: constants of this graph
+        k_prev, v_prev = cache.k[:, :, :start_pos, :w], cache.v[:, :, :start_pos, :dv]
+    k_all = torch.cat([k_prev, kt], dim=2)
+    v_all = torch.cat([v_prev, vt], dim=2)
+    with torch.no_grad():
+        cache.k[:, :, start_pos:start_pos + S, :w] = kt
+        cache.v[:, :, start_pos:start_pos + S, :dv] = vt
+    cache.length = start_pos + S
+    cache.hist = (k_all, v_all)
+    return pe_attention(qt, k_all, v_all, mode="none", scale=scale, causal="bottom_right", compute_dtype=cdt)
+
+
 class FPoPEGroupedQueryAttentionWithCache(FPoPEGroupedQueryAttention):
     """KV-cache variant (src/model/fpope_attention.py:184-327): same constructor, ``k_cache`` /
     ``v_cache`` / ``cache_len`` / ``reset_cache`` and ``forward(x, mask, start_pos, use_cache)``.
     With ``use_cache`` the new keys are transformed once into the cache (pe_attn_cache_append) and
     the new queries attend to all ``cache_len`` cached rows under the bottom-right mask
-    (pe_attn_decode).  A chunk may start at any start_pos up to the current cache length (the
-    length after it is start_pos + S, so an earlier start_pos rewinds); a later one would leave a
-    gap of rows never written and raises."""
+    (pe_attn_decode).  With gradients the chunk runs the differentiable form of the same graph
+    (_cached_attention_autograd).  A chunk may start at any start_pos up to the current cache length
+    (the length after it is start_pos + S, so an earlier start_pos rewinds); a later one would
+    leave a gap of rows never written and raises."""
 
     def __init__(self, hidden_dim: int, num_heads: int, num_kv_heads: int, head_dim: int = 64,
                  d_rope: int = 32, use_qk_norm: bool = True, fpope: Optional[nn.Module] = None,

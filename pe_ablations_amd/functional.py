@@ -677,7 +677,8 @@ def swiglu(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
 
 # ------------------------------------------------------------------------------------------------
 # KV cache (src/model/fpope_attention.py:226-327): caches of transformed keys and values, and the
-# split-key decode attention over them.  Inference only.
+# split-key decode attention over them, without gradients (the modules' cache path under autograd is
+# fpope_attention._cached_attention_autograd).
 
 def _cache_params(*, B, Hq, Hkv, Sq, Sk, Dc, Dr, Dv, mode, dtype, causal, start_q, start_k, scale,
                   mscale, qk_norm, delta, pos_round=0) -> _lib.PeParams:

@@ -140,7 +140,7 @@ class TransformerBlock(nn.Module):
 
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, start_pos: int = 0,
                 use_cache: bool = False) -> torch.Tensor:
-        """``use_cache`` (inference only) routes the attention through its KV cache."""
+        """``use_cache`` routes the attention through its KV cache."""
         h = self.attention_norm(x)
         a = self.attention(h, mask, start_pos, use_cache=True) if use_cache else self.attention(h, mask, start_pos)
         x = x + a
@@ -211,7 +211,7 @@ class Transformer(nn.Module):
                 start_pos: int = 0, use_cache: bool = False) -> dict:
         """{'logits'} and, with ``labels``, {'loss'}: next-token cross entropy over the shifted
         sequence with ignore_index -100 (src/model/transformer.py:313-364).  ``use_cache``
-        (inference only, an addition) feeds the tokens at absolute positions start_pos.. through
+        (an addition) feeds the tokens at absolute positions start_pos.. through
         every layer's KV cache, which must hold exactly start_pos earlier rows."""
         x = self.token_embedding(input_ids)
         for layer in self.layers:
