@@ -15,6 +15,7 @@ mask, and a float mask together with the causal flag; Sq != Sk where the flag is
 
 import functools
 import math
+import random
 
 import pytest
 import torch
@@ -24,7 +25,7 @@ from pe_ablations_amd.attention import GroupedQueryAttention
 from pe_ablations_amd.functional import pe_attention
 from pe_ablations_amd.rope import RotaryEmbedding
 from tests._cmp import err
-from tests.test_gpu_sweep import BASE, DDELTA, DTYPES, bar_for, fp16_rows
+from tests.test_gpu_sweep import BASE, DDELTA, DTYPES, bar_for, draw, fp16_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -44,12 +45,14 @@ def make_mask(kind, B, Hq, Sq, Sk, seed):
     g = torch.Generator().manual_seed(seed)
     if kind == "bool2d":
         m = torch.rand(Sq, Sk, generator=g) > 0.3
-        m[3] = False
+        if Sq > 3:
+            m[3] = False
         return m
     if kind in ("float_b1", "bf16_b1"):
         m = torch.randn(B, 1, Sq, Sk, generator=g) * 2
         m = m.masked_fill(torch.rand(B, 1, Sq, Sk, generator=g) > 0.8, float("-inf"))
-        m[0, 0, 5] = float("-inf")
+        if Sq > 5:
+            m[0, 0, 5] = float("-inf")
         return m.to(torch.bfloat16) if kind == "bf16_b1" else m
     if kind == "perhead":
         return torch.rand(B, Hq, Sq, Sk, generator=g) > 0.5
@@ -97,7 +100,12 @@ def oracle_run(c, x, dout, delta, mask, core):
 
 @pytest.mark.parametrize("i", range(len(CASES)))
 def test_masked_fwd_bwd_matches_oracle(cuda, i):
-    c = CASES[i]
+    check_case(cuda, CASES[i], i)
+
+
+def check_case(cuda, c, i):
+    """Case ``c`` (seeded by ``i``) against the oracle and the reference path (see the module
+    docstring); returns the rows (name, kernel error, path error, bar)."""
     print(f"masked fwd+bwd case {i}: {c}", flush=True)
     dt = DTYPES[c["dt"]]
     B, Hq, Hkv, Sq, Sk, Dr, Dc, Dv = (c[k] for k in ("B", "Hq", "Hkv", "Sq", "Sk", "Dr", "Dc", "Dv"))
@@ -132,6 +140,7 @@ def test_masked_fwd_bwd_matches_oracle(cuda, i):
     out.backward(dout.to(cuda))
     torch.cuda.synchronize()
     kern = {"out": out} | {"d" + n: gx[n].grad for n in names}
+    all_rows = []
     for n, a in kern.items():
         assert a.dtype == dt, (n, a.dtype)
         assert torch.isfinite(a).all(), n
@@ -140,13 +149,43 @@ def test_masked_fwd_bwd_matches_oracle(cuda, i):
             [(n, err(a, exact[n], n), pe, bar_for(pe, BASE[dt]))]
         for name, ke, pe_, bar in rows:
             assert ke < bar, (i, name, "kernel", ke, "reference path", pe_, "bar", bar)
-    if c["mask"] in ("bool2d", "float_b1", "bf16_b1"):  # the fully masked row: zeros, as SDPA returns
-        r = 3 if c["mask"] == "bool2d" else 5
+        all_rows += rows
+    r = {"bool2d": 3, "float_b1": 5, "bf16_b1": 5}.get(c["mask"])
+    if r is not None and r < Sq:  # the fully masked row: zeros, as SDPA returns
         assert (out[0, :, r] == 0).all() and (gx["qr"].grad[0, :, r] == 0).all()
     if c["mode"] == "pope":
         b = exact["ddelta"]
         rel = err(gd.grad, b) / max(1.0, b.abs().max().item())
         assert rel < DDELTA[dt], (i, "ddelta", rel)
+        all_rows.append(("ddelta", rel, None, DDELTA[dt]))
+    return all_rows
+
+
+def draw_masked(seed):
+    """A masked case from the random sweep's draw (tests/test_gpu_sweep.py): mode, dtype (fp16 too),
+    batch, heads, widths and length, plus a mask kind, the causal flag (with a mask both apply) and,
+    without it, a key length that may differ from the query length."""
+    c = draw(seed)
+    r = random.Random(10_000 + seed)
+    c["dt"] = r.choice(["bf16", "bf16", "fp32", "fp16"])
+    c["mask"] = r.choice(["bool2d", "float_b1", "bf16_b1", "perhead", "keypad"])
+    c["Sq"] = c["S"]
+    c["Sk"] = c["S"] if c["causal"] else r.randint(1, 600)
+    if c["mask"] == "keypad" and c["Sk"] < 60:
+        c["mask"] = "bool2d"
+    return c
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_masked_config_matches_oracle(cuda, seed):
+    """Seeds 0-199 were scanned on an MI355X under these bars.  199 passed, the tightest at 0.95 of
+    the bar (seed 2, fp16 dk, equal to the reference path's error) and 0.93 (seed 197, bf16 dv, equal
+    to the path's).  Seed 174 (no PE, D = 32, bf16, causal with a bf16 float mask) missed by 4 %:
+    dk 0.0208 against 2e-2, where the path's error is 0.0179.  The element has |dk| = 4.04, where
+    one bf16 spacing is 0.031, and the kernel and the path round to different neighbours of the exact
+    value.  Net of that rounding the errors are 0.0112 (kernel) and 0.0104 (path), and the kernel's
+    mean dk error is below the path's (1.16e-3 against 1.32e-3).  The first 16 seeds are committed."""
+    check_case(cuda, draw_masked(seed), 300 + seed)
 
 
 def test_grouped_query_attention_with_mask(cuda):
