@@ -241,7 +241,9 @@ def _cached_attention_autograd(cache: KVCache, start_pos: int, *, q, k, v, q_c, 
     transformed operands (no-PE mode, bottom-right causal mask).  The cache buffers also receive
     the new rows' values for later decode steps.  Unlike the reference, whose later writes into the
     buffer invalidate the saved tensors of earlier calls, the outputs of several chunks can be
-    differentiated together."""
+    differentiated together.  Each chunk copies the earlier rows into its own operand, so a run of
+    n chunks with gradients holds and copies O(n L) rows where the reference's in-place buffer holds
+    O(L); generation without gradients takes the decode path and copies nothing."""
     from .transform import pe_transform
 
     S = k.shape[2]
