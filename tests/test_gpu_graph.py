@@ -91,3 +91,37 @@ def test_graph_replay_module_training_step(cuda):
         torch.cuda.synchronize()
         for i, (a, b) in enumerate(zip(outs, eager)):
             assert torch.equal(a, b), (rep, i, (a.float() - b.float()).abs().max().item())
+
+
+def test_graph_replay_masked_step(cuda):
+    """The explicit-mask path (pe_attn_fwd_masked / pe_attn_bwd_masked, generic kernels) captured and
+    replayed: a broadcast key-padding bool mask and a float mask with -inf, replays equal to the eager
+    step bit for bit, also after the mask's contents change in place."""
+    B, Hq, Hkv, S, D = 2, 4, 2, 200, 64
+    gen = torch.Generator(device=cuda).manual_seed(5)
+    mk = lambda h: torch.randn(B, h, S, D, generator=gen, device=cuda).to(torch.bfloat16).requires_grad_(True)
+    q, k, v = mk(Hq), mk(Hkv), mk(Hkv)
+    dO = torch.randn(B, Hq, S, D, generator=gen, device=cuda).to(torch.bfloat16)
+    masks = [(torch.arange(S, device=cuda).view(1, S) < torch.tensor([S, 77], device=cuda).view(B, 1)).view(B, 1, 1, S),
+             torch.randn(B, 1, S, S, generator=gen, device=cuda).masked_fill(
+                 torch.rand(B, 1, S, S, generator=gen, device=cuda) > 0.8, float("-inf"))]
+    for mask in masks:
+        def step():
+            out = pe_attention(q, k, v, mode="none", causal=False, mask=mask)
+            return (out.detach(),) + torch.autograd.grad(out, (q, k, v), dO)
+
+        print(f"graph replay masked {mask.dtype}", flush=True)
+        g, outs = capture(step)
+        for rep in range(3):
+            if rep == 2:
+                with torch.no_grad():
+                    if mask.dtype == torch.bool:
+                        mask.copy_(torch.rand(mask.shape, generator=gen, device=cuda) > 0.3)
+                    else:
+                        mask.copy_(torch.randn(mask.shape, generator=gen, device=cuda))
+            eager = [t.clone() for t in step()]
+            torch.randn(1 << 16, device=cuda).sum().item()
+            g.replay()
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(outs, eager)):
+                assert torch.equal(a, b), (str(mask.dtype), rep, i, (a.float() - b.float()).abs().max().item())

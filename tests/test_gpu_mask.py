@@ -225,3 +225,28 @@ def test_mask_argument_errors(cuda):
         pe_attention(q, q, q, mode="none", causal=False, mask=torch.zeros(16, 16, device=cuda, requires_grad=True))
     with pytest.raises(ValueError, match="mask is on cpu"):
         pe_attention(q, q, q, mode="none", causal=False, mask=torch.ones(16, 16, dtype=torch.bool))
+
+
+def test_masked_module_under_bf16_autocast(cuda):
+    """GroupedQueryAttention(mask) under bf16 autocast: the float mask is rounded to bf16 as autocast
+    rounds SDPA's inputs, and the output and gradients stay within the bf16 scale of the fp32
+    module's (the masked kernels run on bf16 operands)."""
+    torch.manual_seed(8)
+    B, S = 2, 80
+    m = GroupedQueryAttention(256, 4, 2, 64, use_qk_norm=True, rope=RotaryEmbedding(64, 256)).to(cuda)
+    x = torch.randn(B, S, 256, device=cuda)
+    mask = torch.randn(B, 1, S, S, device=cuda).masked_fill(torch.rand(B, 1, S, S, device=cuda) > 0.7, float("-inf"))
+    dout = torch.randn(B, S, 256, device=cuda)
+    res = []
+    for ac in (False, True):
+        xg = x.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=ac):
+            out = m(xg, mask)
+        if ac:
+            assert out.dtype == torch.bfloat16
+        out.float().backward(dout)
+        res.append([out.float()] + [xg.grad] + [p.grad.clone() for p in m.parameters()])
+        m.zero_grad()
+    for i, (a, b) in enumerate(zip(res[1], res[0])):
+        scale = max(1.0, b.abs().max().item())
+        assert torch.isfinite(a).all() and (a - b).abs().max().item() < 3e-2 * scale, (i, (a - b).abs().max().item())
