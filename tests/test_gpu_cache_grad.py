@@ -7,7 +7,8 @@ assignment and runs SDPA over cache[:, :, :start_pos + S] with the bottom-right 
 the gradient of a later chunk's output reaches the earlier chunks' inputs through their cached keys
 and values.  The chunked outputs are the rows of the no-cache causal forward over the whole
 sequence, so the gradients of a loss over the chunks' outputs must equal those of the same loss over
-the full forward's rows: x, every projection weight and the PoPE phase bias, in fp32 to 2e-5 of each
+the full forward's rows: x, every projection weight, the PoPE phase bias and FoPE's Fourier
+coefficients, in fp32 to 2e-5 of each
 gradient's scale (the two sides run different kernels: the fused PoPE forward and backward, against
 the stand-alone transform and the no-PE kernels on transformed operands).  A rewind (a chunk at a
 start_pos inside the cached rows) must equal the full forward over the kept prefix and the new
@@ -18,6 +19,7 @@ import pytest
 import torch
 
 from pe_ablations_amd.attention import GroupedQueryAttention
+from pe_ablations_amd.fpope import FoPEPoPEEmbedding
 from pe_ablations_amd.fpope_attention import FPoPEGroupedQueryAttentionWithCache
 from pe_ablations_amd.pope import PoPEEmbedding
 from pe_ablations_amd.rope import RotaryEmbedding
@@ -30,9 +32,12 @@ def rel(a, b):
     return err(a, b) / max(1.0, b.abs().max().item())
 
 
-def fpope_module(cuda):
+def fpope_module(cuda, fope=False):
     torch.manual_seed(11)
-    pe = PoPEEmbedding(32, 512, delta_init="uniform")
+    if fope:  # Fourier frequencies: their coefficients get gradients through the transform's d(omega)
+        pe = FoPEPoPEEmbedding(32, 512, num_fourier_terms=4, fourier_sigma=0.4, delta_init="uniform")
+    else:
+        pe = PoPEEmbedding(32, 512, delta_init="uniform")
     return FPoPEGroupedQueryAttentionWithCache(256, 4, 2, 64, 32, fpope=pe, max_cache_len=128).to(cuda)
 
 
@@ -41,11 +46,11 @@ def chunked(m, x, chunks):
     return torch.cat([m(x[:, a:b], start_pos=a, use_cache=True) for a, b in chunks], 1)
 
 
-@pytest.mark.parametrize("which", ["fpope", "rope", "nope"])
+@pytest.mark.parametrize("which", ["fpope", "fope", "rope", "nope"])
 def test_cached_chunk_gradients_equal_full_forward(cuda, which):
     print(f"cache grad {which}", flush=True)
-    if which == "fpope":
-        m = fpope_module(cuda)
+    if which in ("fpope", "fope"):
+        m = fpope_module(cuda, fope=which == "fope")
     else:
         torch.manual_seed(12)
         m = GroupedQueryAttention(256, 4, 2, 64, use_qk_norm=True,
