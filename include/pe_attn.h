@@ -162,11 +162,12 @@ int pe_attn_bwd(const pe_attn_params* p,
  * float type whose value is added to the scaled score; element strides may be 0 where it broadcasts
  * (torch's expand) and must not be negative.  A row whose every key is masked gives out = 0, lse =
  * -inf and zero gradients, as torch's SDPA does.  Float values below -FLT_MAX / log2(e) count as
- * -inf.  These calls run the generic kernels with the mask read per score (the tuned causal kernels
- * do not take one) and store no dS: the masked backward needs
- * pe_attn_bwd_masked_workspace_bytes, which grows with S, not S^2.  The forward workspace is
- * pe_attn_fwd_workspace_bytes.  Arguments otherwise as pe_attn_fwd / pe_attn_bwd; the mask has no
- * gradient. */
+ * -inf.  With a 16-bit compute type the forward runs the tuned kernel's mask instantiation, and at
+ * transformed widths 128 / 256 with value widths 64 / 128 so does the backward (the dK/dV pair
+ * kernel and the dQ GEMM over its stored dS, capped as in pe_attn_bwd); fp32 and the other widths
+ * run the generic kernels, which store no dS.  The backward's workspace is
+ * pe_attn_bwd_masked_workspace_bytes, the forward's pe_attn_fwd_workspace_bytes.  Arguments
+ * otherwise as pe_attn_fwd / pe_attn_bwd; the mask has no gradient. */
 size_t pe_attn_bwd_masked_workspace_bytes(const pe_attn_params* p);
 int pe_attn_fwd_masked(const pe_attn_params* p,
                        const pe_tensor_t* qc, const pe_tensor_t* qr,

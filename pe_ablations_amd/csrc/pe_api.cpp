@@ -95,12 +95,18 @@ bool fused_split_bwd(const pe_attn_params* p, const pe_tensor_t* qr, const pe_te
          vec16(dkr);
 }
 
-// masked: the explicit-mask backward (pe_attn_bwd_masked), whose generic gradient kernels write
-// fp32 dq~ / dk~ for the stand-alone inverse transform and store no dS
+// The explicit-mask backward (pe_attn_bwd_masked) at the pair kernel's 16-bit widths runs the same
+// kernels as the unmasked one, without the query-head split; elsewhere it runs the generic kernels,
+// which write fp32 dq~ / dk~ for the stand-alone inverse transform and store no dS.
+bool generic_masked(const pe_attn_params* p, bool masked) {
+  return masked && !(half_dt(p->dtype) && pe::pair_shape(pad_qk(qk_width(p)), pad_v(p->Dv)));
+}
+
 Layout layout(const pe_attn_params* p, bool masked = false) {
   Layout L{};
   L.dqk = pad_qk(qk_width(p));
   L.dv = pad_v(p->Dv);
+  const bool gm = generic_masked(p, masked);
   const size_t e = esz(p);
   const size_t nq = (size_t)p->B * p->Hq * p->Sq, nk = (size_t)p->B * p->Hkv * p->Sk;
   L.q_off = 0;
@@ -122,7 +128,7 @@ Layout layout(const pe_attn_params* p, bool masked = false) {
   L.di_off = L.do_off + align_up(nq * L.dv * e);
   L.l2_off = L.di_off + align_up(nq_pad * 4);
   L.dq_off = L.l2_off + align_up(nq_pad * 4);
-  const bool fb = !masked && fused_bwd(p);
+  const bool fb = !gm && fused_bwd(p);
   L.ksplit = masked ? 1 : key_split(p, L.dqk, L.dv);
   L.dk_off = L.dq_off + (fb ? 0 : align_up(nq * L.dqk * 4));
   // dk~ (unfused) or the split's partial dk~ slices
@@ -144,7 +150,7 @@ Layout layout(const pe_attn_params* p, bool masked = false) {
   // dS of one (batch, kv head) unit: its query heads' regions; as many units per group as the cap
   // holds (at least one)
   const int units = p->B * p->Hkv;
-  const bool store_ds = half_dt(p->dtype) && !masked;
+  const bool store_ds = half_dt(p->dtype) && !gm;
   const size_t unit_bytes = (size_t)(p->Hq / p->Hkv) * L.ds_head * 4096;
   L.ds_group = units;
   if (store_ds && unit_bytes > 0 && (size_t)units * unit_bytes > PE_BWD_DS_CAP_BYTES)
@@ -783,7 +789,8 @@ static int bwd_impl(const pe_attn_params* p, const pe_tensor_t* qc, const pe_ten
   pb.out = out->data; pb.out_dtype = out->dtype;
   for (int i = 0; i < 4; ++i) { pb.do_s[i] = dout->stride[i]; pb.o_s[i] = out->stride[i]; }
   // the bf16 dK/dV kernel reads dO in place when its rows are 16-byte aligned and exactly Dv wide
-  const bool do_direct = half_dt(dt) && !masked && v_direct(p, dout, L.dv);
+  const bool gm = generic_masked(p, masked);
+  const bool do_direct = half_dt(dt) && !gm && v_direct(p, dout, L.dv);
   pb.dO_op = do_direct ? nullptr : bws + L.do_off; pb.op_dtype = p->dtype; pb.width = L.dv;
   pb.Di = (float*)(bws + L.di_off);
   pb.L2 = (float*)(bws + L.l2_off);
@@ -820,8 +827,8 @@ static int bwd_impl(const pe_attn_params* p, const pe_tensor_t* qc, const pe_ten
   stage_mark(PE_STAGE_BWD_DKDV, 0, s);
   // fused form in bf16 with both halves of a column in one wave: the gradient kernels apply the
   // inverse PoPE transform in their epilogues
-  const bool split = !masked && fused_split_bwd(p, qr, kr, dqc, dqr, dkc, dkr);
-  const bool fuse = (!masked && fused_bwd(p)) || split;
+  const bool split = !gm && fused_split_bwd(p, qr, kr, dqc, dqr, dkc, dkr);
+  const bool fuse = (!gm && fused_bwd(p)) || split;
   const int nqg = (p->Sq + 255) / 256, nkg = (p->Sk + 127) / 128;
   if (fuse) {
     c.fuse_inv = 1;

@@ -896,7 +896,9 @@ __device__ __forceinline__ void dk_epilogue(const CoreArgs& a, float* st_epi, in
 // tiles stream through a ring of 4 LDS stages (q~ 32 x DQK, dO 32 x DV, the rows' log2 lse and Di)
 // loaded two steps ahead.
 // (pack_h2 / unpack_h2, pe_common.h: two floats <-> one dword of fp16, round-to-nearest-even)
-template <int HT, int DQK, int DV, int QT, bool QS>
+// MB: the explicit-mask instantiation; role A adds mask_l2 to the scaled scores before its
+// exponentials, so P, the handed-over P and the stored dS carry the mask.
+template <int HT, int DQK, int DV, int QT, bool QS, bool MB = false>
 __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
   using M = MT<HT>;  // HT: the 16-bit operand type, bf16 (0) or fp16 (2)
   constexpr int NW = 8, BMQ = 32 * QT, BNK = 128, NSTG = 4;
@@ -1088,7 +1090,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 #pragma unroll
     for (int i = 0; i < 2 * QT; ++i) pa0[i] = pa1[i] = u32x4{0u, 0u, 0u, 0u};
     f32x16 s[QT];
-    int cur_qt = qb0;  // query tile of step t
+    int cur_qt = qb0, cur_h = h_first;  // query tile and head of step t
     // step t: S of tile t (products right after the barrier), the loads of tile t + 2, P of tile t,
     // then dV of tile t - 1 from the other P buffer
     auto astep = [&](int t, u32x4 (&pn)[2 * QT], u32x4 (&pp)[2 * QT]) {
@@ -1111,8 +1113,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
         // between the score products and the exponentials: 1.4 % faster than after the P hand-off,
         // and every earlier point, inside the score products' chain, measured slower
         if (t + 2 < niter) issue(t + 2);
-        const int q0 = cur_qt * BMQ;
-        if (++cur_qt == nqt) cur_qt = qb0;
+        const int q0 = cur_qt * BMQ, hq = cur_h;
+        if (++cur_qt == nqt) {
+          cur_qt = qb0;
+          ++cur_h;
+        }
 #pragma unroll
         for (int m = 0; m < QT; ++m) {
           const int q0m = q0 + 32 * m;
@@ -1130,8 +1135,16 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           for (int G = 0; G < 4; ++G) {
             const f32x4 lv = lvp[m][G];
             f32x4 p;
+            if constexpr (MB) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[m][4 * G + e] * sl2 - lv[e]);
+              for (int e = 0; e < 4; ++e)
+                p[e] = fast_exp2(fmaf(s[m][4 * G + e], sl2,
+                                      mask_l2(a, b, hq, q0 + 32 * m + (G >> 1) * 16 + g * 8 + (G & 1) * 4 + e, myk)) -
+                                 lv[e]);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[m][4 * G + e] * sl2 - lv[e]);
+            }
             if constexpr (P32) {
               *(f32x4*)(xb + ((4 * m + G) * 64 + lane) * 16) = p;
             } else {
@@ -1671,7 +1684,22 @@ static int run_bwd_generic(int which, const CoreArgs& a, hipStream_t s) {
 template <int DT, int DQK, int DV>
 static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 4;
-  if (a.mask) return run_bwd_generic<DT, DQK, DV, true>(which, a, s);
+  constexpr bool PAIR = DT != 1 && (DQK == 128 || DQK == 256) && (DV == 128 || DV == 64);
+  if constexpr (PAIR) {
+    if (a.mask) {  // explicit mask: the pair kernel's mask instantiation (no query-head split), then the dQ GEMM
+      if (which == 0) {
+        constexpr int QT = DQK == 128 && DV == 64 && DT != 2 ? 2 : 1;
+        const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
+        hipLaunchKernelGGL((dkdv_pair_kernel<DT, DQK, DV, QT, false, true>), dim3(nkb * a.nbh), dim3(512), 0, s, a);
+      } else {
+        const int nqb = (a.Sq + 255) / 256;
+        hipLaunchKernelGGL((dq_gemm_kernel<DT, DQK, 8, 32, 4, 0>), dim3(nqb * a.nbh * (a.Hq / a.Hkv)), dim3(8 * 64), 0, s, a);
+      }
+      return hipGetLastError() == hipSuccess ? 0 : -7;
+    }
+  } else {
+    if (a.mask) return run_bwd_generic<DT, DQK, DV, true>(which, a, s);
+  }
   if constexpr (DT != 1) {
     if (which == 0) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);

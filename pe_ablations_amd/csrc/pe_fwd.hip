@@ -174,7 +174,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fwd_kernel(CoreArgs a, int o_vec) 
 // waves share each SIMD (<= 256 registers per wave), so one wave's softmax overlaps the other's
 // MFMAs.  The running max is raised lazily: O and l are rescaled only when some query's block
 // max exceeds the current one by more than TAU (in log2 units), which bounds p by 2^TAU.
-template <int HT, int DQK, int DV, int BN, int NW, int NDW, int NSTG>
+// MB: the explicit-mask instantiation, which adds mask_l2 to the scaled scores before the softmax.
+template <int HT, int DQK, int DV, int BN, int NW, int NDW, int NSTG, bool MB = false>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(CoreArgs a, int o_vec) {
   using M = MT<HT>;  // HT: the 16-bit operand type, bf16 (0) or fp16 (2)
   constexpr int BM = NW * 32;
@@ -185,7 +186,11 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
   constexpr int SMEM = (NSTG * STAGE) > (BM * SO_STRIDE) ? (NSTG * STAGE) : (BM * SO_STRIDE);
   static_assert(NSTG == 2 || NSTG == 3, "ring depth");
   static_assert(NDW >= 1 && NDW <= NW, "DMA waves");
-  constexpr float TAU = 8.f;
+  // A float mask can make a row's softmax peaky, one key carrying nearly all its weight.  With the
+  // lazy max that key's probability reaches the 16-bit rounding as some 2^x, x in (0, TAU], not as
+  // 1, and its rounding error goes straight into the output (twice the fp16 output error of an exact
+  // running max measured with a N(0, 4) mask); the mask instantiation raises the max exactly.
+  constexpr float TAU = MB ? 0.f : 8.f;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
@@ -304,6 +309,13 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
     // the running max is kept in log2 units; as sl2 > 0 it is the max of the raw scores times
     // sl2, and each probability is one fma and one exp2 of a raw score
     const bool edge = (a.causal && k0 + BN - 1 > qw + off) || (k0 + BN > a.Sk);
+    if constexpr (MB) {  // the scores in log2 units with the mask added; the softmax takes them as they are
+#pragma unroll
+      for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          s[nt][j] = fmaf(s[nt][j], sl2, mask_l2(a, b, h, myq, k0 + nt * 32 + c_logical<0>(j, g)));
+    }
     if (edge) {
 #pragma unroll
       for (int nt = 0; nt < NKT; ++nt)
@@ -318,7 +330,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
     for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[nt][j]);
-    mx = fmaxf(mx, xor32(mx)) * sl2;
+    mx = fmaxf(mx, xor32(mx)) * (MB ? 1.f : sl2);
     if (__any(mx > m + TAU)) {
       const float mn = fmaxf(m, mx);
       const float alpha = fast_exp2(m - mn);
@@ -334,7 +346,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
     for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float p = fast_exp2(fmaf(s[nt][j], sl2, -m));
+        const float p = fast_exp2(MB ? s[nt][j] - m : fmaf(s[nt][j], sl2, -m));
         s[nt][j] = p;
         rs += p;
       }
@@ -405,6 +417,11 @@ static int run_fwd_bf16(const CoreArgs& a, hipStream_t s) {
   const int grid4 = ((a.Sq + 127) / 128) * a.B * a.Hq;
   const int o_vec = (a.dv_real == DV) && ((uintptr_t)a.o % 16 == 0) && ((a.o_ss * 2) % 16 == 0) &&
                     ((a.o_sh * 2) % 16 == 0) && ((a.o_sb * 2) % 16 == 0);
+  if (a.mask) {  // explicit mask: the 64-key tiles of eight waves only
+    hipLaunchKernelGGL((fwd_bf16_kernel<HT, DQK, DV, 64, NW, NDW, NSTG, true>), dim3(grid), dim3(NW * 64), 0, s, a,
+                       o_vec);
+    return hipGetLastError() == hipSuccess ? 0 : -7;
+  }
   // 96-key tiles spread each step's barrier and tile wait over 1.5 times the products (forward
   // 1.37 vs 1.40 ms at S = 16384, 3 % faster at S = 2048); on short sequences the wider diagonal
   // tiles waste more than that saves (S = 512: 0.023 vs 0.021 ms), so they keep 64-key tiles
@@ -438,14 +455,16 @@ bool core_supported(int dqk, int dv) {
 
 template <int DT>
 static int fwd_dt(int dqk, int dv, const CoreArgs& a, hipStream_t s) {
-  if (a.mask) {  // explicit mask: the generic kernel on any operand type
-    if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64, true>(a, s);
-    if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128, true>(a, s);
-    if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64, true>(a, s);
-    if (dqk == 128 && dv == 128) return run_fwd<DT, 128, 128, true>(a, s);
-    if (dqk == 256 && dv == 64) return run_fwd<DT, 256, 64, true>(a, s);
-    if (dqk == 256 && dv == 128) return run_fwd<DT, 256, 128, true>(a, s);
-    return -3;
+  if constexpr (DT == 1) {
+    if (a.mask) {  // explicit mask in fp32: the generic kernel (16-bit: run_fwd_bf16's mask instantiation)
+      if (dqk == 64 && dv == 64) return run_fwd<DT, 64, 64, true>(a, s);
+      if (dqk == 64 && dv == 128) return run_fwd<DT, 64, 128, true>(a, s);
+      if (dqk == 128 && dv == 64) return run_fwd<DT, 128, 64, true>(a, s);
+      if (dqk == 128 && dv == 128) return run_fwd<DT, 128, 128, true>(a, s);
+      if (dqk == 256 && dv == 64) return run_fwd<DT, 256, 64, true>(a, s);
+      if (dqk == 256 && dv == 128) return run_fwd<DT, 256, 128, true>(a, s);
+      return -3;
+    }
   }
   if constexpr (DT != 1) {
     if (dqk == 64 && dv == 64) return run_fwd_bf16<DT, 64, 64>(a, s);

@@ -100,6 +100,9 @@ int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
 int launch_bwd_dkdv(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
 int launch_bwd_dq(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
 bool core_supported(int dqk, int dv);
+// 16-bit widths served by the dK/dV pair kernel (with the dQ GEMM over its stored dS); the explicit-
+// mask backward runs them there too, and the generic kernels elsewhere
+inline bool pair_shape(int dqk, int dv) { return (dqk == 128 || dqk == 256) && (dv == 64 || dv == 128); }
 
 // Elementwise transform: one wave per (b, h, s) row.
 struct PrepArgs {

@@ -212,25 +212,32 @@ def test_bwd_workspace_reserves_the_query_head_split_partials(lib):
     assert abs(8 * (per_batch(8, 8, _lib.PE_DTYPE_FP32) - per_batch(64, 8, _lib.PE_DTYPE_FP32))) < 1 << 20
 
 
-def test_masked_bwd_workspace_grows_with_s_not_s2(lib):
-    """The explicit-mask backward stores no dS: its workspace holds dO, Di / L2 and the fp32 dq~ /
-    dk~ of the generic kernels, linear in S (at the headline widths, 16 heads: 0.61 GB at S = 16384
-    where the causal backward takes 4.40 GB, nearly all of it dS), and it does not depend on the
-    causal flag."""
+def test_masked_bwd_workspace(lib):
+    """The explicit-mask backward's workspace.  In fp32 (and at widths outside the dK/dV pair
+    kernel's) it runs the generic kernels, which store no dS: dO, Di / L2 and the fp32 dq~ / dk~,
+    linear in S (0.61 GB at the headline widths with 16 heads at S = 16384) and independent of the
+    causal flag.  In bf16 at the pair kernel's widths it runs the tuned kernels and takes the
+    unmasked backward's workspace, dS included, without the query-head split's partials."""
     lib.pe_attn_bwd_masked_workspace_bytes.restype = ctypes.c_size_t
     lib.pe_attn_bwd_workspace_bytes.restype = ctypes.c_size_t
 
     def ws(S, **kw):
         return lib.pe_attn_bwd_masked_workspace_bytes(ctypes.byref(params(Hq=16, Hkv=16, Sq=S, Sk=S, Dr=128, Dv=128, **kw)))
 
+    f32 = dict(dtype=_lib.PE_DTYPE_FP32)
     for S in (1024, 16384):
         rows = 16 * S
-        assert ws(S) >= rows * 128 * 2 + 2 * rows * 4 + 2 * rows * 256 * 4
-        # plus the phase gradient's per-block partial sums (three buffers of at most 2048 blocks x Dr)
-        assert ws(S) < rows * 128 * 2 + 2 * rows * 4 + 2 * rows * 256 * 4 + (4 << 20)
-        assert ws(S) == ws(S, causal=_lib.PE_CAUSAL_NONE)
-    assert abs(ws(32768) / ws(16384) - 2) < 0.01
-    assert ws(16384) < lib.pe_attn_bwd_workspace_bytes(ctypes.byref(params(Hq=16, Hkv=16, Sq=16384, Sk=16384, Dr=128, Dv=128)))
+        # dO in fp32, Di and L2, fp32 dq~ and dk~, plus the phase gradient's per-block partial sums
+        assert ws(S, **f32) >= rows * 128 * 4 + 2 * rows * 4 + 2 * rows * 256 * 4
+        assert ws(S, **f32) < rows * 128 * 4 + 2 * rows * 4 + 2 * rows * 256 * 4 + (4 << 20)
+        assert ws(S, **f32) == ws(S, causal=_lib.PE_CAUSAL_NONE, **f32)
+    assert abs(ws(32768, **f32) / ws(16384, **f32) - 2) < 0.01
+    # bf16, headline: 2048 key blocks fill the chip, so the unmasked backward has no split either
+    unmasked = lib.pe_attn_bwd_workspace_bytes(ctypes.byref(params(Hq=16, Hkv=16, Sq=16384, Sk=16384, Dr=128, Dv=128)))
+    assert ws(16384) == unmasked
+    # bf16 at QK width 64 (Dr = 32): generic kernels, no dS
+    small = lib.pe_attn_bwd_masked_workspace_bytes(ctypes.byref(params(Hq=16, Hkv=16, Sq=16384, Sk=16384, Dr=32, Dv=64)))
+    assert small < 16 * 16384 * (64 * 2 + 8 + 2 * 64 * 4) + (4 << 20)
     assert lib.pe_attn_bwd_masked_workspace_bytes(ctypes.byref(params(B=0))) == 0
 
 
