@@ -197,6 +197,8 @@ void set_mask(pe::CoreArgs& c, const pe_tensor_t* m) {
   c.mask = m->data;
   c.m_sb = m->stride[0]; c.m_sh = m->stride[1]; c.m_sq = m->stride[2]; c.m_sk = m->stride[3];
   c.mask_dtype = m->dtype;
+  c.mask_vec = m->stride[3] == 1 && m->stride[2] % 8 == 0 && m->stride[1] % 8 == 0 && m->stride[0] % 8 == 0 &&
+               c.Sk % 8 == 0 && (uintptr_t)m->data % 16 == 0;
 }
 
 int dev_flags[64];  // 0 unknown, 1 gfx950, 2 other

@@ -1054,6 +1054,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 
 
   const int kr = myk < a.Sk ? myk : a.Sk - 1;
+  const int64_t mkofs = MB ? (int64_t)kr * a.m_sk : 0;  // this lane's key in the mask view
   if (!roleB) {
     if (niter > 0) issue(0);
     if (niter > 1) issue(1);
@@ -1118,6 +1119,24 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
           cur_qt = qb0;
           ++cur_h;
         }
+        // MB: the mask of this lane's key at the 16 query rows of each sub-tile, loaded before the
+        // causal masking below (rows past Sq, in the last tile only, read row Sq - 1)
+        float mlv[MB ? QT : 1][16];
+        if constexpr (MB) {
+          const int64_t rb = b * a.m_sb + hq * a.m_sh + mkofs;
+#pragma unroll
+          for (int m = 0; m < QT; ++m) {
+            const int qm = q0 + 32 * m + g * 8;
+            const bool full = q0 + 32 * m + 31 < a.Sq;
+#pragma unroll
+            for (int G = 0; G < 4; ++G)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int q = qm + (G >> 1) * 16 + (G & 1) * 4 + e;
+                mlv[m][4 * G + e] = mask_elem_l2(a, rb + (int64_t)(full ? q : min(q, a.Sq - 1)) * a.m_sq);
+              }
+          }
+        }
 #pragma unroll
         for (int m = 0; m < QT; ++m) {
           const int q0m = q0 + 32 * m;
@@ -1137,10 +1156,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
             f32x4 p;
             if constexpr (MB) {
 #pragma unroll
-              for (int e = 0; e < 4; ++e)
-                p[e] = fast_exp2(fmaf(s[m][4 * G + e], sl2,
-                                      mask_l2(a, b, hq, q0 + 32 * m + (G >> 1) * 16 + g * 8 + (G & 1) * 4 + e, myk)) -
-                                 lv[e]);
+              for (int e = 0; e < 4; ++e) p[e] = fast_exp2(fmaf(s[m][4 * G + e], sl2, mlv[m][4 * G + e]) - lv[e]);
             } else {
 #pragma unroll
               for (int e = 0; e < 4; ++e) p[e] = fast_exp2(s[m][4 * G + e] * sl2 - lv[e]);

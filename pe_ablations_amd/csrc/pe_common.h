@@ -183,12 +183,38 @@ __device__ __forceinline__ void store_from_float(void* p, int64_t i, int dtype, 
 // bool mask, the float's value times log2(e) otherwise (values below -FLT_MAX / log2(e) overflow to
 // -inf, i.e. masked).  q and k are clamped into the view, so padding rows and keys past the end read
 // an element of the view and are masked by the caller.
+template <class A> __device__ __forceinline__ float mask_elem_l2(const A& a, int64_t i) {  // element i
+  if (a.mask_dtype == 3) return ((const uint8_t*)a.mask)[i] ? 0.f : -INFINITY;
+  return load_as_float(a.mask, i, a.mask_dtype) * LOG2E;
+}
 template <class A> __device__ __forceinline__ float mask_l2(const A& a, int b, int h, int q, int k) {
   q = q < a.Sq ? q : a.Sq - 1;
   k = k < a.Sk ? k : a.Sk - 1;
-  const int64_t i = b * a.m_sb + h * a.m_sh + (int64_t)q * a.m_sq + (int64_t)k * a.m_sk;
-  if (a.mask_dtype == 3) return ((const uint8_t*)a.mask)[i] ? 0.f : -INFINITY;
-  return load_as_float(a.mask, i, a.mask_dtype) * LOG2E;
+  return mask_elem_l2(a, b * a.m_sb + h * a.m_sh + (int64_t)q * a.m_sq + (int64_t)k * a.m_sk);
+}
+
+// The mask of 8 consecutive keys at element offset `i` of a mask_vec view (pe_internal.h), in log2
+// units as mask_l2: one 8- or 16-byte load for bool and 16-bit masks, two for fp32.
+template <class A> __device__ __forceinline__ void mask_row8(const A& a, int64_t i, float (&mv)[8]) {
+  if (a.mask_dtype == 3) {
+    const u32x2 w = *(const u32x2*)((const uint8_t*)a.mask + i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mv[e] = ((w[e >> 2] >> ((e & 3) * 8)) & 0xffu) ? 0.f : -INFINITY;
+  } else if (a.mask_dtype == 1) {
+    const f32x4 x0 = *(const f32x4*)((const float*)a.mask + i), x1 = *(const f32x4*)((const float*)a.mask + i + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      mv[e] = x0[e] * LOG2E;
+      mv[4 + e] = x1[e] * LOG2E;
+    }
+  } else {
+    const u32x4 w = *(const u32x4*)((const uint16_t*)a.mask + i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint16_t hv = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+      mv[e] = (a.mask_dtype == 0 ? bf2f(hv) : h2f(hv)) * LOG2E;
+    }
+  }
 }
 
 template <int DT> struct MT;

@@ -310,11 +310,31 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
     // sl2, and each probability is one fma and one exp2 of a raw score
     const bool edge = (a.causal && k0 + BN - 1 > qw + off) || (k0 + BN > a.Sk);
     if constexpr (MB) {  // the scores in log2 units with the mask added; the softmax takes them as they are
+      if (a.mask_vec) {  // values j = 8 hf .. 8 hf + 7 of tile nt are 8 consecutive keys: one vector read
+        const int qc = myq < a.Sq ? myq : a.Sq - 1;
+        const int64_t rowb = b * a.m_sb + h * a.m_sh + (int64_t)qc * a.m_sq;
 #pragma unroll
-      for (int nt = 0; nt < NKT; ++nt)
+        for (int nt = 0; nt < NKT; ++nt)
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-          s[nt][j] = fmaf(s[nt][j], sl2, mask_l2(a, b, h, myq, k0 + nt * 32 + c_logical<0>(j, g)));
+          for (int hf = 0; hf < 2; ++hf) {
+            const int key0 = k0 + nt * 32 + hf * 16 + g * 8;  // c_logical(8 hf + e, g) - e
+            float mv[8];
+            if (key0 < a.Sk) {
+              mask_row8(a, rowb + key0, mv);
+            } else {  // keys past Sk (Sk % 8 == 0: none of the 8 is inside), masked by the edge test below
+#pragma unroll
+              for (int e = 0; e < 8; ++e) mv[e] = 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[nt][hf * 8 + e] = fmaf(s[nt][hf * 8 + e], sl2, mv[e]);
+          }
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            s[nt][j] = fmaf(s[nt][j], sl2, mask_l2(a, b, h, myq, k0 + nt * 32 + c_logical<0>(j, g)));
+      }
     }
     if (edge) {
 #pragma unroll

@@ -94,6 +94,9 @@ struct CoreArgs {
   const void* mask;
   int64_t m_sb, m_sh, m_sq, m_sk;
   int mask_dtype;
+  // set by the host when the view takes 8-element vector reads: unit key stride, every other stride
+  // a multiple of 8 elements, Sk % 8 == 0 and a 16-byte aligned base (mask_row8)
+  int mask_vec;
 };
 
 int launch_fwd(int dt, int dqk, int dv, const CoreArgs& a, hipStream_t s);
