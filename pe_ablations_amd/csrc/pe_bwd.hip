@@ -1091,7 +1091,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 #pragma unroll
     for (int i = 0; i < 2 * QT; ++i) pa0[i] = pa1[i] = u32x4{0u, 0u, 0u, 0u};
     f32x16 s[QT];
-    int cur_qt = qb0, cur_h = h_first;  // query tile and head of step t
+    int cur_qt = qb0;  // query tile of step t
     // step t: S of tile t (products right after the barrier), the loads of tile t + 2, P of tile t,
     // then dV of tile t - 1 from the other P buffer
     auto astep = [&](int t, u32x4 (&pn)[2 * QT], u32x4 (&pp)[2 * QT]) {
@@ -1101,6 +1101,36 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
         // them above role B's priority and drops to the lowest for its dV products (dK/dV 1.5 %
         // faster than with A always below B; A above B throughout measured in between)
         __builtin_amdgcn_s_setprio(3);
+        // MB: the mask of this lane's key at the 16 query rows of each sub-tile (rows past Sq, in the
+        // last tile only, read row Sq - 1), loaded at the start of the step.  The compiler's wait for
+        // them also drains every DMA issued before its use (it cannot see those), so the tile loads of
+        // this step are issued after the exponentials instead, and that wait covers only tile t + 1,
+        // which the step needs landed by its end anyway.
+        float mlv[MB ? QT : 1][16];
+        if constexpr (MB) {
+          const int hq = h_first + (t / nper), q0 = (qb0 + t % nper) * BMQ;
+          const int64_t rb = b * a.m_sb + hq * a.m_sh + mkofs;
+          if (a.m_sq == 0) {  // a mask that does not vary with the query row (key padding): one read
+            const float v = mask_elem_l2(a, rb);
+#pragma unroll
+            for (int m = 0; m < QT; ++m)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) mlv[m][i] = v;
+          } else {
+#pragma unroll
+            for (int m = 0; m < QT; ++m) {
+              const int qm = q0 + 32 * m + g * 8;
+              const bool full = q0 + 32 * m + 31 < a.Sq;
+#pragma unroll
+              for (int G = 0; G < 4; ++G)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const int q = qm + (G >> 1) * 16 + (G & 1) * 4 + e;
+                  mlv[m][4 * G + e] = mask_elem_l2(a, rb + (int64_t)(full ? q : min(q, a.Sq - 1)) * a.m_sq);
+                }
+            }
+          }
+        }
         // the rows' log2 lse, read ahead of the score products so that the exponentials do not wait
         // on them (0.5 % faster)
         const float* sL = (const float*)(st + SQ_BYTES + SO_BYTES);
@@ -1113,30 +1143,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
         // the loads of tile t + 2 (its stage held tile t - 2, released by the last barrier) go out
         // between the score products and the exponentials: 1.4 % faster than after the P hand-off,
         // and every earlier point, inside the score products' chain, measured slower
-        if (t + 2 < niter) issue(t + 2);
-        const int q0 = cur_qt * BMQ, hq = cur_h;
-        if (++cur_qt == nqt) {
-          cur_qt = qb0;
-          ++cur_h;
-        }
-        // MB: the mask of this lane's key at the 16 query rows of each sub-tile, loaded before the
-        // causal masking below (rows past Sq, in the last tile only, read row Sq - 1)
-        float mlv[MB ? QT : 1][16];
-        if constexpr (MB) {
-          const int64_t rb = b * a.m_sb + hq * a.m_sh + mkofs;
-#pragma unroll
-          for (int m = 0; m < QT; ++m) {
-            const int qm = q0 + 32 * m + g * 8;
-            const bool full = q0 + 32 * m + 31 < a.Sq;
-#pragma unroll
-            for (int G = 0; G < 4; ++G)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int q = qm + (G >> 1) * 16 + (G & 1) * 4 + e;
-                mlv[m][4 * G + e] = mask_elem_l2(a, rb + (int64_t)(full ? q : min(q, a.Sq - 1)) * a.m_sq);
-              }
-          }
-        }
+        if (!MB && t + 2 < niter) issue(t + 2);
+        const int q0 = cur_qt * BMQ;
+        if (++cur_qt == nqt) cur_qt = qb0;
 #pragma unroll
         for (int m = 0; m < QT; ++m) {
           const int q0m = q0 + 32 * m;
@@ -1175,6 +1184,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
             *(u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16) = ph[1];
           }
         }
+        if (MB && t + 2 < niter) issue(t + 2);
         __builtin_amdgcn_s_setprio(0);
       }
       if (t >= 1) products(dv, pp, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);
