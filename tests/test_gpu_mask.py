@@ -9,8 +9,11 @@ of the random sweep (tests/test_gpu_sweep.py): the north-star bar (2e-2 bf16, 1e
 fp16) wherever the reference path (the core with the 16-bit fused SDPA's rounding points, or the
 fp32 core) meets it, else 1.25 times that path's error; fp16 with its one-spacing exemption and
 mean-error check.  The masks: bool (Sq, Sk) with a fully masked row, float (B, 1, Sq, Sk) with -inf
-entries and a fully -inf row, per-head bool (B, Hq, Sq, Sk), key padding (B, 1, 1, Sk), a bf16 float
-mask, and a float mask together with the causal flag; Sq != Sk where the flag is off.
+entries and a fully -inf row, per-head bool (B, Hq, Sq, Sk), key padding (B, 1, 1, Sk) (one read per
+step in the dK/dV kernel), bf16 and fp16 float masks, a transposed bool view (unit stride along the
+queries: per-score reads) and a float mask together with the causal flag; Sq != Sk where the flag is
+off.  16-bit operands run the tuned kernels' mask instantiations (the forward's 8-key vector reads
+where the view allows them), fp32 and QK width 64 the generic kernels.
 """
 
 import functools
@@ -38,6 +41,10 @@ CASES = [
     dict(mode="none", dt="fp16", B=1, Hq=2, Hkv=1, Sq=180, Sk=180, Dr=128, Dc=0, Dv=128, mask="bool2d", causal=True),
     dict(mode="rope", dt="bf16", B=2, Hq=4, Hkv=1, Sq=150, Sk=150, Dr=128, Dc=0, Dv=128, mask="bf16_b1", causal=False),
     dict(mode="pope", dt="bf16", B=1, Hq=4, Hkv=2, Sq=333, Sk=333, Dr=128, Dc=0, Dv=128, mask="bool2d", causal=False),
+    # a transposed view (unit stride along the queries): the per-score reads of the forward
+    dict(mode="rope", dt="bf16", B=2, Hq=4, Hkv=2, Sq=200, Sk=232, Dr=64, Dc=0, Dv=64, mask="transposed", causal=False),
+    # an fp16 float mask whose rows take the forward's 8-key vector reads (Sk % 8 == 0)
+    dict(mode="pope", dt="fp16", B=2, Hq=4, Hkv=4, Sq=256, Sk=256, Dr=64, Dc=0, Dv=64, mask="f16_b1", causal=False),
 ]
 
 
@@ -48,12 +55,14 @@ def make_mask(kind, B, Hq, Sq, Sk, seed):
         if Sq > 3:
             m[3] = False
         return m
-    if kind in ("float_b1", "bf16_b1"):
+    if kind in ("float_b1", "bf16_b1", "f16_b1"):
         m = torch.randn(B, 1, Sq, Sk, generator=g) * 2
         m = m.masked_fill(torch.rand(B, 1, Sq, Sk, generator=g) > 0.8, float("-inf"))
         if Sq > 5:
             m[0, 0, 5] = float("-inf")
-        return m.to(torch.bfloat16) if kind == "bf16_b1" else m
+        return m.to({"bf16_b1": torch.bfloat16, "f16_b1": torch.float16}.get(kind, torch.float32))
+    if kind == "transposed":
+        return (torch.rand(B, 1, Sk, Sq, generator=g) > 0.3).transpose(-1, -2)
     if kind == "perhead":
         return torch.rand(B, Hq, Sq, Sk, generator=g) > 0.5
     if kind == "keypad":
@@ -150,7 +159,7 @@ def check_case(cuda, c, i):
         for name, ke, pe_, bar in rows:
             assert ke < bar, (i, name, "kernel", ke, "reference path", pe_, "bar", bar)
         all_rows += rows
-    r = {"bool2d": 3, "float_b1": 5, "bf16_b1": 5}.get(c["mask"])
+    r = {"bool2d": 3, "float_b1": 5, "bf16_b1": 5, "f16_b1": 5}.get(c["mask"])
     if r is not None and r < Sq:  # the fully masked row: zeros, as SDPA returns
         assert (out[0, :, r] == 0).all() and (gx["qr"].grad[0, :, r] == 0).all()
     if c["mode"] == "pope":
