@@ -1120,14 +1120,22 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 #pragma unroll
             for (int m = 0; m < QT; ++m) {
               const int qm = q0 + 32 * m + g * 8;
-              const bool full = q0 + 32 * m + 31 < a.Sq;
+              if (q0 + 32 * m + 31 < a.Sq) {  // every row inside: a per-lane base plus uniform row offsets
+                const int64_t lb = rb + (int64_t)qm * a.m_sq;
 #pragma unroll
-              for (int G = 0; G < 4; ++G)
+                for (int G = 0; G < 4; ++G)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  const int q = qm + (G >> 1) * 16 + (G & 1) * 4 + e;
-                  mlv[m][4 * G + e] = mask_elem_l2(a, rb + (int64_t)(full ? q : min(q, a.Sq - 1)) * a.m_sq);
-                }
+                  for (int e = 0; e < 4; ++e)
+                    mlv[m][4 * G + e] = mask_elem_l2(a, lb + (int64_t)((G >> 1) * 16 + (G & 1) * 4 + e) * a.m_sq);
+              } else {
+#pragma unroll
+                for (int G = 0; G < 4; ++G)
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) {
+                    const int q = qm + (G >> 1) * 16 + (G & 1) * 4 + e;
+                    mlv[m][4 * G + e] = mask_elem_l2(a, rb + (int64_t)min(q, a.Sq - 1) * a.m_sq);
+                  }
+              }
             }
           }
         }
