@@ -1701,7 +1701,8 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
       }
 }
 
-// the generic kernels: fp32 operands, and the explicit-mask instantiations (MB) on any type
+// the generic kernels: fp32 operands, and the explicit-mask instantiations (MB) of fp32 and of the
+// 16-bit widths outside the pair kernel's
 template <int DT, int DQK, int DV, bool MB>
 static int run_bwd_generic(int which, const CoreArgs& a, hipStream_t s) {
   constexpr int NW = 4, BMQ = 32, BN = 32;

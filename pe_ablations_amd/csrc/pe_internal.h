@@ -87,10 +87,11 @@ struct CoreArgs {
   // each), summed in slice order by dkdv_combine in the dQ launch.  1: off (dv and dk written directly)
   int qsplit;
   float* dv_part;
-  // explicit attention mask (SDPA's attn_mask, src/model/attention.py:91-96), read by the generic
-  // kernels' MB instantiations only: element (b, h, q, k) at mask + b m_sb + h m_sh + q m_sq + k m_sk
-  // (element strides, 0 where the mask broadcasts); mask_dtype 3 = bool bytes (nonzero: the key
-  // takes part), else a PE_DTYPE_* float added to the scaled score.  null: no mask.
+  // explicit attention mask (SDPA's attn_mask, src/model/attention.py:91-96), read by the mask (MB)
+  // instantiations of the tuned forward and dK/dV pair kernel and of the generic kernels: element
+  // (b, h, q, k) at mask + b m_sb + h m_sh + q m_sq + k m_sk (element strides, 0 where the mask
+  // broadcasts); mask_dtype 3 = bool bytes (nonzero: the key takes part), else a PE_DTYPE_* float
+  // added to the scaled score.  null: no mask.
   const void* mask;
   int64_t m_sb, m_sh, m_sq, m_sk;
   int mask_dtype;
