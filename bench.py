@@ -26,6 +26,8 @@ More workloads, selected with ``--workload`` (the default is the headline above)
 * ``c2``: PoPE fwd+bwd at B=8, H=12, S=2048, D=64 (~125M GPT shape).
 * ``c3``: FoPE fwd+bwd at B=4, H=16, S=4096, D=128, M=4 frequencies per dim; the FoPE collapse
   (FoPEPoPEEmbedding) runs in each step and the Fourier coefficients get gradients.
+* ``masked``: PoPE fwd+bwd at B=2, H=16, S=4096, D=128 with an explicit bool key-padding mask
+  (GroupedQueryAttention's attn_mask) and no causal mask: every query-key pair is computed.
 * ``split``: the reference's training module shape, split form [content 64 | PoPE 2x32], V 64,
   8 query heads on 4 kv heads, B=8, S=512, one shared (Dr,) phase bias.
 
@@ -48,13 +50,14 @@ stage (read raw rows, write transformed rows), its time from the stage events, G
 replays: the small shapes, such as ``split``, are bound by host time per launch when run eagerly.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--graph]
-                       [--workload fwdbwd|fwd|fwd32|c2|c3|split|decoder|decode]
+                       [--workload fwdbwd|fwd|fwd32|c2|c3|masked|split|decoder|decode]
 """
 
 from __future__ import annotations
 
 import argparse
 import ctypes
+import functools
 import json
 import math
 import os
@@ -88,6 +91,14 @@ ATTN_WORKLOADS = {
     "c3": dict(B=4, Hq=16, Hkv=16, S=4096, Dc=0, Dr=128, Dv=128, dtype="bf16", backward=True, delta="head",
                fope=(4, 0.1, 2048), name="FoPE causal attention fwd+bwd (M=4 frequencies per dim)",
                metric="fused FoPE attn fwd+bwd TFLOP/s @B=4,H=16,S=4096,D=128; % of bf16 MFMA peak"),
+    # explicit mask (GroupedQueryAttention's attn_mask, src/model/attention.py:91-96): a bool key-padding
+    # mask (B, 1, 1, S), batch entry b keeping its first S - 100 b keys, and no causal mask, so every
+    # query-key pair is computed
+    "masked": dict(B=2, Hq=16, Hkv=16, S=4096, Dc=0, Dr=128, Dv=128, dtype="bf16", backward=True, delta="head",
+                   causal=False, mask="keypad",
+                   name="PoPE attention fwd+bwd with an explicit key-padding mask (not causal)",
+                   metric="masked PoPE attn fwd+bwd TFLOP/s @B=2,H=16,S=4096,D=128, key-padding mask; "
+                          "% of bf16 MFMA peak"),
     "split": dict(B=8, Hq=8, Hkv=4, S=512, Dc=64, Dr=32, Dv=64, dtype="bf16", backward=True, delta="shared",
                   name="split-form PoPE attention fwd+bwd at the reference's training shape "
                        "([content 64 | PoPE 2x32], V 64, GQA 8 -> 4)",
@@ -125,10 +136,11 @@ def flops(B, H, S, D):
 
 def attn_flops(w: dict) -> dict:
     """Algorithmic FLOPs of causal attention over transformed operands of width Wqk = Dc + 2*Dr and
-    values of width Dv, with B*Hq*S^2/2 query-key pairs: forward S~ (Wqk) + PV (Dv); backward S~
+    values of width Dv, with B*Hq*S^2/2 query-key pairs (B*Hq*S^2 without the causal mask): forward
+    S~ (Wqk) + PV (Dv); backward S~
     recompute (Wqk), dP (Dv), dV (Dv), dK~ (Wqk) and dQ~ (Wqk).  At Dc = 0, Dr = Dv = D this is
     3, 8 and 11 * B*H*S^2*D."""
-    pairs = w["B"] * w["Hq"] * w["S"] * w["S"] / 2.0
+    pairs = w["B"] * w["Hq"] * w["S"] * w["S"] * (0.5 if w.get("causal", True) else 1.0)
     wqk, dv = w["Dc"] + 2 * w["Dr"], w["Dv"]
     return {
         "fwd": 2.0 * pairs * (wqk + dv),
@@ -191,6 +203,13 @@ def fope_module(torch, w: dict, D: int, seed: int = 33):
     return m
 
 
+def keypad_mask(torch, B: int, S: int, device=None):
+    """The masked workload's bool key-padding mask (B, 1, 1, S): batch entry b keeps its first S - 100 b
+    keys."""
+    keep = torch.tensor([S - 100 * b for b in range(B)], device=device)
+    return (torch.arange(S, device=device).view(1, S) < keep.view(B, 1)).view(B, 1, 1, S)
+
+
 def cpu_baseline(w: dict, heads: int, reps: int):
     """The oracle's eager path (fp32, torch eager, all host threads) forward (+ backward) on `heads`
     query heads of one batch entry of the workload at its full S: one untimed warm-up pass, then
@@ -216,6 +235,9 @@ def cpu_baseline(w: dict, heads: int, reps: int):
     leaves = [t for t in (qr, kr, v, qc, kc, delta) if t is not None]
     if fm is not None:
         leaves.append(fm.fourier_coeffs)
+    causal = w.get("causal", True)
+    # the masked workload's first batch entry (its mask keeps every key)
+    core = functools.partial(O.attention, dtype=torch.float32, mask=keypad_mask(torch, 1, S)) if w.get("mask") else None
 
     def one_pass():
         for t in leaves:
@@ -225,9 +247,11 @@ def cpu_baseline(w: dict, heads: int, reps: int):
             f = freqs if fm is None else O.fope_effective_freqs(
                 fm.base_freqs, fm.fourier_coeffs, freq_table=fm.freq_table, training_length=fm.training_length)
             if Dc:
-                out, _ = O.split_pope_attention(qc, kc, qr, kr, v, f, delta, scale=scale, core_dtype=torch.float32)
+                out, _ = O.split_pope_attention(qc, kc, qr, kr, v, f, delta, scale=scale, causal=causal,
+                                                core_dtype=torch.float32, core=core)
             else:
-                out, _ = O.pope_attention(qr, kr, v, f, delta, scale=scale, clamp=False, core_dtype=torch.float32)
+                out, _ = O.pope_attention(qr, kr, v, f, delta, scale=scale, causal=causal, clamp=False,
+                                          core_dtype=torch.float32, core=core)
             if backward:
                 out.backward(dO.to(out.dtype))
         return time.perf_counter() - t0
@@ -244,7 +268,8 @@ def cpu_baseline(w: dict, heads: int, reps: int):
         "cores": torch.get_num_threads(),
         "cpu": cpu_model(),
         "kind": "port",
-        "sample": f"oracle/pe_oracle.py {fn} {what}, fp32 torch eager, {heads} of {w['Hq']} query heads "
+        "sample": f"oracle/pe_oracle.py {fn} {what}" + (" with the key-padding mask" if core else "")
+                  + f", fp32 torch eager, {heads} of {w['Hq']} query heads "
                   f"of one batch entry (S={S}, Dc={Dc}, Dr={Dr}, Dv={Dv}); 1 warm-up + median of {reps} "
                   f"passes, {dt:.2f} s per pass, {sum(times):.1f} s timed",
         "seconds": dt,
@@ -392,9 +417,13 @@ def run_attention(args, torch, dev, wname: str) -> dict:
     if fm is not None:
         leaves.append(fm.fourier_coeffs)
 
+    mask = keypad_mask(torch, B, S, dev) if w.get("mask") else None
+    causal = w.get("causal", True)
+
     def attn():
         f = freqs if fm is None else fm.kernel_freqs()
-        return pe_attention(q, k, v, mode="pope", q_c=qc, k_c=kc, freqs=f, delta=delta, scale=scale)
+        return pe_attention(q, k, v, mode="pope", q_c=qc, k_c=kc, freqs=f, delta=delta, scale=scale,
+                            causal=causal, mask=mask)
 
     if backward:
         def step():
@@ -437,6 +466,9 @@ def run_attention(args, torch, dev, wname: str) -> dict:
         config.update(Hq=Hq, Hkv=Hkv, Dc=Dc, Dr=Dr, Dv=Dv)
     else:
         config.update(H=Hq, D=Dr)
+    if mask is not None:
+        config.update(mask="bool key padding (B, 1, 1, S), batch entry b keeps its first S - 100 b keys",
+                      causal=False)
     config.update(delta="per-head (Hkv, Dr)" if w["delta"] == "head" else "shared (Dr,)",
                   grads=("q,k,v,delta" + (",q_c,k_c" if Dc else "") + (",fourier_coeffs" if fm else ""))
                   if backward else "none", parallelism="single GPU")
@@ -696,10 +728,10 @@ def decode_cpu_baseline(torch) -> dict:
 # (timed steps, warm-up steps) per workload: about half a second of untimed work, and timed work
 # well under a minute
 # query heads of one batch entry in the CPU baseline's sample (about 10-30 s of CPU work)
-CPU_HEADS = {"fwdbwd": 2, "fwd": 2, "fwd32": 2, "c2": 12, "c3": 16, "split": 8}
-CPU_REPS = {"c2": 40, "c3": 10, "fwd32": 12, "split": 1000}
+CPU_HEADS = {"fwdbwd": 2, "fwd": 2, "fwd32": 2, "c2": 12, "c3": 16, "split": 8, "masked": 4}
+CPU_REPS = {"c2": 40, "c3": 10, "fwd32": 12, "split": 1000, "masked": 4}
 DEFAULT_STEPS = {"fwdbwd": (50, 100), "fwd": (100, 400), "fwd32": (10, 40), "c2": (200, 600), "c3": (100, 250),
-                 "split": (500, 2000), "decoder": (5, 4), "decode": (200, 200)}
+                 "split": (500, 2000), "masked": (50, 150), "decoder": (5, 4), "decode": (200, 200)}
 
 
 def main() -> int:
