@@ -1055,6 +1055,11 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
 
   const int kr = myk < a.Sk ? myk : a.Sk - 1;
   const int64_t mkofs = MB ? (int64_t)kr * a.m_sk : 0;  // this lane's key in the mask view
+  // MB, a mask constant over the query rows and heads (key padding, (B, 1, 1, Sk)): this lane's value
+  // for the whole kernel.  Its loop then reads no mask and issues its tile loads where the unmasked
+  // kernel does.
+  const bool kinv = MB && a.m_sq == 0 && a.m_sh == 0;
+  const float kmask = kinv ? mask_elem_l2(a, b * a.m_sb + mkofs) : 0.f;
   if (!roleB) {
     if (niter > 0) issue(0);
     if (niter > 1) issue(1);
@@ -1110,7 +1115,12 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
         if constexpr (MB) {
           const int hq = h_first + (t / nper), q0 = (qb0 + t % nper) * BMQ;
           const int64_t rb = b * a.m_sb + hq * a.m_sh + mkofs;
-          if (a.m_sq == 0) {  // a mask that does not vary with the query row (key padding): one read
+          if (kinv) {  // one value per lane for the whole kernel, read before the loop
+#pragma unroll
+            for (int m = 0; m < QT; ++m)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) mlv[m][i] = kmask;
+          } else if (a.m_sq == 0) {  // a mask that does not vary with the query row: one read per step
             const float v = mask_elem_l2(a, rb);
 #pragma unroll
             for (int m = 0; m < QT; ++m)
@@ -1151,7 +1161,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
         // the loads of tile t + 2 (its stage held tile t - 2, released by the last barrier) go out
         // between the score products and the exponentials: 1.4 % faster than after the P hand-off,
         // and every earlier point, inside the score products' chain, measured slower
-        if (!MB && t + 2 < niter) issue(t + 2);
+        if ((!MB || kinv) && t + 2 < niter) issue(t + 2);
         const int q0 = cur_qt * BMQ;
         if (++cur_qt == nqt) cur_qt = qb0;
 #pragma unroll
@@ -1192,7 +1202,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pair_kernel(CoreArgs a) {
             *(u32x4*)(xb + ((2 * m + 1) * 64 + lane) * 16) = ph[1];
           }
         }
-        if (MB && t + 2 < niter) issue(t + 2);
+        if (MB && !kinv && t + 2 < niter) issue(t + 2);
         __builtin_amdgcn_s_setprio(0);
       }
       if (t >= 1) products(dv, pp, smem + ((t - 1) % NSTG) * STAGE + SQ_BYTES + cro, co);
