@@ -189,8 +189,10 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
   // A float mask can make a row's softmax peaky, one key carrying nearly all its weight.  With the
   // lazy max that key's probability reaches the 16-bit rounding as some 2^x, x in (0, TAU], not as
   // 1, and its rounding error goes straight into the output (twice the fp16 output error of an exact
-  // running max measured with a N(0, 4) mask); the mask instantiation raises the max exactly.
-  constexpr float TAU = MB ? 0.f : 8.f;
+  // running max measured with a N(0, 4) mask); with a float mask the max is raised exactly.  A bool
+  // mask only removes keys and keeps the lazy max.
+  constexpr float TAU = 8.f;
+  const float tau = MB && a.mask_dtype != 3 ? 0.f : TAU;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
@@ -351,7 +353,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void fwd_bf16_kernel(Core
 #pragma unroll
       for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[nt][j]);
     mx = fmaxf(mx, xor32(mx)) * (MB ? 1.f : sl2);
-    if (__any(mx > m + TAU)) {
+    if (__any(mx > m + tau)) {
       const float mn = fmaxf(m, mx);
       const float alpha = fast_exp2(m - mn);
       m = mn;
