@@ -25,6 +25,51 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 constexpr int MAX_PAIRS_PER_LANE = 4;  // RoPE rows up to 512 dims
 
+// RoPE (mode 1) or no-PE (mode 2) forward of one pair (x0, x1) of a row, src/model/rope.py:35-57:
+// y = mscale * (x0 cos - x1 sin, x0 sin + x1 cos) at angle fl(pos * inv_freq), or y = x; each product
+// and sum rounded on its own, as torch's ops round them.  cs / sn are kept for the gradient.
+__device__ __forceinline__ void rope_pair(int mode, float x0, float x1, float pos, float fr, float ms, float& y0,
+                                          float& y1, float& sn, float& cs) {
+  if (mode == 1) {
+    pe_sincos(mul_nc(pos, fr), sn, cs);
+    y0 = sub_nc(mul_nc(x0, cs), mul_nc(x1, sn)) * ms;
+    y1 = add_nc(mul_nc(x0, sn), mul_nc(x1, cs)) * ms;
+  } else {
+    sn = 0.f; cs = 1.f;
+    y0 = x0; y1 = x1;
+  }
+}
+__device__ __forceinline__ float sq2(float a, float b) { return add_nc(mul_nc(a, a), mul_nc(b, b)); }
+__device__ __forceinline__ float dot2(float a0, float a1, float b0, float b1) {
+  return add_nc(mul_nc(a0, b0), mul_nc(a1, b1));
+}
+// Gradient of one pair through QKNorm (y = z / (||z|| + 1e-6), src/model/normalization.py:54-55) and
+// the rotation: d = dy c1 - z c2 (d = dy without the norm), dx = mscale * rot^T(d) (dx = d for no-PE)
+__device__ __forceinline__ void rope_pair_grad(int mode, bool l2, float g0, float g1, float z0, float z1, float c1,
+                                               float c2, float cs, float sn, float ms, float& dx0, float& dx1) {
+  float d0 = g0, d1 = g1;
+  if (l2) {
+    d0 = sub_nc(mul_nc(g0, c1), mul_nc(z0, c2));
+    d1 = sub_nc(mul_nc(g1, c1), mul_nc(z1, c2));
+  }
+  if (mode == 1) {
+    dx0 = mul_nc(add_nc(mul_nc(d0, cs), mul_nc(d1, sn)), ms);
+    dx1 = mul_nc(sub_nc(mul_nc(d1, cs), mul_nc(d0, sn)), ms);
+  } else {
+    dx0 = d0; dx1 = d1;
+  }
+}
+// QKNorm's row sums (||z||^2, and z . dy in the gradient): each lane or thread sums the pairs of its
+// chunk of 4 consecutive pairs in order, and the chunks' sums are added by an xor butterfly over the
+// chunks (lanes past the row's chunks hold 0, which leaves every sum unchanged).  The scalar and the
+// vector kernels below both follow this order, so they produce bitwise equal rows.
+__device__ __forceinline__ void l2_coefs(float ss, float zd, float& c1, float& c2) {
+  const float n = sqrtf(ss);
+  const float ne = add_nc(n, 1e-6f);
+  c1 = 1.f / ne;
+  c2 = n > 0.f ? zd / mul_nc(mul_nc(n, ne), ne) : 0.f;
+}
+
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -55,35 +100,29 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     }
     used += 2 * a.Dr;
   } else {  // RoPE (mode 1) or plain (mode 2): values kept in registers for the optional L2 norm
-    // lane owns pair i = lane + 64k (RoPE) or elements 2i, 2i+1 (plain, odd widths allowed)
+    // lane owns the chunk of pairs i = 4 lane + k (RoPE) or elements 2i, 2i+1 (plain, odd widths
+    // allowed), the vector kernel's chunk of the same lane index
     float y0[MAX_PAIRS_PER_LANE], y1[MAX_PAIRS_PER_LANE];
     float ss = 0.f;
     const int npairs = (a.Dr + 1) / 2;
 #pragma unroll
     for (int k = 0; k < MAX_PAIRS_PER_LANE; ++k) {
-      const int i = lane + 64 * k;
+      const int i = 4 * lane + k;
       y0[k] = 0.f; y1[k] = 0.f;
       if (i < npairs) {
         const bool has1 = 2 * i + 1 < a.Dr;
         const float x0 = load_as_float(a.xr, xr0 + (2 * i) * a.xr_s[3], a.xr_dtype);
         const float x1 = has1 ? load_as_float(a.xr, xr0 + (2 * i + 1) * a.xr_s[3], a.xr_dtype) : 0.f;
-        if (a.mode == 1) {
-          const float ang = mul_nc(pos, a.freqs[i]);
-          float sn, cs;
-          pe_sincos(ang, sn, cs);
-          y0[k] = sub_nc(mul_nc(x0, cs), mul_nc(x1, sn)) * a.mscale;
-          y1[k] = add_nc(mul_nc(x0, sn), mul_nc(x1, cs)) * a.mscale;
-        } else {
-          y0[k] = x0; y1[k] = x1;
-        }
-        ss += y0[k] * y0[k] + y1[k] * y1[k];
+        float sn, cs;
+        rope_pair(a.mode, x0, x1, pos, a.mode == 1 ? a.freqs[i] : 0.f, a.mscale, y0[k], y1[k], sn, cs);
+        ss = add_nc(ss, sq2(y0[k], y1[k]));
       }
     }
     float den = 1.f;
     if (a.l2norm) den = sqrtf(wave_sum(ss)) + 1e-6f;
 #pragma unroll
     for (int k = 0; k < MAX_PAIRS_PER_LANE; ++k) {
-      const int i = lane + 64 * k;
+      const int i = 4 * lane + k;
       if (i < npairs) {
         store_from_float(a.dst, dbase + a.Dc + 2 * i, a.dst_dtype, a.l2norm ? y0[k] / den : y0[k]);
         if (2 * i + 1 < a.Dr)
@@ -200,43 +239,27 @@ __global__ __launch_bounds__(256) void inv_row_kernel(InvArgs a) {
   float ss = 0.f, zd = 0.f;
 #pragma unroll
   for (int k = 0; k < MAX_PAIRS_PER_LANE; ++k) {
-    const int i = lane + 64 * k;
+    const int i = 4 * lane + k;  // the chunk of 4 pairs of this lane (the vector kernel's order)
     z0[k] = z1[k] = g0[k] = g1[k] = 0.f;
     cs_[k] = 1.f; sn_[k] = 0.f;
     if (i < npairs) {
       const float x0 = load_as_float(a.xr, xr0 + (2 * i) * a.xr_s[3], a.xr_dtype);
       const float x1 = load_as_float(a.xr, xr0 + (2 * i + 1) * a.xr_s[3], a.xr_dtype);
-      if (a.mode == 1) {
-        const float ang = mul_nc(pos, a.freqs[i]);
-        pe_sincos(ang, sn_[k], cs_[k]);
-        z0[k] = sub_nc(mul_nc(x0, cs_[k]), mul_nc(x1, sn_[k])) * a.mscale;
-        z1[k] = add_nc(mul_nc(x0, sn_[k]), mul_nc(x1, cs_[k])) * a.mscale;
-      } else {
-        z0[k] = x0; z1[k] = x1;
-      }
+      rope_pair(a.mode, x0, x1, pos, a.mode == 1 ? a.freqs[i] : 0.f, a.mscale, z0[k], z1[k], sn_[k], cs_[k]);
       g0[k] = a.g[grow + a.Dc + 2 * i];
       g1[k] = a.g[grow + a.Dc + 2 * i + 1];
-      ss += z0[k] * z0[k] + z1[k] * z1[k];
-      zd += z0[k] * g0[k] + z1[k] * g1[k];
+      ss = add_nc(ss, sq2(z0[k], z1[k]));
+      zd = add_nc(zd, dot2(z0[k], z1[k], g0[k], g1[k]));
     }
   }
   float c1 = 1.f, c2 = 0.f;
-  if (a.l2norm) {
-    const float n = sqrtf(wave_sum(ss));
-    zd = wave_sum(zd);
-    const float ne = n + 1e-6f;
-    c1 = 1.f / ne;
-    c2 = n > 0.f ? zd / (n * ne * ne) : 0.f;
-  }
-  const float ms = a.mode == 1 ? a.mscale : 1.f;
+  if (a.l2norm) l2_coefs(wave_sum(ss), wave_sum(zd), c1, c2);
 #pragma unroll
   for (int k = 0; k < MAX_PAIRS_PER_LANE; ++k) {
-    const int i = lane + 64 * k;
+    const int i = 4 * lane + k;
     if (i < npairs) {
-      const float d0 = g0[k] * c1 - z0[k] * c2;
-      const float d1 = g1[k] * c1 - z1[k] * c2;
-      const float dx0v = (d0 * cs_[k] + d1 * sn_[k]) * ms;
-      const float dx1v = (d1 * cs_[k] - d0 * sn_[k]) * ms;
+      float dx0v, dx1v;
+      rope_pair_grad(a.mode, a.l2norm != 0, g0[k], g1[k], z0[k], z1[k], c1, c2, cs_[k], sn_[k], a.mscale, dx0v, dx1v);
       store_from_float(a.dxr, dx0 + (2 * i) * a.dxr_s[3], a.dxr_dtype, dx0v);
       store_from_float(a.dxr, dx0 + (2 * i + 1) * a.dxr_s[3], a.dxr_dtype, dx1v);
     }
@@ -448,8 +471,134 @@ __global__ __launch_bounds__(256) void prebwd_vec_kernel(PreBwdArgs a, int lg_tp
   }
 }
 
+// RoPE / no-PE prologue and its gradient, vector form: thread t of a row owns elements 8t .. 8t + 7
+// of the positional part (the chunk of pairs 4t .. 4t + 3, as lane t of prep_kernel / inv_row_kernel
+// does), TPR = Dr / 8 threads per row, a power of two up to 64, so that a row's threads sit in one
+// wave and exit together.  16-byte loads and stores in any element type; QKNorm's row sums are the
+// chunks' sums added by an xor butterfly over the row's threads.  Same per-element arithmetic and
+// summation order as the scalar kernels: bitwise equal rows.
+__global__ __launch_bounds__(256) void prep_rope_vec_kernel(PrepArgs a, int lg_tpr) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int tpr = 1 << lg_tpr;
+  const int64_t row = gid >> lg_tpr;
+  const int t = (int)(gid & (tpr - 1));
+  if (row >= (int64_t)a.B * a.H * a.S) return;
+  const int s = (int)(row % a.S);
+  const int bh = (int)(row / a.S);
+  const int h = bh % a.H, b = bh / a.H;
+  const float pos = pe_pos(a.start_pos + s, a.pos_round);
+  const int64_t drow = ((int64_t)bh * (a.dst_rows ? a.dst_rows : a.S) + a.dst_row0 + s) * a.width;
+  float x[8], y[8];
+  load8(a.xr, b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + t * 8, a.xr_dtype, x);
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float sn, cs;
+    rope_pair(a.mode, x[2 * k], x[2 * k + 1], pos, a.mode == 1 ? a.freqs[4 * t + k] : 0.f, a.mscale, y[2 * k],
+              y[2 * k + 1], sn, cs);
+    ss = add_nc(ss, sq2(y[2 * k], y[2 * k + 1]));
+  }
+  if (a.l2norm) {
+    for (int m = tpr >> 1; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    const float den = sqrtf(ss) + 1e-6f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = y[e] / den;
+  }
+  store8(a.dst, drow + a.Dc + t * 8, a.dst_dtype, y);
+  if (a.Dc > 0) {
+    const int64_t xc0 = b * a.xc_s[0] + h * a.xc_s[1] + (int64_t)s * a.xc_s[2];
+    for (int j = t; j < a.Dc / 8; j += tpr) {
+      float c[8];
+      load8(a.xc, xc0 + j * 8, a.xc_dtype, c);
+      store8(a.dst, drow + j * 8, a.dst_dtype, c);
+    }
+  }
+  const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = (a.Dc + a.Dr) / 8 + t; j < a.width / 8; j += tpr) store8(a.dst, drow + j * 8, a.dst_dtype, zero);
+}
+
+__global__ __launch_bounds__(256) void inv_rope_vec_kernel(InvArgs a, int lg_tpr) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int tpr = 1 << lg_tpr;
+  const int64_t row = gid >> lg_tpr;
+  const int t = (int)(gid & (tpr - 1));
+  if (row >= (int64_t)a.B * a.H * a.S) return;
+  const int s = (int)(row % a.S);
+  const int bh = (int)(row / a.S);
+  const int h = bh % a.H, b = bh / a.H;
+  const float pos = pe_pos(a.start_pos + s, a.pos_round);
+  const float* grow = a.g + row * a.width;
+  if (a.Dc > 0) {
+    const int64_t dc0 = b * a.dxc_s[0] + h * a.dxc_s[1] + (int64_t)s * a.dxc_s[2];
+    for (int j = t; j < a.Dc / 8; j += tpr) {
+      float c[8];
+      load8(grow, j * 8, 1, c);
+      store8(a.dxc, dc0 + j * 8, a.dxc_dtype, c);
+    }
+  }
+  float x[8], gv[8], z[8], sn[4], cs[4];
+  load8(a.xr, b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + t * 8, a.xr_dtype, x);
+  load8(grow, a.Dc + t * 8, 1, gv);
+  float ss = 0.f, zd = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    rope_pair(a.mode, x[2 * k], x[2 * k + 1], pos, a.mode == 1 ? a.freqs[4 * t + k] : 0.f, a.mscale, z[2 * k],
+              z[2 * k + 1], sn[k], cs[k]);
+    ss = add_nc(ss, sq2(z[2 * k], z[2 * k + 1]));
+    zd = add_nc(zd, dot2(z[2 * k], z[2 * k + 1], gv[2 * k], gv[2 * k + 1]));
+  }
+  float c1 = 1.f, c2 = 0.f;
+  if (a.l2norm) {
+    for (int m = tpr >> 1; m >= 1; m >>= 1) {
+      ss += __shfl_xor(ss, m, 64);
+      zd += __shfl_xor(zd, m, 64);
+    }
+    l2_coefs(ss, zd, c1, c2);
+  }
+  float dx[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    rope_pair_grad(a.mode, a.l2norm != 0, gv[2 * k], gv[2 * k + 1], z[2 * k], z[2 * k + 1], c1, c2, cs[k], sn[k],
+                   a.mscale, dx[2 * k], dx[2 * k + 1]);
+  store8(a.dxr, b * a.dxr_s[0] + h * a.dxr_s[1] + (int64_t)s * a.dxr_s[2] + t * 8, a.dxr_dtype, dx);
+}
+
 bool aligned16(const void* p, int64_t s0, int64_t s1, int64_t s2) {
   return ((uintptr_t)p % 16) == 0 && s0 % 8 == 0 && s1 % 8 == 0 && s2 % 8 == 0;
+}
+
+// rows of a view that 16-byte accesses of 8 elements can read: unit inner stride, every row start
+// 16-byte aligned for the element type (dtype 1 = fp32, else 16-bit)
+static bool rows16(const void* p, int dtype, const int64_t (&st)[4]) {
+  const int64_t e = dtype == 1 ? 4 : 2;
+  return p && st[3] == 1 && ((uintptr_t)p % 16) == 0 && (st[0] * e) % 16 == 0 && (st[1] * e) % 16 == 0 &&
+         (st[2] * e) % 16 == 0;
+}
+
+// log2 of the vector RoPE / no-PE kernels' threads per row (Dr / 8, a power of two up to 64), or -1
+static int rope_vec_lg(int mode, int Dr, int Dc) {
+  if ((mode != 1 && mode != 2) || Dr <= 0 || Dr % 8 != 0 || Dc % 8 != 0 || Dr > 512) return -1;
+  const int tpr = Dr / 8;
+  if (tpr & (tpr - 1)) return -1;
+  int lg = 0;
+  while ((1 << lg) < tpr) ++lg;
+  return lg;
+}
+
+static int prep_rope_vec_lg(const PrepArgs& a) {
+  const int lg = rope_vec_lg(a.mode, a.Dr, a.Dc);
+  if (lg < 0 || a.cdst || a.width % 8 != 0 || ((uintptr_t)a.dst % 16) != 0 || !rows16(a.xr, a.xr_dtype, a.xr_s) ||
+      (a.Dc > 0 && !rows16(a.xc, a.xc_dtype, a.xc_s)))
+    return -1;
+  return lg;
+}
+
+static int inv_rope_vec_lg(const InvArgs& a) {
+  const int lg = rope_vec_lg(a.mode, a.Dr, a.Dc);
+  if (lg < 0 || a.width % 4 != 0 || ((uintptr_t)a.g % 16) != 0 || !rows16(a.xr, a.xr_dtype, a.xr_s) ||
+      !rows16(a.dxr, a.dxr_dtype, a.dxr_s) || (a.Dc > 0 && !rows16(a.dxc, a.dxc_dtype, a.dxc_s)))
+    return -1;
+  return lg;
 }
 
 static bool prep_vec_ok(const PrepArgs& a) {
@@ -481,6 +630,9 @@ int launch_prep(const PrepArgs& a, hipStream_t s) {
   } else if (vec) {
     const int64_t nthr = nrows * (a.Dr / 8);
     hipLaunchKernelGGL(prep_pope_vec_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, a);
+  } else if (const int lg = prep_rope_vec_lg(a); lg >= 0) {
+    const int64_t nthr = nrows << lg;
+    hipLaunchKernelGGL(prep_rope_vec_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, a, lg);
   } else {
     hipLaunchKernelGGL(prep_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
   }
@@ -590,7 +742,10 @@ int launch_inv(const InvArgs& a, int* nblocks_out, hipStream_t s) {
   } else {
     if (nblocks_out) *nblocks_out = 0;
     const int64_t nrows = (int64_t)a.B * a.H * a.S;
-    hipLaunchKernelGGL(inv_row_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+    if (const int lg = inv_rope_vec_lg(a); lg >= 0)
+      hipLaunchKernelGGL(inv_rope_vec_kernel, dim3((unsigned)(((nrows << lg) + 255) / 256)), dim3(256), 0, s, a, lg);
+    else
+      hipLaunchKernelGGL(inv_row_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
   }
   return hipGetLastError() == hipSuccess ? 0 : -7;
 }

@@ -219,6 +219,44 @@ def test_nope_qknorm(cuda):
     run_case(cuda, mode="none", Dr=64, Dv=64, Hq=4, Hkv=4, Sq=96, qk_norm=True, scale=1 / 8, seed=120)
 
 
+@pytest.mark.parametrize("mode,Dr,qk_norm,dtype,mscale", [
+    ("rope", 64, True, torch.bfloat16, 1.0),
+    ("rope", 128, False, torch.bfloat16, 1.25),
+    ("rope", 32, True, torch.float16, 1.0),
+    ("rope", 64, True, torch.float32, 1.0),
+    ("none", 64, True, torch.bfloat16, 1.0),
+    ("none", 128, False, torch.bfloat16, 1.0)])
+def test_rope_vector_prologue_matches_row_kernels(cuda, mode, Dr, qk_norm, dtype, mscale):
+    """RoPE / no-PE operands whose rows take 16-byte accesses go through the vectorised prologue and
+    gradient kernels (8 elements per thread); q and k views that start one element off alignment go
+    through the one-wave-per-row kernels.  Both evaluate the same per-pair arithmetic and add
+    QKNorm's row sums in the same order (chunks of 4 pairs, then an xor butterfly over the chunks),
+    so the outputs and every gradient agree bit for bit."""
+    B, Hq, Hkv, S, Dv = 2, 4, 2, 300, 64
+    g = torch.Generator().manual_seed(130 + Dr)
+    mk = lambda h, d: torch.randn(B, h, S, d, generator=g).to(dtype)
+    q, k, v, do = mk(Hq, Dr), mk(Hkv, Dr), mk(Hkv, Dv), mk(Hq, Dv)
+    freqs = O.rope_inv_freq(Dr).to(cuda) if mode == "rope" else None
+
+    def off(t):  # the same values in a view one element past a 16-byte boundary
+        wide = torch.zeros(*t.shape[:-1], t.shape[-1] + 1, dtype=t.dtype, device=cuda)
+        wide[..., 1:] = t.to(cuda)
+        return wide[..., 1:]
+
+    def run(unaligned):
+        qv, kv = (off(q), off(k)) if unaligned else (q.to(cuda), k.to(cuda))
+        leaves = [qv.requires_grad_(True), kv.requires_grad_(True), v.to(cuda).requires_grad_(True)]
+        out = pe_attention(*leaves, mode=mode, freqs=freqs, qk_norm=qk_norm, rope_mscale=mscale,
+                           scale=Dr ** -0.5)
+        grads = torch.autograd.grad(out, leaves, do.to(cuda))
+        torch.cuda.synchronize()
+        return [out] + list(grads)
+
+    vec, rows = run(False), run(True)
+    for n, a, b in zip(["out", "dq", "dk", "dv"], vec, rows):
+        assert torch.equal(a, b), (mode, Dr, n, md(a, b))
+
+
 # ------------------------------------------------------------- FoPE positions in the input dtype
 
 def test_fope_positions_bf16_fused(cuda):
