@@ -1749,7 +1749,8 @@ static int run_bwd(int which, const CoreArgs& a, hipStream_t s) {
     if (which == 0) {
       const int nkb = (a.Sk + NW * 32 - 1) / (NW * 32);
       if constexpr ((DQK == 128 || DQK == 256) && (DV == 128 || DV == 64)) {
-        // two waves per SIMD (role-split pairs); the one-wave kernel serves the other widths
+        // two waves per SIMD (role-split pairs); the one-wave kernel serves the other widths (at QK
+        // width 64 / V width 64 the pair kernel with 64-query tiles measured 2 % slower)
         // 64-query tiles where they fit the LDS (QK width 128, V width 64: the ~125M GPT shape and the
         // split training form), which halves the per-step barriers and waits per product; on fp16
         // operands the fp32 P exchange of 64-query tiles would not fit (162 KiB), so 32-query tiles
