@@ -99,6 +99,12 @@ ATTN_WORKLOADS = {
                    name="PoPE attention fwd+bwd with an explicit key-padding mask (not causal)",
                    metric="masked PoPE attn fwd+bwd TFLOP/s @B=2,H=16,S=4096,D=128, key-padding mask; "
                           "% of bf16 MFMA peak"),
+    # the ablation's RoPE arm: the reference's GroupedQueryAttention (interleaved RoPE, theta 10000, then
+    # QKNorm, src/model/attention.py:69-96) at the ~125M GPT shape; operands of width Dr, no phase bias
+    "rope": dict(B=8, Hq=12, Hkv=12, S=2048, Dc=0, Dr=64, Dv=64, dtype="bf16", backward=True, delta=None,
+                 mode="rope", qk_norm=True,
+                 name="RoPE + QKNorm causal attention fwd+bwd (GroupedQueryAttention), ~125M GPT shape",
+                 metric="fused RoPE+QKNorm attn fwd+bwd TFLOP/s @B=8,H=12,S=2048,D=64; % of bf16 MFMA peak"),
     "split": dict(B=8, Hq=8, Hkv=4, S=512, Dc=64, Dr=32, Dv=64, dtype="bf16", backward=True, delta="shared",
                   name="split-form PoPE attention fwd+bwd at the reference's training shape "
                        "([content 64 | PoPE 2x32], V 64, GQA 8 -> 4)",
@@ -134,14 +140,19 @@ def flops(B, H, S, D):
     return attn_flops(dict(B=B, Hq=H, S=S, Dc=0, Dr=D, Dv=D))
 
 
+def qk_width(w: dict) -> int:
+    """Width of the transformed q / k rows: content plus 2*Dr for PoPE, plus Dr for RoPE."""
+    return w["Dc"] + (w["Dr"] if w.get("mode", "pope") == "rope" else 2 * w["Dr"])
+
+
 def attn_flops(w: dict) -> dict:
-    """Algorithmic FLOPs of causal attention over transformed operands of width Wqk = Dc + 2*Dr and
-    values of width Dv, with B*Hq*S^2/2 query-key pairs (B*Hq*S^2 without the causal mask): forward
+    """Algorithmic FLOPs of causal attention over transformed operands of width Wqk (qk_width: Dc + 2*Dr
+    for PoPE, Dr for RoPE) and values of width Dv, with B*Hq*S^2/2 query-key pairs (B*Hq*S^2 without the causal mask): forward
     S~ (Wqk) + PV (Dv); backward S~
     recompute (Wqk), dP (Dv), dV (Dv), dK~ (Wqk) and dQ~ (Wqk).  At Dc = 0, Dr = Dv = D this is
     3, 8 and 11 * B*H*S^2*D."""
     pairs = w["B"] * w["Hq"] * w["S"] * w["S"] * (0.5 if w.get("causal", True) else 1.0)
-    wqk, dv = w["Dc"] + 2 * w["Dr"], w["Dv"]
+    wqk, dv = qk_width(w), w["Dv"]
     return {
         "fwd": 2.0 * pairs * (wqk + dv),
         "bwd": 2.0 * pairs * (3 * wqk + 2 * dv),
@@ -157,10 +168,10 @@ def attn_flops(w: dict) -> dict:
 
 def prologue_bytes(w: dict) -> int:
     """Algorithmic HBM bytes of the forward's PE prologue: read the raw q and k rows (content and
-    positional parts), write the transformed rows of width Dc + 2*Dr."""
+    positional parts), write the transformed rows of width qk_width (Dc + 2*Dr for PoPE, Dr for RoPE)."""
     es = 4 if w["dtype"] == "fp32" else 2
     rows = w["B"] * (w["Hq"] + w["Hkv"]) * w["S"]
-    return rows * (w["Dc"] + w["Dr"]) * es + rows * (w["Dc"] + 2 * w["Dr"]) * es
+    return rows * (w["Dc"] + w["Dr"]) * es + rows * qk_width(w) * es
 
 
 def cpu_model() -> str:
@@ -227,10 +238,11 @@ def cpu_baseline(w: dict, heads: int, reps: int):
     qc = torch.randn(1, heads, S, Dc, generator=g).requires_grad_(backward) if Dc else None
     kc = torch.randn(1, hkv, S, Dc, generator=g).requires_grad_(backward) if Dc else None
     dO = torch.randn(1, heads, S, Dv, generator=g)
+    rope = w.get("mode", "pope") == "rope"
     dshape = (hkv, Dr) if w["delta"] == "head" else (Dr,)
-    delta = (torch.rand(*dshape, generator=g) * (-2 * math.pi)).requires_grad_(backward)
+    delta = None if rope else (torch.rand(*dshape, generator=g) * (-2 * math.pi)).requires_grad_(backward)
     fm = fope_module(torch, w, Dr) if w.get("fope") else None
-    freqs = None if fm else O.pope_freqs(Dr)
+    freqs = O.rope_inv_freq(Dr) if rope else (None if fm else O.pope_freqs(Dr))
     scale = 1.0 / math.sqrt(Dc + 2 * Dr) if Dc else 1.0 / math.sqrt(Dr)
     leaves = [t for t in (qr, kr, v, qc, kc, delta) if t is not None]
     if fm is not None:
@@ -246,7 +258,10 @@ def cpu_baseline(w: dict, heads: int, reps: int):
         with torch.set_grad_enabled(backward):
             f = freqs if fm is None else O.fope_effective_freqs(
                 fm.base_freqs, fm.fourier_coeffs, freq_table=fm.freq_table, training_length=fm.training_length)
-            if Dc:
+            if rope:
+                out, _ = O.rope_attention(qr, kr, v, f, qk_norm=w.get("qk_norm", False), causal=causal, scale=scale,
+                                          core=functools.partial(O.attention, dtype=torch.float32))
+            elif Dc:
                 out, _ = O.split_pope_attention(qc, kc, qr, kr, v, f, delta, scale=scale, causal=causal,
                                                 core_dtype=torch.float32, core=core)
             else:
@@ -261,7 +276,7 @@ def cpu_baseline(w: dict, heads: int, reps: int):
     dt = times[len(times) // 2]
     f = attn_flops(dict(w, B=1, Hq=heads))["total" if backward else "fwd"]
     what = "fwd+bwd" if backward else "fwd"
-    fn = "split_pope_attention" if Dc else "pope_attention"
+    fn = "rope_attention" if rope else ("split_pope_attention" if Dc else "pope_attention")
     return {
         "value": f / dt / 1e12,
         "unit": "TFLOP/s",
@@ -408,10 +423,12 @@ def run_attention(args, torch, dev, wname: str) -> dict:
     q, k, v = rnd(Hq, Dr), rnd(Hkv, Dr), rnd(Hkv, Dv)
     qc, kc = (rnd(Hq, Dc), rnd(Hkv, Dc)) if Dc else (None, None)
     dO = torch.randn(B, Hq, S, Dv, generator=g, device=dev).to(dt)
+    mode = w.get("mode", "pope")
     dshape = (Hkv, Dr) if w["delta"] == "head" else (Dr,)
-    delta = (torch.rand(*dshape, generator=g, device=dev) * (-2 * math.pi)).requires_grad_(backward)
+    delta = None if mode == "rope" else (torch.rand(*dshape, generator=g, device=dev) * (-2 * math.pi)).requires_grad_(backward)
     fm = fope_module(torch, w, Dr).to(dev) if w.get("fope") else None
-    freqs = (10000.0 ** (-(torch.arange(0, Dr, dtype=torch.float32) / Dr))).to(dev)
+    # PoPE: one frequency per dim; RoPE: one inverse frequency per interleaved pair
+    freqs = (10000.0 ** (-(torch.arange(0, Dr, 2 if mode == "rope" else 1, dtype=torch.float32) / Dr))).to(dev)
     scale = 1.0 / math.sqrt(Dc + 2 * Dr) if Dc else 1.0 / math.sqrt(Dr)
     leaves = [t for t in (q, k, v, qc, kc, delta) if t is not None]
     if fm is not None:
@@ -422,8 +439,8 @@ def run_attention(args, torch, dev, wname: str) -> dict:
 
     def attn():
         f = freqs if fm is None else fm.kernel_freqs()
-        return pe_attention(q, k, v, mode="pope", q_c=qc, k_c=kc, freqs=f, delta=delta, scale=scale,
-                            causal=causal, mask=mask)
+        return pe_attention(q, k, v, mode=mode, q_c=qc, k_c=kc, freqs=f, delta=delta, scale=scale,
+                            causal=causal, mask=mask, qk_norm=w.get("qk_norm", False))
 
     if backward:
         def step():
@@ -469,9 +486,13 @@ def run_attention(args, torch, dev, wname: str) -> dict:
     if mask is not None:
         config.update(mask="bool key padding (B, 1, 1, S), batch entry b keeps its first S - 100 b keys",
                       causal=False)
-    config.update(delta="per-head (Hkv, Dr)" if w["delta"] == "head" else "shared (Dr,)",
-                  grads=("q,k,v,delta" + (",q_c,k_c" if Dc else "") + (",fourier_coeffs" if fm else ""))
-                  if backward else "none", parallelism="single GPU")
+    if mode == "rope":
+        config.update(pe="RoPE (interleaved pairs, theta 10000) + QKNorm" if w.get("qk_norm") else "RoPE",
+                      grads="q,k,v" if backward else "none", parallelism="single GPU")
+    else:
+        config.update(delta="per-head (Hkv, Dr)" if w["delta"] == "head" else "shared (Dr,)",
+                      grads=("q,k,v,delta" + (",q_c,k_c" if Dc else "") + (",fourier_coeffs" if fm else ""))
+                      if backward else "none", parallelism="single GPU")
     if fm is not None:
         config["fope"] = {"M": w["fope"][0], "coeff_sigma": w["fope"][1], "training_length": w["fope"][2]}
     if getattr(args, "graph", False):
@@ -488,7 +509,7 @@ def run_attention(args, torch, dev, wname: str) -> dict:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": w["dtype"],
-        "data": "synthetic (seeded N(0,1) q/k/v/dO, delta ~ U(-2pi,0))",
+        "data": "synthetic (seeded N(0,1) q/k/v/dO" + (")" if mode == "rope" else ", delta ~ U(-2pi,0))"),
         "config": config,
         "frac_of_peak": round(value / peak, 4),
         "fa_convention_tflops": round((F["fa_convention"] if backward else 2.0 * F["fa_convention"] / 7.0)
@@ -728,10 +749,10 @@ def decode_cpu_baseline(torch) -> dict:
 # (timed steps, warm-up steps) per workload: about half a second of untimed work, and timed work
 # well under a minute
 # query heads of one batch entry in the CPU baseline's sample (about 10-30 s of CPU work)
-CPU_HEADS = {"fwdbwd": 2, "fwd": 2, "fwd32": 2, "c2": 12, "c3": 16, "split": 8, "masked": 4}
-CPU_REPS = {"c2": 40, "c3": 10, "fwd32": 12, "split": 1000, "masked": 4}
+CPU_HEADS = {"fwdbwd": 2, "fwd": 2, "fwd32": 2, "c2": 12, "c3": 16, "split": 8, "masked": 4, "rope": 12}
+CPU_REPS = {"c2": 40, "c3": 10, "fwd32": 12, "split": 1000, "masked": 4, "rope": 40}
 DEFAULT_STEPS = {"fwdbwd": (50, 100), "fwd": (100, 400), "fwd32": (10, 40), "c2": (200, 600), "c3": (100, 250),
-                 "split": (500, 2000), "masked": (50, 150), "decoder": (5, 4), "decode": (200, 200)}
+                 "split": (500, 2000), "masked": (50, 150), "rope": (200, 600), "decoder": (5, 4), "decode": (200, 200)}
 
 
 def main() -> int:

@@ -61,12 +61,18 @@ def test_workload_flops_and_prologue_bytes():
     assert Fs["bwd"] == 2 * pairs * (3 * 128 + 2 * 64)
     assert bench.prologue_bytes(sp) == 8 * (8 + 4) * 512 * ((64 + 32) + (64 + 64)) * 2
     assert bench.prologue_bytes(bench.ATTN_WORKLOADS["fwd32"]) == 2 * bench.prologue_bytes(w)
+    # RoPE: operands keep their width (64), so the C2-shape RoPE step is 7 * B*H*S^2*D / 2 per causal pair
+    rw = bench.ATTN_WORKLOADS["rope"]
+    Fr = bench.attn_flops(rw)
+    rbase = 8 * 12 * 2048 ** 2 * 64
+    assert (Fr["fwd"], Fr["total"]) == (2 * rbase, 7 * rbase)
+    assert bench.prologue_bytes(rw) == 8 * 24 * 2048 * (64 + 64) * 2
 
 
 def test_cpu_baseline_runs_every_form():
     """The cpu_baseline leg on tiny copies of the workloads (fused, FoPE, split form with GQA)."""
     bench = _bench()
-    for name in ("fwdbwd", "c3", "split", "fwd"):
+    for name in ("fwdbwd", "c3", "split", "fwd", "rope"):
         w = dict(bench.ATTN_WORKLOADS[name], S=64)
         cb = bench.cpu_baseline(w, heads=2, reps=1)
         assert cb["value"] > 0 and cb["kind"] == "port" and cb["cores"] >= 1 and cb["cpu"]
