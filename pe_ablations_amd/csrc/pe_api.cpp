@@ -831,7 +831,28 @@ static int bwd_impl(const pe_attn_params* p, const pe_tensor_t* qc, const pe_ten
   // inverse PoPE transform in their epilogues
   const bool split = !gm && fused_split_bwd(p, qr, kr, dqc, dqr, dkc, dkr);
   const bool fuse = (!gm && fused_bwd(p)) || split;
+  // RoPE / no-PE (QKNorm included) at transformed width 64, the reference's head width, with vector
+  // views: the dQ GEMM and the dK/dV kernel apply the gradient in their epilogues instead of the
+  // stand-alone kernels below (the workspace still reserves dq~ / dk~: alignment is a call-time fact)
+  const bool rfuse = !gm && half_dt(dt) && (p->mode == PE_MODE_ROPE || p->mode == PE_MODE_NONE) && p->Dc == 0 &&
+                     p->Dr == 64 && L.dqk == 64 && vec16(qr) && vec16(kr) && vec16(dqr) && vec16(dkr);
   const int nqg = (p->Sq + 255) / 256, nkg = (p->Sk + 127) / 128;
+  auto view = [p](pe::EpiPoPE& e, const pe_tensor_t* x, const pe_tensor_t* dx, int start) {
+    e.x = x->data; e.x_dtype = x->dtype;
+    e.dx = (void*)dx->data; e.dx_dtype = dx->dtype;
+    for (int i = 0; i < 4; ++i) { e.x_s[i] = x->stride[i]; e.dx_s[i] = dx->stride[i]; }
+    e.start_pos = start;
+    e.pos_round = p->position_rounding;
+  };
+  if (rfuse) {
+    c.rope_fuse = 1;
+    c.rope_mode = p->mode;
+    c.rope_l2 = p->qk_l2norm;
+    c.rope_ms = p->rope_mscale;
+    c.freqs = freqs;
+    view(c.eq, qr, dqr, p->start_pos_q);
+    view(c.ek, kr, dkr, p->start_pos_k);
+  }
   if (fuse) {
     c.fuse_inv = 1;
     c.Dr = p->Dr;
@@ -839,13 +860,6 @@ static int bwd_impl(const pe_attn_params* p, const pe_tensor_t* qc, const pe_ten
     c.freqs = freqs;
     c.delta = delta;
     c.delta_hs = p->delta_head_stride;
-    auto view = [p](pe::EpiPoPE& e, const pe_tensor_t* x, const pe_tensor_t* dx, int start) {
-      e.x = x->data; e.x_dtype = x->dtype;
-      e.dx = (void*)dx->data; e.dx_dtype = dx->dtype;
-      for (int i = 0; i < 4; ++i) { e.x_s[i] = x->stride[i]; e.dx_s[i] = dx->stride[i]; }
-      e.start_pos = start;
-      e.pos_round = p->position_rounding;
-    };
     view(c.eq, qr, dqr, p->start_pos_q);
     view(c.ek, kr, dkr, p->start_pos_k);
     if (split) {
@@ -881,7 +895,7 @@ static int bwd_impl(const pe_attn_params* p, const pe_tensor_t* qc, const pe_ten
   stage_mark(PE_STAGE_BWD_DQ, 1, s);
   stage_mark(PE_STAGE_BWD_INV, 0, s);
 
-  for (int side = 0; side < 2 && !fuse; ++side) {
+  for (int side = 0; side < 2 && !fuse && !rfuse; ++side) {
     const bool key = side == 1;
     const pe_tensor_t* xr = key ? kr : qr;
     const pe_tensor_t* dxc = key ? dkc : dqc;

@@ -324,6 +324,37 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_kernel(CoreArgs a) {
 // `kd` = key - off - (first row of the tile) - 8*g; returns true where the key is masked.
 __device__ __forceinline__ bool masked_row(int kd, int j) { return kd > ((j >> 3) << 4) + (j & 7); }
 
+// Fused RoPE / no-PE gradient (CoreArgs::rope_fuse) of NR rows, sequence indices base .. base + NR - 1
+// (valid below nidx) of head h of batch b.  `stage` leaves the scaled dq~ or dk~ rows in st as fp32
+// [NR][64] (barriers included).  8 of the NT threads per row, thread t taking the chunk of pairs
+// 4t .. 4t + 3, with the stand-alone inv_rope_vec_kernel's arithmetic (inv_rope_chunk), so dq / dk
+// are bitwise its results.  (Loading every row's x chunk before `stage`, so that the load latency is
+// paid once, made the dK/dV kernel 4 % slower.)
+template <int HT, int NT, int NR, typename Stage>
+__device__ __forceinline__ void rope_epi_rows(const CoreArgs& a, const EpiPoPE& e, const float* st, int tid, int base,
+                                              int nidx, int b, int h, Stage&& stage) {
+  stage();
+  const int t = tid & 7;
+  float fr4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) fr4[k] = a.rope_mode == 1 ? a.freqs[4 * t + k] : 0.f;
+  const int64_t xb = b * e.x_s[0] + h * e.x_s[1] + t * 8, db = b * e.dx_s[0] + h * e.dx_s[1] + t * 8;
+  for (int r = tid >> 3; r < NR; r += NT / 8) {
+    const int idx = base + r;
+    if (idx >= nidx) break;  // the same for the row's 8 threads
+    float x[8], gv[8], dx[8];
+    load8t<HT>(e.x, xb + (int64_t)idx * e.x_s[2], e.x_dtype, x);
+    const f32x4 g0 = *(const f32x4*)(st + r * 64 + t * 8), g1 = *(const f32x4*)(st + r * 64 + t * 8 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      gv[j] = g0[j];
+      gv[j + 4] = g1[j];
+    }
+    inv_rope_chunk(a.rope_mode, a.rope_l2 != 0, fr4, pe_pos(e.start_pos + idx, e.pos_round), a.rope_ms, 8, x, gv, dx);
+    store8t<HT>(e.dx, db + (int64_t)idx * e.dx_s[2], e.dx_dtype, dx);
+  }
+}
+
 // dK~/dV: a workgroup owns 32*NW keys of one kv head; wave w keeps k~ and v of its 32 keys as MFMA
 // B operands in registers and walks every visible 64-query tile of every query head of its GQA
 // group.  LDS ring of 3 stages (q~ 64 x DQK, dO 64 x DV, the rows' log2 lse and Di): the tile being
@@ -584,7 +615,22 @@ __global__ __launch_bounds__(NW * 64, 1) void dkdv_bf16_kernel(CoreArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  if (a.fuse_inv) {
+  if (DQK == 64 && a.rope_fuse) {
+    if constexpr (DQK == 64) {
+      // RoPE / no-PE gradient: the scaled dk~ rows of the block's keys go through LDS (the ring is
+      // free once every wave has passed the barrier), 8 threads per row
+      static_assert(NSTAGE * STAGE >= BNK * 64 * 4, "staged dk~ rows fit the ring");
+      float* st = (float*)smem;  // [BNK keys][64]
+      rope_epi_rows<HT, NW * 64, BNK>(a, a.ek, st, tid, k0, a.Sk, b, hk, [&] {
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NDK; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) st[(w * 32 + c_row(j, g)) * DQK + t * 32 + l32] = dk[t][j] * a.scale;
+        __syncthreads();
+      });
+    }
+  } else if (a.fuse_inv) {
     // inverse PoPE transform: the scaled dk~ rows go through LDS (the ring is free now) so that
     // one plain loop applies the transform, a fixed dim c per thread; dk is written through the
     // caller's view and dphi / pos*dphi are summed per block in a fixed order
@@ -1696,6 +1742,26 @@ __global__ __launch_bounds__(NW * 64, 1) void dq_gemm_kernel(CoreArgs a) {
           e.part_freq[blk * Dr + tid] = f0;
         }
       }
+      return;
+    }
+  }
+  if constexpr (DQK == 64) {
+    if (a.rope_fuse) {
+      // RoPE / no-PE gradient: the scaled dq~ rows of the block's 256 queries go through LDS (the
+      // ring is free once every wave has passed the barrier), 8 threads per row
+      static_assert(SMEM >= 256 * 64 * 4, "staged dq~ rows fit the ring");
+      float* st = (float*)smem;  // [256 queries][64]
+      rope_epi_rows<HT, NW * 64, 256>(a, a.eq, st, tid, q0, a.Sq, b, h, [&] {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < QT; ++i)
+#pragma unroll
+          for (int t = 0; t < NTH; ++t)
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+              st[(qp * QT * 32 + i * 32 + c_row(j, g)) * DQK + ctile(t, dh) * 32 + l32] = acc[i][t][j] * a.scale;
+        __syncthreads();
+      });
       return;
     }
   }

@@ -711,6 +711,79 @@ __device__ __forceinline__ float inv_pope_elem(float x, float pos, float freq, f
   return inv_pope_elem_cs(x, sn, cs, gc, gs, dx);
 }
 
+// RoPE (mode 1) or no-PE (mode 2) forward of one pair (x0, x1) of a row, src/model/rope.py:35-57:
+// y = mscale * (x0 cos - x1 sin, x0 sin + x1 cos) at angle fl(pos * inv_freq), or y = x; each product
+// and sum rounded on its own, as torch's ops round them.  cs / sn are kept for the gradient.
+__device__ __forceinline__ void rope_pair(int mode, float x0, float x1, float pos, float fr, float ms, float& y0,
+                                          float& y1, float& sn, float& cs) {
+  if (mode == 1) {
+    pe_sincos(mul_nc(pos, fr), sn, cs);
+    y0 = sub_nc(mul_nc(x0, cs), mul_nc(x1, sn)) * ms;
+    y1 = add_nc(mul_nc(x0, sn), mul_nc(x1, cs)) * ms;
+  } else {
+    sn = 0.f; cs = 1.f;
+    y0 = x0; y1 = x1;
+  }
+}
+__device__ __forceinline__ float sq2(float a, float b) { return add_nc(mul_nc(a, a), mul_nc(b, b)); }
+__device__ __forceinline__ float dot2(float a0, float a1, float b0, float b1) {
+  return add_nc(mul_nc(a0, b0), mul_nc(a1, b1));
+}
+// Gradient of one pair through QKNorm (y = z / (||z|| + 1e-6), src/model/normalization.py:54-55) and
+// the rotation: d = dy c1 - z c2 (d = dy without the norm), dx = mscale * rot^T(d) (dx = d for no-PE)
+__device__ __forceinline__ void rope_pair_grad(int mode, bool l2, float g0, float g1, float z0, float z1, float c1,
+                                               float c2, float cs, float sn, float ms, float& dx0, float& dx1) {
+  float d0 = g0, d1 = g1;
+  if (l2) {
+    d0 = sub_nc(mul_nc(g0, c1), mul_nc(z0, c2));
+    d1 = sub_nc(mul_nc(g1, c1), mul_nc(z1, c2));
+  }
+  if (mode == 1) {
+    dx0 = mul_nc(add_nc(mul_nc(d0, cs), mul_nc(d1, sn)), ms);
+    dx1 = mul_nc(sub_nc(mul_nc(d1, cs), mul_nc(d0, sn)), ms);
+  } else {
+    dx0 = d0; dx1 = d1;
+  }
+}
+// QKNorm's row sums (||z||^2, and z . dy in the gradient): each lane or thread sums the pairs of its
+// chunk of 4 consecutive pairs in order, and the chunks' sums are added by an xor butterfly over the
+// chunks (lanes past the row's chunks hold 0, which leaves every sum unchanged).  The scalar and the
+// vector kernels below both follow this order, so they produce bitwise equal rows.
+__device__ __forceinline__ void l2_coefs(float ss, float zd, float& c1, float& c2) {
+  const float n = sqrtf(ss);
+  const float ne = add_nc(n, 1e-6f);
+  c1 = 1.f / ne;
+  c2 = n > 0.f ? zd / mul_nc(mul_nc(n, ne), ne) : 0.f;
+}
+
+// The gradient of one 8-element chunk (pairs 4t .. 4t + 3) of a RoPE / no-PE row through QKNorm: x
+// the raw inputs, g the gradient of the transformed chunk, fr4 the chunk's 4 inverse frequencies
+// (RoPE), tpr threads per row, adjacent and aligned in the wave (QKNorm's row sums by an xor
+// butterfly over them).  Every thread of a row group must call it together.
+__device__ __forceinline__ void inv_rope_chunk(int mode, bool l2, const float (&fr4)[4], float pos, float ms, int tpr,
+                                               const float (&x)[8], const float (&g)[8], float (&dx)[8]) {
+  float z[8], sn[4], cs[4];
+  float ss = 0.f, zd = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    rope_pair(mode, x[2 * k], x[2 * k + 1], pos, fr4[k], ms, z[2 * k], z[2 * k + 1], sn[k], cs[k]);
+    ss = add_nc(ss, sq2(z[2 * k], z[2 * k + 1]));
+    zd = add_nc(zd, dot2(z[2 * k], z[2 * k + 1], g[2 * k], g[2 * k + 1]));
+  }
+  float c1 = 1.f, c2 = 0.f;
+  if (l2) {
+    for (int m = tpr >> 1; m >= 1; m >>= 1) {
+      ss += __shfl_xor(ss, m, 64);
+      zd += __shfl_xor(zd, m, 64);
+    }
+    l2_coefs(ss, zd, c1, c2);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    rope_pair_grad(mode, l2, g[2 * k], g[2 * k + 1], z[2 * k], z[2 * k + 1], c1, c2, cs[k], sn[k], ms, dx[2 * k],
+                   dx[2 * k + 1]);
+}
+
 // Launch-order remap.  Blocks are issued heaviest first (LPT for the causal triangle) and, when the
 // number of (batch, head) pairs divides by the 8 XCDs, every block of one head lands on the same
 // XCD (hardware dispatch is round-robin over XCDs) so its K/V stays in that XCD's L2.

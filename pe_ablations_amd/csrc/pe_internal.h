@@ -76,6 +76,11 @@ struct CoreArgs {
   int fuse_inv; int Dr; int Dc;
   const float* freqs; const float* delta; int64_t delta_hs;
   EpiPoPE eq, ek;
+  // fused RoPE / no-PE gradient (16-bit compute, transformed width 64, no content part, vector views):
+  // the dQ GEMM and the dK/dV kernel apply the QKNorm and rotation backward of their staged dq~ / dk~
+  // rows and write dq / dk through eq / ek (x, dx, start_pos, pos_round); freqs holds the inverse
+  // frequencies.  rope_mode 1 = RoPE, 2 = no PE; rope_l2 = QKNorm; rope_ms = mscale
+  int rope_fuse, rope_mode, rope_l2; float rope_ms;
   int n_cu;  // compute units of the device: launchers pick smaller blocks when a grid would not fill them
   // backward head group: the gradient kernels cover the (batch, kv head) units bh0 .. bh0 + nbh - 1
   // (flattened b * Hkv + hk) and their query heads; dS holds that group only, indexed from its first

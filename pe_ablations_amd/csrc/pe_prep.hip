@@ -25,51 +25,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 constexpr int MAX_PAIRS_PER_LANE = 4;  // RoPE rows up to 512 dims
 
-// RoPE (mode 1) or no-PE (mode 2) forward of one pair (x0, x1) of a row, src/model/rope.py:35-57:
-// y = mscale * (x0 cos - x1 sin, x0 sin + x1 cos) at angle fl(pos * inv_freq), or y = x; each product
-// and sum rounded on its own, as torch's ops round them.  cs / sn are kept for the gradient.
-__device__ __forceinline__ void rope_pair(int mode, float x0, float x1, float pos, float fr, float ms, float& y0,
-                                          float& y1, float& sn, float& cs) {
-  if (mode == 1) {
-    pe_sincos(mul_nc(pos, fr), sn, cs);
-    y0 = sub_nc(mul_nc(x0, cs), mul_nc(x1, sn)) * ms;
-    y1 = add_nc(mul_nc(x0, sn), mul_nc(x1, cs)) * ms;
-  } else {
-    sn = 0.f; cs = 1.f;
-    y0 = x0; y1 = x1;
-  }
-}
-__device__ __forceinline__ float sq2(float a, float b) { return add_nc(mul_nc(a, a), mul_nc(b, b)); }
-__device__ __forceinline__ float dot2(float a0, float a1, float b0, float b1) {
-  return add_nc(mul_nc(a0, b0), mul_nc(a1, b1));
-}
-// Gradient of one pair through QKNorm (y = z / (||z|| + 1e-6), src/model/normalization.py:54-55) and
-// the rotation: d = dy c1 - z c2 (d = dy without the norm), dx = mscale * rot^T(d) (dx = d for no-PE)
-__device__ __forceinline__ void rope_pair_grad(int mode, bool l2, float g0, float g1, float z0, float z1, float c1,
-                                               float c2, float cs, float sn, float ms, float& dx0, float& dx1) {
-  float d0 = g0, d1 = g1;
-  if (l2) {
-    d0 = sub_nc(mul_nc(g0, c1), mul_nc(z0, c2));
-    d1 = sub_nc(mul_nc(g1, c1), mul_nc(z1, c2));
-  }
-  if (mode == 1) {
-    dx0 = mul_nc(add_nc(mul_nc(d0, cs), mul_nc(d1, sn)), ms);
-    dx1 = mul_nc(sub_nc(mul_nc(d1, cs), mul_nc(d0, sn)), ms);
-  } else {
-    dx0 = d0; dx1 = d1;
-  }
-}
-// QKNorm's row sums (||z||^2, and z . dy in the gradient): each lane or thread sums the pairs of its
-// chunk of 4 consecutive pairs in order, and the chunks' sums are added by an xor butterfly over the
-// chunks (lanes past the row's chunks hold 0, which leaves every sum unchanged).  The scalar and the
-// vector kernels below both follow this order, so they produce bitwise equal rows.
-__device__ __forceinline__ void l2_coefs(float ss, float zd, float& c1, float& c2) {
-  const float n = sqrtf(ss);
-  const float ne = add_nc(n, 1e-6f);
-  c1 = 1.f / ne;
-  c2 = n > 0.f ? zd / mul_nc(mul_nc(n, ne), ne) : 0.f;
-}
-
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -536,30 +491,12 @@ __global__ __launch_bounds__(256) void inv_rope_vec_kernel(InvArgs a, int lg_tpr
       store8(a.dxc, dc0 + j * 8, a.dxc_dtype, c);
     }
   }
-  float x[8], gv[8], z[8], sn[4], cs[4];
+  float x[8], gv[8], dx[8], fr4[4];
   load8(a.xr, b * a.xr_s[0] + h * a.xr_s[1] + (int64_t)s * a.xr_s[2] + t * 8, a.xr_dtype, x);
   load8(grow, a.Dc + t * 8, 1, gv);
-  float ss = 0.f, zd = 0.f;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    rope_pair(a.mode, x[2 * k], x[2 * k + 1], pos, a.mode == 1 ? a.freqs[4 * t + k] : 0.f, a.mscale, z[2 * k],
-              z[2 * k + 1], sn[k], cs[k]);
-    ss = add_nc(ss, sq2(z[2 * k], z[2 * k + 1]));
-    zd = add_nc(zd, dot2(z[2 * k], z[2 * k + 1], gv[2 * k], gv[2 * k + 1]));
-  }
-  float c1 = 1.f, c2 = 0.f;
-  if (a.l2norm) {
-    for (int m = tpr >> 1; m >= 1; m >>= 1) {
-      ss += __shfl_xor(ss, m, 64);
-      zd += __shfl_xor(zd, m, 64);
-    }
-    l2_coefs(ss, zd, c1, c2);
-  }
-  float dx[8];
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    rope_pair_grad(a.mode, a.l2norm != 0, gv[2 * k], gv[2 * k + 1], z[2 * k], z[2 * k + 1], c1, c2, cs[k], sn[k],
-                   a.mscale, dx[2 * k], dx[2 * k + 1]);
+  for (int k = 0; k < 4; ++k) fr4[k] = a.mode == 1 ? a.freqs[4 * t + k] : 0.f;
+  inv_rope_chunk(a.mode, a.l2norm != 0, fr4, pos, a.mscale, tpr, x, gv, dx);
   store8(a.dxr, b * a.dxr_s[0] + h * a.dxr_s[1] + (int64_t)s * a.dxr_s[2] + t * 8, a.dxr_dtype, dx);
 }
 

@@ -223,15 +223,17 @@ def test_nope_qknorm(cuda):
     ("rope", 64, True, torch.bfloat16, 1.0),
     ("rope", 128, False, torch.bfloat16, 1.25),
     ("rope", 32, True, torch.float16, 1.0),
+    ("rope", 64, True, torch.float16, 1.25),
     ("rope", 64, True, torch.float32, 1.0),
     ("none", 64, True, torch.bfloat16, 1.0),
     ("none", 128, False, torch.bfloat16, 1.0)])
 def test_rope_vector_prologue_matches_row_kernels(cuda, mode, Dr, qk_norm, dtype, mscale):
     """RoPE / no-PE operands whose rows take 16-byte accesses go through the vectorised prologue and
-    gradient kernels (8 elements per thread); q and k views that start one element off alignment go
-    through the one-wave-per-row kernels.  Both evaluate the same per-pair arithmetic and add
-    QKNorm's row sums in the same order (chunks of 4 pairs, then an xor butterfly over the chunks),
-    so the outputs and every gradient agree bit for bit."""
+    gradient kernels (8 elements per thread); at width 64 in 16-bit the gradient runs in the dQ GEMM's
+    and the dK/dV kernel's epilogues instead, on their staged rows.  q and k views that start one
+    element off alignment go through the one-wave-per-row kernels.  All of them evaluate the same
+    per-pair arithmetic and add QKNorm's row sums in the same order (chunks of 4 pairs, then an xor
+    butterfly over the chunks), so the outputs and every gradient agree bit for bit."""
     B, Hq, Hkv, S, Dv = 2, 4, 2, 300, 64
     g = torch.Generator().manual_seed(130 + Dr)
     mk = lambda h, d: torch.randn(B, h, S, d, generator=g).to(dtype)
