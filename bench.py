@@ -389,10 +389,14 @@ def prologue_entry(w: dict, ms: float, headline: bool) -> dict:
         try:
             with open(TRAFFIC_FILE) as f:
                 kern = json.load(f).get("kernels", {})
-            # per step: the key transform with the query phase table in one dispatch and the query
-            # transform in another (older summaries: a dispatch per operand and one for the table)
-            parts = ((("prep_vec_and_table_kernel", 1), ("prep_pope_vec_kernel", 1)) if "prep_vec_and_table_kernel" in kern
-                     else (("prep_pope_vec_kernel", 2), ("phase_table_kernel", 1)))
+            # per step: both transforms and the query phase table in one dispatch (older summaries:
+            # the key transform with the table, then the query transform; or one dispatch each)
+            if "prep_k_qheads_kernel" in kern:
+                parts = (("prep_k_qheads_kernel", 1),)
+            elif "prep_vec_and_table_kernel" in kern:
+                parts = (("prep_vec_and_table_kernel", 1), ("prep_pope_vec_kernel", 1))
+            else:
+                parts = (("prep_pope_vec_kernel", 2), ("phase_table_kernel", 1))
             t = 0.0
             for name, per in parts:
                 v = kern[name]

@@ -456,12 +456,14 @@ static int fwd_impl(const pe_attn_params* p, const pe_norm_params* nrm, const pe
     a.norm_w = nrm->k_weight; a.norm_w_dtype = nrm->weight_dtype; a.norm_eps = nrm->eps;
     if ((rc = pe::launch_prep_norm(a, s))) return rc;
   } else {
-    // small shapes: both sides in one launch; else keys first, with the query phase table in the
-    // same launch, and the queries, which read the table, after it
+    // small shapes: both sides in one launch; larger ones without a content part: both sides in
+    // one launch with each query phase evaluated once for several heads; else keys first, with the
+    // query phase table in the same launch, and the queries, which read the table, after it
     fill_prep(a, p, 1, kc, kr, freqs, delta, ws + L.k_off, L.dqk);
     pe::PrepArgs aq;
     fill_prep(aq, p, 0, qc, qr, freqs, nullptr, ws + L.q_off, L.dqk);
     rc = qtab ? pe::launch_prep_qk(a, aq, qtab, s) : 1;
+    if (rc == 1 && qtab) rc = pe::launch_prep_k_qheads(a, aq, qtab, s);
     if (rc == 1) {
       if (qtab) rc = pe::launch_prep_and_table(a, freqs, p->start_pos_q, p->Sq, p->Dr, p->position_rounding, qtab, s);
       else rc = pe::launch_prep(a, s);

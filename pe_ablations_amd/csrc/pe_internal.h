@@ -156,6 +156,10 @@ int launch_prep_and_table(const PrepArgs& a, const float* freqs, int start, int 
 // without launching when the shape or layout does not qualify (the caller then takes the two-launch
 // path)
 int launch_prep_qk(const PrepArgs& ak, const PrepArgs& aq, float* tab, hipStream_t s);
+// both sides of a larger vectorised PoPE prologue in one launch (ak: keys; aq: queries without a
+// content part or padding, aq.tab null): query threads evaluate each phase once for several heads
+// and the rows of b = 0 write tab; returns 1 without launching when the layout does not qualify
+int launch_prep_k_qheads(const PrepArgs& ak, const PrepArgs& aq, float* tab, hipStream_t s);
 // PoPE prologue with the RMSNorm fused in: one workgroup per token (all heads)
 int launch_prep_norm(const PrepArgs& a, hipStream_t s);
 

@@ -608,9 +608,89 @@ __global__ __launch_bounds__(256) void prep_qk_vec_kernel(PrepArgs ak, PrepArgs 
   else prep_pope_vec_body(aq, (int64_t)(blockIdx.x - nkblk) * 256 + threadIdx.x, tab);
 }
 
+// Query rows without a content part or padding, QHG heads per thread: thread (b, head group, s,
+// chunk t) evaluates the sin / cos of its 8 phases fl(pos * freq) once, then transforms chunk t of
+// the rows (b, h, s) of the group's heads, whose x chunks it loads up front.  A query phase does
+// not depend on the head, so the table (cos row then sin row per position) that the dQ epilogue
+// reads is written by the threads of (b, group) = (0, 0), and no table read sits on this path.
+// Per element the arithmetic is prep_pope_vec_body's, so the rows and the table are bitwise those
+// of the table launch plus the table-reading query launch.
+constexpr int QHG = 8;
+__device__ __forceinline__ void prep_pope_qheads_body(const PrepArgs& a, int64_t gid, float* tab) {
+  const int tpr = a.Dr >> 3, ngrp = (a.H + QHG - 1) / QHG;
+  const int64_t unit = gid / tpr;
+  const int t = (int)(gid - unit * tpr);
+  if (unit >= (int64_t)a.B * ngrp * a.S) return;
+  const int s = (int)(unit % a.S);
+  const int64_t bg = unit / a.S;
+  const int hg = (int)(bg % ngrp), b = (int)(bg / ngrp), h0 = hg * QHG;
+  const uint16_t* xb = (const uint16_t*)a.xr + b * a.xr_s[0] + (int64_t)s * a.xr_s[2] + t * 8;
+  u32x4 xv[QHG];
+#pragma unroll
+  for (int j = 0; j < QHG; ++j)
+    if (h0 + j < a.H) xv[j] = *(const u32x4*)(xb + (int64_t)(h0 + j) * a.xr_s[1]);
+  const float pos = pe_pos(a.start_pos + s, a.pos_round);
+  const f32x4 f0 = *(const f32x4*)(a.freqs + t * 8), f1 = *(const f32x4*)(a.freqs + t * 8 + 4);
+  float cs[8], sn[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pe_sincos(mul_nc(pos, e < 4 ? f0[e] : f1[e - 4]), sn[e], cs[e]);
+  if (tab && (b | hg) == 0) {
+    float* tr = tab + (int64_t)s * 2 * a.Dr + t * 8;
+    *(f32x4*)tr = f32x4{cs[0], cs[1], cs[2], cs[3]};
+    *(f32x4*)(tr + 4) = f32x4{cs[4], cs[5], cs[6], cs[7]};
+    *(f32x4*)(tr + a.Dr) = f32x4{sn[0], sn[1], sn[2], sn[3]};
+    *(f32x4*)(tr + a.Dr + 4) = f32x4{sn[4], sn[5], sn[6], sn[7]};
+  }
+#pragma unroll
+  for (int j = 0; j < QHG; ++j) {
+    const int h = h0 + j;
+    if (h >= a.H) break;
+    float x[8], cv[8], sv[8];
+    unpack8(xv[j], x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float mu = softplus_f(x[e]);
+      cv[e] = mul_nc(mu, cs[e]);
+      sv[e] = mul_nc(mu, sn[e]);
+    }
+    uint16_t* drow = (uint16_t*)a.dst + ((int64_t)(b * a.H + h) * (a.dst_rows ? a.dst_rows : a.S) + a.dst_row0 + s) * a.width;
+    *(u32x4*)(drow + t * 8) =
+        u32x4{pack_bf2(cv[0], cv[1]), pack_bf2(cv[2], cv[3]), pack_bf2(cv[4], cv[5]), pack_bf2(cv[6], cv[7])};
+    *(u32x4*)(drow + a.Dr + t * 8) =
+        u32x4{pack_bf2(sv[0], sv[1]), pack_bf2(sv[2], sv[3]), pack_bf2(sv[4], sv[5]), pack_bf2(sv[6], sv[7])};
+  }
+}
+
+// The whole PoPE prologue in one launch: nkblk blocks of key rows (vector-bound: a sin / cos and a
+// softplus per element) interleaved evenly with nqblk blocks of query rows (memory-bound: a
+// softplus per element, phases shared over QHG heads), so that both kinds share every CU.  Block i
+// is the query block cq(i) = floor(i * nqblk / n) when cq(i + 1) > cq(i), else the key block
+// i - cq(i); over the n = nkblk + nqblk blocks this takes each index of either kind once.
+__global__ __launch_bounds__(256) void prep_k_qheads_kernel(PrepArgs ak, PrepArgs aq, unsigned nkblk, unsigned nqblk,
+                                                            float* tab) {
+  const uint64_t i = blockIdx.x, n = (uint64_t)nkblk + nqblk;
+  const uint64_t cq = i * nqblk / n, cq1 = (i + 1) * nqblk / n;
+  if (cq1 > cq) prep_pope_qheads_body(aq, (int64_t)cq * 256 + threadIdx.x, tab);
+  else prep_pope_vec_body(ak, (int64_t)(i - cq) * 256 + threadIdx.x);
+}
+
 // prologues of at most this many 256-thread blocks (keys and queries together) take one launch:
 // they are bound by launch latency, not by the queries' extra sin / cos
 constexpr int64_t PREP_QK_MAX_BLOCKS = 1024;
+
+int launch_prep_k_qheads(const PrepArgs& ak, const PrepArgs& aq, float* tab, hipStream_t s) {
+  if (!prep_vec_ok(ak) || !prep_vec_query_ok(aq) || ak.cdst || aq.cdst || aq.tab || !ak.is_key || aq.Dr != ak.Dr ||
+      !tab || (uintptr_t)tab % 16 != 0)
+    return 1;
+  const int64_t nk = (int64_t)ak.B * ak.H * ak.S * (ak.Dr / 8);
+  const int64_t nq = (int64_t)aq.B * ((aq.H + QHG - 1) / QHG) * aq.S * (aq.Dr / 8);
+  const int64_t nkblk = (nk + 255) / 256, nqblk = (nq + 255) / 256;
+  if (nk == 0 || nq == 0) return 1;
+  if (nkblk + nqblk > 0x7fffffff) return -2;
+  hipLaunchKernelGGL(prep_k_qheads_kernel, dim3((unsigned)(nkblk + nqblk)), dim3(256), 0, s, ak, aq, (unsigned)nkblk,
+                     (unsigned)nqblk, tab);
+  return hipGetLastError() == hipSuccess ? 0 : -7;
+}
 
 int launch_prep_qk(const PrepArgs& ak, const PrepArgs& aq, float* tab, hipStream_t s) {
   if (!prep_vec_ok(ak) || !prep_vec_ok(aq) || ak.cdst || aq.cdst || aq.tab || !ak.is_key || aq.is_key ||
