@@ -201,8 +201,9 @@ typedef struct {
 } pe_norm_params;
 
 /* Forward that allocates nothing: pe_attn_fwd with the workspace taken from a static device array
- * of PE_NOALLOC_SCRATCH_BYTES held by the library on each GPU (from code-object load to process
- * exit).  No counterpart in the reference: it is for callers that cannot allocate device memory
+ * of PE_NOALLOC_SCRATCH_BYTES held by the library on each GPU from the load of its code object
+ * (under the HIP runtime's default deferred loading: the first call of this entry on that GPU) to
+ * process exit).  No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Calls whose
  * forward workspace (pe_attn_fwd_workspace_bytes) exceeds the scratch return PE_ERR_SCRATCH_LIMIT.
  * All calls on one GPU share its scratch: calls that overlap in time on one GPU (different streams

@@ -76,3 +76,46 @@ def test_noalloc_forward_fp32_and_limit(cuda):
     rc, _, _ = _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc=True)
     assert rc == _lib.ERRORS["PE_ERR_SCRATCH_LIMIT"]
     assert "static scratch" in L.pe_attn_strerror(rc).decode()
+
+
+_RESERVE_PROBE = r"""
+import sys, torch
+sys.path[:0] = [{root!r}, {tests!r}]
+from test_zz_no_alloc import _case, _run
+from pe_ablations_amd import _lib
+cuda = torch.device("cuda:0")
+torch.zeros(1, device=cuda)
+torch.cuda.synchronize()
+def outside_torch():
+    return torch.cuda.mem_get_info()[0] + torch.cuda.memory_reserved()
+f0 = outside_torch()
+L = _lib.lib()
+q, k, v, freqs, delta, cfg = _case(cuda, 1, 2, 300, 128, 2)
+assert _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc=False)[0] == 0
+f1 = outside_torch()
+assert _run(L, cuda, q, k, v, freqs, delta, cfg, noalloc=True)[0] == 0
+f2 = outside_torch()
+print("RESULT", f0 - f1, f1 - f2)
+"""
+
+
+def test_scratch_is_reserved_only_once_noalloc_runs(cuda):
+    """The 128 MiB scratch lives in the code object of the translation unit that defines it, which
+    the HIP runtime loads on the first use of that code object (deferred loading, its default): the
+    first pe_attn_fwd_noalloc call resolves the symbol.  A fresh process that loads the library and
+    runs the workspace forward therefore holds no scratch; the first no-alloc call then takes it.
+    Device memory outside torch's caching allocator is compared in a child process (this one may
+    already hold the scratch from the tests above)."""
+    import os
+    import subprocess
+    import sys
+    tests = os.path.dirname(os.path.abspath(__file__))
+    env = {k: v for k, v in os.environ.items() if k != "HIP_ENABLE_DEFERRED_LOADING"}
+    r = subprocess.run([sys.executable, "-c", _RESERVE_PROBE.format(root=os.path.dirname(tests), tests=tests)],
+                       capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stderr[-2000:]
+    line = [ln for ln in r.stdout.splitlines() if ln.startswith("RESULT")][-1]
+    before, at_first_noalloc = (int(x) for x in line.split()[1:])
+    mib = 1 << 20
+    assert before < 64 * mib, before / mib          # code objects of the kernels used, no scratch
+    assert at_first_noalloc >= 128 * mib, at_first_noalloc / mib
