@@ -37,8 +37,10 @@ Parity pins (each checked in ``tests/test_oracle.py``):
 * RoPE ...................... complex-multiply formulation, norm preservation, NTK / YaRN closed forms
 * whole decoder ............. S = 1 reduction to wo.wv (tests/test_decoder_host.py), zero layers,
                                causal prefix, loss at init; the SwiGLU gate order and the pre-norm
-                               placement are restated from the source only (parity unpinned beyond
-                               reading for those two)
+                               residuals by closed-form logit ratios of a hand-set one-token decoder
+* reference vectors ......... PoPE / FoPE transforms bit for bit, and the RoPE family within one
+                               float32 rounding, against outputs of the reference's own modules
+                               (tests/golden/pe_transforms.npz, tests/test_golden.py)
 """
 
 from __future__ import annotations
