@@ -78,6 +78,42 @@ def test_config2_gpt125m_fwd_bwd_bf16(cuda):
     check_slices(res, q, k, v, do, freqs, delta, 1 / math.sqrt(D), heads=[0, 11], batches=range(B), tol=2e-2)
 
 
+def test_one_launch_prologue_projection_views_ragged_heads_start_pos(cuda):
+    """A shape that takes the one-launch PoPE prologue (more than 1024 blocks; queries in groups of
+    eight heads): six heads (a single, ragged group), three batch entries, the projections'
+    (B, S, H, D) layout seen as (B, H, S, D) views, and positions starting at 37 on both sides.
+    Every (b, h) slice of two heads is checked against the oracle at the north-star bar."""
+    B, H, S, D, start = 3, 6, 2000, 64, 37
+    assert B * H * S * (D // 8) // 256 > 1024          # the launch the small path does not take
+    g = torch.Generator().manual_seed(7)
+    q, k, v, do = (torch.randn(B, S, H, D, generator=g).to(torch.bfloat16).transpose(1, 2) for _ in range(4))
+    delta = torch.rand(H, D, generator=g) * (-2 * math.pi)
+    freqs = O.pope_freqs(D)
+    scale = 1 / math.sqrt(D)
+    qg, kg, vg = (t.to(cuda).requires_grad_(True) for t in (q, k, v))
+    assert qg.stride(1) == D and qg.stride(2) == H * D   # still the projection layout on the GPU
+    dg = delta.to(cuda).requires_grad_(True)
+    out, lse = pe_attention(qg, kg, vg, mode="pope", freqs=freqs.to(cuda), delta=dg, scale=scale,
+                            start_pos_q=start, start_pos_k=start, return_lse=True)
+    out.backward(do.to(cuda))
+    torch.cuda.synchronize()
+    res = {"out": out.detach().cpu(), "lse": lse.cpu(), "dq": qg.grad.cpu(), "dk": kg.grad.cpu(),
+           "dv": vg.grad.cpu(), "ddelta": dg.grad.cpu()}
+    for h in (0, 5):
+        dd = torch.zeros(D, dtype=torch.float64)
+        for b in range(B):
+            ref = O.pope_attention_chunked(q[b, h].float(), k[b, h].float(), v[b, h].float(), freqs, delta[h],
+                                           dout=do[b, h].float(), scale=scale, start_q=start, start_k=start,
+                                           operand_dtype=torch.bfloat16, chunk=1024)
+            both = {n: err_both(res[n][b, h], ref[n]) for n in ("out", "lse", "dq", "dk", "dv")}
+            print(f"prologue case h={h} b={b} " + " ".join(f"{n}: raw {r:.2e} net {nt:.2e}"
+                                                           for n, (r, nt) in both.items()), flush=True)
+            for n, (r, _) in both.items():
+                assert r < 2e-2, (h, b, n, r)
+            dd += ref["ddelta"]
+        assert md(res["ddelta"][h], dd) / max(1.0, dd.abs().max().item()) < 2e-2
+
+
 def test_config3_fope_fwd_bwd_bf16(cuda):
     """C3: FoPE, B=4, H=16, S=4096, D=128, 4 frequencies per dim (base + 3 ~ U(0, theta_0)),
     coefficients ~ N(0, 0.1^2), floor 2pi/2048, bf16 fwd+bwd."""
